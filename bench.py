@@ -1,0 +1,203 @@
+"""Decode-step benchmark of the MI355X int8 KV path.
+
+One step = quantize-and-append of the new K/V token of every (sequence, head)
++ split-K decode attention over the 8192-token int8 history + merge, on one
+GPU with all inputs resident in HBM. Prints one JSON line.
+
+  python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pop2-bezier_amd"))
+
+METRIC = "decode-attention µs/step + achieved HBM GB/s (% of peak), B=32 ctx=8192 int8 KV"
+HBM_PEAK_GBPS = 8000.0
+SEED = 20261011
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--batch", type=int, default=32)
+    p.add_argument("--heads", type=int, default=16)
+    p.add_argument("--head-dim", type=int, default=128)
+    p.add_argument("--context", type=int, default=8192)
+    p.add_argument("--split", type=int, default=0, help="tokens per split (0 = library policy)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-rows", type=int, default=64, help="head rows timed for the CPU baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_attn_partial_b32_ctx8192.json"),
+                   help="JSON with measured HBM bytes per partial launch (rocprofv3 --pmc), if present")
+    return p.parse_args()
+
+
+def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args) -> dict:
+    """The reference's Candle CPU decode (restated in C, oracle/) on a bounded sample of head rows."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle  # noqa: E402  (CPU baseline leg only)
+
+    rows_total = q.shape[0]
+    n = min(args.cpu_rows, rows_total)
+    n -= n % heads
+    n = max(n, heads)
+    L = args.context
+    q_h = q[:n].float().reshape(n, -1).cpu().numpy()
+    k_h = kc[:n, :L].cpu().numpy()
+    v_h = vc[:n, :L].cpu().numpy()
+    ks_h = ks[:n, :L].cpu().numpy()
+    vs_h = vs[:n, :L].cpu().numpy()
+    sk_h = kn.float().reshape(rows_total, -1)[:n].cpu().numpy()
+    sv_h = vn.float().reshape(rows_total, -1)[:n].cpu().numpy()
+    past_h = past[: n // heads].cpu().numpy().astype(np.uint32)
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.cpu_baseline(q_h, k_h, v_h, ks_h, vs_h, sk_h, sv_h, past_h, heads, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or reps >= 1000:
+            break
+    per_rep_us = el / reps * 1e6
+    us_per_step = per_rep_us * rows_total / n
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(us_per_step, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": f"{n} of {rows_total} head rows x {L} tokens (Candle CPU path restated in C, "
+                      f"oracle/ppk_oracle.c cpu_baseline_decode), {reps} reps in {el:.1f} s, scaled x{rows_total / n:g}",
+            "cpu_model": model}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the int8 KV decode path shards by "
+                                   "sequence or head with no collective on the hot path (see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        return 2
+    import torch
+    import ppk
+    from ppk import synthetic
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, L = args.batch, args.heads, args.head_dim, args.context
+    rows, cap = B * H, L + 1
+    print(f"# bench: B={B} H={H} D={D} ctx={L} building arenas", file=sys.stderr, flush=True)
+    kc = torch.empty((rows, cap, D), dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((rows, cap), dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    synthetic.fill_history(kc, vc, ks, vs, L, H, SEED)
+    g = torch.Generator(device=dev).manual_seed(SEED + 1)
+    q = torch.randn((rows, 1, D), generator=g, device=dev).to(torch.bfloat16)
+    kn = synthetic.history_chunk(SEED, 2, 0, rows, H, 0, 1, D, dev, torch.bfloat16).reshape(B, H, 1, D).contiguous()
+    vn = synthetic.history_chunk(SEED, 3, 0, rows, H, 0, 1, D, dev, torch.bfloat16).reshape(B, H, 1, D).contiguous()
+    past = torch.full((B,), L, dtype=torch.int32, device=dev)
+    out = torch.empty((rows, 1, D), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    append = ppk.AppendKV(kn, vn, past, kc, vc, ks, vs)
+    attn = ppk.DecodeAttention(q, kc, vc, ks, vs, kn.reshape(rows, 1, D), vn.reshape(rows, 1, D), past, H,
+                               args.split, max_past=L, out=out)
+    split = attn.split_tokens
+
+    def step():
+        append()
+        attn()
+
+    print("# bench: warmup", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: every partial-kernel launch is bracketed by HIP events on
+    # its own stream by the library's tracer.
+    ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_PARTIAL, reset=True)
+    ppk.set_profiling(True)
+    stream = torch.cuda.current_stream(dev)
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        step()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    step_ms = t_start.elapsed_time(t_end) / args.steps
+    launches, partial_ms = ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_PARTIAL, reset=True)
+    partial_avg_ms = partial_ms / max(launches, 1)
+
+    # Algorithmic bytes: history K+V codes and scales of every row, the query,
+    # the new K/V token (read by append, its bf16 copy read by the merge as the
+    # current token) and the outputs: sum_b L_b*H*(2D+8) + q + current k,v + out.
+    hist_bytes = rows * L * (2 * D + 8)
+    q_bytes = rows * D * 2
+    partial_bytes = hist_bytes + q_bytes
+    step_bytes = hist_bytes + q_bytes + 2 * rows * D * 2 + rows * D * 4 + 2 * rows * (D + 4)
+    achieved = partial_bytes / (partial_avg_ms * 1e-3) / 1e9
+    step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
+
+    traffic = None
+    if os.path.exists(args.traffic):
+        try:
+            with open(args.traffic) as f:
+                t = json.load(f)
+            if t.get("split") == split and t.get("workload") == f"B{B}H{H}D{D}L{L}":
+                traffic = t.get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    result = {
+        "metric": METRIC,
+        "value": round(step_ms * 1e3, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels, quantised on device; bf16 q and new K/V)",
+        "config": {"workload": "BASELINE config 5: decode step = append + split-K attention + merge",
+                   "batch": B, "heads": H, "head_dim": D, "context": L, "capacity": cap, "kv": "int8 + f32 scales",
+                   "query": "bf16", "split_tokens": split, "splits": attn.nsplits},
+        "tokens_per_s": round(B / (step_ms * 1e-3), 1),
+        "step_hbm_gbps": round(step_gbps, 1),
+        "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "kernel": "ppk_attn_partial_d%d" % D, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": partial_bytes,
+                     "avg_launch_us": round(partial_avg_ms * 1e3, 2), "launches": launches},
+    }
+    if not args.no_cpu_baseline:
+        print("# bench: cpu baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, H, args)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,201 @@
+/*
+ * ppk_int8_kv.h -- C-ABI of the MI355X (gfx950) int8 KV-cache decode path.
+ *
+ * Two hand-written CDNA4 kernels sit behind this boundary:
+ *   1. quantize(-and-append): per (head, token) row of D channels,
+ *        s    = max(absmax / 127, 1e-12)            (IEEE fp32 division)
+ *        code = clamp(round_half_even(x / s), -127, 127) stored as a byte
+ *      written either densely or into a KV arena at slot past[b] + j;
+ *   2. split-K single-query decode attention over the int8 arena
+ *      (partial kernel + cross-split merge kernel).
+ *
+ * Every device buffer is caller-owned; the library never frees or allocates
+ * caller memory. All work is stream-ordered on the hipStream_t passed in
+ * (as void*), with no implicit synchronisation. Code objects for gfx950 are
+ * built ahead of time and loaded with hipModuleLoad by ppk_context_create.
+ *
+ * Status codes follow the reference C-ABI (app/native/aten_hip/cpp/painter_ffi.h:20-25):
+ *   0 success; 1 precondition/preparation failure, nothing was enqueued;
+ *   2 invalid output (self-check mismatch); 3 execution uncertain, never replay.
+ * Error text is thread-local (app/native/aten_hip/cpp/painter_ffi.cpp:12,18-19).
+ *
+ * Reference semantics: app/src/model/int8_kv_ops.rs:5-103 and
+ * app/src/model/int8_kv.cu:1-59 (head_dim 64, capacity <= 1024 there; this
+ * library extends them to head_dim 64/128/256 and any capacity < 2^31 / D).
+ */
+#ifndef PPK_INT8_KV_H
+#define PPK_INT8_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define PPK_API __attribute__((visibility("default")))
+#else
+#define PPK_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PPK_ABI_VERSION 1u
+
+enum {
+  PPK_OK = 0,
+  PPK_PRECONDITION = 1,
+  PPK_INVALID_OUTPUT = 2,
+  PPK_EXECUTION_UNCERTAIN = 3
+};
+
+/* Element types of floating tensors crossing the boundary. */
+enum { PPK_F32 = 0, PPK_BF16 = 1, PPK_F16 = 2 };
+
+/* Device-side status bits written by the quantize kernels when a flag word is supplied. */
+enum {
+  PPK_FLAG_NONFINITE = 1u, /* an input row held NaN or +-Inf (reference CPU path rejects these, int8_kv_ops.rs:16) */
+  PPK_FLAG_OVERFLOW = 2u   /* past[b] + tokens > capacity: that row was not written */
+};
+
+/* Attention flags. */
+enum {
+  /* Dequantise history as bf16(code * scale) before the dot products, exactly as
+     pp_i8_load does (app/src/model/int8_kv.cu:23-27). Default (0) dequantises in
+     fp32 with the per-token scale folded into the score and the probability. */
+  PPK_ATTN_BF16_HISTORY = 1u
+};
+
+typedef struct ppk_context ppk_context;
+
+/* ABI version, checked by loaders like pp_aten_abi_version
+   (painter_ffi.h:58, app/src/inference/aten_ffi.rs:277-280). */
+PPK_API uint32_t ppk_abi_version(void);
+
+/* Last error of the calling thread, UTF-8, at most 6000 bytes (pp_aten_last_error). */
+PPK_API const char* ppk_last_error(void);
+
+/* Load the gfx950 code object (code_object_path may be NULL: the .hsaco beside
+   this library) on HIP device `device` and resolve every kernel before any
+   launch. Replaces the runtime JIT + module cache of int8_kv_ops.rs:111-119 and
+   app/src/model/hip_kernel.rs:99-149 with an ahead-of-time code object. */
+PPK_API int32_t ppk_context_create(int32_t device, const char* code_object_path, ppk_context** out);
+PPK_API int32_t ppk_context_release(ppk_context* ctx);
+
+/* Dense quantize: src[rows, tokens, D] -> codes[rows, tokens, D], scales[rows, tokens].
+   Replaces int8_kv_ops::quantize (app/src/model/int8_kv_ops.rs:11-29), i.e. the
+   cuda::Scale + cuda::Pack custom ops (int8_kv_ops.rs:120-142, int8_kv.cu:8-18). */
+typedef struct PpkQuantizeArgs {
+  uint32_t struct_size;
+  uint32_t src_dtype;      /* PPK_F32 / PPK_BF16 / PPK_F16 */
+  const void* src;         /* [rows * tokens, D] contiguous */
+  uint8_t* codes;          /* [rows * tokens, D] two's-complement int8 */
+  float* scales;           /* [rows * tokens] */
+  uint64_t rows;           /* number of (head, token) rows: heads * tokens */
+  uint32_t head_dim;       /* D: 64, 128 or 256 */
+  uint32_t reserved;
+  uint32_t* flags;         /* optional device word, PPK_FLAG_* bits OR-ed in */
+} PpkQuantizeArgs;
+PPK_API int32_t ppk_quantize(ppk_context* ctx, void* stream, const PpkQuantizeArgs* args);
+
+/* Fused quantize + append of new K and V tokens into the int8 arenas at slot
+   past[b] + j (the commit path of Int8LayerCache::query/query_batch,
+   app/src/model/int8_cache.rs:293-359, writing through LayerCache slot
+   placement, app/src/model/cache.rs:122-154,301-478; AMD variant kv_i8_commit,
+   app/native/aten_hip/cpp/kv_int8.cpp:47-54, whose x(1/127) scale this does
+   NOT follow). Uncommitted (partial) queries need no call: their placeholder
+   slot is never read (int8_cache.rs:304-310). */
+typedef struct PpkAppendArgs {
+  uint32_t struct_size;
+  uint32_t src_dtype;      /* PPK_F32 / PPK_BF16 / PPK_F16 */
+  const void* k_src;       /* [batch, heads, tokens, D] contiguous */
+  const void* v_src;       /* [batch, heads, tokens, D] contiguous */
+  const uint32_t* past;    /* device U32[batch]: committed length of each sequence */
+  uint8_t* k_codes;        /* arena [batch*heads, capacity, D] */
+  uint8_t* v_codes;        /* arena [batch*heads, capacity, D] */
+  float* k_scales;         /* arena [batch*heads, capacity] */
+  float* v_scales;         /* arena [batch*heads, capacity] */
+  uint32_t batch, heads, tokens, head_dim, capacity;
+  uint32_t reserved;
+  uint32_t* flags;         /* optional device word, PPK_FLAG_* bits OR-ed in */
+} PpkAppendArgs;
+PPK_API int32_t ppk_quantize_append(ppk_context* ctx, void* stream, const PpkAppendArgs* args);
+
+/* Dequantize codes[rows, tokens, D] * scales[rows, tokens] to out_dtype;
+   round_bf16 != 0 rounds the fp32 product to bf16 first (the reference's
+   dequantize(.., BF16)). Replaces int8_kv_ops::dequantize
+   (int8_kv_ops.rs:30-40, pp_i8_unpack int8_kv.cu:19-22). */
+typedef struct PpkDequantizeArgs {
+  uint32_t struct_size;
+  uint32_t out_dtype;
+  const uint8_t* codes;
+  const float* scales;
+  void* out;
+  uint64_t rows;           /* heads * tokens */
+  uint32_t head_dim;
+  uint32_t round_bf16;
+} PpkDequantizeArgs;
+PPK_API int32_t ppk_dequantize(ppk_context* ctx, void* stream, const PpkDequantizeArgs* args);
+
+/* Single-query decode attention over int8 history plus the current token.
+   For row r (sequence b = r / heads, p = past[b]):
+     scores_t = softmax_scale * <q_r, K_r[t]>    t < p   (dequantised history)
+     score_p  = softmax_scale * <q_r, sk_r>              (current token, unquantised)
+     out_r    = sum_t softmax(scores)_t * V_r[t]  with V_r[p] = sv_r
+   Rows with p > capacity produce NaN (int8_kv.cu:33,51).
+   Replaces int8_kv_ops::attention (int8_kv_ops.rs:41-55) / cuda::Attention
+   (int8_kv_ops.rs:143-161) and kernels pp_i8_attention + pp_i8_merge
+   (int8_kv.cu:28-59). */
+typedef struct PpkAttentionArgs {
+  uint32_t struct_size;
+  uint32_t q_dtype;        /* dtype of q */
+  uint32_t scratch_dtype;  /* dtype of sk and sv */
+  uint32_t out_dtype;      /* PPK_F32 (reference) or PPK_BF16 / PPK_F16 */
+  uint32_t flags;          /* PPK_ATTN_* */
+  uint32_t rows;           /* batch * heads */
+  uint32_t heads;
+  uint32_t capacity;       /* arena tokens per row */
+  uint32_t head_dim;       /* 64, 128 or 256 */
+  uint32_t split_tokens;   /* tokens per split; 0 = automatic. Result does not depend on it. */
+  uint32_t max_past;       /* host upper bound of max(past); 0 = capacity. Rows beyond it give NaN. */
+  float softmax_scale;     /* 0 = 1/sqrt(head_dim) */
+  const void* q;           /* [rows, D] */
+  const uint8_t* k_codes;  /* [rows, capacity, D], 16-byte aligned */
+  const uint8_t* v_codes;  /* [rows, capacity, D], 16-byte aligned */
+  const float* k_scales;   /* [rows, capacity] */
+  const float* v_scales;   /* [rows, capacity] */
+  const void* sk;          /* [rows, D] current key (not yet quantised) */
+  const void* sv;          /* [rows, D] current value */
+  const uint32_t* past;    /* device U32[rows / heads] */
+  void* out;               /* [rows, D] */
+  void* workspace;         /* ppk_attention_workspace_bytes() bytes, 256-byte aligned */
+  uint64_t workspace_bytes;
+} PpkAttentionArgs;
+PPK_API int32_t ppk_attention_workspace_bytes(ppk_context* ctx, const PpkAttentionArgs* args, uint64_t* bytes);
+/* The launch plan the library would use for args: tokens per split, number
+   of splits and workspace bytes (ctx may be NULL: assumes 256 CUs). The
+   reference chooses split = 128 by default, clamped to 32..1024
+   (int8_kv_ops.rs:52); its result does not depend on the split. */
+PPK_API int32_t ppk_attention_plan(ppk_context* ctx, const PpkAttentionArgs* args, uint32_t* split_tokens,
+                                   uint32_t* nsplits, uint64_t* workspace_bytes);
+PPK_API int32_t ppk_decode_attention(ppk_context* ctx, void* stream, const PpkAttentionArgs* args);
+
+/* Known-answer self-check on the context's device, the three checks of
+   int8_kv_ops::prepare (int8_kv_ops.rs:56-103) plus their fp32-history twins.
+   Returns 2 with the failing check in ppk_last_error() on a numeric mismatch. */
+PPK_API int32_t ppk_prepare(ppk_context* ctx);
+
+/* Tracing: when enabled, the library brackets every launch of the named kernel
+   with HIP events on the launch stream; stats resolve them (blocking on the
+   recorded events only). Kernel ids below. The reference keeps launch counters
+   only (app/src/model/hip_kernel.rs:8-21). */
+enum { PPK_KERNEL_QUANTIZE = 0, PPK_KERNEL_APPEND = 1, PPK_KERNEL_DEQUANTIZE = 2,
+       PPK_KERNEL_ATTN_PARTIAL = 3, PPK_KERNEL_ATTN_MERGE = 4, PPK_KERNEL_COUNT = 5 };
+PPK_API int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable);
+PPK_API int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint64_t* launches,
+                                 double* total_ms, uint32_t reset);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PPK_INT8_KV_H */

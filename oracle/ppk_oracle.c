@@ -1,0 +1,365 @@
+/*
+ * ppk_oracle.c -- CPU restatement of the reference's int8 KV decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the
+ * checker (or the timed CPU baseline), never as the product path.
+ *
+ * Each function names the reference lines it restates. The reference
+ * (Rust/Candle + NVRTC CUDA + Windows HIPRTC) cannot be compiled in this
+ * image, so this restatement is pinned by closed forms, an independent numpy
+ * restatement and the reference's own known-answer checks (tests/).
+ *
+ * Built with: gcc -O2 -fno-fast-math -ffp-contract=off (oracle/build.py),
+ * so every float operation is the single IEEE-754 binary32 operation written.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* bf16 round-to-nearest-even of an f32, kept in f32 (Candle's to_dtype(BF16),
+   i.e. half::bf16::from_f32, and pp_round_bf16, app/src/model/int8_kv.cu:3-7). */
+static float round_bf16(float x) {
+  if (x != x) return x;
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/*
+ * quantize, app/src/model/int8_kv_ops.rs:11-21 (CPU branch), one row of d
+ * channels at a time:
+ *   s = (max_i |x_i| / 127).max(1e-12)            -- :17, f32::max ignores NaN
+ *   code_i = (x_i / s).round_ties_even().clamp(-127, 127) as i8 as u8   -- :18
+ * Rust's `as i8` maps NaN to 0 (f32::clamp keeps NaN); the CUDA path does the
+ * same through __float2int_rn (int8_kv.cu:17). The CPU branch rejects
+ * non-finite rows first (:16); nonfinite_rows counts them instead so callers
+ * can assert the same condition. Returns the number of non-finite rows.
+ */
+size_t oracle_quantize(const float* x, size_t rows, size_t d, uint8_t* codes, float* scales) {
+  size_t bad = 0;
+  for (size_t r = 0; r < rows; ++r) {
+    const float* row = x + r * d;
+    float amax = 0.0f;
+    int finite = 1;
+    for (size_t i = 0; i < d; ++i) {
+      amax = fmaxf(amax, fabsf(row[i]));
+      if (!isfinite(row[i])) finite = 0;
+    }
+    bad += finite ? 0 : 1;
+    const float s = fmaxf(amax / 127.0f, 1e-12f);
+    scales[r] = s;
+    for (size_t i = 0; i < d; ++i) {
+      float q = rintf(row[i] / s); /* default rounding mode: ties to even */
+      int code;
+      if (q != q) code = 0;
+      else code = (int)fminf(fmaxf(q, -127.0f), 127.0f);
+      codes[r * d + i] = (uint8_t)(int8_t)code;
+    }
+  }
+  return bad;
+}
+
+/*
+ * dequantize, int8_kv_ops.rs:33-35 (CPU branch) / pp_i8_unpack int8_kv.cu:19-22:
+ *   y = (code as i8) as f32 * s[row]   (one f32 multiply)
+ * round_bf16 != 0 applies Candle's .to_dtype(BF16) (int8_kv_ops.rs:35,68).
+ */
+void oracle_dequantize(const uint8_t* codes, const float* scales, size_t rows, size_t d, int round,
+                       float* out) {
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t i = 0; i < d; ++i) {
+      const float y = (float)(int8_t)codes[r * d + i] * scales[r];
+      out[r * d + i] = round ? round_bf16(y) : y;
+    }
+}
+
+/*
+ * append placement, Int8LayerCache::query_batch commit path
+ * (app/src/model/int8_cache.rs:326-359) through LayerCache slot placement
+ * (app/src/model/cache.rs:301-478): the new tokens of sequence b are
+ * quantized (a1) and land at slots past[b] .. past[b]+tokens-1 of every head
+ * row bh = b*heads + h of the [B*H, capacity, d] arenas; nothing else changes.
+ * Rows whose slots would pass capacity are skipped (the reference refuses the
+ * whole call on the host before writing, cache.rs:221-223). Returns the
+ * number of skipped (row, token) pairs.
+ */
+size_t oracle_append(const float* src, size_t batch, size_t heads, size_t tokens, size_t d, const uint32_t* past,
+                     size_t capacity, uint8_t* codes, float* scales) {
+  size_t skipped = 0;
+  uint8_t* tmp = (uint8_t*)malloc(d);
+  for (size_t b = 0; b < batch; ++b)
+    for (size_t h = 0; h < heads; ++h)
+      for (size_t t = 0; t < tokens; ++t) {
+        const size_t bh = b * heads + h;
+        const uint64_t slot = (uint64_t)past[b] + t;
+        if (slot >= capacity) {
+          ++skipped;
+          continue;
+        }
+        float s;
+        oracle_quantize(src + (bh * tokens + t) * d, 1, d, tmp, &s);
+        memcpy(codes + (bh * capacity + slot) * d, tmp, d);
+        scales[bh * capacity + slot] = s;
+      }
+  free(tmp);
+  return skipped;
+}
+
+/*
+ * Decode attention, the semantics of int8_kv_ops::attention
+ * (int8_kv_ops.rs:41-55) as computed by pp_i8_attention + pp_i8_merge
+ * (int8_kv.cu:28-59) and checked by the host formula of int8_kv_ops.rs:69-73,
+ * 94-98, accumulated in f64:
+ *   row r, sequence b = r / heads, p = past[b]
+ *   K_t = dequant(k[r, t]) for t < p,  K_p = sk[r]  (current token unquantized, :36-37)
+ *   V_t likewise with sv[r]                         (:49)
+ *   s_t = scale * <q_r, K_t>;  out_r = sum_t e^{s_t - max s} V_t / sum_t e^{s_t - max s}
+ * dequant is the f32 product code * scale (history_bf16 = 0; Candle's CPU
+ * dequantize to F32) or its bf16 rounding (history_bf16 = 1; pp_i8_load,
+ * int8_kv.cu:23-27). p > capacity yields NaN (:33,51,58).
+ */
+void oracle_attention(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
+                      const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
+                      size_t capacity, size_t d, float scale, int history_bf16, double* out) {
+  double* scores = NULL;
+  size_t cap_scores = 0;
+  for (size_t r = 0; r < rows; ++r) {
+    const uint32_t p = past[r / heads];
+    double* o = out + r * d;
+    if (p > capacity) {
+      for (size_t i = 0; i < d; ++i) o[i] = NAN;
+      continue;
+    }
+    if (cap_scores < (size_t)p + 1) {
+      cap_scores = (size_t)p + 1;
+      scores = (double*)realloc(scores, cap_scores * sizeof(double));
+    }
+    const float* qr = q + r * d;
+    double mx = -INFINITY;
+    for (size_t t = 0; t <= p; ++t) {
+      double acc = 0.0;
+      for (size_t i = 0; i < d; ++i) {
+        float kv;
+        if (t == p) kv = sk[r * d + i];
+        else {
+          kv = (float)(int8_t)k[(r * capacity + t) * d + i] * ks[r * capacity + t];
+          if (history_bf16) kv = round_bf16(kv);
+        }
+        acc += (double)qr[i] * (double)kv;
+      }
+      scores[t] = acc * (double)scale;
+      if (scores[t] > mx) mx = scores[t];
+    }
+    double z = 0.0;
+    for (size_t t = 0; t <= p; ++t) {
+      scores[t] = exp(scores[t] - mx);
+      z += scores[t];
+    }
+    for (size_t i = 0; i < d; ++i) o[i] = 0.0;
+    for (size_t t = 0; t <= p; ++t) {
+      const double w = scores[t];
+      for (size_t i = 0; i < d; ++i) {
+        float vv;
+        if (t == p) vv = sv[r * d + i];
+        else {
+          vv = (float)(int8_t)v[(r * capacity + t) * d + i] * vs[r * capacity + t];
+          if (history_bf16) vv = round_bf16(vv);
+        }
+        o[i] += w * (double)vv;
+      }
+    }
+    for (size_t i = 0; i < d; ++i) o[i] /= z;
+  }
+  free(scores);
+}
+
+/*
+ * The reference kernel's own f32 split-K arithmetic, restated operation by
+ * operation (int8_kv.cu:28-59 generalised from 64 channels to d and from the
+ * 0.125 constant to `scale`): partitions of `split` tokens over [0, capacity]
+ * (cuda::Attention launches ceil((capacity+1)/split), int8_kv_ops.rs:153);
+ * per partition the local max m, z = sum e^{s-m} (expf), y_d = sum e^{s-m} v_d,
+ * bf16-rounded history (pp_i8_load); merge M = max m, out = sum e^{m-M} y / sum
+ * e^{m-M} z, NaN when the denominator is not positive or p > capacity.
+ * Summation order differs from the device's (a tree of shuffles); results
+ * agree with the f64 oracle to the reference's own 2e-5 check tolerance.
+ */
+void oracle_attention_splitk_reference(const float* q, const uint8_t* k, const uint8_t* v, const float* ks,
+                                       const float* vs, const float* sk, const float* sv, const uint32_t* past,
+                                       size_t rows, size_t heads, size_t capacity, size_t d, float scale,
+                                       size_t split, float* out) {
+  const size_t splits = (capacity + 1 + split - 1) / split;
+  float* part = (float*)malloc(splits * (d + 2) * sizeof(float));
+  float* sc = (float*)malloc(split * sizeof(float));
+  for (size_t r = 0; r < rows; ++r) {
+    const uint32_t p = past[r / heads];
+    const int valid = p <= capacity;
+    const size_t length = (size_t)p + 1;
+    for (size_t part_i = 0; part_i < splits; ++part_i) {
+      const size_t begin = part_i * split;
+      const size_t end = valid ? (begin + split < length ? begin + split : length) : 0;
+      float m = -3.402823466e38f;
+      for (size_t t = 0; t < split; ++t) {
+        const size_t at = begin + t;
+        float s = -3.402823466e38f;
+        if (at < end) {
+          float dot = 0.0f;
+          for (size_t i = 0; i < d; ++i) {
+            const float kv = at == p ? sk[r * d + i]
+                                     : round_bf16((float)(int8_t)k[(r * capacity + at) * d + i] * ks[r * capacity + at]);
+            dot += q[r * d + i] * kv;
+          }
+          s = dot * scale;
+        }
+        sc[t] = s;
+        m = fmaxf(m, s);
+      }
+      float z = 0.0f;
+      for (size_t t = 0; t < split; ++t) {
+        const float e = begin + t < end ? expf(sc[t] - m) : 0.0f;
+        sc[t] = e;
+        z += e;
+      }
+      float* rec = part + part_i * (d + 2);
+      rec[0] = m;
+      rec[1] = z;
+      for (size_t i = 0; i < d; ++i) {
+        float sum = 0.0f;
+        for (size_t at = begin; at < end; ++at) {
+          const float value = at == p ? sv[r * d + i]
+                                      : round_bf16((float)(int8_t)v[(r * capacity + at) * d + i] * vs[r * capacity + at]);
+          sum += sc[at - begin] * value;
+        }
+        rec[2 + i] = valid ? sum : NAN;
+      }
+    }
+    float M = -3.402823466e38f;
+    for (size_t s = 0; s < splits; ++s) M = fmaxf(M, part[s * (d + 2)]);
+    for (size_t i = 0; i < d; ++i) {
+      float z = 0.0f, y = 0.0f;
+      for (size_t s = 0; s < splits; ++s) {
+        const float w = expf(part[s * (d + 2)] - M);
+        z += part[s * (d + 2) + 1] * w;
+        y += part[s * (d + 2) + 2 + i] * w;
+      }
+      out[r * d + i] = z > 0.0f ? y / z : NAN;
+    }
+  }
+  free(part);
+  free(sc);
+}
+
+/* ------------------------------------------------------------------------
+ * CPU baseline: the reference's Candle CPU decode for an int8 history,
+ * op for op (app/src/model/mod.rs:716-720, batch.rs:211-222):
+ *   1. dequantize history K and V to dense f32 tensors (int8_kv_ops.rs:33-35)
+ *      and concatenate the current token (cache.rs query_int8_prefill :133-141)
+ *   2. scores = q . K^T                 (gemm, cpu_backend/mod.rs:1380-1450)
+ *   3. scores = scores * (1/sqrt(d))    (affine, cpu_backend/mod.rs:311-317)
+ *   4. softmax_last_dim: max, exp(x - max), sum, divide (candle-nn)
+ *   5. out = probs . V                  (gemm)
+ * in f32, parallel over (b, h) rows like Candle's Rayon pool
+ * (vendor/candle-core/src/utils.rs:327-346). The timed baseline of bench.py.
+ * ------------------------------------------------------------------------ */
+typedef struct {
+  const float* q;
+  const uint8_t *k, *v;
+  const float *ks, *vs, *sk, *sv;
+  const uint32_t* past;
+  size_t rows, heads, capacity, d;
+  float scale;
+  float* out;
+  size_t row_begin, row_end;
+} BaselineJob;
+
+static void* baseline_worker(void* arg) {
+  const BaselineJob* j = (const BaselineJob*)arg;
+  const size_t d = j->d;
+  float* kd = NULL;
+  float* vd = NULL;
+  float* sc = NULL;
+  size_t have = 0;
+  for (size_t r = j->row_begin; r < j->row_end; ++r) {
+    const uint32_t p = j->past[r / j->heads];
+    float* o = j->out + r * d;
+    if (p > j->capacity) {
+      for (size_t i = 0; i < d; ++i) o[i] = NAN;
+      continue;
+    }
+    const size_t n = (size_t)p + 1;
+    if (have < n) {
+      have = n;
+      kd = (float*)realloc(kd, n * d * sizeof(float));
+      vd = (float*)realloc(vd, n * d * sizeof(float));
+      sc = (float*)realloc(sc, n * sizeof(float));
+    }
+    /* 1. dequantize + concatenate */
+    oracle_dequantize(j->k + r * j->capacity * d, j->ks + r * j->capacity, p, d, 0, kd);
+    oracle_dequantize(j->v + r * j->capacity * d, j->vs + r * j->capacity, p, d, 0, vd);
+    memcpy(kd + (size_t)p * d, j->sk + r * d, d * sizeof(float));
+    memcpy(vd + (size_t)p * d, j->sv + r * d, d * sizeof(float));
+    /* 2. q . K^T */
+    const float* qr = j->q + r * d;
+    for (size_t t = 0; t < n; ++t) {
+      float acc = 0.0f;
+      for (size_t i = 0; i < d; ++i) acc += qr[i] * kd[t * d + i];
+      sc[t] = acc;
+    }
+    /* 3. affine */
+    for (size_t t = 0; t < n; ++t) sc[t] = sc[t] * j->scale;
+    /* 4. softmax_last_dim */
+    float mx = -INFINITY;
+    for (size_t t = 0; t < n; ++t) mx = fmaxf(mx, sc[t]);
+    float z = 0.0f;
+    for (size_t t = 0; t < n; ++t) {
+      sc[t] = expf(sc[t] - mx);
+      z += sc[t];
+    }
+    for (size_t t = 0; t < n; ++t) sc[t] /= z;
+    /* 5. probs . V */
+    for (size_t i = 0; i < d; ++i) o[i] = 0.0f;
+    for (size_t t = 0; t < n; ++t)
+      for (size_t i = 0; i < d; ++i) o[i] += sc[t] * vd[t * d + i];
+  }
+  free(kd);
+  free(vd);
+  free(sc);
+  return NULL;
+}
+
+/* Runs the baseline over rows [0, rows) with `threads` POSIX threads. */
+int cpu_baseline_decode(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
+                        const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
+                        size_t capacity, size_t d, float scale, size_t threads, float* out) {
+  if (threads < 1) threads = 1;
+  if (threads > rows) threads = rows;
+  pthread_t* tid = (pthread_t*)malloc(threads * sizeof(pthread_t));
+  BaselineJob* jobs = (BaselineJob*)malloc(threads * sizeof(BaselineJob));
+  for (size_t t = 0; t < threads; ++t) {
+    BaselineJob jb = {q, k, v, ks, vs, sk, sv, past, rows, heads, capacity, d, scale, out,
+                      rows * t / threads, rows * (t + 1) / threads};
+    jobs[t] = jb;
+  }
+  int rc = 0;
+  char* started = (char*)calloc(threads, 1);
+  for (size_t t = 1; t < threads; ++t) {
+    if (pthread_create(&tid[t], NULL, baseline_worker, &jobs[t]) == 0) started[t] = 1;
+    else rc = -1;
+  }
+  baseline_worker(&jobs[0]);
+  for (size_t t = 1; t < threads; ++t) {
+    if (started[t]) pthread_join(tid[t], NULL);
+    else baseline_worker(&jobs[t]); /* run a job whose thread failed to start inline */
+  }
+  free(started);
+  free(tid);
+  free(jobs);
+  return rc;
+}

@@ -1,0 +1,451 @@
+// C-ABI shim over the gfx950 code object: context/module management,
+// argument validation (status 1, nothing enqueued), stream-ordered launches
+// (status 3 once a launch was attempted) and optional event tracing.
+//
+// Conventions follow the reference C-ABI: status codes and thread-local last
+// error (app/native/aten_hip/cpp/painter_ffi.h:20-25, painter_ffi.cpp:12-29);
+// validation of every span before the first enqueue (app/src/model/hip_attention.rs:63-88).
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "ppk_internal.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class Op>
+int32_t call(Op&& op) {
+  g_last_error.clear();
+  try {
+    op();
+    return PPK_OK;
+  } catch (const ppk::PreconditionError& e) {
+    g_last_error = e.what();
+    if (g_last_error.size() > 6000) g_last_error.resize(6000);
+    return PPK_PRECONDITION;
+  } catch (const ppk::InvalidOutputError& e) {
+    g_last_error = e.what();
+    if (g_last_error.size() > 6000) g_last_error.resize(6000);
+    return PPK_INVALID_OUTPUT;
+  } catch (const ppk::UncertainError& e) {
+    g_last_error = e.what();
+    if (g_last_error.size() > 6000) g_last_error.resize(6000);
+    return PPK_EXECUTION_UNCERTAIN;
+  } catch (const std::exception& e) {
+    g_last_error = std::string("HIP_EXECUTION_UNCERTAIN: ") + e.what();
+    if (g_last_error.size() > 6000) g_last_error.resize(6000);
+    return PPK_EXECUTION_UNCERTAIN;
+  } catch (...) {
+    g_last_error = "HIP_EXECUTION_UNCERTAIN: unrecognised native exception";
+    return PPK_EXECUTION_UNCERTAIN;
+  }
+}
+
+const char* kFnNames[ppk::kFnCount] = {
+    "ppk_quantize_d64", "ppk_quantize_d128", "ppk_quantize_d256", "ppk_dequantize",
+    "ppk_attn_partial_d64", "ppk_attn_partial_d128", "ppk_attn_partial_d256",
+    "ppk_attn_partial_bf16h_d64", "ppk_attn_partial_bf16h_d128", "ppk_attn_partial_bf16h_d256",
+    "ppk_attn_merge_d64", "ppk_attn_merge_d128", "ppk_attn_merge_d256",
+};
+
+std::string default_code_object() {
+  Dl_info info{};
+  if (dladdr(reinterpret_cast<void*>(&ppk_abi_version), &info) == 0 || !info.dli_fname)
+    throw ppk::PreconditionError("cannot locate libppk to find the default code object");
+  std::string path(info.dli_fname);
+  const auto slash = path.find_last_of('/');
+  path = (slash == std::string::npos) ? std::string(".") : path.substr(0, slash);
+  return path + "/ppk_kernels.hsaco";
+}
+
+void check_prep(hipError_t status, const char* what) {
+  if (status != hipSuccess) throw ppk::PreconditionError(std::string(what) + ": " + hipGetErrorString(status));
+}
+
+int dim_index(uint32_t head_dim) {
+  switch (head_dim) {
+    case 64: return 0;
+    case 128: return 1;
+    case 256: return 2;
+    default: throw ppk::PreconditionError("head_dim must be 64, 128 or 256, got " + std::to_string(head_dim));
+  }
+}
+
+bool valid_dtype(uint32_t t) { return t == PPK_F32 || t == PPK_BF16 || t == PPK_F16; }
+size_t dtype_bytes(uint32_t t) { return t == PPK_F32 ? 4 : 2; }
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+template <class Args>
+void launch(ppk_context* ctx, int prof_kernel, ppk::Fn fn, uint32_t grid, uint32_t block, uint32_t lds,
+            hipStream_t stream, Args& args) {
+  void* params[] = {&args};
+  ppk::EventPair ev;
+  bool traced = false;
+  if (ctx->profiling) {
+    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
+    if (ctx->pool.empty()) {
+      if (hipEventCreate(&ev.start) != hipSuccess || hipEventCreate(&ev.stop) != hipSuccess)
+        throw ppk::PreconditionError("hipEventCreate failed for tracing");
+    } else {
+      ev = ctx->pool.back();
+      ctx->pool.pop_back();
+    }
+    traced = true;
+  }
+  if (traced && hipEventRecord(ev.start, stream) != hipSuccess)
+    throw ppk::UncertainError(std::string("event record before ") + kFnNames[fn]);
+  const hipError_t st =
+      hipModuleLaunchKernel(ctx->fn[fn], grid, 1, 1, block, 1, 1, lds, stream, params, nullptr);
+  if (st != hipSuccess) throw ppk::UncertainError(std::string(kFnNames[fn]) + ": " + hipGetErrorString(st));
+  if (traced) {
+    if (hipEventRecord(ev.stop, stream) != hipSuccess)
+      throw ppk::UncertainError(std::string("event record after ") + kFnNames[fn]);
+    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
+    ctx->pending[prof_kernel].push_back(ev);
+  } else {
+    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
+    ctx->launches[prof_kernel] += 1;
+  }
+}
+
+}  // namespace
+
+namespace ppk {
+
+DeviceGuard::DeviceGuard(int device) {
+  if (hipGetDevice(&previous_) != hipSuccess) previous_ = -1;
+  if (previous_ != device) {
+    const hipError_t st = hipSetDevice(device);
+    if (st != hipSuccess) throw PreconditionError(std::string("hipSetDevice: ") + hipGetErrorString(st));
+    changed_ = true;
+  }
+}
+DeviceGuard::~DeviceGuard() {
+  if (changed_ && previous_ >= 0) (void)hipSetDevice(previous_);
+}
+
+AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) {
+  require(a.struct_size >= sizeof(PpkAttentionArgs), "PpkAttentionArgs.struct_size too small");
+  AttentionPlan plan;
+  plan.head_dim = a.head_dim;
+  dim_index(a.head_dim);
+  require(valid_dtype(a.q_dtype) && valid_dtype(a.scratch_dtype) && valid_dtype(a.out_dtype),
+          "INT8 attention dtype must be f32, bf16 or f16");
+  require((a.flags & ~uint32_t(PPK_ATTN_BF16_HISTORY)) == 0, "unknown INT8 attention flags");
+  require(a.heads > 0 && a.rows > 0 && a.rows % a.heads == 0, "INT8 attention geometry differs: rows % heads");
+  require(a.capacity > 0, "INT8 attention capacity must be positive");
+  require(uint64_t(a.capacity) * a.head_dim <= (uint64_t(1) << 40), "INT8 attention capacity too large");
+  require(a.max_past <= a.capacity, "max_past exceeds capacity");
+  require(std::isfinite(a.softmax_scale) && a.softmax_scale >= 0.f, "softmax_scale must be finite and >= 0");
+
+  const uint32_t tpl = 64u / (a.head_dim / 16u);
+  const uint64_t span = a.max_past ? a.max_past : a.capacity;
+  uint32_t split;
+  if (a.split_tokens) {
+    split = std::min<uint32_t>(std::max<uint32_t>(a.split_tokens, tpl), 8192u);
+    split = (split + tpl - 1) / tpl * tpl;
+  } else {
+    // Smallest power-of-two split (>= 64 tokens) whose block count fits one
+    // resident round of one-wave blocks (about 20 per CU at 90 VGPRs).
+    const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 20;
+    split = 64;
+    while (split < 8192 && uint64_t(a.rows) * ((span + split - 1) / split) > budget) split <<= 1;
+  }
+  plan.split = split;
+  plan.nsplits = uint32_t(std::max<uint64_t>(1, (span + split - 1) / split));
+  require(uint64_t(plan.nsplits) * a.rows <= 0x7fffffffu, "INT8 attention grid too large");
+  plan.y_bytes = (uint64_t(a.rows) * plan.nsplits * a.head_dim * 4 + 255) / 256 * 256;
+  plan.mz_bytes = (uint64_t(a.rows) * plan.nsplits * 2 * 4 + 255) / 256 * 256;
+  plan.workspace_bytes = plan.y_bytes + plan.mz_bytes;
+  return plan;
+}
+
+void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a) {
+  require(a.struct_size >= sizeof(PpkQuantizeArgs), "PpkQuantizeArgs.struct_size too small");
+  const int di = dim_index(a.head_dim);
+  require(valid_dtype(a.src_dtype), "INT8 KV source dtype must be f32, bf16 or f16");
+  require(a.rows > 0, "INT8 KV requires dense [heads,tokens,D] with heads*tokens > 0");
+  require(a.rows <= (uint64_t(1) << 36), "INT8 KV dimensions overflow");
+  require(a.src && a.codes && a.scales, "INT8 KV null pointer");
+  require(aligned(a.src, dtype_bytes(a.src_dtype)) && aligned(a.codes, 4) && aligned(a.scales, 4) &&
+              (!a.flags || aligned(a.flags, 4)),
+          "INT8 KV operand misaligned");
+  QuantizeArgs k{};
+  k.src[0] = a.src;
+  k.codes[0] = a.codes;
+  k.scales[0] = a.scales;
+  k.flags = a.flags;
+  k.rows = a.rows;
+  k.src_dtype = a.src_dtype;
+  k.ntensors = 1;
+  const uint64_t grid = (a.rows + 3) / 4;
+  require(grid <= 0x7fffffffu, "INT8 KV quantize grid too large");
+  DeviceGuard guard(ctx->device);
+  launch(ctx, PPK_KERNEL_QUANTIZE, Fn(kQuantize64 + di), uint32_t(grid), 256, 0, stream, k);
+}
+
+void run_append(ppk_context* ctx, hipStream_t stream, const PpkAppendArgs& a) {
+  require(a.struct_size >= sizeof(PpkAppendArgs), "PpkAppendArgs.struct_size too small");
+  const int di = dim_index(a.head_dim);
+  require(valid_dtype(a.src_dtype), "INT8 KV source dtype must be f32, bf16 or f16");
+  require(a.batch > 0 && a.heads > 0 && a.tokens > 0 && a.capacity > 0,
+          "INT8 batch requires [B,H,tokens,D] scratch with B, H, tokens, capacity > 0");
+  require(a.k_src && a.v_src && a.past && a.k_codes && a.v_codes && a.k_scales && a.v_scales,
+          "INT8 append null pointer");
+  require(aligned(a.k_src, dtype_bytes(a.src_dtype)) && aligned(a.v_src, dtype_bytes(a.src_dtype)) &&
+              aligned(a.k_codes, 4) && aligned(a.v_codes, 4) && aligned(a.k_scales, 4) &&
+              aligned(a.v_scales, 4) && aligned(a.past, 4) && (!a.flags || aligned(a.flags, 4)),
+          "INT8 append operand misaligned");
+  const uint64_t rows = uint64_t(a.batch) * a.heads * a.tokens;
+  require(rows <= (uint64_t(1) << 36), "INT8 physical head rows overflow");
+  QuantizeArgs k{};
+  k.src[0] = a.k_src;
+  k.src[1] = a.v_src;
+  k.codes[0] = a.k_codes;
+  k.codes[1] = a.v_codes;
+  k.scales[0] = a.k_scales;
+  k.scales[1] = a.v_scales;
+  k.past = a.past;
+  k.flags = a.flags;
+  k.rows = rows;
+  k.heads = a.heads;
+  k.tokens = a.tokens;
+  k.capacity = a.capacity;
+  k.src_dtype = a.src_dtype;
+  k.ntensors = 2;
+  const uint64_t grid = (2 * rows + 3) / 4;
+  require(grid <= 0x7fffffffu, "INT8 append grid too large");
+  DeviceGuard guard(ctx->device);
+  launch(ctx, PPK_KERNEL_APPEND, Fn(kQuantize64 + di), uint32_t(grid), 256, 0, stream, k);
+}
+
+void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArgs& a) {
+  require(a.struct_size >= sizeof(PpkDequantizeArgs), "PpkDequantizeArgs.struct_size too small");
+  dim_index(a.head_dim);
+  require(valid_dtype(a.out_dtype), "INT8 dequantize dtype must be f32, bf16 or f16");
+  require(a.rows > 0 && a.rows <= (uint64_t(1) << 36), "INT8 dequantize rows out of range");
+  require(a.codes && a.scales && a.out, "INT8 dequantize null pointer");
+  require(aligned(a.codes, 16) && aligned(a.out, 16) && aligned(a.scales, 4), "INT8 dequantize operand misaligned");
+  DequantizeArgs k{};
+  k.codes = a.codes;
+  k.scales = a.scales;
+  k.out = a.out;
+  k.rows = a.rows;
+  k.head_dim = a.head_dim;
+  k.out_dtype = a.out_dtype;
+  k.round_bf16 = a.round_bf16 ? 1u : 0u;
+  const uint64_t chunks = a.rows * (a.head_dim / 16);
+  const uint64_t grid = std::min<uint64_t>((chunks + 255) / 256, uint64_t(std::max(ctx->cu_count, 1)) * 32);
+  DeviceGuard guard(ctx->device);
+  launch(ctx, PPK_KERNEL_DEQUANTIZE, kDequantize, uint32_t(grid), 256, 0, stream, k);
+}
+
+void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a) {
+  const AttentionPlan plan = plan_attention(ctx, a);
+  require(a.q && a.k_codes && a.v_codes && a.k_scales && a.v_scales && a.sk && a.sv && a.past && a.out,
+          "INT8 attention null pointer");
+  require(aligned(a.k_codes, 16) && aligned(a.v_codes, 16), "INT8 codes must be 16-byte aligned");
+  require(aligned(a.k_scales, 4) && aligned(a.v_scales, 4) && aligned(a.past, 4), "INT8 scales/lengths misaligned");
+  require(aligned(a.q, dtype_bytes(a.q_dtype)) && aligned(a.sk, dtype_bytes(a.scratch_dtype)) &&
+              aligned(a.sv, dtype_bytes(a.scratch_dtype)) && aligned(a.out, dtype_bytes(a.out_dtype)),
+          "INT8 attention float operand misaligned");
+  require(a.workspace && aligned(a.workspace, 256), "INT8 attention workspace missing or not 256-byte aligned");
+  require(a.workspace_bytes >= plan.workspace_bytes,
+          "INT8 attention workspace too small: need " + std::to_string(plan.workspace_bytes) + " bytes");
+  const int di = dim_index(a.head_dim);
+  const float scale = a.softmax_scale > 0.f ? a.softmax_scale : 1.0f / std::sqrt(float(a.head_dim));
+  const float scale_log2 = scale * 1.4426950408889634f;
+
+  PartialArgs p{};
+  p.q = a.q;
+  p.k = a.k_codes;
+  p.v = a.v_codes;
+  p.ks = a.k_scales;
+  p.vs = a.v_scales;
+  p.past = a.past;
+  p.part_y = static_cast<float*>(a.workspace);
+  p.part_mz = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + plan.y_bytes);
+  p.rows = a.rows;
+  p.heads = a.heads;
+  p.capacity = a.capacity;
+  p.split_tokens = plan.split;
+  p.nsplits = plan.nsplits;
+  p.q_dtype = a.q_dtype;
+  p.scale_log2 = scale_log2;
+
+  MergeArgs m{};
+  m.q = a.q;
+  m.sk = a.sk;
+  m.sv = a.sv;
+  m.past = a.past;
+  m.part_y = p.part_y;
+  m.part_mz = p.part_mz;
+  m.out = a.out;
+  m.rows = a.rows;
+  m.heads = a.heads;
+  m.capacity = a.capacity;
+  m.split_tokens = plan.split;
+  m.nsplits = plan.nsplits;
+  m.q_dtype = a.q_dtype;
+  m.scratch_dtype = a.scratch_dtype;
+  m.out_dtype = a.out_dtype;
+  m.scale_log2 = scale_log2;
+
+  const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
+  const Fn partial = Fn((bf16h ? kPartialBf16h64 : kPartial64) + di);
+  const uint32_t lds = 2 * plan.split * 4;
+  DeviceGuard guard(ctx->device);
+  launch(ctx, PPK_KERNEL_ATTN_PARTIAL, partial, plan.nsplits * a.rows, 64, lds, stream, p);
+  launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMerge64 + di), a.rows, 64, 0, stream, m);
+}
+
+}  // namespace ppk
+
+extern "C" {
+
+uint32_t ppk_abi_version(void) { return PPK_ABI_VERSION; }
+
+const char* ppk_last_error(void) { return g_last_error.c_str(); }
+
+int32_t ppk_context_create(int32_t device, const char* code_object_path, ppk_context** out) {
+  if (out) *out = nullptr;
+  return call([&] {
+    ppk::require(out != nullptr, "ppk_context_create: null output pointer");
+    int count = 0;
+    check_prep(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    ppk::require(device >= 0 && device < count, "HIP device ordinal out of range");
+    auto ctx = std::make_unique<ppk_context>();
+    ctx->device = device;
+    ppk::DeviceGuard guard(device);
+    hipDeviceProp_t prop{};
+    check_prep(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    ppk::require(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0,
+                 std::string("code object is built for gfx950, device is ") + prop.gcnArchName);
+    ctx->cu_count = prop.multiProcessorCount;
+    ctx->code_object = code_object_path ? std::string(code_object_path) : default_code_object();
+    check_prep(hipModuleLoad(&ctx->module, ctx->code_object.c_str()),
+               ("hipModuleLoad " + ctx->code_object).c_str());
+    for (int i = 0; i < ppk::kFnCount; ++i) {
+      const hipError_t st = hipModuleGetFunction(&ctx->fn[i], ctx->module, kFnNames[i]);
+      if (st != hipSuccess) {
+        (void)hipModuleUnload(ctx->module);
+        ctx->module = nullptr;
+        throw ppk::PreconditionError(std::string("kernel symbol missing: ") + kFnNames[i]);
+      }
+    }
+    *out = ctx.release();
+  });
+}
+
+int32_t ppk_context_release(ppk_context* ctx) {
+  return call([&] {
+    if (!ctx) return;
+    std::unique_ptr<ppk_context> owned(ctx);
+    ppk::DeviceGuard guard(ctx->device);
+    for (auto& list : ctx->pending)
+      for (auto& ev : list) {
+        (void)hipEventDestroy(ev.start);
+        (void)hipEventDestroy(ev.stop);
+      }
+    for (auto& ev : ctx->pool) {
+      (void)hipEventDestroy(ev.start);
+      (void)hipEventDestroy(ev.stop);
+    }
+    if (ctx->module) (void)hipModuleUnload(ctx->module);
+  });
+}
+
+int32_t ppk_quantize(ppk_context* ctx, void* stream, const PpkQuantizeArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_quantize: null context or arguments");
+    ppk::run_quantize(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_quantize_append(ppk_context* ctx, void* stream, const PpkAppendArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_quantize_append: null context or arguments");
+    ppk::run_append(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_dequantize(ppk_context* ctx, void* stream, const PpkDequantizeArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_dequantize: null context or arguments");
+    ppk::run_dequantize(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_attention_workspace_bytes(ppk_context* ctx, const PpkAttentionArgs* args, uint64_t* bytes) {
+  if (bytes) *bytes = 0;
+  return call([&] {
+    ppk::require(args && bytes, "ppk_attention_workspace_bytes: null argument");
+    *bytes = ppk::plan_attention(ctx, *args).workspace_bytes;
+  });
+}
+
+int32_t ppk_attention_plan(ppk_context* ctx, const PpkAttentionArgs* args, uint32_t* split_tokens,
+                           uint32_t* nsplits, uint64_t* workspace_bytes) {
+  return call([&] {
+    ppk::require(args != nullptr, "ppk_attention_plan: null arguments");
+    const ppk::AttentionPlan plan = ppk::plan_attention(ctx, *args);
+    if (split_tokens) *split_tokens = plan.split;
+    if (nsplits) *nsplits = plan.nsplits;
+    if (workspace_bytes) *workspace_bytes = plan.workspace_bytes;
+  });
+}
+
+int32_t ppk_decode_attention(ppk_context* ctx, void* stream, const PpkAttentionArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_decode_attention: null context or arguments");
+    ppk::run_attention(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_prepare(ppk_context* ctx) {
+  return call([&] {
+    ppk::require(ctx != nullptr, "ppk_prepare: null context");
+    ppk::prepare_self_check(ctx);
+  });
+}
+
+int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable) {
+  return call([&] {
+    ppk::require(ctx != nullptr, "ppk_context_set_profiling: null context");
+    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
+    ctx->profiling = enable != 0;
+  });
+}
+
+int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint64_t* launches, double* total_ms,
+                                 uint32_t reset) {
+  return call([&] {
+    ppk::require(ctx && kernel < PPK_KERNEL_COUNT, "ppk_context_kernel_stats: bad context or kernel id");
+    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
+    ppk::DeviceGuard guard(ctx->device);
+    for (auto& ev : ctx->pending[kernel]) {
+      const hipError_t st = hipEventSynchronize(ev.stop);
+      if (st != hipSuccess) throw ppk::UncertainError(std::string("hipEventSynchronize: ") + hipGetErrorString(st));
+      float ms = 0.f;
+      if (hipEventElapsedTime(&ms, ev.start, ev.stop) != hipSuccess)
+        throw ppk::UncertainError("hipEventElapsedTime failed");
+      ctx->launches[kernel] += 1;
+      ctx->total_ms[kernel] += ms;
+      ctx->pool.push_back(ev);
+    }
+    ctx->pending[kernel].clear();
+    if (launches) *launches = ctx->launches[kernel];
+    if (total_ms) *total_ms = ctx->total_ms[kernel];
+    if (reset) {
+      ctx->launches[kernel] = 0;
+      ctx->total_ms[kernel] = 0.0;
+    }
+  });
+}
+
+}  // extern "C"

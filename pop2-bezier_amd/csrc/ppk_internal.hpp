@@ -1,0 +1,95 @@
+// Host-side internals shared by the C-ABI shim (ppk_abi.cpp) and the
+// int8_kv_ops host mirror (int8_kv_ops.cpp). Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/ppk_int8_kv.h"
+#include "ppk_kernel_args.h"
+
+namespace ppk {
+
+// Error classes map onto the ABI status codes; the message prefixes are the
+// ones the reference's failure classifier keys on
+// (app/src/model/hip_kernel.rs:79-81,162-170; app/src/inference.rs:84-92).
+struct PreconditionError : std::runtime_error {
+  explicit PreconditionError(const std::string& m) : std::runtime_error("HIP_PREPARATION: " + m) {}
+};
+struct UncertainError : std::runtime_error {
+  explicit UncertainError(const std::string& m) : std::runtime_error("HIP_EXECUTION_UNCERTAIN: " + m) {}
+};
+struct InvalidOutputError : std::runtime_error {
+  explicit InvalidOutputError(const std::string& m) : std::runtime_error("INVALID_OUTPUT: " + m) {}
+};
+
+inline void require(bool ok, const std::string& message) {
+  if (!ok) throw PreconditionError(message);
+}
+
+enum Fn : int {
+  kQuantize64, kQuantize128, kQuantize256, kDequantize,
+  kPartial64, kPartial128, kPartial256,
+  kPartialBf16h64, kPartialBf16h128, kPartialBf16h256,
+  kMerge64, kMerge128, kMerge256,
+  kFnCount
+};
+
+struct EventPair {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
+}  // namespace ppk
+
+struct ppk_context {
+  int device = -1;
+  int cu_count = 0;
+  hipModule_t module = nullptr;
+  hipFunction_t fn[ppk::kFnCount] = {};
+  std::string code_object;
+
+  std::mutex prof_mutex;
+  bool profiling = false;
+  std::vector<ppk::EventPair> pending[PPK_KERNEL_COUNT];
+  std::vector<ppk::EventPair> pool;
+  uint64_t launches[PPK_KERNEL_COUNT] = {};
+  double total_ms[PPK_KERNEL_COUNT] = {};
+};
+
+namespace ppk {
+
+// Restores the caller's current HIP device on scope exit.
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device);
+  ~DeviceGuard();
+  DeviceGuard(const DeviceGuard&) = delete;
+  DeviceGuard& operator=(const DeviceGuard&) = delete;
+
+ private:
+  int previous_ = -1;
+  bool changed_ = false;
+};
+
+// Validated launch plans. Validation throws PreconditionError before any
+// enqueue; launch throws UncertainError once a launch has been attempted.
+struct AttentionPlan {
+  uint32_t head_dim = 0, split = 0, nsplits = 0;
+  uint64_t y_bytes = 0, mz_bytes = 0, workspace_bytes = 0;
+};
+AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
+
+void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a);
+void run_append(ppk_context* ctx, hipStream_t stream, const PpkAppendArgs& a);
+void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArgs& a);
+void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a);
+
+// int8_kv_ops::prepare known-answer checks (int8_kv_ops.cpp).
+void prepare_self_check(ppk_context* ctx);
+
+}  // namespace ppk

@@ -1,0 +1,74 @@
+// Kernel argument blocks shared by the gfx950 code object (ppk_kernels.hip)
+// and the host shim (ppk_abi.cpp). Each kernel takes one of these by value,
+// so hipModuleLaunchKernel passes a single pointer to it.
+#pragma once
+#include <stdint.h>
+
+namespace ppk {
+
+// Wave64 lanes; every kernel here is written for 64-wide wavefronts.
+constexpr int kWave = 64;
+// Bytes one lane moves per global load in the attention kernels (dwordx4).
+constexpr int kLaneBytes = 16;
+
+// Quantize one (row, token) of D channels per wave, either densely
+// (dst index = src index) or into an arena slot past[b] + token.
+struct QuantizeArgs {
+  const void* src[2];       // K and V sources ([rows_per_tensor, D]); src[1] unused if ntensors == 1
+  uint8_t* codes[2];        // dense [rows, D] or arena [bh, capacity, D]
+  float* scales[2];         // dense [rows] or arena [bh, capacity]
+  const uint32_t* past;     // nullptr = dense mode
+  uint32_t* flags;          // optional
+  uint64_t rows;            // (bh * tokens) rows per tensor
+  uint32_t heads;           // append mode: sequence b = bh / heads
+  uint32_t tokens;          // append mode: tokens per bh row
+  uint32_t capacity;        // append mode
+  uint32_t src_dtype;       // PPK_F32 / PPK_BF16 / PPK_F16
+  uint32_t ntensors;        // 1 or 2
+  uint32_t pad;
+};
+
+struct DequantizeArgs {
+  const uint8_t* codes;     // [rows, D]
+  const float* scales;      // [rows]
+  void* out;                // [rows, D]
+  uint64_t rows;
+  uint32_t head_dim;
+  uint32_t out_dtype;
+  uint32_t round_bf16;
+  uint32_t pad;
+};
+
+// Split-K partial pass: block (split, row) covers history tokens
+// [split * split_tokens, min(+split_tokens, past)). Output record per block:
+//   y[D] floats at part_y + (row * nsplits + split) * D
+//   (m, z) at part_mz + (row * nsplits + split) * 2, m in log2 units
+struct PartialArgs {
+  const void* q;            // [rows, D]
+  const uint8_t* k;         // [rows, capacity, D]
+  const uint8_t* v;
+  const float* ks;          // [rows, capacity]
+  const float* vs;
+  const uint32_t* past;     // [rows / heads]
+  float* part_y;
+  float* part_mz;
+  uint32_t rows, heads, capacity, split_tokens, nsplits, q_dtype;
+  float scale_log2;         // softmax_scale * log2(e)
+  uint32_t pad;
+};
+
+struct MergeArgs {
+  const void* q;            // [rows, D]
+  const void* sk;           // [rows, D]
+  const void* sv;           // [rows, D]
+  const uint32_t* past;
+  const float* part_y;
+  const float* part_mz;
+  void* out;                // [rows, D]
+  uint32_t rows, heads, capacity, split_tokens, nsplits;
+  uint32_t q_dtype, scratch_dtype, out_dtype;
+  float scale_log2;
+  uint32_t pad;
+};
+
+}  // namespace ppk

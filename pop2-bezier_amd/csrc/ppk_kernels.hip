@@ -1,0 +1,401 @@
+// gfx950 (CDNA4) kernels of the int8 KV-cache decode path, written for
+// 64-wide wavefronts. Built ahead of time into a code object
+// (hipcc --genco --offload-arch=gfx950) and launched by ppk_abi.cpp.
+//
+//   ppk_quantize_d{64,128,256}         quantize rows densely or append into arenas
+//   ppk_dequantize                     codes * scales -> f32/bf16/f16
+//   ppk_attn_partial[_bf16h]_d{..}     split-K partial softmax-attention
+//   ppk_attn_merge_d{..}               cross-split merge + current token
+//
+// Semantics follow app/src/model/int8_kv_ops.rs:11-40 and
+// app/src/model/int8_kv.cu:8-59; the design (wave-per-row quantize, one-wave
+// split blocks streaming 1 KiB per load, scale folding) is this file's own.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ppk_kernel_args.h"
+
+namespace {
+
+using u4 = uint32_t __attribute__((ext_vector_type(4)));
+using f4 = float __attribute__((ext_vector_type(4)));
+
+enum { kF32 = 0, kBF16 = 1, kF16 = 2 };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+
+__device__ __forceinline__ float load_elem(const void* p, size_t i, uint32_t dtype) {
+  if (dtype == kF32) return static_cast<const float*>(p)[i];
+  const uint16_t h = static_cast<const uint16_t*>(p)[i];
+  return dtype == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+// Round-to-nearest-even to bfloat16, returned as the 16 stored bits. NaN stays
+// a quiet NaN (the carry trick alone could turn some NaN payloads into Inf).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+  if (x != x) return 0x7fc0u;
+  uint32_t u = __float_as_uint(x);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+// The same rounding kept in fp32 (the value a bf16 tensor would hold).
+__device__ __forceinline__ float round_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+__device__ __forceinline__ void store_elem(void* p, size_t i, uint32_t dtype, float x) {
+  if (dtype == kF32) static_cast<float*>(p)[i] = x;
+  else static_cast<uint16_t*>(p)[i] = dtype == kBF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+}
+
+// Signed byte k of a dword as float; hipcc folds the sign-extension into an
+// SDWA operand of v_cvt_f32_i32 (one VALU op per byte).
+__device__ __forceinline__ float sbyte(uint32_t w, int k) { return float(int(int8_t(w >> (8 * k)))); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_xor1(float x) { return dpp_f32<0xB1>(x); }  // quad_perm [1,0,3,2]
+__device__ __forceinline__ float dpp_xor2(float x) { return dpp_f32<0x4E>(x); }  // quad_perm [2,3,0,1]
+__device__ __forceinline__ float dpp_half_mirror(float x) { return dpp_f32<0x141>(x); }
+__device__ __forceinline__ float dpp_mirror(float x) { return dpp_f32<0x140>(x); }
+
+// Sum over the LPT consecutive lanes that hold one token (LPT in {4, 8, 16});
+// every lane of the group receives the total. DPP adds, no LDS traffic.
+template <int LPT>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp_xor1(x);
+  x += dpp_xor2(x);
+  if constexpr (LPT >= 8) x += dpp_half_mirror(x);
+  if constexpr (LPT >= 16) x += dpp_mirror(x);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 1: quantize (dense) / quantize-and-append (arena).
+// One wave per (tensor, row); D/64 channels per lane.
+// Bit-exact contract (int8_kv_ops.rs:17-18, int8_kv.cu:13,17):
+//   s = max(absmax / 127, 1e-12); code = clamp(rne(x / s), -127, 127).
+// NaN quotients become code 0 (as a float->int conversion of NaN does on
+// the reference GPU path); the absmax ignores NaN like fmaxf / f32::max.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ void quantize_body(const ppk::QuantizeArgs& a) {
+#pragma clang fp contract(off)
+  constexpr int EPL = D / ppk::kWave;
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = uint64_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
+  if (wave >= a.rows * a.ntensors) return;  // uniform per wave
+  const uint32_t tensor = wave >= a.rows ? 1u : 0u;
+  const uint64_t r = wave - (tensor ? a.rows : 0);
+  const void* src = tensor ? a.src[1] : a.src[0];
+
+  float x[EPL];
+  bool finite = true;
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    x[e] = load_elem(src, r * D + size_t(lane) * EPL + e, a.src_dtype);
+    finite = finite && __builtin_isfinite(x[e]);
+    amax = fmaxf(amax, fabsf(x[e]));
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(amax / 127.0f, 1e-12f);
+
+  size_t dst = r;
+  if (a.past) {
+    const uint64_t bh = r / a.tokens;
+    const uint32_t tok = uint32_t(r - bh * a.tokens);
+    const uint64_t slot = uint64_t(a.past[bh / a.heads]) + tok;
+    if (slot >= a.capacity) {
+      if (lane == 0 && a.flags) atomicOr(a.flags, 2u);
+      return;
+    }
+    dst = bh * a.capacity + slot;
+  }
+
+  uint32_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float qf = rintf(x[e] / s);
+    const int qi = (qf != qf) ? 0 : int(fminf(fmaxf(qf, -127.f), 127.f));
+    packed |= (uint32_t(qi) & 0xffu) << (8 * e);
+  }
+  uint8_t* codes = (tensor ? a.codes[1] : a.codes[0]) + dst * D + size_t(lane) * EPL;
+  if constexpr (EPL == 1) *codes = uint8_t(packed);
+  else if constexpr (EPL == 2) *reinterpret_cast<uint16_t*>(codes) = uint16_t(packed);
+  else *reinterpret_cast<uint32_t*>(codes) = packed;
+  if (lane == 0) (tensor ? a.scales[1] : a.scales[0])[dst] = s;
+
+  if (a.flags) {
+    const bool any_bad = __any(!finite);
+    if (any_bad && lane == 0) atomicOr(a.flags, 1u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantize: 16 codes per thread (one dwordx4), grid-stride.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dequantize_body(const ppk::DequantizeArgs& a) {
+#pragma clang fp contract(off)
+  const uint32_t chunks_per_row = a.head_dim / 16;
+  const uint64_t chunks = a.rows * chunks_per_row;
+  const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+  for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < chunks; i += stride) {
+    const uint64_t row = i / chunks_per_row;
+    const u4 raw = *reinterpret_cast<const u4*>(a.codes + i * 16);
+    const float s = a.scales[row];
+    float f[16];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float v = sbyte(raw[w], k) * s;
+        f[4 * w + k] = a.round_bf16 ? round_bf16(v) : v;
+      }
+    if (a.out_dtype == kF32) {
+      f4* o = reinterpret_cast<f4*>(static_cast<float*>(a.out) + i * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) o[w] = f4{f[4 * w], f[4 * w + 1], f[4 * w + 2], f[4 * w + 3]};
+    } else {
+      uint32_t h[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const uint16_t lo = a.out_dtype == kBF16 ? f32_to_bf16_bits(f[2 * w]) : f32_to_f16_bits(f[2 * w]);
+        const uint16_t hi = a.out_dtype == kBF16 ? f32_to_bf16_bits(f[2 * w + 1]) : f32_to_f16_bits(f[2 * w + 1]);
+        h[w] = uint32_t(lo) | (uint32_t(hi) << 16);
+      }
+      u4* o = reinterpret_cast<u4*>(static_cast<uint16_t*>(a.out) + i * 16);
+      o[0] = u4{h[0], h[1], h[2], h[3]};
+      o[1] = u4{h[4], h[5], h[6], h[7]};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 2a: split-K partial attention. One wave per (split, row).
+//
+// Lane layout: LPT = D/16 lanes share one token, each holding 16 channels, so
+// one dwordx4 load per lane moves 1 KiB = TPL = 64/LPT whole tokens. The dot
+// product is 16 FMAs per lane plus a DPP group sum; the per-token scale is
+// applied once to the sum (default) instead of to every element.
+//
+// Phase K streams this split's K codes and leaves log2-domain scores in LDS
+// (over the staged K scales); phase V streams V codes and accumulates
+// p_t * vscale_t * code_t per channel. No running-max rescale is needed
+// because the exact split max is known before phase V.
+// ---------------------------------------------------------------------------
+template <int D, bool BF16H>
+__device__ __forceinline__ void attn_partial_body(const ppk::PartialArgs& a) {
+  constexpr int LPT = D / 16;
+  constexpr int TPL = ppk::kWave / LPT;
+  constexpr int U = 8;  // 1 KiB loads in flight per wave per batch
+  extern __shared__ float lds[];
+
+  const int lane = threadIdx.x;
+  const int j = lane / LPT;  // token within a load tile
+  const int c = lane % LPT;  // 16-channel chunk
+  // Flat grid, split index fastest: consecutive blocks stream consecutive
+  // stretches of one row's history.
+  const uint32_t row = blockIdx.x / a.nsplits;
+  const uint32_t split = blockIdx.x - row * a.nsplits;
+  const uint32_t S = a.split_tokens;
+  const size_t rec = size_t(row) * a.nsplits + split;
+  float* out_y = a.part_y + rec * D;
+  float* out_mz = a.part_mz + rec * 2;
+
+  const uint32_t p = a.past[row / a.heads];
+  const uint32_t begin = split * S;
+  const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.nsplits) * S;
+  const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
+  if (n == 0) {
+    for (int i = lane; i < D; i += ppk::kWave) out_y[i] = 0.f;
+    if (lane == 0) { out_mz[0] = -INFINITY; out_mz[1] = 0.f; }
+    return;
+  }
+
+  float* s_lds = lds;       // K scales, then log2-domain scores
+  float* vs_lds = lds + S;  // V scales
+  const size_t tok0 = size_t(row) * a.capacity + begin;
+  for (uint32_t t = lane; t < n; t += ppk::kWave) {
+    s_lds[t] = a.ks[tok0 + t];
+    vs_lds[t] = a.vs[tok0 + t];
+  }
+  float qr[16];
+  {
+    const size_t qo = size_t(row) * D + size_t(c) * 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qr[i] = load_elem(a.q, qo + i, a.q_dtype);
+  }
+  __syncthreads();
+
+  const uint8_t* kb = a.k + tok0 * D + size_t(c) * 16;
+  const uint8_t* vb = a.v + tok0 * D + size_t(c) * 16;
+  const uint32_t ntiles = (n + TPL - 1) / TPL;
+  const float sl2 = a.scale_log2;
+
+  float mloc = -INFINITY;
+  for (uint32_t t0 = 0; t0 < ntiles; t0 += U) {
+    u4 raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t tc = min((t0 + u) * TPL + j, n - 1);  // clamp: always in bounds
+      raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(kb + size_t(tc) * D));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t tok = (t0 + u) * TPL + j;
+      const float kscale = s_lds[min(tok, n - 1)];
+      float d = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float kv = BF16H ? round_bf16(sbyte(raw[u][w], k) * kscale) : sbyte(raw[u][w], k);
+          d = fmaf(qr[4 * w + k], kv, d);
+        }
+      d = group_sum<LPT>(d);
+      float sc = BF16H ? d * sl2 : d * kscale * sl2;
+      sc = tok < n ? sc : -INFINITY;
+      mloc = fmaxf(mloc, sc);
+      if (c == 0 && tok < n) s_lds[tok] = sc;
+    }
+  }
+  float m = mloc;
+#pragma unroll
+  for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __syncthreads();
+
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  float z = 0.f;
+  for (uint32_t t0 = 0; t0 < ntiles; t0 += U) {
+    u4 raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t tc = min((t0 + u) * TPL + j, n - 1);
+      raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(vb + size_t(tc) * D));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t tok = (t0 + u) * TPL + j;
+      const uint32_t tc = min(tok, n - 1);
+      const float pr = tok < n ? __builtin_amdgcn_exp2f(s_lds[tc] - m) : 0.f;
+      const float vscale = vs_lds[tc];
+      z += pr;
+      const float wgt = BF16H ? pr : pr * vscale;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float vv = BF16H ? round_bf16(sbyte(raw[u][w], k) * vscale) : sbyte(raw[u][w], k);
+          acc[4 * w + k] = fmaf(wgt, vv, acc[4 * w + k]);
+        }
+    }
+  }
+#pragma unroll
+  for (int o = LPT; o < ppk::kWave; o <<= 1) {
+    z += __shfl_xor(z, o);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] += __shfl_xor(acc[i], o);
+  }
+  if (j == 0) {
+    f4* o = reinterpret_cast<f4*>(out_y + c * 16);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = f4{acc[4 * w], acc[4 * w + 1], acc[4 * w + 2], acc[4 * w + 3]};
+  }
+  if (lane == 0) { out_mz[0] = m; out_mz[1] = z; }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel 2b: merge. One wave per row: scores the current (unquantised) token,
+// combines it with every split's (m, z, y) by log-sum-exp weights, divides.
+// Rows with past > capacity (or beyond the launched coverage) give NaN.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
+  constexpr int EPL = D / ppk::kWave;
+  const int lane = threadIdx.x;
+  const uint32_t row = blockIdx.x;
+  const uint32_t p = a.past[row / a.heads];
+  const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.nsplits) * a.split_tokens;
+
+  float sv[EPL];
+  float d = 0.f;
+  const size_t base = size_t(row) * D + size_t(lane) * EPL;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    d = fmaf(load_elem(a.q, base + e, a.q_dtype), load_elem(a.sk, base + e, a.scratch_dtype), d);
+    sv[e] = load_elem(a.sv, base + e, a.scratch_dtype);
+  }
+  const float s_cur = wave_sum(d) * a.scale_log2;
+
+  const float* mz = a.part_mz + size_t(row) * a.nsplits * 2;
+  const float* py = a.part_y + size_t(row) * a.nsplits * D + size_t(lane) * EPL;
+  float m = s_cur;
+  for (uint32_t s = lane; s < a.nsplits; s += ppk::kWave) m = fmaxf(m, mz[2 * s]);
+  m = wave_max(m);
+
+  float y[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) y[e] = 0.f;
+  float zsum = 0.f;
+  for (uint32_t s = 0; s < a.nsplits; ++s) {
+    const float w = __builtin_amdgcn_exp2f(mz[2 * s] - m);
+    zsum = fmaf(w, mz[2 * s + 1], zsum);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) y[e] = fmaf(w, py[size_t(s) * D + e], y[e]);
+  }
+  const float wc = __builtin_amdgcn_exp2f(s_cur - m);
+  zsum += wc;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float o = valid ? fmaf(wc, sv[e], y[e]) / zsum : __builtin_nanf("");
+    store_elem(a.out, base + e, a.out_dtype, o);
+  }
+}
+
+}  // namespace
+
+#define PPK_QUANTIZE(D)                                                                \
+  extern "C" __global__ __launch_bounds__(256) void ppk_quantize_d##D(ppk::QuantizeArgs a) { \
+    quantize_body<D>(a);                                                               \
+  }
+PPK_QUANTIZE(64)
+PPK_QUANTIZE(128)
+PPK_QUANTIZE(256)
+
+extern "C" __global__ __launch_bounds__(256) void ppk_dequantize(ppk::DequantizeArgs a) { dequantize_body(a); }
+
+#define PPK_ATTN(D)                                                                          \
+  extern "C" __global__ __launch_bounds__(64) void ppk_attn_partial_d##D(ppk::PartialArgs a) { \
+    attn_partial_body<D, false>(a);                                                          \
+  }                                                                                          \
+  extern "C" __global__ __launch_bounds__(64) void ppk_attn_partial_bf16h_d##D(ppk::PartialArgs a) { \
+    attn_partial_body<D, true>(a);                                                           \
+  }                                                                                          \
+  extern "C" __global__ __launch_bounds__(64) void ppk_attn_merge_d##D(ppk::MergeArgs a) {   \
+    attn_merge_body<D>(a);                                                                   \
+  }
+PPK_ATTN(64)
+PPK_ATTN(128)
+PPK_ATTN(256)

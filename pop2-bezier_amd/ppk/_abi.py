@@ -1,0 +1,117 @@
+"""ctypes binding of include/ppk_int8_kv.h (libppk.so beside this file).
+
+The structures below mirror the C layout field for field; tests/ compares
+their sizes and offsets with the C compiler's.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libppk.so")
+HSACO_PATH = os.path.join(HERE, "ppk_kernels.hsaco")
+
+PPK_ABI_VERSION = 1
+PPK_OK, PPK_PRECONDITION, PPK_INVALID_OUTPUT, PPK_EXECUTION_UNCERTAIN = 0, 1, 2, 3
+PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
+PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW = 1, 2
+PPK_ATTN_BF16_HISTORY = 1
+(PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE,
+ PPK_KERNEL_ATTN_PARTIAL, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_COUNT) = range(6)
+
+_u32, _u64, _ptr, _f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_float
+
+
+class PpkQuantizeArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("src_dtype", _u32), ("src", _ptr), ("codes", _ptr), ("scales", _ptr),
+                ("rows", _u64), ("head_dim", _u32), ("reserved", _u32), ("flags", _ptr)]
+
+
+class PpkAppendArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("src_dtype", _u32), ("k_src", _ptr), ("v_src", _ptr), ("past", _ptr),
+                ("k_codes", _ptr), ("v_codes", _ptr), ("k_scales", _ptr), ("v_scales", _ptr),
+                ("batch", _u32), ("heads", _u32), ("tokens", _u32), ("head_dim", _u32), ("capacity", _u32),
+                ("reserved", _u32), ("flags", _ptr)]
+
+
+class PpkDequantizeArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("out_dtype", _u32), ("codes", _ptr), ("scales", _ptr), ("out", _ptr),
+                ("rows", _u64), ("head_dim", _u32), ("round_bf16", _u32)]
+
+
+class PpkAttentionArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("q_dtype", _u32), ("scratch_dtype", _u32), ("out_dtype", _u32),
+                ("flags", _u32), ("rows", _u32), ("heads", _u32), ("capacity", _u32), ("head_dim", _u32),
+                ("split_tokens", _u32), ("max_past", _u32), ("softmax_scale", _f32),
+                ("q", _ptr), ("k_codes", _ptr), ("v_codes", _ptr), ("k_scales", _ptr), ("v_scales", _ptr),
+                ("sk", _ptr), ("sv", _ptr), ("past", _ptr), ("out", _ptr), ("workspace", _ptr),
+                ("workspace_bytes", _u64)]
+
+
+# Every function the header declares: name -> (restype, argtypes).
+FUNCTIONS = {
+    "ppk_abi_version": (_u32, []),
+    "ppk_last_error": (ctypes.c_char_p, []),
+    "ppk_context_create": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_char_p, ctypes.POINTER(_ptr)]),
+    "ppk_context_release": (ctypes.c_int32, [_ptr]),
+    "ppk_quantize": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkQuantizeArgs)]),
+    "ppk_quantize_append": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkAppendArgs)]),
+    "ppk_dequantize": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDequantizeArgs)]),
+    "ppk_attention_workspace_bytes": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkAttentionArgs),
+                                                       ctypes.POINTER(_u64)]),
+    "ppk_attention_plan": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkAttentionArgs), ctypes.POINTER(_u32),
+                                            ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
+    "ppk_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkAttentionArgs)]),
+    "ppk_prepare": (ctypes.c_int32, [_ptr]),
+    "ppk_context_set_profiling": (ctypes.c_int32, [_ptr, ctypes.c_int32]),
+    "ppk_context_kernel_stats": (ctypes.c_int32, [_ptr, _u32, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double),
+                                                  _u32]),
+}
+
+
+class PpkError(RuntimeError):
+    status = -1
+
+
+class PpkPreconditionError(PpkError):
+    """Status 1: invalid arguments or preparation failure; nothing was enqueued."""
+    status = PPK_PRECONDITION
+
+
+class PpkInvalidOutputError(PpkError):
+    """Status 2: a numeric self-check failed."""
+    status = PPK_INVALID_OUTPUT
+
+
+class PpkExecutionUncertainError(PpkError):
+    """Status 3: a launch was attempted and failed; never replay the work."""
+    status = PPK_EXECUTION_UNCERTAIN
+
+
+_ERRORS = {1: PpkPreconditionError, 2: PpkInvalidOutputError, 3: PpkExecutionUncertainError}
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libppk.so. Raises if it was not built: there is no fallback path."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libppk.so missing at {LIB_PATH}: run python pop2-bezier_amd/build.py "
+                               "(the int8 KV path has no CPU or eager fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in FUNCTIONS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        if L.ppk_abi_version() != PPK_ABI_VERSION:
+            raise RuntimeError(f"libppk ABI {L.ppk_abi_version()} != expected {PPK_ABI_VERSION}")
+        _lib = L
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != PPK_OK:
+        msg = (lib().ppk_last_error() or b"").decode("utf-8", "replace")
+        raise _ERRORS.get(status, PpkError)(f"{what} failed with status {status}: {msg}")

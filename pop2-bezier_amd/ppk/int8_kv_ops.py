@@ -1,0 +1,260 @@
+"""Torch-tensor mirror of the reference's int8 KV custom-op API.
+
+Same entry points, argument meaning and error behaviour as
+app/src/model/int8_kv_ops.rs (quantize :11-29, dequantize :30-40,
+attention :41-55, prepare :56-103), plus `append`, the fused commit that
+Int8LayerCache::query_batch performs (app/src/model/int8_cache.rs:326-359).
+torch supplies device memory and the stream; every computation runs in the
+gfx950 kernels behind libppk.so. CPU tensors are refused, as the reference's
+device-only branches refuse them (int8_kv_ops.rs:28,54).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _abi
+from ._abi import check, lib
+
+_DTYPES = {torch.float32: _abi.PPK_F32, torch.bfloat16: _abi.PPK_BF16, torch.float16: _abi.PPK_F16}
+_HEAD_DIMS = (64, 128, 256)
+_contexts: dict[int, ctypes.c_void_p] = {}
+
+
+def context(device: torch.device | int | None = None) -> ctypes.c_void_p:
+    """The library context of a HIP device (code object loaded once per device)."""
+    if device is None:
+        index = torch.cuda.current_device()
+    elif isinstance(device, int):
+        index = device
+    else:
+        index = torch.device(device).index
+        if index is None:
+            index = torch.cuda.current_device()
+    ctx = _contexts.get(index)
+    if ctx is None:
+        ctx = ctypes.c_void_p()
+        check(lib().ppk_context_create(index, None, ctypes.byref(ctx)), "ppk_context_create")
+        _contexts[index] = ctx
+    return ctx
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require(cond: bool, message: str) -> None:
+    if not cond:
+        raise ValueError(message)
+
+
+def _device_only(*tensors: torch.Tensor, what: str) -> None:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(f"{what} is unavailable on this native provider")
+    for t in tensors:
+        _require(t.device == dev, "INT8 attention device mismatch")
+
+
+def _geometry(t: torch.Tensor) -> tuple[int, int]:
+    """geometry() of int8_kv_ops.rs:5-10, with D in {64, 128, 256}."""
+    _require(t.dim() == 3 and t.shape[0] > 0 and t.shape[1] > 0 and t.shape[2] in _HEAD_DIMS and t.is_contiguous(),
+             "INT8 KV requires dense [heads,tokens,D] with D in {64,128,256}")
+    return t.shape[0], t.shape[1]
+
+
+def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """[heads, tokens, D] float -> (uint8 codes [heads, tokens, D], float32 scales [heads, tokens])."""
+    h, n = _geometry(x)
+    _require(x.dtype in _DTYPES, "INT8 KV quantize input must be float32, bfloat16 or float16")
+    _device_only(x, what="KV INT8")
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty((h, n), dtype=torch.float32, device=x.device)
+    a = _abi.PpkQuantizeArgs(struct_size=ctypes.sizeof(_abi.PpkQuantizeArgs), src_dtype=_DTYPES[x.dtype],
+                             src=x.data_ptr(), codes=codes.data_ptr(), scales=scales.data_ptr(), rows=h * n,
+                             head_dim=x.shape[2], flags=None)
+    check(lib().ppk_quantize(context(x.device), _stream(x), ctypes.byref(a)), "ppk_quantize")
+    return codes, scales
+
+
+def dequantize(packed: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """codes * scale, rounded to `dtype` (bf16: round-to-nearest-even of the f32 product)."""
+    h, n = _geometry(packed)
+    _require(packed.dtype == torch.uint8 and scale.dtype == torch.float32 and tuple(scale.shape) == (h, n)
+             and scale.is_contiguous() and packed.device == scale.device, "INT8 KV scales differ")
+    _require(dtype in _DTYPES, "INT8 dequantize dtype must be float32, bfloat16 or float16")
+    _device_only(packed, scale, what="KV INT8 dequantization")
+    out = torch.empty(packed.shape, dtype=dtype, device=packed.device)
+    a = _abi.PpkDequantizeArgs(struct_size=ctypes.sizeof(_abi.PpkDequantizeArgs), out_dtype=_DTYPES[dtype],
+                               codes=packed.data_ptr(), scales=scale.data_ptr(), out=out.data_ptr(), rows=h * n,
+                               head_dim=packed.shape[2], round_bf16=0)
+    check(lib().ppk_dequantize(context(packed.device), _stream(packed), ctypes.byref(a)), "ppk_dequantize")
+    return out
+
+
+def append(k_new: torch.Tensor, v_new: torch.Tensor, past: torch.Tensor, k_codes: torch.Tensor,
+           v_codes: torch.Tensor, k_scales: torch.Tensor, v_scales: torch.Tensor,
+           flags: torch.Tensor | None = None) -> None:
+    """Quantize k_new/v_new [B, H, T, D] and write them at slots past[b]..past[b]+T-1 of the
+    arenas [B*H, capacity, D] (codes) and [B*H, capacity] (scales), in place."""
+    _require(k_new.dim() == 4 and k_new.shape == v_new.shape and k_new.dtype == v_new.dtype
+             and k_new.dtype in _DTYPES and k_new.is_contiguous() and v_new.is_contiguous(),
+             "INT8 batch requires [B,H,T,D] scratch and matching row histories")
+    b, h, t, d = k_new.shape
+    _require(d in _HEAD_DIMS and b > 0 and h > 0 and t > 0, "INT8 batch requires [B,H,T,D] with D in {64,128,256}")
+    rows, cap = _geometry(k_codes)[0], k_codes.shape[1]
+    _require(rows == b * h and k_codes.shape == v_codes.shape and k_codes.shape[2] == d
+             and k_codes.dtype == torch.uint8 and v_codes.dtype == torch.uint8 and v_codes.is_contiguous(),
+             "INT8 packed arenas must be uint8 [B*H, capacity, D]")
+    for s in (k_scales, v_scales):
+        _require(tuple(s.shape) == (rows, cap) and s.dtype == torch.float32 and s.is_contiguous(),
+                 "INT8 scale arenas must be float32 [B*H, capacity]")
+    _require(tuple(past.shape) == (b,) and past.dtype in (torch.int32, torch.uint32) and past.is_contiguous(),
+             "INT8 append lengths must be U32[B]")
+    if flags is not None:
+        _require(flags.dtype in (torch.int32, torch.uint32) and flags.numel() >= 1, "flags must be one 32-bit word")
+    _device_only(k_new, v_new, past, k_codes, v_codes, k_scales, v_scales, what="KV INT8")
+    a = _abi.PpkAppendArgs(struct_size=ctypes.sizeof(_abi.PpkAppendArgs), src_dtype=_DTYPES[k_new.dtype],
+                           k_src=k_new.data_ptr(), v_src=v_new.data_ptr(), past=past.data_ptr(),
+                           k_codes=k_codes.data_ptr(), v_codes=v_codes.data_ptr(), k_scales=k_scales.data_ptr(),
+                           v_scales=v_scales.data_ptr(), batch=b, heads=h, tokens=t, head_dim=d, capacity=cap,
+                           flags=flags.data_ptr() if flags is not None else None)
+    check(lib().ppk_quantize_append(context(k_new.device), _stream(k_new), ctypes.byref(a)), "ppk_quantize_append")
+
+
+def attention_args(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *, bf16_history: bool = False,
+                   max_past: int = 0, out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
+                   softmax_scale: float = 0.0) -> tuple[_abi.PpkAttentionArgs, torch.Tensor]:
+    """Validate like int8_kv_ops::attention and build the ABI argument block (workspace unset)."""
+    rows, capacity = _geometry(k)
+    d = k.shape[2]
+    _require(heads > 0 and rows % heads == 0 and v.shape == k.shape and v.is_contiguous()
+             and k.dtype == torch.uint8 and v.dtype == torch.uint8, "INT8 attention geometry differs")
+    for t in (q, sk, sv):
+        _require(t.numel() == rows * d and t.shape[0] == rows and t.shape[-1] == d and t.dtype in _DTYPES
+                 and t.is_contiguous(), "INT8 scratch must be float[head_rows,1,D]")
+    _require(sk.dtype == sv.dtype, "INT8 scratch key/value dtypes differ")
+    for t in (ks, vs):
+        _require(tuple(t.shape) == (rows, capacity) and t.dtype == torch.float32 and t.is_contiguous(),
+                 "INT8 scales must be F32[head_rows,capacity]")
+    _require(tuple(past.shape) == (rows // heads,) and past.dtype in (torch.int32, torch.uint32)
+             and past.is_contiguous(), "INT8 attention lengths differ")
+    _device_only(q, k, v, ks, vs, sk, sv, past, what="KV INT8 fused attention")
+    if out is None:
+        out = torch.empty((rows, 1, d), dtype=out_dtype, device=q.device)
+    _require(out.numel() == rows * d and out.dtype in _DTYPES and out.is_contiguous() and out.device == q.device,
+             "INT8 attention output must be a dense float tensor of rows*D elements")
+    a = _abi.PpkAttentionArgs(
+        struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), q_dtype=_DTYPES[q.dtype], scratch_dtype=_DTYPES[sk.dtype],
+        out_dtype=_DTYPES[out.dtype], flags=_abi.PPK_ATTN_BF16_HISTORY if bf16_history else 0, rows=rows,
+        heads=heads, capacity=capacity, head_dim=d, split_tokens=split_tokens, max_past=max_past,
+        softmax_scale=softmax_scale, q=q.data_ptr(), k_codes=k.data_ptr(), v_codes=v.data_ptr(),
+        k_scales=ks.data_ptr(), v_scales=vs.data_ptr(), sk=sk.data_ptr(), sv=sv.data_ptr(), past=past.data_ptr(),
+        out=out.data_ptr(), workspace=None, workspace_bytes=0)
+    return a, out
+
+
+def workspace_bytes(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = None) -> int:
+    n = ctypes.c_uint64()
+    check(lib().ppk_attention_workspace_bytes(ctx, ctypes.byref(args), ctypes.byref(n)),
+          "ppk_attention_workspace_bytes")
+    return n.value
+
+
+def plan(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = None) -> tuple[int, int, int]:
+    """(tokens per split, number of splits, workspace bytes) the library chooses for args."""
+    split, nsplits, nbytes = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+    check(lib().ppk_attention_plan(ctx, ctypes.byref(args), ctypes.byref(split), ctypes.byref(nsplits),
+                                   ctypes.byref(nbytes)), "ppk_attention_plan")
+    return split.value, nsplits.value, nbytes.value
+
+
+def attention(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *, bf16_history: bool = False,
+              max_past: int = 0, out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0) -> torch.Tensor:
+    """int8_kv_ops::attention: q/sk/sv [rows,1,D], k/v uint8 [rows,cap,D], ks/vs f32 [rows,cap],
+    past U32 [rows/heads] -> out [rows,1,D] (float32 by default)."""
+    a, out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
+                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale)
+    ctx = context(q.device)
+    nbytes = workspace_bytes(a, ctx)
+    # The caching allocator is stream-ordered: the block is not reused before
+    # the kernels queued on this stream have consumed it.
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = nbytes
+    check(lib().ppk_decode_attention(ctx, _stream(q), ctypes.byref(a)), "ppk_decode_attention")
+    return out
+
+
+class DecodeAttention:
+    """A prepared attention call for a fixed set of buffers (bench / serving loops): the argument
+    block and workspace are built once; __call__ only enqueues the two kernels."""
+
+    def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *,
+                 bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype = torch.float32):
+        self.args, self.out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens,
+                                             bf16_history=bf16_history, max_past=max_past, out=out,
+                                             out_dtype=out_dtype)
+        self.ctx = context(q.device)
+        self.split_tokens, self.nsplits, nbytes = plan(self.args, self.ctx)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        self.args.workspace = self.workspace.data_ptr()
+        self.args.workspace_bytes = nbytes
+        self._keep = (q, k, v, ks, vs, sk, sv, past)
+        self._ref = ctypes.byref(self.args)
+        self._fn = lib().ppk_decode_attention
+        self.device = q.device
+
+    def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_decode_attention")
+        return self.out
+
+
+class AppendKV:
+    """A prepared quantize-and-append call for fixed buffers."""
+
+    def __init__(self, k_new, v_new, past, k_codes, v_codes, k_scales, v_scales, flags=None):
+        b, h, t, d = k_new.shape
+        self.args = _abi.PpkAppendArgs(
+            struct_size=ctypes.sizeof(_abi.PpkAppendArgs), src_dtype=_DTYPES[k_new.dtype], k_src=k_new.data_ptr(),
+            v_src=v_new.data_ptr(), past=past.data_ptr(), k_codes=k_codes.data_ptr(), v_codes=v_codes.data_ptr(),
+            k_scales=k_scales.data_ptr(), v_scales=v_scales.data_ptr(), batch=b, heads=h, tokens=t, head_dim=d,
+            capacity=k_codes.shape[1], flags=flags.data_ptr() if flags is not None else None)
+        # Validate through the one-shot path's checks once.
+        _require(k_new.is_contiguous() and v_new.is_contiguous() and k_codes.shape[0] == b * h,
+                 "INT8 batch requires [B,H,T,D] scratch and matching row histories")
+        self.ctx = context(k_new.device)
+        self._keep = (k_new, v_new, past, k_codes, v_codes, k_scales, v_scales, flags)
+        self._ref = ctypes.byref(self.args)
+        self._fn = lib().ppk_quantize_append
+        self.device = k_new.device
+
+    def __call__(self, stream: torch.cuda.Stream | None = None) -> None:
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_quantize_append")
+
+
+def prepare(device: torch.device | int | None = None) -> None:
+    """int8_kv_ops::prepare: run the private known-answer checks on the device."""
+    check(lib().ppk_prepare(context(device)), "ppk_prepare")
+
+
+def set_profiling(enable: bool, device: torch.device | int | None = None) -> None:
+    check(lib().ppk_context_set_profiling(context(device), int(bool(enable))), "ppk_context_set_profiling")
+
+
+def kernel_stats(kernel: int, device: torch.device | int | None = None, reset: bool = False) -> tuple[int, float]:
+    """(launches, total milliseconds) of a traced kernel (PPK_KERNEL_*)."""
+    n = ctypes.c_uint64()
+    ms = ctypes.c_double()
+    check(lib().ppk_context_kernel_stats(context(device), kernel, ctypes.byref(n), ctypes.byref(ms), int(reset)),
+          "ppk_context_kernel_stats")
+    return n.value, ms.value
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,113 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/ppk_int8_kv.h declares, its argument structs match the C layout, and
+host-side validation refuses bad arguments with status 1 before any launch."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import ppk
+from ppk import _abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ppk_int8_kv.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^PPK_API\s+[\w\s\*]+?\b(ppk_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _abi.lib()
+    names = declared_functions()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(lib, name), f"libppk.so does not export {name}"
+        assert name in _abi.FUNCTIONS, f"ctypes binding lacks {name}"
+    out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = sorted(set(re.findall(r" T (ppk_\w+)", out.stdout)))
+    assert exported == names, "exported C symbols differ from the header's declarations"
+
+
+def test_code_object_is_built_for_gfx950():
+    assert os.path.exists(_abi.HSACO_PATH)
+    blob = open(_abi.HSACO_PATH, "rb").read()
+    assert b"gfx950" in blob
+    for kernel in (b"ppk_quantize_d128", b"ppk_attn_partial_d128", b"ppk_attn_merge_d128", b"ppk_dequantize"):
+        assert kernel in blob
+
+
+def test_abi_version():
+    assert _abi.lib().ppk_abi_version() == _abi.PPK_ABI_VERSION == 1
+
+
+@pytest.fixture(scope="module")
+def c_layout(tmp_path_factory):
+    """sizeof/offsetof of every argument struct, as the C compiler lays them out."""
+    src = tmp_path_factory.mktemp("abi") / "layout.c"
+    exe = src.with_suffix("")
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs):
+        name = cls.__name__
+        lines.append(f'printf("{name} size %zu\\n", sizeof({name}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{name} {field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0;}")
+    src.write_text("\n".join(lines))
+    subprocess.run(["gcc", "-std=c11", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    return {tuple(line.split()[:2]): int(line.split()[2]) for line in out.splitlines()}
+
+
+@pytest.mark.parametrize("cls", [_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs,
+                                 _abi.PpkAttentionArgs])
+def test_struct_layout_matches_c(c_layout, cls):
+    name = cls.__name__
+    assert c_layout[(name, "size")] == ctypes.sizeof(cls)
+    for field, _ in cls._fields_:
+        assert c_layout[(name, field)] == getattr(cls, field).offset, f"{name}.{field}"
+
+
+def _attn_args(**kw) -> _abi.PpkAttentionArgs:
+    a = _abi.PpkAttentionArgs(struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), q_dtype=0, scratch_dtype=0,
+                              out_dtype=0, flags=0, rows=512, heads=16, capacity=8193, head_dim=128,
+                              split_tokens=0, max_past=8192, softmax_scale=0.0)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_plan_sizes_workspace_without_a_device():
+    split, nsplits, nbytes = ppk.int8_kv_ops.plan(_attn_args())
+    assert split % 8 == 0 and split >= 64
+    assert nsplits == -(-8192 // split)
+    assert nbytes >= 512 * nsplits * (128 + 2) * 4
+    # An explicit split is honoured (rounded up to whole 1 KiB tiles).
+    split, nsplits, _ = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
+    assert (split, nsplits) == (104, -(-8192 // 104))
+    # Result does not depend on the split, so the workspace query is the only contract.
+    assert ppk.int8_kv_ops.workspace_bytes(_attn_args(split_tokens=128)) == 512 * 64 * 128 * 4 + 512 * 64 * 2 * 4
+
+
+@pytest.mark.parametrize("bad", [dict(head_dim=96), dict(rows=30, heads=16), dict(heads=0), dict(capacity=0),
+                                 dict(q_dtype=7), dict(flags=8), dict(max_past=9000),
+                                 dict(softmax_scale=float("nan")), dict(struct_size=8)])
+def test_invalid_attention_arguments_are_refused_before_launch(bad):
+    with pytest.raises(ppk.PpkPreconditionError):
+        ppk.int8_kv_ops.plan(_attn_args(**bad))
+    assert "HIP_PREPARATION" in _abi.lib().ppk_last_error().decode()
+
+
+def test_null_context_calls_return_status_1():
+    lib = _abi.lib()
+    a = _attn_args()
+    assert lib.ppk_decode_attention(None, None, ctypes.byref(a)) == _abi.PPK_PRECONDITION
+    q = _abi.PpkQuantizeArgs(struct_size=ctypes.sizeof(_abi.PpkQuantizeArgs))
+    assert lib.ppk_quantize(None, None, ctypes.byref(q)) == _abi.PPK_PRECONDITION
+    assert lib.ppk_prepare(None) == _abi.PPK_PRECONDITION
+    assert lib.ppk_context_release(None) == _abi.PPK_OK

@@ -1,0 +1,183 @@
+"""GPU parity of kernel 2 (split-K decode attention + merge) against the f64 oracle.
+
+Tolerance: |gpu - oracle| <= 2e-3 + 1e-2 * |oracle| (
+max-abs 2e-3, relative 1e-2 vs the fp32-dequantised attention). The
+bf16-history mode reproduces pp_i8_load (app/src/model/int8_kv.cu:23-27) and is
+held to the reference's own self-check tolerance, 2e-5 absolute
+(app/src/model/int8_kv_ops.rs:73,101).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import ppk
+from helpers import SEED, assert_close, bf16_bits_to_f32, kv_values, to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+
+class Case:
+    """A seeded decode problem: arenas filled by the GPU quantize kernel, lengths per sequence."""
+
+    def __init__(self, device, B, H, D, lengths, cap, q_dtype=torch.float32, scratch_dtype=torch.float32,
+                 seed=SEED, heavy=True):
+        rng = np.random.default_rng(seed)
+        self.B, self.H, self.D, self.cap = B, H, D, cap
+        rows = B * H
+        self.rows = rows
+        self.past = np.asarray(lengths, np.uint32)
+        assert self.past.shape == (B,)
+        lmax = int(min(self.past.max(), cap))
+        kvals = kv_values(rng, B, H, max(lmax, 1), D, heavy=heavy).reshape(rows, max(lmax, 1), D)
+        vvals = kv_values(rng, B, H, max(lmax, 1), D, heavy=heavy).reshape(rows, max(lmax, 1), D)
+        self.kc = torch.zeros((rows, cap, D), dtype=torch.uint8, device=device)
+        self.vc = torch.zeros_like(self.kc)
+        self.ks = torch.full((rows, cap), float("nan"), dtype=torch.float32, device=device)  # NaN beyond history
+        self.vs = torch.full((rows, cap), float("nan"), dtype=torch.float32, device=device)
+        if lmax:
+            c, s = ppk.quantize(torch.from_numpy(kvals[:, :lmax]).to(device))
+            self.kc[:, :lmax], self.ks[:, :lmax] = c, s
+            c, s = ppk.quantize(torch.from_numpy(vvals[:, :lmax]).to(device))
+            self.vc[:, :lmax], self.vs[:, :lmax] = c, s
+        self.q32, self.q = self._floats(rng.standard_normal((rows, 1, D)).astype(np.float32), q_dtype, device)
+        self.sk32, self.sk = self._floats(kv_values(rng, B, H, 1, D).reshape(rows, 1, D), scratch_dtype, device)
+        self.sv32, self.sv = self._floats(kv_values(rng, B, H, 1, D).reshape(rows, 1, D), scratch_dtype, device)
+        self.past_t = torch.from_numpy(self.past.view(np.int32)).to(device)
+
+    @staticmethod
+    def _floats(x32, dtype, device):
+        if dtype == torch.float32:
+            return x32, torch.from_numpy(x32).to(device)
+        if dtype == torch.float16:
+            h = x32.astype(np.float16)
+            return h.astype(np.float32), torch.from_numpy(h).to(device)
+        bits = to_bf16_bits(x32)
+        return bf16_bits_to_f32(bits), torch.from_numpy(bits.view(np.int16)).to(device).view(torch.bfloat16)
+
+    def run(self, split=0, **kw):
+        out = ppk.attention(self.q, self.kc, self.vc, self.ks, self.vs, self.sk, self.sv, self.past_t, self.H,
+                            split, **kw)
+        torch.cuda.synchronize()
+        return out.float().reshape(self.rows, self.D).cpu().numpy()
+
+    def reference(self, history_bf16=False, scale=None):
+        # Scales beyond the history are NaN on the device; the oracle never reads them.
+        return oracle.attention(self.q32, self.kc.cpu().numpy(), self.vc.cpu().numpy(), self.ks.cpu().numpy(),
+                                self.vs.cpu().numpy(), self.sk32, self.sv32, self.past, self.H, scale=scale,
+                                history_bf16=history_bf16)
+
+
+def test_config1_b1_h16_d64_ctx512(device):
+    """fp32 q, 512 cached tokens + 1 new, scale 1/sqrt(64)."""
+    c = Case(device, 1, 16, 64, [512], 513, heavy=False)
+    assert_close(c.run(), c.reference(), what="config 1")
+    got = c.run(bf16_history=True)
+    assert_close(got, c.reference(history_bf16=True), atol=2e-5, rtol=0, what="config 1 bf16 history")
+
+
+def test_config3_24_layers_one_stream(device):
+    """24 layers x (B=1, H=16, D=128, 2048 int8 tokens), bf16 q; per layer append then
+    attention, all sequenced on one stream; every layer checked."""
+    B, H, D, L = 1, 16, 128, 2048
+    layers = []
+    for layer in range(24):
+        layers.append(Case(device, B, H, D, [L], L + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16,
+                           seed=SEED + 100 + layer))
+    outs = []
+    for c in layers:
+        k_new = c.sk.reshape(B, H, 1, D)
+        v_new = c.sv.reshape(B, H, 1, D)
+        ppk.append(k_new, v_new, c.past_t, c.kc, c.vc, c.ks, c.vs)
+        outs.append(ppk.attention(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H))
+    torch.cuda.synchronize()
+    for layer, (c, o) in enumerate(zip(layers, outs)):
+        assert_close(o.reshape(c.rows, D).cpu().numpy(), c.reference(), what=f"layer {layer}")
+        # The append wrote slot L with the quantised current token, bit-exactly.
+        codes, scales, _ = oracle.quantize(c.sk32.reshape(c.rows, 1, D))
+        assert np.array_equal(c.kc[:, L:L + 1].cpu().numpy(), codes)
+        assert np.array_equal(c.ks[:, L:L + 1].cpu().numpy(), scales)
+
+
+def test_config4_ragged_parallel_branches(device):
+    """B=8, H=16, D=128, lengths ~ U[256, 4096], bf16 q."""
+    rng = np.random.default_rng(SEED + 4)
+    lengths = rng.integers(256, 4097, size=8)
+    c = Case(device, 8, 16, 128, lengths, 4097, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    ref = c.reference()
+    assert_close(c.run(), ref, what="config 4 auto split")
+    assert_close(c.run(split=256), ref, what="config 4 split 256")
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_edge_lengths(device, d):
+    """Empty history (output = sv exactly), one token, tile tails, full capacity, p > capacity (NaN)."""
+    cap = 77
+    lengths = [0, 1, 7, 9, 33, 76, 77, 78]
+    c = Case(device, len(lengths), 2, d, lengths, cap)
+    got = c.run()
+    ref = c.reference()
+    assert_close(got, ref, what=f"edge lengths d={d}")
+    assert np.array_equal(got[0:2], c.sv32.reshape(c.rows, d)[0:2])  # p = 0: softmax over the current token only
+    assert np.isnan(got[-2:]).all()
+
+
+@pytest.mark.parametrize("split", [32, 64, 128, 256, 1024, 4096])
+def test_split_invariance(device, split):
+    """The reference checks splits 32 and 128 (int8_kv_ops.rs:100); every split gives the same result."""
+    c = Case(device, 2, 4, 128, [1000, 3001], 3001, seed=SEED + 9)
+    assert_close(c.run(split=split), c.reference(), what=f"split {split}")
+
+
+def test_bf16_history_mode_matches_reference_kernel_semantics(device):
+    c = Case(device, 2, 2, 64, [300, 41], 301)
+    ref = c.reference(history_bf16=True)
+    for split in (32, 128):
+        assert_close(c.run(split=split, bf16_history=True), ref, atol=2e-5, rtol=0, what=f"bf16 split {split}")
+
+
+@pytest.mark.parametrize("q_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_operand_and_output_dtypes(device, q_dtype, out_dtype):
+    c = Case(device, 1, 4, 128, [200], 256, q_dtype=q_dtype, scratch_dtype=q_dtype)
+    got = c.run(out_dtype=out_dtype)
+    ref = c.reference()
+    if out_dtype == torch.float32:
+        assert_close(got, ref, what="f32 out")
+    else:
+        # Output rounding adds at most half an ulp of the narrow type.
+        eps = 2.0 ** -8 if out_dtype == torch.bfloat16 else 2.0 ** -11
+        assert_close(got, ref, atol=2e-3, rtol=1e-2 + eps, what=f"{out_dtype} out")
+
+
+def test_softmax_scale_override(device):
+    c = Case(device, 1, 2, 64, [50], 64)
+    assert_close(c.run(softmax_scale=0.3), c.reference(scale=0.3), what="scale 0.3")
+
+
+def test_max_past_hint_beyond_coverage_is_nan(device):
+    """Rows longer than the host's max_past hint are not covered by the launch: NaN, never wrong numbers."""
+    c = Case(device, 2, 2, 64, [10, 100], 128)
+    got = c.run(max_past=50)
+    assert np.isfinite(got[:2]).all() and np.isnan(got[2:]).all()
+    assert_close(got[:2], c.reference()[:2], what="covered rows")
+
+
+def test_reference_offset_views(device):
+    """Known-answer (iii) layout: every operand a one-row-offset view of a larger buffer (int8_kv_ops.rs:77-90)."""
+    rows, cap, heads, d = 4, 67, 2, 64
+    rng = np.random.default_rng(SEED + 5)
+    c = Case(device, 2, 2, d, [0, 66], cap, seed=SEED + 5)
+    big = {}
+    for name in ("kc", "vc", "ks", "vs", "q", "sk", "sv"):
+        t = getattr(c, name)
+        b = torch.zeros((t.shape[0] + 1,) + tuple(t.shape[1:]), dtype=t.dtype, device=device)
+        b[1:] = t
+        big[name] = b[1:]
+    pbig = torch.tensor([999, 0, 66], dtype=torch.int32, device=device)[1:]
+    out = ppk.attention(big["q"], big["kc"], big["vc"], big["ks"], big["vs"], big["sk"], big["sv"], pbig, heads)
+    torch.cuda.synchronize()
+    assert_close(out.reshape(rows, d).cpu().numpy(), c.reference(), what="offset views")
+    del rng

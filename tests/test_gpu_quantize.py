@@ -1,0 +1,167 @@
+"""GPU parity of kernel 1 (quantize / quantize-and-append) and dequantize.
+
+Codes and scales must be bit-exact with the oracle (oracle/ppk_oracle.c,
+restating app/src/model/int8_kv_ops.rs:11-21). Everything runs through the
+C-ABI (libppk.so) via the ppk package.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import ppk
+from helpers import SEED, bf16_bits_to_f32, kv_values, to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _to_device(x32: np.ndarray, dtype: torch.dtype, device) -> tuple[torch.Tensor, np.ndarray]:
+    """Device tensor of dtype plus the exact float32 values it holds (the oracle's input)."""
+    if dtype == torch.float32:
+        return torch.from_numpy(np.ascontiguousarray(x32)).to(device), x32
+    if dtype == torch.float16:
+        h = x32.astype(np.float16)
+        return torch.from_numpy(h).to(device), h.astype(np.float32)
+    bits = to_bf16_bits(x32)
+    t = torch.from_numpy(bits.view(np.int16)).to(device).view(torch.bfloat16)
+    return t, bf16_bits_to_f32(bits)
+
+
+def test_prepare_known_answer_checks(device):
+    """int8_kv_ops::prepare's three checks (int8_kv_ops.rs:56-103), run on the device."""
+    ppk.prepare(device)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_quantize_bit_exact(device, d, dt):
+    rng = np.random.default_rng(SEED + d)
+    x = kv_values(rng, 1, 16, 257, d).reshape(16, 257, d)
+    xt, x32 = _to_device(x, DTYPES[dt], device)
+    codes, scales = ppk.quantize(xt)
+    ref_codes, ref_scales, _ = oracle.quantize(x32)
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+
+
+def _special_rows(d: int) -> np.ndarray:
+    rows = []
+    rows.append(np.zeros(d, np.float32))                                       # zero row -> scale 1e-12
+    r = np.zeros(d, np.float32); r[:5] = [0.5, 1.5, 2.5, -2.5, 127.0]; rows.append(r)   # ties at scale 1
+    r = np.full(d, -3.0, np.float32); r[7] = -11.0; rows.append(r)              # all negative
+    rows.append(np.full(d, 1e-40, np.float32))                                  # subnormal inputs
+    r = np.zeros(d, np.float32); r[3] = 3e38; r[4] = -1e38; rows.append(r)     # near-max magnitudes
+    r = np.zeros(d, np.float32); r[0] = 1e-10; rows.append(r)                   # absmax/127 below the floor
+    r = np.arange(d, dtype=np.float32) - d / 2; rows.append(r)                  # ramp
+    r = np.linspace(-254.0, 254.0, d, dtype=np.float32); rows.append(r)        # many exact half-steps
+    return np.stack(rows)[None]
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_quantize_special_rows(device, d):
+    x = _special_rows(d)
+    codes, scales = ppk.quantize(torch.from_numpy(x).to(device))
+    ref_codes, ref_scales, _ = oracle.quantize(x)
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+    assert scales[0, 0].item() == np.float32(1e-12)
+    assert scales[0, 1].item() == 1.0
+
+
+def test_quantize_nonfinite_rows_flagged(device):
+    d = 128
+    x = np.random.default_rng(SEED).standard_normal((1, 4, d)).astype(np.float32)
+    x[0, 1, 5] = np.nan
+    x[0, 2, 9] = np.inf
+    x[0, 3, :] = np.nan
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    xt = torch.from_numpy(x).to(device)
+    codes = torch.empty((1, 4, d), dtype=torch.uint8, device=device)
+    scales = torch.empty((1, 4), dtype=torch.float32, device=device)
+    import ctypes
+    a = ppk._abi.PpkQuantizeArgs(struct_size=ctypes.sizeof(ppk._abi.PpkQuantizeArgs), src_dtype=0,
+                                 src=xt.data_ptr(), codes=codes.data_ptr(), scales=scales.data_ptr(), rows=4,
+                                 head_dim=d, flags=flags.data_ptr())
+    ppk._abi.check(ppk._abi.lib().ppk_quantize(ppk.context(device), None, ctypes.byref(a)), "ppk_quantize")
+    torch.cuda.synchronize()
+    assert flags.item() & ppk.PPK_FLAG_NONFINITE
+    ref_codes, ref_scales, bad = oracle.quantize(x)
+    assert bad == 3
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+
+
+def _arenas(rng, rows, cap, d, filled):
+    codes = rng.integers(-127, 128, size=(rows, cap, d)).astype(np.int8).view(np.uint8)
+    scales = rng.random((rows, cap), dtype=np.float32) * 0.1
+    codes[:, filled:] = 0xAB  # sentinel bytes beyond the committed history
+    scales[:, filled:] = -7.0
+    return codes, scales
+
+
+def test_append_config2_bit_exact(device):
+    """B=1, H=16, D=128, one fp16 token into capacity 4096 holding 1000 tokens."""
+    rng = np.random.default_rng(SEED)
+    B, H, D, cap, filled = 1, 16, 128, 4096, 1000
+    kc, ks = _arenas(rng, B * H, cap, D, filled)
+    vc, vs = _arenas(rng, B * H, cap, D, filled)
+    k_new = kv_values(rng, B, H, 1, D)
+    v_new = kv_values(rng, B, H, 1, D)
+    kt, k32 = _to_device(k_new, torch.float16, device)
+    vt, v32 = _to_device(v_new, torch.float16, device)
+    past_np = np.array([filled], np.uint32)
+    dk, dv = torch.from_numpy(kc.copy()).to(device), torch.from_numpy(vc.copy()).to(device)
+    dks, dvs = torch.from_numpy(ks.copy()).to(device), torch.from_numpy(vs.copy()).to(device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    ppk.append(kt, vt, torch.from_numpy(past_np.view(np.int32)).to(device), dk, dv, dks, dvs, flags)
+    torch.cuda.synchronize()
+    assert flags.item() == 0
+    for codes, scales, src, got_c, got_s in ((kc, ks, k32, dk, dks), (vc, vs, v32, dv, dvs)):
+        exp_c, exp_s = codes.copy(), scales.copy()
+        assert oracle.append(src, past_np, exp_c, exp_s) == 0
+        assert np.array_equal(got_c.cpu().numpy(), exp_c)
+        assert np.array_equal(got_s.cpu().numpy().view(np.uint32), exp_s.view(np.uint32))
+
+
+@pytest.mark.parametrize("d", [64, 256])
+def test_append_ragged_multi_token_with_overflow(device, d):
+    rng = np.random.default_rng(SEED + 7)
+    B, H, T, cap = 3, 2, 3, 40
+    past_np = np.array([0, 17, cap - 2], np.uint32)  # last sequence: token 2 would land past capacity
+    kc, ks = _arenas(rng, B * H, cap, d, 0)
+    vc, vs = _arenas(rng, B * H, cap, d, 0)
+    k_new = kv_values(rng, B, H, T, d, heavy=False)
+    v_new = kv_values(rng, B, H, T, d, heavy=False)
+    kt, k32 = _to_device(k_new, torch.bfloat16, device)
+    vt, v32 = _to_device(v_new, torch.bfloat16, device)
+    dk, dv = torch.from_numpy(kc.copy()).to(device), torch.from_numpy(vc.copy()).to(device)
+    dks, dvs = torch.from_numpy(ks.copy()).to(device), torch.from_numpy(vs.copy()).to(device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    ppk.append(kt, vt, torch.from_numpy(past_np.view(np.int32)).to(device), dk, dv, dks, dvs, flags)
+    torch.cuda.synchronize()
+    assert flags.item() & ppk.PPK_FLAG_OVERFLOW
+    for codes, scales, src, got_c, got_s in ((kc, ks, k32, dk, dks), (vc, vs, v32, dv, dvs)):
+        exp_c, exp_s = codes.copy(), scales.copy()
+        assert oracle.append(src, past_np, exp_c, exp_s) == H  # one token of each head of sequence 2
+        assert np.array_equal(got_c.cpu().numpy(), exp_c)
+        assert np.array_equal(got_s.cpu().numpy().view(np.uint32), exp_s.view(np.uint32))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_dequantize_matches_oracle(device, d, dt):
+    rng = np.random.default_rng(SEED + 3)
+    x = kv_values(rng, 1, 8, 33, d).reshape(8, 33, d)
+    codes, scales = ppk.quantize(torch.from_numpy(x).to(device))
+    out = ppk.dequantize(codes, scales, DTYPES[dt]).cpu()
+    ref = oracle.dequantize(codes.cpu().numpy(), scales.cpu().numpy())
+    if dt == "f32":
+        assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
+    elif dt == "bf16":
+        assert np.array_equal(out.view(torch.int16).numpy().view(np.uint16), to_bf16_bits(ref))
+    else:
+        assert np.array_equal(out.numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
