@@ -1,8 +1,9 @@
 """Decode-step benchmark of the MI355X int8 KV path.
 
 One step = quantize-and-append of the new K/V token of every (sequence, head)
-+ split-K decode attention over the 8192-token int8 history + merge, on one
-GPU with all inputs resident in HBM. Prints one JSON line.
++ decode attention over the 8192-token int8 history and the current token
+(ppk_decode_step), on one GPU with all inputs resident in HBM. Prints one
+JSON line.
 
   python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--no-cpu-baseline]
 """
@@ -35,6 +36,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=64, help="head rows timed for the CPU baseline sample")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="run one plain 1 GiB elementwise copy (torch.neg, f32) first: the known-size kernel that "
+                        "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
     p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_attn_partial_b32_ctx8192.json"),
                    help="JSON with measured HBM bytes per partial launch (rocprofv3 --pmc), if present")
     return p.parse_args()
@@ -115,14 +119,18 @@ def main() -> int:
     out = torch.empty((rows, 1, D), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
-    append = ppk.AppendKV(kn, vn, past, kc, vc, ks, vs)
-    attn = ppk.DecodeAttention(q, kc, vc, ks, vs, kn.reshape(rows, 1, D), vn.reshape(rows, 1, D), past, H,
-                               args.split, max_past=L, out=out)
-    split = attn.split_tokens
+    # The current token is both attended from its bf16 copy (sk, sv) and
+    # committed into slot L of the arenas, in one launch.
+    step = ppk.DecodeStep(q, kc, vc, ks, vs, kn.reshape(rows, 1, D), vn.reshape(rows, 1, D), past, H,
+                          split_tokens=args.split, max_past=L, out=out)
+    split = step.split_tokens
 
-    def step():
-        append()
-        attn()
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     print("# bench: warmup", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
@@ -131,7 +139,7 @@ def main() -> int:
 
     # Timed region: every partial-kernel launch is bracketed by HIP events on
     # its own stream by the library's tracer.
-    ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_PARTIAL, reset=True)
+    ppk.kernel_stats(ppk.PPK_KERNEL_ATTENTION, reset=True)
     ppk.set_profiling(True)
     stream = torch.cuda.current_stream(dev)
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -143,25 +151,26 @@ def main() -> int:
     torch.cuda.synchronize()
     ppk.set_profiling(False)
     step_ms = t_start.elapsed_time(t_end) / args.steps
-    launches, partial_ms = ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_PARTIAL, reset=True)
-    partial_avg_ms = partial_ms / max(launches, 1)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_ATTENTION, reset=True)
+    kernel_avg_ms = kernel_ms / max(launches, 1)
 
-    # Algorithmic bytes: history K+V codes and scales of every row, the query,
-    # the new K/V token (read by append, its bf16 copy read by the merge as the
-    # current token) and the outputs: sum_b L_b*H*(2D+8) + q + current k,v + out.
+    # Algorithmic bytes of one step: history K+V codes and scales of every
+    # row, the bf16 query, the bf16 current K/V token (read once: quantised
+    # into the arena and scored as the current token), the f32 output and the
+    # appended codes + scales: sum_b L_b*H*(2D+8) + q + current k,v + out + append.
     hist_bytes = rows * L * (2 * D + 8)
-    q_bytes = rows * D * 2
-    partial_bytes = hist_bytes + q_bytes
-    step_bytes = hist_bytes + q_bytes + 2 * rows * D * 2 + rows * D * 4 + 2 * rows * (D + 4)
-    achieved = partial_bytes / (partial_avg_ms * 1e-3) / 1e9
+    step_bytes = hist_bytes + rows * D * 2 + 2 * rows * D * 2 + rows * D * 4 + 2 * rows * (D + 4)
+    kernel_bytes = step_bytes if step.ngroups == 1 else hist_bytes + rows * D * 2 + 2 * rows * (D + 4) + 2 * rows * D * 2
+    achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
 
+    kname = "ppk_decode_d%d" % D
     traffic = None
     if os.path.exists(args.traffic):
         try:
             with open(args.traffic) as f:
                 t = json.load(f)
-            if t.get("split") == split and t.get("workload") == f"B{B}H{H}D{D}L{L}":
+            if t.get("split") == split and t.get("workload") == f"B{B}H{H}D{D}L{L}" and t.get("kernel") == kname:
                 traffic = t.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
@@ -179,16 +188,18 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels, quantised on device; bf16 q and new K/V)",
-        "config": {"workload": "BASELINE config 5: decode step = append + split-K attention + merge",
+        "config": {"workload": "BASELINE config 5: decode step = append of the current token + attention over "
+                               "the int8 history (ppk_decode_step)",
                    "batch": B, "heads": H, "head_dim": D, "context": L, "capacity": cap, "kv": "int8 + f32 scales",
-                   "query": "bf16", "split_tokens": split, "splits": attn.nsplits},
+                   "query": "bf16", "tokens_per_wave": split, "blocks_per_row": step.ngroups,
+                   "launches_per_step": 1 if step.ngroups == 1 else 2},
         "tokens_per_s": round(B / (step_ms * 1e-3), 1),
         "step_hbm_gbps": round(step_gbps, 1),
         "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
-        "roofline": {"bound": "hbm", "kernel": "ppk_attn_partial_d%d" % D, "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": partial_bytes,
-                     "avg_launch_us": round(partial_avg_ms * 1e3, 2), "launches": launches},
+                     "traffic": traffic, "algorithmic_bytes_per_launch": kernel_bytes,
+                     "avg_launch_us": round(kernel_avg_ms * 1e3, 2), "launches": launches},
     }
     if not args.no_cpu_baseline:
         print("# bench: cpu baseline", file=sys.stderr, flush=True)

@@ -155,7 +155,7 @@ typedef struct PpkAttentionArgs {
   uint32_t heads;
   uint32_t capacity;       /* arena tokens per row */
   uint32_t head_dim;       /* 64, 128 or 256 */
-  uint32_t split_tokens;   /* tokens per split; 0 = automatic. Result does not depend on it. */
+  uint32_t split_tokens;   /* history tokens per wave; 0 = automatic. Result does not depend on it. */
   uint32_t max_past;       /* host upper bound of max(past); 0 = capacity. Rows beyond it give NaN. */
   float softmax_scale;     /* 0 = 1/sqrt(head_dim) */
   const void* q;           /* [rows, D] */
@@ -167,17 +167,38 @@ typedef struct PpkAttentionArgs {
   const void* sv;          /* [rows, D] current value */
   const uint32_t* past;    /* device U32[rows / heads] */
   void* out;               /* [rows, D] */
-  void* workspace;         /* ppk_attention_workspace_bytes() bytes, 256-byte aligned */
+  void* workspace;         /* ppk_attention_workspace_bytes() bytes, 256-byte aligned (may be NULL if 0) */
   uint64_t workspace_bytes;
 } PpkAttentionArgs;
 PPK_API int32_t ppk_attention_workspace_bytes(ppk_context* ctx, const PpkAttentionArgs* args, uint64_t* bytes);
-/* The launch plan the library would use for args: tokens per split, number
-   of splits and workspace bytes (ctx may be NULL: assumes 256 CUs). The
+/* The launch plan the library would use for args: history tokens per wave,
+   number of blocks (groups) per row and workspace bytes (ctx may be NULL:
+   assumes 256 CUs). One group per row means a single launch. The
    reference chooses split = 128 by default, clamped to 32..1024
    (int8_kv_ops.rs:52); its result does not depend on the split. */
 PPK_API int32_t ppk_attention_plan(ppk_context* ctx, const PpkAttentionArgs* args, uint32_t* split_tokens,
                                    uint32_t* nsplits, uint64_t* workspace_bytes);
 PPK_API int32_t ppk_decode_attention(ppk_context* ctx, void* stream, const PpkAttentionArgs* args);
+
+/* One decode step in as few launches as the plan allows (one when a block of
+   waves covers a whole row): quantise the current token k_new/v_new[row] and
+   append it at slot past[b] of the attention arenas, then attend over
+   [0, past[b]) plus the unquantised current token (attn.sk / attn.sv).
+   Equivalent to ppk_quantize_append(tokens = 1) followed by
+   ppk_decode_attention on the same arenas: the commit path of
+   forward_embedding / forward_batched_embedding (app/src/model/mod.rs:699-705,
+   app/src/model/batch.rs:152-161), where query_int8 appends before
+   int8_kv_ops::attention reads the pre-append history. past[b] >= capacity
+   skips that row's append and sets PPK_FLAG_OVERFLOW. */
+typedef struct PpkDecodeStepArgs {
+  uint32_t struct_size;
+  uint32_t new_dtype;      /* dtype of k_new / v_new */
+  const void* k_new;       /* [rows, D] */
+  const void* v_new;       /* [rows, D] */
+  uint32_t* flags;         /* optional device word, PPK_FLAG_* bits OR-ed in */
+  PpkAttentionArgs attn;
+} PpkDecodeStepArgs;
+PPK_API int32_t ppk_decode_step(ppk_context* ctx, void* stream, const PpkDecodeStepArgs* args);
 
 /* Known-answer self-check on the context's device, the three checks of
    int8_kv_ops::prepare (int8_kv_ops.rs:56-103) plus their fp32-history twins.
@@ -189,7 +210,8 @@ PPK_API int32_t ppk_prepare(ppk_context* ctx);
    recorded events only). Kernel ids below. The reference keeps launch counters
    only (app/src/model/hip_kernel.rs:8-21). */
 enum { PPK_KERNEL_QUANTIZE = 0, PPK_KERNEL_APPEND = 1, PPK_KERNEL_DEQUANTIZE = 2,
-       PPK_KERNEL_ATTN_PARTIAL = 3, PPK_KERNEL_ATTN_MERGE = 4, PPK_KERNEL_COUNT = 5 };
+       PPK_KERNEL_ATTENTION = 3, /* the decode kernel, with or without the fused append */
+       PPK_KERNEL_ATTN_MERGE = 4, PPK_KERNEL_COUNT = 5 };
 PPK_API int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable);
 PPK_API int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint64_t* launches,
                                  double* total_ms, uint32_t reset);

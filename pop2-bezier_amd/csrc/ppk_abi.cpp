@@ -48,8 +48,8 @@ int32_t call(Op&& op) {
 
 const char* kFnNames[ppk::kFnCount] = {
     "ppk_quantize_d64", "ppk_quantize_d128", "ppk_quantize_d256", "ppk_dequantize",
-    "ppk_attn_partial_d64", "ppk_attn_partial_d128", "ppk_attn_partial_d256",
-    "ppk_attn_partial_bf16h_d64", "ppk_attn_partial_bf16h_d128", "ppk_attn_partial_bf16h_d256",
+    "ppk_decode_d64", "ppk_decode_d128", "ppk_decode_d256",
+    "ppk_decode_bf16h_d64", "ppk_decode_bf16h_d128", "ppk_decode_bf16h_d256",
     "ppk_attn_merge_d64", "ppk_attn_merge_d128", "ppk_attn_merge_d256",
 };
 
@@ -150,17 +150,32 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
     split = std::min<uint32_t>(std::max<uint32_t>(a.split_tokens, tpl), 8192u);
     split = (split + tpl - 1) / tpl * tpl;
   } else {
-    // Smallest power-of-two split (>= 64 tokens) whose block count fits one
-    // resident round of one-wave blocks (about 20 per CU at 90 VGPRs).
-    const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 20;
+    // Smallest power-of-two tokens per wave (>= 64) that keeps the launch
+    // within about 16 resident waves per CU: each wave then streams one long
+    // contiguous stretch of K and of V.
+    const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 16;
     split = 64;
-    while (split < 8192 && uint64_t(a.rows) * ((span + split - 1) / split) > budget) split <<= 1;
+    while (split < 2048 && uint64_t(a.rows) * ((span + split - 1) / split) > budget) split <<= 1;
   }
+  const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
+  // Up to 8 waves per block, K/V scale staging within 64 KiB of LDS.
+  const uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(8, 8192 / split));
   plan.split = split;
-  plan.nsplits = uint32_t(std::max<uint64_t>(1, (span + split - 1) / split));
-  require(uint64_t(plan.nsplits) * a.rows <= 0x7fffffffu, "INT8 attention grid too large");
-  plan.y_bytes = (uint64_t(a.rows) * plan.nsplits * a.head_dim * 4 + 255) / 256 * 256;
-  plan.mz_bytes = (uint64_t(a.rows) * plan.nsplits * 2 * 4 + 255) / 256 * 256;
+  if (waves_per_row <= max_waves) {
+    plan.waves = uint32_t(waves_per_row);
+    plan.ngroups = 1;
+  } else {
+    plan.waves = uint32_t(max_waves);
+    plan.ngroups = uint32_t((waves_per_row + max_waves - 1) / max_waves);
+  }
+  require(uint64_t(plan.ngroups) * a.rows <= 0x7fffffffu, "INT8 attention grid too large");
+  // Per wave: staged K scales (then scores) and V scales; after the waves are
+  // done the same LDS holds one (m, z, pad, pad, y[D]) record per wave.
+  plan.lds_bytes = 4u * std::max<uint32_t>(2u * plan.waves * split, plan.waves * (a.head_dim + 4u));
+  if (plan.ngroups > 1) {
+    plan.y_bytes = (uint64_t(a.rows) * plan.ngroups * a.head_dim * 4 + 255) / 256 * 256;
+    plan.mz_bytes = (uint64_t(a.rows) * plan.ngroups * 2 * 4 + 255) / 256 * 256;
+  }
   plan.workspace_bytes = plan.y_bytes + plan.mz_bytes;
   return plan;
 }
@@ -245,7 +260,7 @@ void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArg
   launch(ctx, PPK_KERNEL_DEQUANTIZE, kDequantize, uint32_t(grid), 256, 0, stream, k);
 }
 
-void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a) {
+void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a, const PpkDecodeStepArgs* step) {
   const AttentionPlan plan = plan_attention(ctx, a);
   require(a.q && a.k_codes && a.v_codes && a.k_scales && a.v_scales && a.sk && a.sv && a.past && a.out,
           "INT8 attention null pointer");
@@ -254,54 +269,77 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   require(aligned(a.q, dtype_bytes(a.q_dtype)) && aligned(a.sk, dtype_bytes(a.scratch_dtype)) &&
               aligned(a.sv, dtype_bytes(a.scratch_dtype)) && aligned(a.out, dtype_bytes(a.out_dtype)),
           "INT8 attention float operand misaligned");
-  require(a.workspace && aligned(a.workspace, 256), "INT8 attention workspace missing or not 256-byte aligned");
-  require(a.workspace_bytes >= plan.workspace_bytes,
-          "INT8 attention workspace too small: need " + std::to_string(plan.workspace_bytes) + " bytes");
+  if (plan.workspace_bytes) {
+    require(a.workspace && aligned(a.workspace, 256), "INT8 attention workspace missing or not 256-byte aligned");
+    require(a.workspace_bytes >= plan.workspace_bytes,
+            "INT8 attention workspace too small: need " + std::to_string(plan.workspace_bytes) + " bytes");
+  }
+  if (step) {
+    require(step->struct_size >= sizeof(PpkDecodeStepArgs), "PpkDecodeStepArgs.struct_size too small");
+    require(valid_dtype(step->new_dtype), "INT8 decode step new-token dtype must be f32, bf16 or f16");
+    require(step->k_new && step->v_new, "INT8 decode step null new-token pointer");
+    require(aligned(step->k_new, dtype_bytes(step->new_dtype)) && aligned(step->v_new, dtype_bytes(step->new_dtype)) &&
+                (!step->flags || aligned(step->flags, 4)),
+            "INT8 decode step operand misaligned");
+  }
   const int di = dim_index(a.head_dim);
   const float scale = a.softmax_scale > 0.f ? a.softmax_scale : 1.0f / std::sqrt(float(a.head_dim));
   const float scale_log2 = scale * 1.4426950408889634f;
 
-  PartialArgs p{};
-  p.q = a.q;
-  p.k = a.k_codes;
-  p.v = a.v_codes;
-  p.ks = a.k_scales;
-  p.vs = a.v_scales;
-  p.past = a.past;
-  p.part_y = static_cast<float*>(a.workspace);
-  p.part_mz = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + plan.y_bytes);
-  p.rows = a.rows;
-  p.heads = a.heads;
-  p.capacity = a.capacity;
-  p.split_tokens = plan.split;
-  p.nsplits = plan.nsplits;
-  p.q_dtype = a.q_dtype;
-  p.scale_log2 = scale_log2;
-
-  MergeArgs m{};
-  m.q = a.q;
-  m.sk = a.sk;
-  m.sv = a.sv;
-  m.past = a.past;
-  m.part_y = p.part_y;
-  m.part_mz = p.part_mz;
-  m.out = a.out;
-  m.rows = a.rows;
-  m.heads = a.heads;
-  m.capacity = a.capacity;
-  m.split_tokens = plan.split;
-  m.nsplits = plan.nsplits;
-  m.q_dtype = a.q_dtype;
-  m.scratch_dtype = a.scratch_dtype;
-  m.out_dtype = a.out_dtype;
-  m.scale_log2 = scale_log2;
+  DecodeArgs d{};
+  d.q = a.q;
+  // The arenas are written only by the fused append, at slot past[b].
+  d.k = const_cast<uint8_t*>(a.k_codes);
+  d.v = const_cast<uint8_t*>(a.v_codes);
+  d.ks = const_cast<float*>(a.k_scales);
+  d.vs = const_cast<float*>(a.v_scales);
+  d.sk = a.sk;
+  d.sv = a.sv;
+  d.past = a.past;
+  d.part_y = plan.workspace_bytes ? static_cast<float*>(a.workspace) : nullptr;
+  d.part_mz = plan.workspace_bytes ? reinterpret_cast<float*>(static_cast<char*>(a.workspace) + plan.y_bytes) : nullptr;
+  d.out = a.out;
+  if (step) {
+    d.k_new = step->k_new;
+    d.v_new = step->v_new;
+    d.flags = step->flags;
+    d.new_dtype = step->new_dtype;
+    d.append = 1;
+  }
+  d.rows = a.rows;
+  d.heads = a.heads;
+  d.capacity = a.capacity;
+  d.split_tokens = plan.split;
+  d.ngroups = plan.ngroups;
+  d.q_dtype = a.q_dtype;
+  d.scratch_dtype = a.scratch_dtype;
+  d.out_dtype = a.out_dtype;
+  d.scale_log2 = scale_log2;
 
   const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
-  const Fn partial = Fn((bf16h ? kPartialBf16h64 : kPartial64) + di);
-  const uint32_t lds = 2 * plan.split * 4;
+  const Fn decode = Fn((bf16h ? kDecodeBf16h64 : kDecode64) + di);
   DeviceGuard guard(ctx->device);
-  launch(ctx, PPK_KERNEL_ATTN_PARTIAL, partial, plan.nsplits * a.rows, 64, lds, stream, p);
-  launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMerge64 + di), a.rows, 64, 0, stream, m);
+  launch(ctx, PPK_KERNEL_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d);
+  if (plan.ngroups > 1) {
+    MergeArgs m{};
+    m.q = a.q;
+    m.sk = a.sk;
+    m.sv = a.sv;
+    m.past = a.past;
+    m.part_y = d.part_y;
+    m.part_mz = d.part_mz;
+    m.out = a.out;
+    m.rows = a.rows;
+    m.heads = a.heads;
+    m.capacity = a.capacity;
+    m.split_tokens = plan.split * plan.waves;  // tokens per group
+    m.nsplits = plan.ngroups;
+    m.q_dtype = a.q_dtype;
+    m.scratch_dtype = a.scratch_dtype;
+    m.out_dtype = a.out_dtype;
+    m.scale_log2 = scale_log2;
+    launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMerge64 + di), a.rows, 64, 0, stream, m);
+  }
 }
 
 }  // namespace ppk
@@ -395,7 +433,7 @@ int32_t ppk_attention_plan(ppk_context* ctx, const PpkAttentionArgs* args, uint3
     ppk::require(args != nullptr, "ppk_attention_plan: null arguments");
     const ppk::AttentionPlan plan = ppk::plan_attention(ctx, *args);
     if (split_tokens) *split_tokens = plan.split;
-    if (nsplits) *nsplits = plan.nsplits;
+    if (nsplits) *nsplits = plan.ngroups;
     if (workspace_bytes) *workspace_bytes = plan.workspace_bytes;
   });
 }
@@ -404,6 +442,13 @@ int32_t ppk_decode_attention(ppk_context* ctx, void* stream, const PpkAttentionA
   return call([&] {
     ppk::require(ctx && args, "ppk_decode_attention: null context or arguments");
     ppk::run_attention(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_decode_step(ppk_context* ctx, void* stream, const PpkDecodeStepArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_decode_step: null context or arguments");
+    ppk::run_attention(ctx, static_cast<hipStream_t>(stream), args->attn, args);
   });
 }
 

@@ -34,8 +34,8 @@ inline void require(bool ok, const std::string& message) {
 
 enum Fn : int {
   kQuantize64, kQuantize128, kQuantize256, kDequantize,
-  kPartial64, kPartial128, kPartial256,
-  kPartialBf16h64, kPartialBf16h128, kPartialBf16h256,
+  kDecode64, kDecode128, kDecode256,
+  kDecodeBf16h64, kDecodeBf16h128, kDecodeBf16h256,
   kMerge64, kMerge128, kMerge256,
   kFnCount
 };
@@ -79,7 +79,11 @@ class DeviceGuard {
 // Validated launch plans. Validation throws PreconditionError before any
 // enqueue; launch throws UncertainError once a launch has been attempted.
 struct AttentionPlan {
-  uint32_t head_dim = 0, split = 0, nsplits = 0;
+  uint32_t head_dim = 0;
+  uint32_t split = 0;    // history tokens per wave
+  uint32_t waves = 0;    // waves per block
+  uint32_t ngroups = 0;  // blocks per row; 1 = final output in the same launch
+  uint32_t lds_bytes = 0;
   uint64_t y_bytes = 0, mz_bytes = 0, workspace_bytes = 0;
 };
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
@@ -87,7 +91,9 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
 void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a);
 void run_append(ppk_context* ctx, hipStream_t stream, const PpkAppendArgs& a);
 void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArgs& a);
-void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a);
+// step == nullptr: attention only; otherwise the fused decode step.
+void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a,
+                   const PpkDecodeStepArgs* step = nullptr);
 
 // int8_kv_ops::prepare known-answer checks (int8_kv_ops.cpp).
 void prepare_self_check(ppk_context* ctx);

@@ -39,20 +39,31 @@ struct DequantizeArgs {
   uint32_t pad;
 };
 
-// Split-K partial pass: block (split, row) covers history tokens
-// [split * split_tokens, min(+split_tokens, past)). Output record per block:
-//   y[D] floats at part_y + (row * nsplits + split) * D
-//   (m, z) at part_mz + (row * nsplits + split) * 2, m in log2 units
-struct PartialArgs {
+// Decode attention: block (group g, row r) of W = blockDim.x / 64 waves covers
+// history tokens [g*W*S, (g+1)*W*S) of row r, S = split_tokens per wave.
+// ngroups == 1: the block writes the final output row (current token included).
+// ngroups > 1: it writes a partial record for the merge kernel:
+//   y[D] floats at part_y + (row * ngroups + g) * D
+//   (m, z) at part_mz + (row * ngroups + g) * 2, m in log2 units.
+// append != 0: group 0 of each row first quantises k_new/v_new[row] into
+// slot past[b] of the arenas k/v/ks/vs (never read by this launch).
+struct DecodeArgs {
   const void* q;            // [rows, D]
-  const uint8_t* k;         // [rows, capacity, D]
-  const uint8_t* v;
-  const float* ks;          // [rows, capacity]
-  const float* vs;
+  uint8_t* k;               // [rows, capacity, D]
+  uint8_t* v;
+  float* ks;                // [rows, capacity]
+  float* vs;
+  const void* sk;           // [rows, D] current key (unquantised)
+  const void* sv;
   const uint32_t* past;     // [rows / heads]
   float* part_y;
   float* part_mz;
-  uint32_t rows, heads, capacity, split_tokens, nsplits, q_dtype;
+  void* out;                // [rows, D]
+  const void* k_new;        // [rows, D] token to append (append != 0)
+  const void* v_new;
+  uint32_t* flags;          // optional
+  uint32_t rows, heads, capacity, split_tokens, ngroups;
+  uint32_t q_dtype, scratch_dtype, out_dtype, new_dtype, append;
   float scale_log2;         // softmax_scale * log2(e)
   uint32_t pad;
 };

@@ -4,8 +4,8 @@
 //
 //   ppk_quantize_d{64,128,256}         quantize rows densely or append into arenas
 //   ppk_dequantize                     codes * scales -> f32/bf16/f16
-//   ppk_attn_partial[_bf16h]_d{..}     split-K partial softmax-attention
-//   ppk_attn_merge_d{..}               cross-split merge + current token
+//   ppk_decode[_bf16h]_d{..}           decode attention (+ fused append, + in-block merge)
+//   ppk_attn_merge_d{..}               cross-group merge + current token
 //
 // Semantics follow app/src/model/int8_kv_ops.rs:11-40 and
 // app/src/model/int8_kv.cu:8-59; the design (wave-per-row quantize, one-wave
@@ -97,29 +97,51 @@ __device__ __forceinline__ float wave_sum(float x) {
 // NaN quotients become code 0 (as a float->int conversion of NaN does on
 // the reference GPU path); the absmax ignores NaN like fmaxf / f32::max.
 // ---------------------------------------------------------------------------
+// Quantise one row of D values (src[src_row*D ...]) into codes[0..D) and
+// *scale; the whole wave participates. Returns true if the row held a
+// non-finite value (reported through flags when given).
 template <int D>
-__device__ __forceinline__ void quantize_body(const ppk::QuantizeArgs& a) {
+__device__ __forceinline__ void quantize_row(const void* src, size_t src_row, uint32_t dtype, uint8_t* codes,
+                                             float* scale, uint32_t* flags, int lane) {
 #pragma clang fp contract(off)
   constexpr int EPL = D / ppk::kWave;
+  float x[EPL];
+  bool finite = true;
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    x[e] = load_elem(src, src_row * D + size_t(lane) * EPL + e, dtype);
+    finite = finite && __builtin_isfinite(x[e]);
+    amax = fmaxf(amax, fabsf(x[e]));
+  }
+  amax = wave_max(amax);
+  const float s = fmaxf(amax / 127.0f, 1e-12f);
+  uint32_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float qf = rintf(x[e] / s);
+    const int qi = (qf != qf) ? 0 : int(fminf(fmaxf(qf, -127.f), 127.f));
+    packed |= (uint32_t(qi) & 0xffu) << (8 * e);
+  }
+  uint8_t* out = codes + size_t(lane) * EPL;
+  if constexpr (EPL == 1) *out = uint8_t(packed);
+  else if constexpr (EPL == 2) *reinterpret_cast<uint16_t*>(out) = uint16_t(packed);
+  else *reinterpret_cast<uint32_t*>(out) = packed;
+  if (lane == 0) *scale = s;
+  if (flags) {
+    const bool any_bad = __any(!finite);
+    if (any_bad && lane == 0) atomicOr(flags, 1u);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void quantize_body(const ppk::QuantizeArgs& a) {
   const int lane = threadIdx.x & 63;
   const uint64_t wave = uint64_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64;
   if (wave >= a.rows * a.ntensors) return;  // uniform per wave
   const uint32_t tensor = wave >= a.rows ? 1u : 0u;
   const uint64_t r = wave - (tensor ? a.rows : 0);
   const void* src = tensor ? a.src[1] : a.src[0];
-
-  float x[EPL];
-  bool finite = true;
-  float amax = 0.f;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    x[e] = load_elem(src, r * D + size_t(lane) * EPL + e, a.src_dtype);
-    finite = finite && __builtin_isfinite(x[e]);
-    amax = fmaxf(amax, fabsf(x[e]));
-  }
-  amax = wave_max(amax);
-  const float s = fmaxf(amax / 127.0f, 1e-12f);
-
   size_t dst = r;
   if (a.past) {
     const uint64_t bh = r / a.tokens;
@@ -131,24 +153,8 @@ __device__ __forceinline__ void quantize_body(const ppk::QuantizeArgs& a) {
     }
     dst = bh * a.capacity + slot;
   }
-
-  uint32_t packed = 0;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const float qf = rintf(x[e] / s);
-    const int qi = (qf != qf) ? 0 : int(fminf(fmaxf(qf, -127.f), 127.f));
-    packed |= (uint32_t(qi) & 0xffu) << (8 * e);
-  }
-  uint8_t* codes = (tensor ? a.codes[1] : a.codes[0]) + dst * D + size_t(lane) * EPL;
-  if constexpr (EPL == 1) *codes = uint8_t(packed);
-  else if constexpr (EPL == 2) *reinterpret_cast<uint16_t*>(codes) = uint16_t(packed);
-  else *reinterpret_cast<uint32_t*>(codes) = packed;
-  if (lane == 0) (tensor ? a.scales[1] : a.scales[0])[dst] = s;
-
-  if (a.flags) {
-    const bool any_bad = __any(!finite);
-    if (any_bad && lane == 0) atomicOr(a.flags, 1u);
-  }
+  quantize_row<D>(src, r, a.src_dtype, (tensor ? a.codes[1] : a.codes[0]) + dst * D,
+                  (tensor ? a.scales[1] : a.scales[0]) + dst, a.flags, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -191,61 +197,50 @@ __device__ __forceinline__ void dequantize_body(const ppk::DequantizeArgs& a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2a: split-K partial attention. One wave per (split, row).
+// Kernel 2a: decode attention. A block of W waves covers W*S consecutive
+// history tokens of one row (group g of the row); each wave streams its own S
+// tokens, the block combines its waves through LDS. With one group per row
+// the block also scores the current token and writes the final output, so a
+// decode step is a single launch; otherwise it writes a partial (m, z, y)
+// record for the merge kernel. Optionally the block first quantises the new
+// K/V token of its row into slot past[b] (a slot attention never reads).
 //
-// Lane layout: LPT = D/16 lanes share one token, each holding 16 channels, so
-// one dwordx4 load per lane moves 1 KiB = TPL = 64/LPT whole tokens. The dot
-// product is 16 FMAs per lane plus a DPP group sum; the per-token scale is
-// applied once to the sum (default) instead of to every element.
-//
-// Phase K streams this split's K codes and leaves log2-domain scores in LDS
+// Lane layout inside a wave: LPT = D/16 lanes share one token, each holding
+// 16 channels, so one dwordx4 load per lane moves 1 KiB = TPL = 64/LPT whole
+// tokens. The dot product is 16 FMAs per lane plus a DPP group sum; the
+// per-token scale is applied once to the sum (default) instead of to every
+// element. Phase K streams K codes and leaves log2-domain scores in LDS
 // (over the staged K scales); phase V streams V codes and accumulates
-// p_t * vscale_t * code_t per channel. No running-max rescale is needed
-// because the exact split max is known before phase V.
+// p_t * vscale_t * code_t per channel. The exact wave max is known before
+// phase V, so no running rescale is needed.
 // ---------------------------------------------------------------------------
+struct WavePartial {
+  float m;         // max log2-domain score (-inf if the wave had no tokens)
+  float z;         // sum of 2^(s - m)
+  float acc[16];   // sum of 2^(s - m) * v over this lane's 16 channels (valid in lanes j == 0)
+};
+
 template <int D, bool BF16H>
-__device__ __forceinline__ void attn_partial_body(const ppk::PartialArgs& a) {
+__device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_t row, uint32_t begin, uint32_t n,
+                                               const float (&qr)[16], float* s_lds, float* vs_lds, int lane,
+                                               WavePartial& out) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
   constexpr int U = 8;  // 1 KiB loads in flight per wave per batch
-  extern __shared__ float lds[];
-
-  const int lane = threadIdx.x;
   const int j = lane / LPT;  // token within a load tile
   const int c = lane % LPT;  // 16-channel chunk
-  // Flat grid, split index fastest: consecutive blocks stream consecutive
-  // stretches of one row's history.
-  const uint32_t row = blockIdx.x / a.nsplits;
-  const uint32_t split = blockIdx.x - row * a.nsplits;
-  const uint32_t S = a.split_tokens;
-  const size_t rec = size_t(row) * a.nsplits + split;
-  float* out_y = a.part_y + rec * D;
-  float* out_mz = a.part_mz + rec * 2;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out.acc[i] = 0.f;
+  out.m = -INFINITY;
+  out.z = 0.f;
+  if (n == 0) return;  // uniform per wave
 
-  const uint32_t p = a.past[row / a.heads];
-  const uint32_t begin = split * S;
-  const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.nsplits) * S;
-  const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
-  if (n == 0) {
-    for (int i = lane; i < D; i += ppk::kWave) out_y[i] = 0.f;
-    if (lane == 0) { out_mz[0] = -INFINITY; out_mz[1] = 0.f; }
-    return;
-  }
-
-  float* s_lds = lds;       // K scales, then log2-domain scores
-  float* vs_lds = lds + S;  // V scales
   const size_t tok0 = size_t(row) * a.capacity + begin;
   for (uint32_t t = lane; t < n; t += ppk::kWave) {
     s_lds[t] = a.ks[tok0 + t];
     vs_lds[t] = a.vs[tok0 + t];
   }
-  float qr[16];
-  {
-    const size_t qo = size_t(row) * D + size_t(c) * 16;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) qr[i] = load_elem(a.q, qo + i, a.q_dtype);
-  }
-  __syncthreads();
+  __builtin_amdgcn_wave_barrier();
 
   const uint8_t* kb = a.k + tok0 * D + size_t(c) * 16;
   const uint8_t* vb = a.v + tok0 * D + size_t(c) * 16;
@@ -282,11 +277,8 @@ __device__ __forceinline__ void attn_partial_body(const ppk::PartialArgs& a) {
   float m = mloc;
 #pragma unroll
   for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-  __syncthreads();
+  __builtin_amdgcn_wave_barrier();
 
-  float acc[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
   float z = 0.f;
   for (uint32_t t0 = 0; t0 < ntiles; t0 += U) {
     u4 raw[U];
@@ -308,7 +300,7 @@ __device__ __forceinline__ void attn_partial_body(const ppk::PartialArgs& a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const float vv = BF16H ? round_bf16(sbyte(raw[u][w], k) * vscale) : sbyte(raw[u][w], k);
-          acc[4 * w + k] = fmaf(wgt, vv, acc[4 * w + k]);
+          out.acc[4 * w + k] = fmaf(wgt, vv, out.acc[4 * w + k]);
         }
     }
   }
@@ -316,14 +308,112 @@ __device__ __forceinline__ void attn_partial_body(const ppk::PartialArgs& a) {
   for (int o = LPT; o < ppk::kWave; o <<= 1) {
     z += __shfl_xor(z, o);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] += __shfl_xor(acc[i], o);
+    for (int i = 0; i < 16; ++i) out.acc[i] += __shfl_xor(out.acc[i], o);
   }
-  if (j == 0) {
-    f4* o = reinterpret_cast<f4*>(out_y + c * 16);
+  out.m = m;
+  out.z = z;
+}
+
+template <int D, bool BF16H>
+__device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
+  constexpr int LPT = D / 16;
+  constexpr int EPL = D / ppk::kWave;
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int W = blockDim.x >> 6;
+  const int c = lane % LPT;
+  const uint32_t row = blockIdx.x / a.ngroups;
+  const uint32_t group = blockIdx.x - row * a.ngroups;
+  const uint32_t S = a.split_tokens;
+  const uint32_t p = a.past[row / a.heads];
+  const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.ngroups) * W * S;
+
+  // Fused commit of the current token (kernel 1 inside this launch).
+  if (a.append && group == 0) {
+    const bool kw = wave == 0, vw = wave == (W > 1 ? 1 : 0);
+    if (kw || vw) {
+      if (p >= a.capacity) {
+        if (lane == 0 && a.flags) atomicOr(a.flags, 2u);
+      } else {
+        const size_t slot = size_t(row) * a.capacity + p;
+        if (kw) quantize_row<D>(a.k_new, row, a.new_dtype, a.k + slot * D, a.ks + slot, a.flags, lane);
+        if (vw) quantize_row<D>(a.v_new, row, a.new_dtype, a.v + slot * D, a.vs + slot, a.flags, lane);
+      }
+    }
+  }
+
+  float qr[16];
+  {
+    const size_t qo = size_t(row) * D + size_t(c) * 16;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) o[w] = f4{acc[4 * w], acc[4 * w + 1], acc[4 * w + 2], acc[4 * w + 3]};
+    for (int i = 0; i < 16; ++i) qr[i] = load_elem(a.q, qo + i, a.q_dtype);
   }
-  if (lane == 0) { out_mz[0] = m; out_mz[1] = z; }
+  const uint32_t begin = (group * W + wave) * S;
+  const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
+  WavePartial part;
+  wave_attention<D, BF16H>(a, row, begin, n, qr, lds + size_t(wave) * 2 * S, lds + size_t(wave) * 2 * S + S, lane,
+                           part);
+
+  // Combine the block's waves through LDS (the staging area is reused).
+  // Record of wave w at mrg + w * R: m, z, 2 pad floats, y[D] (16-byte aligned).
+  constexpr int R = D + 4;
+  __syncthreads();
+  float* mrg = lds;
+  if (lane < LPT) {
+    f4* o = reinterpret_cast<f4*>(mrg + wave * R + 4 + c * 16);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
+  }
+  if (lane == 0) {
+    mrg[wave * R] = part.m;
+    mrg[wave * R + 1] = part.z;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  const bool final_out = a.ngroups == 1;
+  float s_cur = -INFINITY;
+  float sv[EPL];
+  if (final_out) {
+    // Current token: every lane holds q for its 16-channel chunk.
+    float d = 0.f;
+    const size_t so = size_t(row) * D + size_t(c) * 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d = fmaf(qr[i], load_elem(a.sk, so + i, a.scratch_dtype), d);
+    s_cur = group_sum<LPT>(d) * a.scale_log2;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) sv[e] = load_elem(a.sv, size_t(row) * D + size_t(lane) * EPL + e, a.scratch_dtype);
+  }
+  float m = s_cur;
+  for (int w = 0; w < W; ++w) m = fmaxf(m, mrg[w * R]);
+  float y[EPL], zsum = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) y[e] = 0.f;
+  for (int w = 0; w < W; ++w) {
+    const float wt = mrg[w * R] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrg[w * R] - m);
+    zsum = fmaf(wt, mrg[w * R + 1], zsum);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) y[e] = fmaf(wt, mrg[w * R + 4 + lane * EPL + e], y[e]);
+  }
+  if (final_out) {
+    const float wc = __builtin_amdgcn_exp2f(s_cur - m);
+    zsum += wc;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float o = valid ? fmaf(wc, sv[e], y[e]) / zsum : __builtin_nanf("");
+      store_elem(a.out, size_t(row) * D + size_t(lane) * EPL + e, a.out_dtype, o);
+    }
+  } else {
+    const size_t rec = size_t(row) * a.ngroups + group;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) a.part_y[rec * D + size_t(lane) * EPL + e] = y[e];
+    if (lane == 0) {
+      a.part_mz[rec * 2] = m;
+      a.part_mz[rec * 2 + 1] = zsum;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -360,7 +450,7 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   for (int e = 0; e < EPL; ++e) y[e] = 0.f;
   float zsum = 0.f;
   for (uint32_t s = 0; s < a.nsplits; ++s) {
-    const float w = __builtin_amdgcn_exp2f(mz[2 * s] - m);
+    const float w = mz[2 * s] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mz[2 * s] - m);
     zsum = fmaf(w, mz[2 * s + 1], zsum);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) y[e] = fmaf(w, py[size_t(s) * D + e], y[e]);
@@ -387,11 +477,11 @@ PPK_QUANTIZE(256)
 extern "C" __global__ __launch_bounds__(256) void ppk_dequantize(ppk::DequantizeArgs a) { dequantize_body(a); }
 
 #define PPK_ATTN(D)                                                                          \
-  extern "C" __global__ __launch_bounds__(64) void ppk_attn_partial_d##D(ppk::PartialArgs a) { \
-    attn_partial_body<D, false>(a);                                                          \
+  extern "C" __global__ __launch_bounds__(512) void ppk_decode_d##D(ppk::DecodeArgs a) {     \
+    decode_body<D, false>(a);                                                                \
   }                                                                                          \
-  extern "C" __global__ __launch_bounds__(64) void ppk_attn_partial_bf16h_d##D(ppk::PartialArgs a) { \
-    attn_partial_body<D, true>(a);                                                           \
+  extern "C" __global__ __launch_bounds__(512) void ppk_decode_bf16h_d##D(ppk::DecodeArgs a) { \
+    decode_body<D, true>(a);                                                                 \
   }                                                                                          \
   extern "C" __global__ __launch_bounds__(64) void ppk_attn_merge_d##D(ppk::MergeArgs a) {   \
     attn_merge_body<D>(a);                                                                   \

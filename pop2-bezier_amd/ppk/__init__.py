@@ -4,16 +4,17 @@ The product path is libppk.so (C-ABI, include/ppk_int8_kv.h) plus the gfx950
 code object ppk_kernels.hsaco; this package binds them for torch callers.
 """
 from ._abi import (PPK_ABI_VERSION, PPK_ATTN_BF16_HISTORY, PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW,
-                   PPK_KERNEL_APPEND, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_ATTN_PARTIAL, PPK_KERNEL_DEQUANTIZE,
+                   PPK_KERNEL_APPEND, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_ATTENTION, PPK_KERNEL_DEQUANTIZE,
                    PPK_KERNEL_QUANTIZE, PpkError, PpkExecutionUncertainError, PpkInvalidOutputError,
                    PpkPreconditionError)
-from .int8_kv_ops import (AppendKV, DecodeAttention, append, attention, context, dequantize, kernel_stats,
-                          prepare, quantize, set_profiling)
+from .int8_kv_ops import (AppendKV, DecodeAttention, DecodeStep, append, attention, context, decode_step,
+                          dequantize, kernel_stats, prepare, quantize, set_profiling)
 
 __all__ = [
     "PPK_ABI_VERSION", "PPK_ATTN_BF16_HISTORY", "PPK_FLAG_NONFINITE", "PPK_FLAG_OVERFLOW",
-    "PPK_KERNEL_APPEND", "PPK_KERNEL_ATTN_MERGE", "PPK_KERNEL_ATTN_PARTIAL", "PPK_KERNEL_DEQUANTIZE",
+    "PPK_KERNEL_APPEND", "PPK_KERNEL_ATTN_MERGE", "PPK_KERNEL_ATTENTION", "PPK_KERNEL_DEQUANTIZE",
     "PPK_KERNEL_QUANTIZE", "PpkError", "PpkExecutionUncertainError", "PpkInvalidOutputError",
-    "PpkPreconditionError", "AppendKV", "DecodeAttention", "append", "attention", "context", "dequantize",
+    "PpkPreconditionError", "AppendKV", "DecodeAttention", "DecodeStep", "append", "attention", "context",
+    "decode_step", "dequantize",
     "kernel_stats", "prepare", "quantize", "set_profiling",
 ]

@@ -18,7 +18,7 @@ PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
 PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW = 1, 2
 PPK_ATTN_BF16_HISTORY = 1
 (PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE,
- PPK_KERNEL_ATTN_PARTIAL, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_COUNT) = range(6)
+ PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_COUNT) = range(6)
 
 _u32, _u64, _ptr, _f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_float
 
@@ -49,6 +49,11 @@ class PpkAttentionArgs(ctypes.Structure):
                 ("workspace_bytes", _u64)]
 
 
+class PpkDecodeStepArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("new_dtype", _u32), ("k_new", _ptr), ("v_new", _ptr), ("flags", _ptr),
+                ("attn", PpkAttentionArgs)]
+
+
 # Every function the header declares: name -> (restype, argtypes).
 FUNCTIONS = {
     "ppk_abi_version": (_u32, []),
@@ -63,6 +68,7 @@ FUNCTIONS = {
     "ppk_attention_plan": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkAttentionArgs), ctypes.POINTER(_u32),
                                             ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
     "ppk_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkAttentionArgs)]),
+    "ppk_decode_step": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDecodeStepArgs)]),
     "ppk_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_context_set_profiling": (ctypes.c_int32, [_ptr, ctypes.c_int32]),
     "ppk_context_kernel_stats": (ctypes.c_int32, [_ptr, _u32, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double),

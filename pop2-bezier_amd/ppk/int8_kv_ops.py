@@ -164,7 +164,8 @@ def workspace_bytes(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = N
 
 
 def plan(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = None) -> tuple[int, int, int]:
-    """(tokens per split, number of splits, workspace bytes) the library chooses for args."""
+    """(history tokens per wave, blocks per row, workspace bytes) the library chooses for args.
+    One block per row means the whole step is a single launch (no workspace)."""
     split, nsplits, nbytes = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
     check(lib().ppk_attention_plan(ctx, ctypes.byref(args), ctypes.byref(split), ctypes.byref(nsplits),
                                    ctypes.byref(nbytes)), "ppk_attention_plan")
@@ -181,11 +182,42 @@ def attention(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, 
     nbytes = workspace_bytes(a, ctx)
     # The caching allocator is stream-ordered: the block is not reused before
     # the kernels queued on this stream have consumed it.
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     a.workspace = ws.data_ptr()
     a.workspace_bytes = nbytes
     check(lib().ppk_decode_attention(ctx, _stream(q), ctypes.byref(a)), "ppk_decode_attention")
     return out
+
+
+def decode_step(q, k, v, ks, vs, sk, sv, past, heads: int, k_new: torch.Tensor | None = None,
+                v_new: torch.Tensor | None = None, split_tokens: int = 0, *, flags: torch.Tensor | None = None,
+                bf16_history: bool = False, max_past: int = 0, out_dtype: torch.dtype = torch.float32,
+                softmax_scale: float = 0.0) -> torch.Tensor:
+    """Commit + attend in one call: quantise k_new/v_new [rows, D] (default: sk/sv) into slot past[b] of the
+    arenas, then attention over [0, past[b]) plus the current token, as forward_embedding's commit path does
+    (query_int8 then int8_kv_ops::attention, app/src/model/mod.rs:699-705)."""
+    a, out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
+                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale)
+    step = _step_args(a, sk if k_new is None else k_new, sv if v_new is None else v_new, flags, k.shape[2])
+    ctx = context(q.device)
+    nbytes = workspace_bytes(a, ctx)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    step.attn.workspace = ws.data_ptr()
+    step.attn.workspace_bytes = nbytes
+    check(lib().ppk_decode_step(ctx, _stream(q), ctypes.byref(step)), "ppk_decode_step")
+    return out
+
+
+def _step_args(a: _abi.PpkAttentionArgs, k_new: torch.Tensor, v_new: torch.Tensor, flags, d: int
+               ) -> _abi.PpkDecodeStepArgs:
+    _require(k_new.dtype == v_new.dtype and k_new.dtype in _DTYPES and k_new.numel() == a.rows * d
+             and v_new.numel() == a.rows * d and k_new.is_contiguous() and v_new.is_contiguous(),
+             "INT8 decode step new token must be float[rows,D]")
+    if flags is not None:
+        _require(flags.dtype in (torch.int32, torch.uint32) and flags.numel() >= 1, "flags must be one 32-bit word")
+    return _abi.PpkDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkDecodeStepArgs), new_dtype=_DTYPES[k_new.dtype],
+                                  k_new=k_new.data_ptr(), v_new=v_new.data_ptr(),
+                                  flags=flags.data_ptr() if flags is not None else None, attn=a)
 
 
 class DecodeAttention:
@@ -199,8 +231,8 @@ class DecodeAttention:
                                              bf16_history=bf16_history, max_past=max_past, out=out,
                                              out_dtype=out_dtype)
         self.ctx = context(q.device)
-        self.split_tokens, self.nsplits, nbytes = plan(self.args, self.ctx)
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+        self.split_tokens, self.ngroups, nbytes = plan(self.args, self.ctx)
+        self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.workspace = self.workspace.data_ptr()
         self.args.workspace_bytes = nbytes
         self._keep = (q, k, v, ks, vs, sk, sv, past)
@@ -211,6 +243,34 @@ class DecodeAttention:
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
         check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_decode_attention")
+        return self.out
+
+
+class DecodeStep:
+    """A prepared decode step (append of the current token + attention) for fixed buffers: the argument
+    block and workspace are built once; __call__ enqueues one launch (two when the plan splits rows)."""
+
+    def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, k_new=None, v_new=None, split_tokens: int = 0, *,
+                 flags=None, bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype = torch.float32):
+        a, self.out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
+                                     max_past=max_past, out=out, out_dtype=out_dtype)
+        k_new = sk if k_new is None else k_new
+        v_new = sv if v_new is None else v_new
+        self.args = _step_args(a, k_new, v_new, flags, k.shape[2])
+        self.ctx = context(q.device)
+        self.split_tokens, self.ngroups, nbytes = plan(self.args.attn, self.ctx)
+        self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        self.args.attn.workspace = self.workspace.data_ptr()
+        self.args.attn.workspace_bytes = nbytes
+        self._keep = (q, k, v, ks, vs, sk, sv, past, k_new, v_new, flags)
+        self._ref = ctypes.byref(self.args)
+        self._fn = lib().ppk_decode_step
+        self.device = q.device
+
+    def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_decode_step")
         return self.out
 
 

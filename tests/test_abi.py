@@ -25,7 +25,7 @@ def declared_functions() -> list[str]:
 def test_library_exports_every_declared_symbol():
     lib = _abi.lib()
     names = declared_functions()
-    assert len(names) >= 13
+    assert len(names) >= 14
     for name in names:
         assert hasattr(lib, name), f"libppk.so does not export {name}"
         assert name in _abi.FUNCTIONS, f"ctypes binding lacks {name}"
@@ -38,7 +38,8 @@ def test_code_object_is_built_for_gfx950():
     assert os.path.exists(_abi.HSACO_PATH)
     blob = open(_abi.HSACO_PATH, "rb").read()
     assert b"gfx950" in blob
-    for kernel in (b"ppk_quantize_d128", b"ppk_attn_partial_d128", b"ppk_attn_merge_d128", b"ppk_dequantize"):
+    for kernel in (b"ppk_quantize_d128", b"ppk_decode_d128", b"ppk_decode_bf16h_d128", b"ppk_attn_merge_d128",
+                   b"ppk_dequantize"):
         assert kernel in blob
 
 
@@ -52,7 +53,8 @@ def c_layout(tmp_path_factory):
     src = tmp_path_factory.mktemp("abi") / "layout.c"
     exe = src.with_suffix("")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
-    for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs):
+    for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs,
+                _abi.PpkDecodeStepArgs):
         name = cls.__name__
         lines.append(f'printf("{name} size %zu\\n", sizeof({name}));')
         for field, _ in cls._fields_:
@@ -65,7 +67,7 @@ def c_layout(tmp_path_factory):
 
 
 @pytest.mark.parametrize("cls", [_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs,
-                                 _abi.PpkAttentionArgs])
+                                 _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs])
 def test_struct_layout_matches_c(c_layout, cls):
     name = cls.__name__
     assert c_layout[(name, "size")] == ctypes.sizeof(cls)
@@ -83,15 +85,18 @@ def _attn_args(**kw) -> _abi.PpkAttentionArgs:
 
 
 def test_plan_sizes_workspace_without_a_device():
-    split, nsplits, nbytes = ppk.int8_kv_ops.plan(_attn_args())
-    assert split % 8 == 0 and split >= 64
-    assert nsplits == -(-8192 // split)
-    assert nbytes >= 512 * nsplits * (128 + 2) * 4
-    # An explicit split is honoured (rounded up to whole 1 KiB tiles).
-    split, nsplits, _ = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
-    assert (split, nsplits) == (104, -(-8192 // 104))
-    # Result does not depend on the split, so the workspace query is the only contract.
-    assert ppk.int8_kv_ops.workspace_bytes(_attn_args(split_tokens=128)) == 512 * 64 * 128 * 4 + 512 * 64 * 2 * 4
+    # Config 5 on 256 CUs: 8 waves x 1024 tokens cover a row, so one block per
+    # row finishes the step in one launch and needs no workspace.
+    split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args())
+    assert (split, groups, nbytes) == (1024, 1, 0)
+    # An explicit per-wave split is honoured (rounded up to whole 1 KiB tiles);
+    # 8 waves per block, so ceil(ceil(8192/104)/8) blocks per row.
+    split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
+    assert (split, groups) == (104, -(-(-(-8192 // 104)) // 8))
+    assert nbytes == 512 * groups * 128 * 4 + -(-(512 * groups * 2 * 4) // 256) * 256
+    # Few rows: split-K across blocks plus the merge kernel (config 3 shape).
+    split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048))
+    assert split == 64 and groups == 4 and nbytes == 16 * 4 * 128 * 4 + 16 * 4 * 2 * 4
 
 
 @pytest.mark.parametrize("bad", [dict(head_dim=96), dict(rows=30, heads=16), dict(heads=0), dict(capacity=0),
@@ -110,4 +115,6 @@ def test_null_context_calls_return_status_1():
     q = _abi.PpkQuantizeArgs(struct_size=ctypes.sizeof(_abi.PpkQuantizeArgs))
     assert lib.ppk_quantize(None, None, ctypes.byref(q)) == _abi.PPK_PRECONDITION
     assert lib.ppk_prepare(None) == _abi.PPK_PRECONDITION
+    step = _abi.PpkDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkDecodeStepArgs), attn=a)
+    assert lib.ppk_decode_step(None, None, ctypes.byref(step)) == _abi.PPK_PRECONDITION
     assert lib.ppk_context_release(None) == _abi.PPK_OK

@@ -181,3 +181,53 @@ def test_reference_offset_views(device):
     torch.cuda.synchronize()
     assert_close(out.reshape(rows, d).cpu().numpy(), c.reference(), what="offset views")
     del rng
+
+
+@pytest.mark.parametrize("split", [0, 64])
+def test_decode_step_fused_append_equals_separate_calls(device, split):
+    """ppk_decode_step == ppk_quantize_append(tokens=1) then ppk_decode_attention on the same arenas,
+    both for the one-launch plan (split 0 here: one block per row) and the split-K plan (split 64)."""
+    B, H, D, cap = 4, 8, 128, 600
+    lengths = [0, 17, 300, 599]
+    c = Case(device, B, H, D, lengths, cap, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16, seed=SEED + 31)
+    ref = c.reference()
+    kc0, vc0, ks0, vs0 = c.kc.clone(), c.vc.clone(), c.ks.clone(), c.vs.clone()
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, split_tokens=split, flags=flags)
+    torch.cuda.synchronize()
+    assert flags.item() == 0
+    assert_close(out.reshape(c.rows, D).cpu().numpy(), ref, what=f"decode step split {split}")
+    # Arenas: slot past[b] of every head row holds the quantised current token, nothing else changed.
+    codes, scales, _ = oracle.quantize(c.sk32.reshape(c.rows, 1, D))
+    vcodes, vscales, _ = oracle.quantize(c.sv32.reshape(c.rows, 1, D))
+    exp_k, exp_v = kc0.cpu().numpy(), vc0.cpu().numpy()
+    exp_ks, exp_vs = ks0.cpu().numpy(), vs0.cpu().numpy()
+    for r in range(c.rows):
+        p = int(c.past[r // H])
+        exp_k[r, p], exp_ks[r, p] = codes[r, 0], scales[r, 0]
+        exp_v[r, p], exp_vs[r, p] = vcodes[r, 0], vscales[r, 0]
+    assert np.array_equal(c.kc.cpu().numpy(), exp_k)
+    assert np.array_equal(c.vc.cpu().numpy(), exp_v)
+    np.testing.assert_array_equal(c.ks.cpu().numpy(), exp_ks)  # NaN sentinels compare equal here
+    np.testing.assert_array_equal(c.vs.cpu().numpy(), exp_vs)
+
+
+def test_decode_step_full_capacity_row_flags_overflow(device):
+    B, H, D, cap = 2, 2, 64, 40
+    c = Case(device, B, H, D, [10, cap], cap, seed=SEED + 32)
+    ref = c.reference()
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, flags=flags)
+    torch.cuda.synchronize()
+    assert flags.item() & ppk.PPK_FLAG_OVERFLOW
+    assert_close(out.reshape(c.rows, D).cpu().numpy(), ref, what="full row still attends")
+
+
+def test_decode_step_config5_shape_one_launch_plan(device):
+    """BASELINE config 5 rows and context at reduced batch: the auto plan covers each row with one block."""
+    B, H, D, L = 4, 16, 128, 8192
+    c = Case(device, B, H, D, [L] * B, L + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16, seed=SEED + 33)
+    step = ppk.DecodeStep(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, max_past=L)
+    out = step()
+    torch.cuda.synchronize()
+    assert_close(out.reshape(c.rows, D).cpu().numpy(), c.reference(), what="config 5 shape")
