@@ -39,7 +39,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run one plain 1 GiB elementwise copy (torch.neg, f32) first: the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
-    p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic_attn_partial_b32_ctx8192.json"),
+    p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "ppk_decode_d128_b32_h16_ctx8192_traffic.json"),
                    help="JSON with measured HBM bytes per partial launch (rocprofv3 --pmc), if present")
     return p.parse_args()
 

@@ -158,8 +158,8 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
     while (split < 2048 && uint64_t(a.rows) * ((span + split - 1) / split) > budget) split <<= 1;
   }
   const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
-  // Up to 8 waves per block, K/V scale staging within 64 KiB of LDS.
-  const uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(8, 8192 / split));
+  // Up to 16 waves per block; one float of LDS per history token of the block.
+  const uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
   plan.split = split;
   if (waves_per_row <= max_waves) {
     plan.waves = uint32_t(waves_per_row);
@@ -169,9 +169,9 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
     plan.ngroups = uint32_t((waves_per_row + max_waves - 1) / max_waves);
   }
   require(uint64_t(plan.ngroups) * a.rows <= 0x7fffffffu, "INT8 attention grid too large");
-  // Per wave: staged K scales (then scores) and V scales; after the waves are
-  // done the same LDS holds one (m, z, pad, pad, y[D]) record per wave.
-  plan.lds_bytes = 4u * std::max<uint32_t>(2u * plan.waves * split, plan.waves * (a.head_dim + 4u));
+  // Per wave: one log2-domain score per token; after the waves are done the
+  // same LDS holds one (m, z, pad, pad, y[D]) record per wave.
+  plan.lds_bytes = 4u * std::max<uint32_t>(plan.waves * split, plan.waves * (a.head_dim + 4u));
   if (plan.ngroups > 1) {
     plan.y_bytes = (uint64_t(a.rows) * plan.ngroups * a.head_dim * 4 + 255) / 256 * 256;
     plan.mz_bytes = (uint64_t(a.rows) * plan.ngroups * 2 * 4 + 255) / 256 * 256;

@@ -31,6 +31,29 @@ __device__ __forceinline__ float load_elem(const void* p, size_t i, uint32_t dty
   return dtype == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
 
+// N consecutive elements starting at element i, widened to f32: one dtype
+// branch, then N independent loads in flight together.
+template <int N>
+__device__ __forceinline__ void load_vec(const void* p, size_t i, uint32_t dtype, float (&out)[N]) {
+  if (dtype == kF32) {
+    const float* f = static_cast<const float*>(p) + i;
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = f[e];
+  } else {
+    const uint16_t* h = static_cast<const uint16_t*>(p) + i;
+    uint16_t b[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) b[e] = h[e];
+    if (dtype == kBF16) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) out[e] = bf16_to_f32(b[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < N; ++e) out[e] = f16_to_f32(b[e]);
+    }
+  }
+}
+
 // Round-to-nearest-even to bfloat16, returned as the 16 stored bits. NaN stays
 // a quiet NaN (the carry trick alone could turn some NaN payloads into Inf).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
@@ -106,11 +129,11 @@ __device__ __forceinline__ void quantize_row(const void* src, size_t src_row, ui
 #pragma clang fp contract(off)
   constexpr int EPL = D / ppk::kWave;
   float x[EPL];
+  load_vec<EPL>(src, src_row * D + size_t(lane) * EPL, dtype, x);
   bool finite = true;
   float amax = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
-    x[e] = load_elem(src, src_row * D + size_t(lane) * EPL + e, dtype);
     finite = finite && __builtin_isfinite(x[e]);
     amax = fmaxf(amax, fabsf(x[e]));
   }
@@ -209,10 +232,11 @@ __device__ __forceinline__ void dequantize_body(const ppk::DequantizeArgs& a) {
 // 16 channels, so one dwordx4 load per lane moves 1 KiB = TPL = 64/LPT whole
 // tokens. The dot product is 16 FMAs per lane plus a DPP group sum; the
 // per-token scale is applied once to the sum (default) instead of to every
-// element. Phase K streams K codes and leaves log2-domain scores in LDS
-// (over the staged K scales); phase V streams V codes and accumulates
+// element. Phase K streams K codes and scales and leaves log2-domain scores
+// in LDS; phase V streams V codes and scales and accumulates
 // p_t * vscale_t * code_t per channel. The exact wave max is known before
-// phase V, so no running rescale is needed.
+// phase V, so no running rescale is needed. Each wave keeps two batches of
+// loads in flight (the next batch is issued before the current is consumed).
 // ---------------------------------------------------------------------------
 struct WavePartial {
   float m;         // max log2-domain score (-inf if the wave had no tokens)
@@ -220,58 +244,107 @@ struct WavePartial {
   float acc[16];   // sum of 2^(s - m) * v over this lane's 16 channels (valid in lanes j == 0)
 };
 
+// One batch = U load tiles = U*TPL consecutive tokens of this wave's range.
+// Codes come as one dwordx4 per lane per tile; the batch's per-token scales
+// come as one coalesced dword per lane (lane l holds token l of the batch)
+// and reach each token's lane group through a cross-lane read.
+template <int D, int U>
+__device__ __forceinline__ void load_batch(const uint8_t* base, const float* scales, uint32_t t0, uint32_t n, int j,
+                                           int lane, u4 (&raw)[U], float& scale) {
+  constexpr int TPL = ppk::kWave / (D / 16);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t tc = min((t0 + u) * TPL + j, n - 1);  // clamp: always in bounds
+    raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(base + size_t(tc) * D));
+  }
+  scale = __builtin_nontemporal_load(scales + min(t0 * TPL + uint32_t(lane % (U * TPL)), n - 1));
+}
+
 template <int D, bool BF16H>
-__device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_t row, uint32_t begin, uint32_t n,
-                                               const float (&qr)[16], float* s_lds, float* vs_lds, int lane,
-                                               WavePartial& out) {
+__device__ __forceinline__ float score_batch(const u4 (&raw)[4], float scale_lane, uint32_t t0, uint32_t n, int j,
+                                             int c, const float (&qr)[16], float sl2, float* s_lds, float mloc) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
-  constexpr int U = 8;  // 1 KiB loads in flight per wave per batch
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t tok = (t0 + u) * TPL + j;
+    const float kscale = __shfl(scale_lane, u * TPL + j);
+    float d = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float kv = BF16H ? round_bf16(sbyte(raw[u][w], k) * kscale) : sbyte(raw[u][w], k);
+        d = fmaf(qr[4 * w + k], kv, d);
+      }
+    d = group_sum<LPT>(d);
+    float sc = BF16H ? d * sl2 : d * kscale * sl2;
+    sc = tok < n ? sc : -INFINITY;
+    mloc = fmaxf(mloc, sc);
+    if (c == 0 && tok < n) s_lds[tok] = sc;
+  }
+  return mloc;
+}
+
+template <int D, bool BF16H>
+__device__ __forceinline__ void accumulate_batch(const u4 (&raw)[4], float scale_lane, uint32_t t0, uint32_t n, int j,
+                                                 float m, const float* s_lds, float& z, float (&acc)[16]) {
+  constexpr int LPT = D / 16;
+  constexpr int TPL = ppk::kWave / LPT;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t tok = (t0 + u) * TPL + j;
+    const float vscale = __shfl(scale_lane, u * TPL + j);
+    const float e = __builtin_amdgcn_exp2f(s_lds[min(tok, n - 1)] - m);  // branch-free; masked below
+    const float pr = tok < n ? e : 0.f;
+    z += pr;
+    const float wgt = BF16H ? pr : pr * vscale;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float vv = BF16H ? round_bf16(sbyte(raw[u][w], k) * vscale) : sbyte(raw[u][w], k);
+        acc[4 * w + k] = fmaf(wgt, vv, acc[4 * w + k]);
+      }
+  }
+}
+
+// Streams this wave's n tokens (from `begin`) of one row: phase K scores,
+// phase V accumulation. Two batches (A, B) ping-pong so the next batch's loads
+// are always in flight while the current one is consumed; addresses past the
+// end clamp to the last token and those tokens are masked out.
+template <int D, bool BF16H>
+__device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_t row, uint32_t begin, uint32_t n,
+                                               const float (&qr)[16], float* s_lds, int lane, WavePartial& out) {
+  constexpr int LPT = D / 16;
+  constexpr int TPL = ppk::kWave / LPT;
+  constexpr int U = 4;  // tiles per batch
   const int j = lane / LPT;  // token within a load tile
   const int c = lane % LPT;  // 16-channel chunk
-#pragma unroll
-  for (int i = 0; i < 16; ++i) out.acc[i] = 0.f;
   out.m = -INFINITY;
   out.z = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out.acc[i] = 0.f;
   if (n == 0) return;  // uniform per wave
 
   const size_t tok0 = size_t(row) * a.capacity + begin;
-  for (uint32_t t = lane; t < n; t += ppk::kWave) {
-    s_lds[t] = a.ks[tok0 + t];
-    vs_lds[t] = a.vs[tok0 + t];
-  }
-  __builtin_amdgcn_wave_barrier();
-
   const uint8_t* kb = a.k + tok0 * D + size_t(c) * 16;
   const uint8_t* vb = a.v + tok0 * D + size_t(c) * 16;
+  const float* ksb = a.ks + tok0;
+  const float* vsb = a.vs + tok0;
   const uint32_t ntiles = (n + TPL - 1) / TPL;
   const float sl2 = a.scale_log2;
 
   float mloc = -INFINITY;
-  for (uint32_t t0 = 0; t0 < ntiles; t0 += U) {
-    u4 raw[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tc = min((t0 + u) * TPL + j, n - 1);  // clamp: always in bounds
-      raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(kb + size_t(tc) * D));
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tok = (t0 + u) * TPL + j;
-      const float kscale = s_lds[min(tok, n - 1)];
-      float d = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float kv = BF16H ? round_bf16(sbyte(raw[u][w], k) * kscale) : sbyte(raw[u][w], k);
-          d = fmaf(qr[4 * w + k], kv, d);
-        }
-      d = group_sum<LPT>(d);
-      float sc = BF16H ? d * sl2 : d * kscale * sl2;
-      sc = tok < n ? sc : -INFINITY;
-      mloc = fmaxf(mloc, sc);
-      if (c == 0 && tok < n) s_lds[tok] = sc;
+  {
+    u4 ra[U], rb[U];
+    float sa, sb;
+    load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
+    for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
+      load_batch<D, U>(kb, ksb, t0 + U, n, j, lane, rb, sb);
+      mloc = score_batch<D, BF16H>(ra, sa, t0, n, j, c, qr, sl2, s_lds, mloc);
+      load_batch<D, U>(kb, ksb, t0 + 2 * U, n, j, lane, ra, sa);
+      mloc = score_batch<D, BF16H>(rb, sb, t0 + U, n, j, c, qr, sl2, s_lds, mloc);
     }
   }
   float m = mloc;
@@ -280,28 +353,15 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   __builtin_amdgcn_wave_barrier();
 
   float z = 0.f;
-  for (uint32_t t0 = 0; t0 < ntiles; t0 += U) {
-    u4 raw[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tc = min((t0 + u) * TPL + j, n - 1);
-      raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(vb + size_t(tc) * D));
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tok = (t0 + u) * TPL + j;
-      const uint32_t tc = min(tok, n - 1);
-      const float pr = tok < n ? __builtin_amdgcn_exp2f(s_lds[tc] - m) : 0.f;
-      const float vscale = vs_lds[tc];
-      z += pr;
-      const float wgt = BF16H ? pr : pr * vscale;
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float vv = BF16H ? round_bf16(sbyte(raw[u][w], k) * vscale) : sbyte(raw[u][w], k);
-          out.acc[4 * w + k] = fmaf(wgt, vv, out.acc[4 * w + k]);
-        }
+  {
+    u4 ra[U], rb[U];
+    float sa, sb;
+    load_batch<D, U>(vb, vsb, 0, n, j, lane, ra, sa);
+    for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
+      load_batch<D, U>(vb, vsb, t0 + U, n, j, lane, rb, sb);
+      accumulate_batch<D, BF16H>(ra, sa, t0, n, j, m, s_lds, z, out.acc);
+      load_batch<D, U>(vb, vsb, t0 + 2 * U, n, j, lane, ra, sa);
+      accumulate_batch<D, BF16H>(rb, sb, t0 + U, n, j, m, s_lds, z, out.acc);
     }
   }
 #pragma unroll
@@ -344,16 +404,11 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   }
 
   float qr[16];
-  {
-    const size_t qo = size_t(row) * D + size_t(c) * 16;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) qr[i] = load_elem(a.q, qo + i, a.q_dtype);
-  }
+  load_vec<16>(a.q, size_t(row) * D + size_t(c) * 16, a.q_dtype, qr);
   const uint32_t begin = (group * W + wave) * S;
   const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
   WavePartial part;
-  wave_attention<D, BF16H>(a, row, begin, n, qr, lds + size_t(wave) * 2 * S, lds + size_t(wave) * 2 * S + S, lane,
-                           part);
+  wave_attention<D, BF16H>(a, row, begin, n, qr, lds + size_t(wave) * S, lane, part);
 
   // Combine the block's waves through LDS (the staging area is reused).
   // Record of wave w at mrg + w * R: m, z, 2 pad floats, y[D] (16-byte aligned).
@@ -377,14 +432,16 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   float s_cur = -INFINITY;
   float sv[EPL];
   if (final_out) {
-    // Current token: every lane holds q for its 16-channel chunk.
-    float d = 0.f;
+    // Current token: each lane dots its 16-channel chunk of q and sk.
+    float qv[16], kv[16];
     const size_t so = size_t(row) * D + size_t(c) * 16;
+    load_vec<16>(a.q, so, a.q_dtype, qv);
+    load_vec<16>(a.sk, so, a.scratch_dtype, kv);
+    load_vec<EPL>(a.sv, size_t(row) * D + size_t(lane) * EPL, a.scratch_dtype, sv);
+    float d = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) d = fmaf(qr[i], load_elem(a.sk, so + i, a.scratch_dtype), d);
+    for (int i = 0; i < 16; ++i) d = fmaf(qv[i], kv[i], d);
     s_cur = group_sum<LPT>(d) * a.scale_log2;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) sv[e] = load_elem(a.sv, size_t(row) * D + size_t(lane) * EPL + e, a.scratch_dtype);
   }
   float m = s_cur;
   for (int w = 0; w < W; ++w) m = fmaxf(m, mrg[w * R]);
@@ -429,14 +486,14 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   const uint32_t p = a.past[row / a.heads];
   const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.nsplits) * a.split_tokens;
 
-  float sv[EPL];
+  float sv[EPL], qv[EPL], kv[EPL];
   float d = 0.f;
   const size_t base = size_t(row) * D + size_t(lane) * EPL;
+  load_vec<EPL>(a.q, base, a.q_dtype, qv);
+  load_vec<EPL>(a.sk, base, a.scratch_dtype, kv);
+  load_vec<EPL>(a.sv, base, a.scratch_dtype, sv);
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    d = fmaf(load_elem(a.q, base + e, a.q_dtype), load_elem(a.sk, base + e, a.scratch_dtype), d);
-    sv[e] = load_elem(a.sv, base + e, a.scratch_dtype);
-  }
+  for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kv[e], d);
   const float s_cur = wave_sum(d) * a.scale_log2;
 
   const float* mz = a.part_mz + size_t(row) * a.nsplits * 2;
@@ -477,10 +534,10 @@ PPK_QUANTIZE(256)
 extern "C" __global__ __launch_bounds__(256) void ppk_dequantize(ppk::DequantizeArgs a) { dequantize_body(a); }
 
 #define PPK_ATTN(D)                                                                          \
-  extern "C" __global__ __launch_bounds__(512) void ppk_decode_d##D(ppk::DecodeArgs a) {     \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_d##D(ppk::DecodeArgs a) {     \
     decode_body<D, false>(a);                                                                \
   }                                                                                          \
-  extern "C" __global__ __launch_bounds__(512) void ppk_decode_bf16h_d##D(ppk::DecodeArgs a) { \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_bf16h_d##D(ppk::DecodeArgs a) { \
     decode_body<D, true>(a);                                                                 \
   }                                                                                          \
   extern "C" __global__ __launch_bounds__(64) void ppk_attn_merge_d##D(ppk::MergeArgs a) {   \

@@ -19,6 +19,7 @@ import glob
 import json
 import os
 import re
+import shlex
 import statistics
 import sys
 
@@ -39,7 +40,8 @@ def trace(args) -> None:
     stats = _rows(_one(args.dir, "kernel_stats.csv"))
     disp = _rows(_one(args.dir, "kernel_trace.csv"))
     lines = [f"# rocprofv3 kernel trace: {args.title}", "", "Command (from the repository root):", "",
-             f"    {args.command}", "", "## Per-kernel durations (ppk kernels, all dispatches)", "",
+             f"    {args.command}", "", "Summarised with:", "", f"    {_self_command()}", "",
+             "## Per-kernel durations (ppk kernels, all dispatches)", "",
              "| kernel | calls | avg µs | min µs | max µs | total ms |", "|---|---|---|---|---|---|"]
     for r in sorted(stats, key=lambda r: -float(r.get("totaldurationns", 0))):
         name = r.get("name", "")
@@ -110,7 +112,7 @@ def traffic(args) -> None:
            "dispatches": {"kernel_fetch": len(kf), "kernel_write": len(kw)}}
     _write(args.out_json, json.dumps(res, indent=1) + "\n")
     md = [f"# HBM traffic per launch: {args.kernel}, {args.workload}", "", "Commands (from the repository root):", "",
-          f"    {args.command}", "",
+          f"    {args.command}", "", "Summarised with:", "", f"    {_self_command()}", "",
           f"- FETCH_SIZE median {res['fetch_kib_raw_median']:.0f} KiB/dispatch over {len(kf)} dispatches; "
           f"WRITE_SIZE median {res['write_kib_raw_median']:.0f} KiB over {len(kw)}",
           f"- calibration: one {args.calib_bytes} B-in / {args.calib_bytes} B-out elementwise kernel "
@@ -120,6 +122,10 @@ def traffic(args) -> None:
           f"- algorithmic bytes per launch: {args.algorithmic_bytes} -> traffic / algorithmic = "
           f"{res['traffic_over_algorithmic']:.4f}"]
     _write(args.out_md, "\n".join(md) + "\n")
+
+
+def _self_command() -> str:
+    return "python3 pop2-bezier_amd/ppk/rocprof_summary.py " + shlex.join(sys.argv[1:])
 
 
 def _write(path: str, text: str) -> None:

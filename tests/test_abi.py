@@ -90,13 +90,13 @@ def test_plan_sizes_workspace_without_a_device():
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args())
     assert (split, groups, nbytes) == (1024, 1, 0)
     # An explicit per-wave split is honoured (rounded up to whole 1 KiB tiles);
-    # 8 waves per block, so ceil(ceil(8192/104)/8) blocks per row.
+    # up to 16 waves per block, so ceil(ceil(8192/104)/16) blocks per row.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
-    assert (split, groups) == (104, -(-(-(-8192 // 104)) // 8))
+    assert (split, groups) == (104, -(-(-(-8192 // 104)) // 16))
     assert nbytes == 512 * groups * 128 * 4 + -(-(512 * groups * 2 * 4) // 256) * 256
     # Few rows: split-K across blocks plus the merge kernel (config 3 shape).
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048))
-    assert split == 64 and groups == 4 and nbytes == 16 * 4 * 128 * 4 + 16 * 4 * 2 * 4
+    assert split == 64 and groups == 2 and nbytes == 16 * 2 * 128 * 4 + 256
 
 
 @pytest.mark.parametrize("bad", [dict(head_dim=96), dict(rows=30, heads=16), dict(heads=0), dict(capacity=0),
