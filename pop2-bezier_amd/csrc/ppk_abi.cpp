@@ -151,9 +151,10 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
     split = (split + tpl - 1) / tpl * tpl;
   } else {
     // Smallest power-of-two tokens per wave (>= 64) that keeps the launch
-    // within about 16 resident waves per CU: each wave then streams one long
-    // contiguous stretch of K and of V.
-    const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 16;
+    // within about two rounds of 16 resident waves per CU: each wave then
+    // streams one long contiguous stretch of K and of V, and the second round
+    // evens out the blocks' finishing times.
+    const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 32;
     split = 64;
     while (split < 2048 && uint64_t(a.rows) * ((span + split - 1) / split) > budget) split <<= 1;
   }

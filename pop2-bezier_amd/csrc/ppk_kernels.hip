@@ -260,25 +260,94 @@ __device__ __forceinline__ void load_batch(const uint8_t* base, const float* sca
   scale = __builtin_nontemporal_load(scales + min(t0 * TPL + uint32_t(lane % (U * TPL)), n - 1));
 }
 
+// q in exact integer form for the K-phase dot products: every lane's 16
+// channels become q_int = rne(q / qmax * Q), Q = 127 * 2^14, split into three
+// signed bytes hi*2^14 + mid*2^7 + lo (each in [-127, 127]) packed four
+// channels per dword. <codes, part> is then an exact v_dot4_i32_i8 sum, and
+// the three partial sums recombine in fp32 to q_int . codes with fp32
+// rounding only; q_int carries 22 bits of q relative to the row's max |q|.
+struct QInt {
+  int hi[4], mid[4], lo[4];
+  float unscale;  // qmax / Q (NaN if q held a non-finite value)
+};
+
+template <int LPT>
+__device__ __forceinline__ float group_max(float x) {
+  x = fmaxf(x, dpp_xor1(x));
+  x = fmaxf(x, dpp_xor2(x));
+  if constexpr (LPT >= 8) x = fmaxf(x, dpp_half_mirror(x));
+  if constexpr (LPT >= 16) x = fmaxf(x, dpp_mirror(x));
+  return x;
+}
+
+template <int LPT>
+__device__ __forceinline__ QInt quantize_query(const float (&qr)[16]) {
+  constexpr float Q = 2080768.0f;  // 127 * 16384
+  float amax = 0.f;
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    amax = fmaxf(amax, fabsf(qr[i]));
+    finite = finite && __builtin_isfinite(qr[i]);
+  }
+  amax = group_max<LPT>(amax);  // every lane of a token group holds the whole row of q
+  const float bad = group_max<LPT>(finite ? 0.f : 1.f);
+  const float inv = amax > 0.f ? Q / amax : 0.f;
+  QInt r;
+  r.unscale = bad > 0.f ? __builtin_nanf("") : amax / Q;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t h = 0, m = 0, l = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float x = fminf(fmaxf(rintf(qr[4 * w + k] * inv), -Q), Q);
+      const int qi = finite ? int(x) : 0;
+      const int hi = (qi + 8192) >> 14;   // [-127, 127]
+      const int r1 = qi - hi * 16384;     // [-8192, 8191]
+      const int mid = (r1 + 64) >> 7;     // [-64, 64]
+      const int lo = r1 - mid * 128;      // [-64, 63]
+      h |= (uint32_t(hi) & 0xffu) << (8 * k);
+      m |= (uint32_t(mid) & 0xffu) << (8 * k);
+      l |= (uint32_t(lo) & 0xffu) << (8 * k);
+    }
+    r.hi[w] = int(h);
+    r.mid[w] = int(m);
+    r.lo[w] = int(l);
+  }
+  return r;
+}
+
+// Phase K for one batch of 4 tiles: scores (log2 domain) into LDS, running max.
 template <int D, bool BF16H>
 __device__ __forceinline__ float score_batch(const u4 (&raw)[4], float scale_lane, uint32_t t0, uint32_t n, int j,
-                                             int c, const float (&qr)[16], float sl2, float* s_lds, float mloc) {
+                                             int c, const float (&qr)[16], const QInt& qi, float sl2, float* s_lds,
+                                             float mloc) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const uint32_t tok = (t0 + u) * TPL + j;
     const float kscale = __shfl(scale_lane, u * TPL + j);
-    float d = 0.f;
+    float sc;
+    if constexpr (BF16H) {
+      // pp_i8_load semantics: every element is bf16(code * scale) before the fp32 dot.
+      float d = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+      for (int w = 0; w < 4; ++w)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float kv = BF16H ? round_bf16(sbyte(raw[u][w], k) * kscale) : sbyte(raw[u][w], k);
-        d = fmaf(qr[4 * w + k], kv, d);
+        for (int k = 0; k < 4; ++k) d = fmaf(qr[4 * w + k], round_bf16(sbyte(raw[u][w], k) * kscale), d);
+      sc = group_sum<LPT>(d) * sl2;
+    } else {
+      int sh = 0, sm = 0, sl = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        sh = __builtin_amdgcn_sdot4(int(raw[u][w]), qi.hi[w], sh, false);
+        sm = __builtin_amdgcn_sdot4(int(raw[u][w]), qi.mid[w], sm, false);
+        sl = __builtin_amdgcn_sdot4(int(raw[u][w]), qi.lo[w], sl, false);
       }
-    d = group_sum<LPT>(d);
-    float sc = BF16H ? d * sl2 : d * kscale * sl2;
+      const float f = fmaf(float(sh), 16384.f, fmaf(float(sm), 128.f, float(sl)));
+      sc = group_sum<LPT>(f) * (kscale * sl2);
+    }
     sc = tok < n ? sc : -INFINITY;
     mloc = fmaxf(mloc, sc);
     if (c == 0 && tok < n) s_lds[tok] = sc;
@@ -286,26 +355,36 @@ __device__ __forceinline__ float score_batch(const u4 (&raw)[4], float scale_lan
   return mloc;
 }
 
+// Phase V for one batch: lane l owns token l of the batch (the layout of the
+// scale load), turns its score into p = 2^(s - m) once, adds it to z and
+// forms the weight p * vscale; each tile's token groups then fetch their
+// token's weight with one cross-lane read and accumulate weight * code.
 template <int D, bool BF16H>
 __device__ __forceinline__ void accumulate_batch(const u4 (&raw)[4], float scale_lane, uint32_t t0, uint32_t n, int j,
-                                                 float m, const float* s_lds, float& z, float (&acc)[16]) {
+                                                 int lane, float m, const float* s_lds, float& z, float (&acc)[16]) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
+  constexpr int TPB = 4 * TPL;  // tokens per batch (<= 64)
+  const uint32_t tl = t0 * TPL + uint32_t(lane % TPB);
+  const float e = __builtin_amdgcn_exp2f(s_lds[min(tl, n - 1)] - m);
+  const float pr = (tl < n && lane < TPB) ? e : 0.f;
+  z += pr;
+  const float w_lane = BF16H ? pr : pr * scale_lane;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const uint32_t tok = (t0 + u) * TPL + j;
-    const float vscale = __shfl(scale_lane, u * TPL + j);
-    const float e = __builtin_amdgcn_exp2f(s_lds[min(tok, n - 1)] - m);  // branch-free; masked below
-    const float pr = tok < n ? e : 0.f;
-    z += pr;
-    const float wgt = BF16H ? pr : pr * vscale;
+    const float wgt = __shfl(w_lane, u * TPL + j);
+    if constexpr (BF16H) {
+      const float vscale = __shfl(scale_lane, u * TPL + j);
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+      for (int w = 0; w < 4; ++w)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float vv = BF16H ? round_bf16(sbyte(raw[u][w], k) * vscale) : sbyte(raw[u][w], k);
-        acc[4 * w + k] = fmaf(wgt, vv, acc[4 * w + k]);
-      }
+        for (int k = 0; k < 4; ++k) acc[4 * w + k] = fmaf(wgt, round_bf16(sbyte(raw[u][w], k) * vscale), acc[4 * w + k]);
+    } else {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[4 * w + k] = fmaf(wgt, sbyte(raw[u][w], k), acc[4 * w + k]);
+    }
   }
 }
 
@@ -333,19 +412,25 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   const float* ksb = a.ks + tok0;
   const float* vsb = a.vs + tok0;
   const uint32_t ntiles = (n + TPL - 1) / TPL;
-  const float sl2 = a.scale_log2;
+  QInt qi{};
+  float sl2 = a.scale_log2;
+  if constexpr (!BF16H) {
+    qi = quantize_query<LPT>(qr);
+    sl2 *= qi.unscale;
+  }
 
+  // Batch A of the last phase-K iteration already fetches phase V's first
+  // batch, so the V stream starts without a full memory latency.
+  u4 ra[U], rb[U];
+  float sa, sb;
   float mloc = -INFINITY;
-  {
-    u4 ra[U], rb[U];
-    float sa, sb;
-    load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
-    for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
-      load_batch<D, U>(kb, ksb, t0 + U, n, j, lane, rb, sb);
-      mloc = score_batch<D, BF16H>(ra, sa, t0, n, j, c, qr, sl2, s_lds, mloc);
-      load_batch<D, U>(kb, ksb, t0 + 2 * U, n, j, lane, ra, sa);
-      mloc = score_batch<D, BF16H>(rb, sb, t0 + U, n, j, c, qr, sl2, s_lds, mloc);
-    }
+  load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
+  for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
+    load_batch<D, U>(kb, ksb, t0 + U, n, j, lane, rb, sb);
+    mloc = score_batch<D, BF16H>(ra, sa, t0, n, j, c, qr, qi, sl2, s_lds, mloc);
+    const bool last = t0 + 2 * U >= ntiles;
+    load_batch<D, U>(last ? vb : kb, last ? vsb : ksb, last ? 0u : t0 + 2 * U, n, j, lane, ra, sa);
+    mloc = score_batch<D, BF16H>(rb, sb, t0 + U, n, j, c, qr, qi, sl2, s_lds, mloc);
   }
   float m = mloc;
 #pragma unroll
@@ -354,19 +439,17 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
 
   float z = 0.f;
   {
-    u4 ra[U], rb[U];
-    float sa, sb;
-    load_batch<D, U>(vb, vsb, 0, n, j, lane, ra, sa);
     for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
       load_batch<D, U>(vb, vsb, t0 + U, n, j, lane, rb, sb);
-      accumulate_batch<D, BF16H>(ra, sa, t0, n, j, m, s_lds, z, out.acc);
+      accumulate_batch<D, BF16H>(ra, sa, t0, n, j, lane, m, s_lds, z, out.acc);
       load_batch<D, U>(vb, vsb, t0 + 2 * U, n, j, lane, ra, sa);
-      accumulate_batch<D, BF16H>(rb, sb, t0 + U, n, j, m, s_lds, z, out.acc);
+      accumulate_batch<D, BF16H>(rb, sb, t0 + U, n, j, lane, m, s_lds, z, out.acc);
     }
   }
+  // Each token's p was added once, by its owning lane: sum over the wave.
+  z = wave_sum(z);
 #pragma unroll
   for (int o = LPT; o < ppk::kWave; o <<= 1) {
-    z += __shfl_xor(z, o);
 #pragma unroll
     for (int i = 0; i < 16; ++i) out.acc[i] += __shfl_xor(out.acc[i], o);
   }

@@ -85,10 +85,10 @@ def _attn_args(**kw) -> _abi.PpkAttentionArgs:
 
 
 def test_plan_sizes_workspace_without_a_device():
-    # Config 5 on 256 CUs: 8 waves x 1024 tokens cover a row, so one block per
+    # Config 5 on 256 CUs: 16 waves x 512 tokens cover a row, so one block per
     # row finishes the step in one launch and needs no workspace.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args())
-    assert (split, groups, nbytes) == (1024, 1, 0)
+    assert (split, groups, nbytes) == (512, 1, 0)
     # An explicit per-wave split is honoured (rounded up to whole 1 KiB tiles);
     # up to 16 waves per block, so ceil(ceil(8192/104)/16) blocks per row.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
