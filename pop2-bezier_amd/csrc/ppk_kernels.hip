@@ -257,7 +257,9 @@ __device__ __forceinline__ void load_batch(const uint8_t* base, const float* sca
     const uint32_t tc = min((t0 + u) * TPL + j, n - 1);  // clamp: always in bounds
     raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(base + size_t(tc) * D));
   }
-  scale = __builtin_nontemporal_load(scales + min(t0 * TPL + uint32_t(lane % (U * TPL)), n - 1));
+  // Scales stay cacheable: a batch's 4*TPL scales need not start on a cache
+  // line (capacity is arbitrary), and the next batch reuses the shared line.
+  scale = scales[min(t0 * TPL + uint32_t(lane % (U * TPL)), n - 1)];
 }
 
 // q in exact integer form for the K-phase dot products: every lane's 16

@@ -231,3 +231,109 @@ def test_decode_step_config5_shape_one_launch_plan(device):
     out = step()
     torch.cuda.synchronize()
     assert_close(out.reshape(c.rows, D).cpu().numpy(), c.reference(), what="config 5 shape")
+
+
+def _golden(name):
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def test_golden_reference_known_answers_through_the_abi(device):
+    """The reference's procedural checks (ii) and (iii) (int8_kv_ops.rs:63-101), expected values from its
+    host formula (tests/golden): bf16-history mode at the reference's 2e-5, fp32 mode vs the oracle."""
+    def t(x, dtype=None):
+        return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+
+    g = _golden("kat_attention_ii.npz")
+    kc, ks = t(g["codes"]), t(g["scales"])
+    q, sc = t(g["q"]).reshape(2, 1, 64), t(g["scratch"]).reshape(2, 1, 64)
+    past = t(g["past"].view(np.int32))
+    for split in (32, 128):
+        out = ppk.attention(q, kc, kc, ks, ks, sc, sc, past, 1, split, bf16_history=True)
+        got = out.reshape(2, 64).cpu().numpy()
+        assert np.abs(got - g["expected_bf16_history"]).max() < 2e-5
+    g = _golden("kat_attention_iii.npz")
+    args = [t(g[k]) for k in ("k_codes", "v_codes", "k_scales", "v_scales")]
+    q, sk, sv = (t(g[k]).reshape(4, 1, 64) for k in ("q", "sk", "sv"))
+    past = t(g["past"].view(np.int32))
+    ref32 = oracle.attention(g["q"], g["k_codes"], g["v_codes"], g["k_scales"], g["v_scales"], g["sk"], g["sv"],
+                             g["past"], 2)
+    for split in (32, 128):
+        out = ppk.attention(q, args[0], args[1], args[2], args[3], sk, sv, past, 2, split, bf16_history=True)
+        assert np.abs(out.reshape(4, 64).cpu().numpy() - g["expected_bf16_history"]).max() < 2e-5
+        out = ppk.attention(q, args[0], args[1], args[2], args[3], sk, sv, past, 2, split)
+        assert_close(out.reshape(4, 64).cpu().numpy(), ref32, what=f"kat iii fp32 split {split}")
+
+
+def test_golden_config2_append(device):
+    g = _golden("config2_append.npz")
+    cap, past = int(g["capacity"]), g["past"]
+    rng = np.random.default_rng(SEED)
+    arenas = {}
+    for name in ("k", "v"):
+        codes = rng.integers(0, 256, size=(16, cap, 128)).astype(np.uint8)
+        scales = rng.random((16, cap)).astype(np.float32)
+        arenas[name] = (codes, scales, torch.from_numpy(codes.copy()).to(device),
+                        torch.from_numpy(scales.copy()).to(device))
+    kn = torch.from_numpy(g["k_new_f16"]).to(device)
+    vn = torch.from_numpy(g["v_new_f16"]).to(device)
+    ppk.append(kn, vn, torch.from_numpy(past.view(np.int32)).to(device), arenas["k"][2], arenas["v"][2],
+               arenas["k"][3], arenas["v"][3])
+    torch.cuda.synchronize()
+    slot = int(past[0])
+    for name in ("k", "v"):
+        codes, scales, dc, ds = arenas[name]
+        exp_c, exp_s = codes.copy(), scales.copy()
+        exp_c[:, slot] = g[f"{name}_codes"][:, 0]
+        exp_s[:, slot] = g[f"{name}_scales"][:, 0]
+        assert np.array_equal(dc.cpu().numpy(), exp_c)
+        assert np.array_equal(ds.cpu().numpy().view(np.uint32), exp_s.view(np.uint32))
+
+
+def test_config5_full_size_sampled_rows_and_properties(device):
+    """BASELINE config 5 at full size (B=32, H=16, D=128, 8192 int8 tokens, heavy-tailed K/V, bf16 q):
+    sampled rows against the oracle, the whole append bit-exact, and plan invariance over all rows."""
+    from ppk import synthetic
+
+    B, H, D, L = 32, 16, 128, 8192
+    rows, cap, seed = B * H, L + 1, SEED + 55
+    kc = torch.empty((rows, cap, D), dtype=torch.uint8, device=device)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((rows, cap), dtype=torch.float32, device=device)
+    vs = torch.empty_like(ks)
+    synthetic.fill_history(kc, vc, ks, vs, L, H, seed)
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn((rows, 1, D), generator=g, device=device).to(torch.bfloat16)
+    kn = synthetic.history_chunk(seed, 2, 0, rows, H, 0, 1, D, device, torch.bfloat16)
+    vn = synthetic.history_chunk(seed, 3, 0, rows, H, 0, 1, D, device, torch.bfloat16)
+    past = torch.full((B,), L, dtype=torch.int32, device=device)
+    out = ppk.decode_step(q, kc, vc, ks, vs, kn, vn, past, H, max_past=L)
+    out_split = ppk.attention(q, kc, vc, ks, vs, kn, vn, past, H, 256, max_past=L)  # split-K + merge plan
+    torch.cuda.synchronize()
+    got = out.reshape(rows, D).cpu().numpy()
+    got_split = out_split.reshape(rows, D).cpu().numpy()
+    assert np.isfinite(got).all()
+    # Plan invariance on every row (both plans are fp32 accumulations of the same terms).
+    np.testing.assert_allclose(got, got_split, rtol=1e-4, atol=1e-5)
+    # The appended slot L of every row is the oracle's quantisation of the bf16 current token.
+    for src, codes, scales in ((kn, kc, ks), (vn, vc, vs)):
+        c, s, _ = oracle.quantize(src.float().reshape(rows, 1, D).cpu().numpy())
+        assert np.array_equal(codes[:, L:L + 1].cpu().numpy(), c)
+        assert np.array_equal(scales[:, L:L + 1].cpu().numpy().view(np.uint32), s.view(np.uint32))
+    # Sampled rows (first, last, heavy-tailed heads, a spread) against the f64 oracle.
+    sample = sorted({0, 1, 15, 16, 255, 256, 511} | set(np.random.default_rng(seed).choice(rows, 17, replace=False)))
+    idx = torch.tensor(sample, device=device)
+    r_q = q.float().reshape(rows, D)[idx].cpu().numpy()
+    r_k, r_v = kc[idx, :L].cpu().numpy(), vc[idx, :L].cpu().numpy()
+    r_ks, r_vs = ks[idx, :L].cpu().numpy(), vs[idx, :L].cpu().numpy()
+    r_sk = kn.float().reshape(rows, D)[idx].cpu().numpy()
+    r_sv = vn.float().reshape(rows, D)[idx].cpu().numpy()
+    ref = oracle.attention(r_q, r_k, r_v, r_ks, r_vs, r_sk, r_sv, np.full(len(sample), L, np.uint32), 1)
+    assert_close(got[sample], ref, what="config 5 sampled rows")
+    # The history codes of the first sampled chunk are the oracle's quantisation of its source values.
+    src = synthetic.history_chunk(seed, 0, 0, 16, H, 0, L, D, device).float().cpu().numpy()
+    c, s, _ = oracle.quantize(src)
+    assert np.array_equal(kc[:16, :L].cpu().numpy(), c)
+    assert np.array_equal(ks[:16, :L].cpu().numpy().view(np.uint32), s.view(np.uint32))
