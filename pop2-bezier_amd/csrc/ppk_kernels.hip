@@ -319,15 +319,15 @@ __device__ __forceinline__ QInt quantize_query(const float (&qr)[16]) {
   return r;
 }
 
-// Phase K for one batch of 4 tiles: scores (log2 domain) into LDS, running max.
-template <int D, bool BF16H>
-__device__ __forceinline__ float score_batch(const u4 (&raw)[4], float scale_lane, uint32_t t0, uint32_t n, int j,
+// Phase K for one batch of U tiles: scores (log2 domain) into LDS, running max.
+template <int D, bool BF16H, int U>
+__device__ __forceinline__ float score_batch(const u4 (&raw)[U], float scale_lane, uint32_t t0, uint32_t n, int j,
                                              int c, const float (&qr)[16], const QInt& qi, float sl2, float* s_lds,
                                              float mloc) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < U; ++u) {
     const uint32_t tok = (t0 + u) * TPL + j;
     const float kscale = __shfl(scale_lane, u * TPL + j);
     float sc;
@@ -361,19 +361,20 @@ __device__ __forceinline__ float score_batch(const u4 (&raw)[4], float scale_lan
 // scale load), turns its score into p = 2^(s - m) once, adds it to z and
 // forms the weight p * vscale; each tile's token groups then fetch their
 // token's weight with one cross-lane read and accumulate weight * code.
-template <int D, bool BF16H>
-__device__ __forceinline__ void accumulate_batch(const u4 (&raw)[4], float scale_lane, uint32_t t0, uint32_t n, int j,
+template <int D, bool BF16H, int U>
+__device__ __forceinline__ void accumulate_batch(const u4 (&raw)[U], float scale_lane, uint32_t t0, uint32_t n, int j,
                                                  int lane, float m, const float* s_lds, float& z, float (&acc)[16]) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
-  constexpr int TPB = 4 * TPL;  // tokens per batch (<= 64)
+  constexpr int TPB = U * TPL;  // tokens per batch (<= 64)
+  static_assert(TPB <= ppk::kWave, "one scale per lane per batch");
   const uint32_t tl = t0 * TPL + uint32_t(lane % TPB);
   const float e = __builtin_amdgcn_exp2f(s_lds[min(tl, n - 1)] - m);
   const float pr = (tl < n && lane < TPB) ? e : 0.f;
   z += pr;
   const float w_lane = BF16H ? pr : pr * scale_lane;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < U; ++u) {
     const float wgt = __shfl(w_lane, u * TPL + j);
     if constexpr (BF16H) {
       const float vscale = __shfl(scale_lane, u * TPL + j);
@@ -429,10 +430,10 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
   for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
     load_batch<D, U>(kb, ksb, t0 + U, n, j, lane, rb, sb);
-    mloc = score_batch<D, BF16H>(ra, sa, t0, n, j, c, qr, qi, sl2, s_lds, mloc);
+    mloc = score_batch<D, BF16H, U>(ra, sa, t0, n, j, c, qr, qi, sl2, s_lds, mloc);
     const bool last = t0 + 2 * U >= ntiles;
     load_batch<D, U>(last ? vb : kb, last ? vsb : ksb, last ? 0u : t0 + 2 * U, n, j, lane, ra, sa);
-    mloc = score_batch<D, BF16H>(rb, sb, t0 + U, n, j, c, qr, qi, sl2, s_lds, mloc);
+    mloc = score_batch<D, BF16H, U>(rb, sb, t0 + U, n, j, c, qr, qi, sl2, s_lds, mloc);
   }
   float m = mloc;
 #pragma unroll
@@ -443,9 +444,9 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   {
     for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
       load_batch<D, U>(vb, vsb, t0 + U, n, j, lane, rb, sb);
-      accumulate_batch<D, BF16H>(ra, sa, t0, n, j, lane, m, s_lds, z, out.acc);
+      accumulate_batch<D, BF16H, U>(ra, sa, t0, n, j, lane, m, s_lds, z, out.acc);
       load_batch<D, U>(vb, vsb, t0 + 2 * U, n, j, lane, ra, sa);
-      accumulate_batch<D, BF16H>(rb, sb, t0 + U, n, j, lane, m, s_lds, z, out.acc);
+      accumulate_batch<D, BF16H, U>(rb, sb, t0 + U, n, j, lane, m, s_lds, z, out.acc);
     }
   }
   // Each token's p was added once, by its owning lane: sum over the wave.
