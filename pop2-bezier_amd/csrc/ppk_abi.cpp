@@ -160,7 +160,19 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   }
   const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
   // Up to 16 waves per block; one float of LDS per history token of the block.
-  const uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
+  uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
+  const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
+  const uint64_t row_bytes = span * (2ull * a.head_dim + 8);
+  if (!a.split_tokens && a.rows < cus && row_bytes > (128u << 10)) {
+    // Few, long rows: one block per row would leave most CUs idle (a CU
+    // alone streams only a few tens of GB/s). Split rows into blocks of about
+    // 64 KiB of history, then shrink blocks until the launch covers every CU;
+    // the merge kernel joins the groups.
+    const uint64_t wave_bytes = uint64_t(split) * (2ull * a.head_dim + 8);
+    uint64_t w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (64u << 10) / wave_bytes));
+    while (w > 1 && a.rows * ((waves_per_row + w - 1) / w) < cus) --w;
+    max_waves = w;
+  }
   plan.split = split;
   if (waves_per_row <= max_waves) {
     plan.waves = uint32_t(waves_per_row);

@@ -94,9 +94,12 @@ def test_plan_sizes_workspace_without_a_device():
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
     assert (split, groups) == (104, -(-(-(-8192 // 104)) // 16))
     assert nbytes == 512 * groups * 128 * 4 + -(-(512 * groups * 2 * 4) // 256) * 256
-    # Few rows: split-K across blocks plus the merge kernel (config 3 shape).
+    # Few long rows (config 3 shape): rows split into 2-wave blocks so the launch covers all 256 CUs,
+    # joined by the merge kernel.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048))
-    assert split == 64 and groups == 2 and nbytes == 16 * 2 * 128 * 4 + 256
+    assert split == 64 and groups == 16 and nbytes == 16 * 16 * 128 * 4 + 16 * 16 * 2 * 4
+    # Few short rows (config 1 shape): one block per row, one launch.
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=513, max_past=512, head_dim=64)) == (64, 1, 0)
 
 
 @pytest.mark.parametrize("bad", [dict(head_dim=96), dict(rows=30, heads=16), dict(heads=0), dict(capacity=0),

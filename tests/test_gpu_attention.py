@@ -337,3 +337,41 @@ def test_config5_full_size_sampled_rows_and_properties(device):
     c, s, _ = oracle.quantize(src)
     assert np.array_equal(kc[:16, :L].cpu().numpy(), c)
     assert np.array_equal(ks[:16, :L].cpu().numpy().view(np.uint32), s.view(np.uint32))
+
+
+def test_config3_decode_steps_captured_in_a_hip_graph(device):
+    """Config 3 is launch-bound (24 layers x one decode step each): the prepared steps are captured in a
+    HIP graph and replayed; every replay, separated by unrelated eager work and synchronisations, must
+    reproduce the eager outputs bit for bit (the steps contain no memset, only kernel launches)."""
+    B, H, D, L = 1, 16, 128, 2048
+    layers = [Case(device, B, H, D, [L], L + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16,
+                   seed=SEED + 200 + i) for i in range(24)]
+    steps = [ppk.DecodeStep(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, max_past=L) for c in layers]
+    for st in steps:
+        st()
+    torch.cuda.synchronize()
+    eager = [st.out.clone() for st in steps]
+    for c, e in zip(layers, eager):
+        assert_close(e.reshape(c.rows, D).cpu().numpy(), c.reference(), what="config 3 eager")
+
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):  # warm the capture stream
+        for st in steps:
+            st()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for st in steps:
+            st()
+    for replay in range(3):
+        for st in steps:
+            st.out.fill_(float("nan"))
+        junk = torch.randn(1 << 20, device=device).sin_().sum()  # unrelated eager work
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(junk)
+        for i, (st, e) in enumerate(zip(steps, eager)):
+            assert torch.equal(st.out, e), f"replay {replay}, layer {i} differs from eager"
