@@ -33,6 +33,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--head-dim", type=int, default=128)
     p.add_argument("--context", type=int, default=8192)
     p.add_argument("--split", type=int, default=0, help="tokens per split (0 = library policy)")
+    p.add_argument("--kv", choices=("int8", "bf16", "f32"), default="int8",
+                   help="int8 (default, the headline workload) or the float-KV decode path over a bf16/f32 store")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=64, help="head rows timed for the CPU baseline sample")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -90,6 +92,102 @@ def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args) -> dict:
             "cpu_model": model}
 
 
+def bench_float(args) -> int:
+    """The float-KV decode path (ppk_float_decode_attention) on a B x H x ctx bf16/f32 store that already
+    holds the current token; one step = one attention call over every row's ctx tokens."""
+    import numpy as np
+    import torch
+    import ppk
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, L = args.batch, args.heads, args.head_dim, args.context
+    rows = B * H
+    kv_dtype = torch.bfloat16 if args.kv == "bf16" else torch.float32
+    eb = 2 if args.kv == "bf16" else 4
+    print(f"# bench: float KV {args.kv} B={B} H={H} D={D} ctx={L} building store", file=sys.stderr, flush=True)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    k = torch.randn((rows, L, D), generator=g, device=dev, dtype=kv_dtype)
+    v = torch.randn((rows, L, D), generator=g, device=dev, dtype=kv_dtype)
+    q = torch.randn((rows, 1, D), generator=g, device=dev, dtype=torch.float32)
+    lengths = torch.full((B,), L, dtype=torch.int32, device=dev)
+    call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L)
+    torch.cuda.synchronize()
+    print("# bench: warmup", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        call()
+    stream = torch.cuda.current_stream(dev)
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        call()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t_start.elapsed_time(t_end) / args.steps
+
+    ppk.kernel_stats(ppk.PPK_KERNEL_FLOAT_ATTENTION, reset=True)
+    ppk.set_profiling(True)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_FLOAT_ATTENTION, reset=True)
+    kernel_avg_ms = kernel_ms / max(launches, 1)
+
+    # Algorithmic bytes: every row's K and V (L tokens x D x element size), the f32 query and output.
+    kv_bytes = rows * L * 2 * D * eb
+    step_bytes = kv_bytes + rows * D * 4 + rows * D * 4
+    kernel_bytes = step_bytes if call.ngroups == 1 else kv_bytes + rows * D * 4 + rows * call.ngroups * (D + 2) * 4
+    achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
+    step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
+    kname = f"ppk_fdecode_{args.kv}_d{D}"
+    result = {
+        "metric": f"float-KV decode-attention µs/step + achieved HBM GB/s (% of peak), B={B} ctx={L} {args.kv} KV",
+        "value": round(step_ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": args.kv,
+        "data": f"synthetic (seeded torch.randn {args.kv} K/V and f32 q on the device)",
+        "config": {"workload": "float-KV decode attention (ppk_float_decode_attention, the reference's "
+                               "fused_attention::decode_attention)", "batch": B, "heads": H, "head_dim": D,
+                   "context": L, "kv": args.kv, "query": "f32", "tokens_per_wave": call.split_tokens,
+                   "blocks_per_row": call.ngroups, "launches_per_step": 1 if call.ngroups == 1 else 2},
+        "step_hbm_gbps": round(step_gbps, 1), "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": kernel_bytes, "avg_launch_us": round(kernel_avg_ms * 1e3, 2),
+                     "launches": launches},
+    }
+    if not args.no_cpu_baseline:
+        print("# bench: cpu baseline", file=sys.stderr, flush=True)
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle  # noqa: E402  (CPU baseline leg only)
+
+        n = max(1, min(args.cpu_rows, rows))
+        if eb == 2:
+            k_h = k[:n].view(torch.int16).cpu().numpy().view(np.uint16)
+            v_h = v[:n].view(torch.int16).cpu().numpy().view(np.uint16)
+        else:
+            k_h, v_h = k[:n].cpu().numpy(), v[:n].cpu().numpy()
+        q_h = q[:n].cpu().numpy()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle.attention_float(q_h, k_h, v_h, None, 1)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds or reps >= 1000:
+                break
+        result["cpu_baseline"] = {
+            "value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/step", "cores": 1, "kind": "port",
+            "sample": f"{n} of {rows} head rows x {L} tokens (oracle_attention_float, f64 scalar), {reps} reps "
+                      f"in {el:.1f} s, scaled x{rows / n:g}"}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -97,6 +195,8 @@ def main() -> int:
                                    "sequence or head with no collective on the hot path (see DESIGN.md)",
                           "n_gpus": args.gpus}))
         return 2
+    if args.kv != "int8":
+        return bench_float(args)
     import torch
     import ppk
     from ppk import synthetic

@@ -8,6 +8,8 @@
  *      written either densely or into a KV arena at slot past[b] + j;
  *   2. split-K single-query decode attention over the int8 arena
  *      (partial kernel + cross-split merge kernel).
+ * The same attention kernel design also serves the float (bf16/f32) KV
+ * decode path (ppk_float_decode_attention).
  *
  * Every device buffer is caller-owned; the library never frees or allocates
  * caller memory. All work is stream-ordered on the hipStream_t passed in
@@ -200,6 +202,54 @@ typedef struct PpkDecodeStepArgs {
 } PpkDecodeStepArgs;
 PPK_API int32_t ppk_decode_step(ppk_context* ctx, void* stream, const PpkDecodeStepArgs* args);
 
+/* Float-KV decode attention: the non-int8 decode path over unquantised bf16
+   or f32 K/V, where the current token is already stored. For row r
+   (sequence b = r / heads):
+     n     = lengths ? lengths[b] : size        (total attended tokens)
+     out_r = sum_{t<n} softmax_t(softmax_scale * <q_r, K_r[t]>) * V_r[t]
+   n == 0 or n > size gives NaN (decode_attention.hip:15,50); so does n beyond
+   max_length when max_length is set. Replaces fused_attention::decode_attention
+   (app/src/model/fused_attention.rs:8-30) / hip_attention::decode_attention
+   (app/src/model/hip_attention.rs:47-113) and kernels pp_attention_f32/bf16 +
+   pp_attention_merge (app/src/model/decode_attention.hip:9-66). The reference
+   requires head_dim 64, size <= 1024, F32 q and F32 output; this entry point
+   also takes head_dim 128/256, any size and bf16/f16 q or output. Row strides
+   are in elements (Candle's stride()[0]); within a row, tokens are dense. */
+typedef struct PpkFloatAttentionArgs {
+  uint32_t struct_size;
+  uint32_t kv_dtype;       /* PPK_BF16 or PPK_F32 (dtype of k and v) */
+  uint32_t q_dtype;        /* PPK_F32 (reference), PPK_BF16 or PPK_F16 */
+  uint32_t out_dtype;      /* PPK_F32 (reference), PPK_BF16 or PPK_F16 */
+  uint32_t rows;           /* batch * heads */
+  uint32_t heads;
+  uint32_t size;           /* stored tokens per row (the K/V view's length) */
+  uint32_t head_dim;       /* 64, 128 or 256 */
+  uint32_t split_tokens;   /* tokens per wave; 0 = automatic. Result does not depend on it. */
+  uint32_t max_length;     /* host upper bound of max(lengths); 0 = size. Needs lengths. */
+  float softmax_scale;     /* 0 = 1/sqrt(head_dim) (the reference's 0.125 at head_dim 64) */
+  uint32_t reserved;
+  uint64_t q_row_stride;   /* elements between rows of q; 0 = head_dim */
+  uint64_t k_row_stride;   /* elements between rows of k; 0 = size * head_dim; 16-byte multiple */
+  uint64_t v_row_stride;   /* elements between rows of v; 0 = size * head_dim; 16-byte multiple */
+  const void* q;           /* rows x [head_dim] */
+  const void* k;           /* rows x [size, head_dim], 16-byte aligned */
+  const void* v;           /* rows x [size, head_dim], 16-byte aligned */
+  const uint32_t* lengths; /* device U32[rows / heads], or NULL (every row attends size tokens) */
+  void* out;               /* [rows, head_dim] */
+  void* workspace;         /* ppk_float_attention_plan() bytes, 256-byte aligned (may be NULL if 0) */
+  uint64_t workspace_bytes;
+} PpkFloatAttentionArgs;
+/* Launch plan for args (ctx may be NULL: assumes 256 CUs), as ppk_attention_plan. */
+PPK_API int32_t ppk_float_attention_plan(ppk_context* ctx, const PpkFloatAttentionArgs* args,
+                                         uint32_t* split_tokens, uint32_t* nsplits, uint64_t* workspace_bytes);
+PPK_API int32_t ppk_float_decode_attention(ppk_context* ctx, void* stream, const PpkFloatAttentionArgs* args);
+/* The float path's private known-answer check: hip_attention::validate_split_k
+   (app/src/model/hip_attention.rs:18-45; bf16 and f32 stores of 257 tokens,
+   split 0 and 128 within 1e-4 of an f32 softmax reference and of each other)
+   and the zero-input check of prepare_optional_kernels (app/src/model/mod.rs:440-451).
+   Returns 2 with the failing check in ppk_last_error() on a numeric mismatch. */
+PPK_API int32_t ppk_float_attention_prepare(ppk_context* ctx);
+
 /* Known-answer self-check on the context's device, the three checks of
    int8_kv_ops::prepare (int8_kv_ops.rs:56-103) plus their fp32-history twins.
    Returns 2 with the failing check in ppk_last_error() on a numeric mismatch. */
@@ -211,7 +261,8 @@ PPK_API int32_t ppk_prepare(ppk_context* ctx);
    only (app/src/model/hip_kernel.rs:8-21). */
 enum { PPK_KERNEL_QUANTIZE = 0, PPK_KERNEL_APPEND = 1, PPK_KERNEL_DEQUANTIZE = 2,
        PPK_KERNEL_ATTENTION = 3, /* the decode kernel, with or without the fused append */
-       PPK_KERNEL_ATTN_MERGE = 4, PPK_KERNEL_COUNT = 5 };
+       PPK_KERNEL_ATTN_MERGE = 4, PPK_KERNEL_FLOAT_ATTENTION = 5, PPK_KERNEL_FLOAT_MERGE = 6,
+       PPK_KERNEL_COUNT = 7 };
 PPK_API int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable);
 PPK_API int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint64_t* launches,
                                  double* total_ms, uint32_t reset);

@@ -41,6 +41,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_attention.restype = None
         L.oracle_attention_splitk_reference.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, Z, P]
         L.oracle_attention_splitk_reference.restype = None
+        L.oracle_attention_float.argtypes = [P, P, P, ctypes.c_int, Z, Z, P, Z, Z, Z, Z, ctypes.c_float, P]
+        L.oracle_attention_float.restype = None
         L.cpu_baseline_decode.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, Z, P]
         L.cpu_baseline_decode.restype = ctypes.c_int
         _lib = L
@@ -151,4 +153,26 @@ def cpu_baseline(q, k, v, ks, vs, sk, sv, past, heads: int, threads: int, scale:
                                    d, float(scale), int(threads), _p(out))
     if rc != 0:
         raise RuntimeError("cpu_baseline_decode: a worker thread failed to start (ran inline)")
+    return out
+
+
+def attention_float(q, k, v, lengths, heads: int, scale: float | None = None) -> np.ndarray:
+    """Float-KV decode attention (see oracle_attention_float). k/v: float32 or bfloat16 bits (uint16)
+    arrays [rows, size, d] (row-strided views allowed); lengths: uint32 [rows // heads] or None."""
+    kv_bf16 = k.dtype == np.uint16
+    assert v.dtype == k.dtype and k.shape == v.shape
+    rows, size, d = k.shape
+    elem = 2 if kv_bf16 else 4
+    for a in (k, v):
+        assert a.strides[2] == elem and a.strides[1] == d * elem, "tokens must be dense"
+    q = _c(q, np.float32).reshape(rows, d)
+    if lengths is not None:
+        lengths = _c(lengths, np.uint32)
+        assert lengths.size == rows // heads
+    if scale is None:
+        scale = 1.0 / np.sqrt(d)
+    out = np.empty((rows, d), np.float64)
+    lib().oracle_attention_float(_p(q), k.ctypes.data, v.ctypes.data, int(kv_bf16), k.strides[0] // elem,
+                                 v.strides[0] // elem, _p(lengths) if lengths is not None else None, rows, heads,
+                                 size, d, float(scale), _p(out))
     return out

@@ -363,3 +363,65 @@ int cpu_baseline_decode(const float* q, const uint8_t* k, const uint8_t* v, cons
   free(jobs);
   return rc;
 }
+
+/*
+ * Float-KV decode attention, the semantics of fused_attention::decode_attention
+ * (app/src/model/fused_attention.rs:8-30) as computed by pp_attention_part and
+ * pp_attention_merge (app/src/model/decode_attention.hip:9-66), in f64:
+ *   row r, sequence b = r / heads; n = lengths ? lengths[b] : size
+ *   (n counts every attended token; the current one is already in the cache)
+ *   s_t = scale * <q_r, K_r[t]>, t < n;  out_r = sum_t e^{s_t - max} V_r[t] / sum_t e^{s_t - max}
+ *   n == 0 or n > size yields NaN (decode_attention.hip:15,50).
+ * K/V elements are bf16 (kv_bf16 = 1, raw 16-bit patterns) or f32; rows are
+ * k_row_stride / v_row_stride elements apart, tokens d elements apart.
+ */
+void oracle_attention_float(const float* q, const void* k, const void* v, int kv_bf16, size_t k_row_stride,
+                            size_t v_row_stride, const uint32_t* lengths, size_t rows, size_t heads, size_t size,
+                            size_t d, float scale, double* out) {
+  double* scores = (double*)malloc((size ? size : 1) * sizeof(double));
+  for (size_t r = 0; r < rows; ++r) {
+    const size_t n = lengths ? lengths[r / heads] : size;
+    double* o = out + r * d;
+    if (n == 0 || n > size) {
+      for (size_t i = 0; i < d; ++i) o[i] = NAN;
+      continue;
+    }
+    double mx = -INFINITY;
+    for (size_t t = 0; t < n; ++t) {
+      double acc = 0.0;
+      for (size_t i = 0; i < d; ++i) {
+        const size_t at = r * k_row_stride + t * d + i;
+        float kv;
+        if (kv_bf16) {
+          const uint32_t bits = (uint32_t)((const uint16_t*)k)[at] << 16;
+          memcpy(&kv, &bits, 4);
+        } else {
+          kv = ((const float*)k)[at];
+        }
+        acc += (double)q[r * d + i] * (double)kv;
+      }
+      scores[t] = acc * (double)scale;
+      if (scores[t] > mx) mx = scores[t];
+    }
+    double z = 0.0;
+    for (size_t t = 0; t < n; ++t) {
+      scores[t] = exp(scores[t] - mx);
+      z += scores[t];
+    }
+    for (size_t i = 0; i < d; ++i) o[i] = 0.0;
+    for (size_t t = 0; t < n; ++t)
+      for (size_t i = 0; i < d; ++i) {
+        const size_t at = r * v_row_stride + t * d + i;
+        float vv;
+        if (kv_bf16) {
+          const uint32_t bits = (uint32_t)((const uint16_t*)v)[at] << 16;
+          memcpy(&vv, &bits, 4);
+        } else {
+          vv = ((const float*)v)[at];
+        }
+        o[i] += scores[t] * (double)vv;
+      }
+    for (size_t i = 0; i < d; ++i) o[i] /= z;
+  }
+  free(scores);
+}

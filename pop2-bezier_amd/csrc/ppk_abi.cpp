@@ -51,6 +51,9 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_decode_d64", "ppk_decode_d128", "ppk_decode_d256",
     "ppk_decode_bf16h_d64", "ppk_decode_bf16h_d128", "ppk_decode_bf16h_d256",
     "ppk_attn_merge_d64", "ppk_attn_merge_d128", "ppk_attn_merge_d256",
+    "ppk_fdecode_bf16_d64", "ppk_fdecode_bf16_d128", "ppk_fdecode_bf16_d256",
+    "ppk_fdecode_f32_d64", "ppk_fdecode_f32_d128", "ppk_fdecode_f32_d256",
+    "ppk_fmerge_d64", "ppk_fmerge_d128", "ppk_fmerge_d256",
 };
 
 std::string default_code_object() {
@@ -129,10 +132,60 @@ DeviceGuard::~DeviceGuard() {
   if (changed_ && previous_ >= 0) (void)hipSetDevice(previous_);
 }
 
+AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim) {
+  AttentionPlan plan;
+  plan.head_dim = head_dim;
+  uint32_t split;
+  if (explicit_split) {
+    split = std::min<uint32_t>(std::max<uint32_t>(explicit_split, tpl), 8192u);
+    split = (split + tpl - 1) / tpl * tpl;
+  } else {
+    // Smallest power-of-two tokens per wave (>= 64) that keeps the launch
+    // within about two rounds of 16 resident waves per CU: each wave then
+    // streams one long contiguous stretch of K and of V, and the second round
+    // evens out the blocks' finishing times.
+    const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 32;
+    split = 64;
+    while (split < 2048 && uint64_t(rows) * ((span + split - 1) / split) > budget) split <<= 1;
+  }
+  const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
+  // Up to 16 waves per block; one float of LDS per history token of the block.
+  uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
+  const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
+  const uint64_t row_bytes = span * token_bytes;
+  if (!explicit_split && rows < cus && row_bytes > (128u << 10)) {
+    // Few, long rows: one block per row would leave most CUs idle (a CU
+    // alone streams only a few tens of GB/s). Split rows into blocks of about
+    // 64 KiB of history, then shrink blocks until the launch covers every CU;
+    // the merge kernel joins the groups.
+    const uint64_t wave_bytes = uint64_t(split) * token_bytes;
+    uint64_t w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (64u << 10) / wave_bytes));
+    while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) --w;
+    max_waves = w;
+  }
+  plan.split = split;
+  if (waves_per_row <= max_waves) {
+    plan.waves = uint32_t(waves_per_row);
+    plan.ngroups = 1;
+  } else {
+    plan.waves = uint32_t(max_waves);
+    plan.ngroups = uint32_t((waves_per_row + max_waves - 1) / max_waves);
+  }
+  require(uint64_t(plan.ngroups) * rows <= 0x7fffffffu, "attention grid too large");
+  // Per wave: one log2-domain score per token; after the waves are done the
+  // same LDS holds one (m, z, pad, pad, y[D]) record per wave.
+  plan.lds_bytes = 4u * std::max<uint32_t>(plan.waves * split, plan.waves * (head_dim + 4u));
+  if (plan.ngroups > 1) {
+    plan.y_bytes = (uint64_t(rows) * plan.ngroups * head_dim * 4 + 255) / 256 * 256;
+    plan.mz_bytes = (uint64_t(rows) * plan.ngroups * 2 * 4 + 255) / 256 * 256;
+  }
+  plan.workspace_bytes = plan.y_bytes + plan.mz_bytes;
+  return plan;
+}
+
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) {
   require(a.struct_size >= sizeof(PpkAttentionArgs), "PpkAttentionArgs.struct_size too small");
-  AttentionPlan plan;
-  plan.head_dim = a.head_dim;
   dim_index(a.head_dim);
   require(valid_dtype(a.q_dtype) && valid_dtype(a.scratch_dtype) && valid_dtype(a.out_dtype),
           "INT8 attention dtype must be f32, bf16 or f16");
@@ -145,52 +198,8 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
 
   const uint32_t tpl = 64u / (a.head_dim / 16u);
   const uint64_t span = a.max_past ? a.max_past : a.capacity;
-  uint32_t split;
-  if (a.split_tokens) {
-    split = std::min<uint32_t>(std::max<uint32_t>(a.split_tokens, tpl), 8192u);
-    split = (split + tpl - 1) / tpl * tpl;
-  } else {
-    // Smallest power-of-two tokens per wave (>= 64) that keeps the launch
-    // within about two rounds of 16 resident waves per CU: each wave then
-    // streams one long contiguous stretch of K and of V, and the second round
-    // evens out the blocks' finishing times.
-    const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 32;
-    split = 64;
-    while (split < 2048 && uint64_t(a.rows) * ((span + split - 1) / split) > budget) split <<= 1;
-  }
-  const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
-  // Up to 16 waves per block; one float of LDS per history token of the block.
-  uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
-  const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
-  const uint64_t row_bytes = span * (2ull * a.head_dim + 8);
-  if (!a.split_tokens && a.rows < cus && row_bytes > (128u << 10)) {
-    // Few, long rows: one block per row would leave most CUs idle (a CU
-    // alone streams only a few tens of GB/s). Split rows into blocks of about
-    // 64 KiB of history, then shrink blocks until the launch covers every CU;
-    // the merge kernel joins the groups.
-    const uint64_t wave_bytes = uint64_t(split) * (2ull * a.head_dim + 8);
-    uint64_t w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (64u << 10) / wave_bytes));
-    while (w > 1 && a.rows * ((waves_per_row + w - 1) / w) < cus) --w;
-    max_waves = w;
-  }
-  plan.split = split;
-  if (waves_per_row <= max_waves) {
-    plan.waves = uint32_t(waves_per_row);
-    plan.ngroups = 1;
-  } else {
-    plan.waves = uint32_t(max_waves);
-    plan.ngroups = uint32_t((waves_per_row + max_waves - 1) / max_waves);
-  }
-  require(uint64_t(plan.ngroups) * a.rows <= 0x7fffffffu, "INT8 attention grid too large");
-  // Per wave: one log2-domain score per token; after the waves are done the
-  // same LDS holds one (m, z, pad, pad, y[D]) record per wave.
-  plan.lds_bytes = 4u * std::max<uint32_t>(plan.waves * split, plan.waves * (a.head_dim + 4u));
-  if (plan.ngroups > 1) {
-    plan.y_bytes = (uint64_t(a.rows) * plan.ngroups * a.head_dim * 4 + 255) / 256 * 256;
-    plan.mz_bytes = (uint64_t(a.rows) * plan.ngroups * 2 * 4 + 255) / 256 * 256;
-  }
-  plan.workspace_bytes = plan.y_bytes + plan.mz_bytes;
-  return plan;
+  // Per history token: K and V codes plus two fp32 scales.
+  return plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
 }
 
 void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a) {
@@ -355,6 +364,90 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   }
 }
 
+// Float-KV decode attention (app/src/model/hip_attention.rs:47-113). The
+// reference requires head_dim 64, size <= 1024 and F32 Q/out; here head_dim
+// 64/128/256, any size, and f32/bf16/f16 Q and output are accepted. Every
+// span is checked against the stated strides before the first enqueue.
+AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttentionArgs& a) {
+  require(a.struct_size >= sizeof(PpkFloatAttentionArgs), "PpkFloatAttentionArgs.struct_size too small");
+  dim_index(a.head_dim);
+  require(a.kv_dtype == PPK_BF16 || a.kv_dtype == PPK_F32, "float attention K/V dtype must be bf16 or f32");
+  require(valid_dtype(a.q_dtype) && valid_dtype(a.out_dtype), "float attention Q/out dtype must be f32, bf16 or f16");
+  require(a.heads > 0 && a.rows > 0 && a.rows % a.heads == 0, "float attention geometry differs: rows % heads");
+  require(a.size > 0, "float attention requires at least one stored token per row");
+  require(a.max_length <= a.size, "max_length exceeds size");
+  require(a.max_length == 0 || a.lengths != nullptr, "max_length requires per-sequence lengths");
+  require(std::isfinite(a.softmax_scale) && a.softmax_scale >= 0.f, "softmax_scale must be finite and >= 0");
+  const uint64_t eb = a.kv_dtype == PPK_BF16 ? 2 : 4;
+  const uint64_t row_elems = uint64_t(a.size) * a.head_dim;
+  require(row_elems <= (uint64_t(1) << 40), "float attention size too large");
+  const uint64_t ks = a.k_row_stride ? a.k_row_stride : row_elems;
+  const uint64_t vs = a.v_row_stride ? a.v_row_stride : row_elems;
+  require(ks >= row_elems && vs >= row_elems, "float attention K/V row stride smaller than size * head_dim");
+  require((ks * eb) % 16 == 0 && (vs * eb) % 16 == 0, "float attention K/V row stride must be a multiple of 16 bytes");
+  require(uint64_t(a.rows) * std::max(ks, vs) <= (uint64_t(1) << 46), "float attention K/V span too large");
+  const uint32_t tpl = 64u / (a.head_dim / uint32_t(16 / eb));
+  const uint64_t span = a.max_length ? a.max_length : a.size;
+  return plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
+}
+
+void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a) {
+  const AttentionPlan plan = plan_float_attention(ctx, a);
+  require(a.q && a.k && a.v && a.out, "float attention null pointer");
+  require(aligned(a.k, 16) && aligned(a.v, 16), "float attention K/V must be 16-byte aligned");
+  require(aligned(a.q, dtype_bytes(a.q_dtype)) && aligned(a.out, dtype_bytes(a.out_dtype)) &&
+              (!a.lengths || aligned(a.lengths, 4)),
+          "float attention operand misaligned");
+  const uint64_t qs = a.q_row_stride ? a.q_row_stride : a.head_dim;
+  require(qs >= a.head_dim, "float attention Q row stride smaller than head_dim");
+  if (plan.workspace_bytes) {
+    require(a.workspace && aligned(a.workspace, 256), "float attention workspace missing or not 256-byte aligned");
+    require(a.workspace_bytes >= plan.workspace_bytes,
+            "float attention workspace too small: need " + std::to_string(plan.workspace_bytes) + " bytes");
+  }
+  const int di = dim_index(a.head_dim);
+  const float scale = a.softmax_scale > 0.f ? a.softmax_scale : 1.0f / std::sqrt(float(a.head_dim));
+  const uint64_t row_elems = uint64_t(a.size) * a.head_dim;
+
+  FloatDecodeArgs d{};
+  d.q = a.q;
+  d.k = a.k;
+  d.v = a.v;
+  d.lengths = a.lengths;
+  d.part_y = plan.workspace_bytes ? static_cast<float*>(a.workspace) : nullptr;
+  d.part_mz = plan.workspace_bytes ? reinterpret_cast<float*>(static_cast<char*>(a.workspace) + plan.y_bytes) : nullptr;
+  d.out = a.out;
+  d.q_stride = qs;
+  d.k_stride = a.k_row_stride ? a.k_row_stride : row_elems;
+  d.v_stride = a.v_row_stride ? a.v_row_stride : row_elems;
+  d.rows = a.rows;
+  d.heads = a.heads;
+  d.size = a.size;
+  d.split_tokens = plan.split;
+  d.ngroups = plan.ngroups;
+  d.q_dtype = a.q_dtype;
+  d.out_dtype = a.out_dtype;
+  d.scale_log2 = scale * 1.4426950408889634f;
+
+  const Fn decode = Fn((a.kv_dtype == PPK_BF16 ? kFDecodeBf16_64 : kFDecodeF32_64) + di);
+  DeviceGuard guard(ctx->device);
+  launch(ctx, PPK_KERNEL_FLOAT_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d);
+  if (plan.ngroups > 1) {
+    FloatMergeArgs m{};
+    m.lengths = a.lengths;
+    m.part_y = d.part_y;
+    m.part_mz = d.part_mz;
+    m.out = a.out;
+    m.rows = a.rows;
+    m.heads = a.heads;
+    m.size = a.size;
+    m.split_tokens = plan.split * plan.waves;  // tokens per group
+    m.nsplits = plan.ngroups;
+    m.out_dtype = a.out_dtype;
+    launch(ctx, PPK_KERNEL_FLOAT_MERGE, Fn(kFMerge64 + di), a.rows, 64, 0, stream, m);
+  }
+}
+
 }  // namespace ppk
 
 extern "C" {
@@ -462,6 +555,32 @@ int32_t ppk_decode_step(ppk_context* ctx, void* stream, const PpkDecodeStepArgs*
   return call([&] {
     ppk::require(ctx && args, "ppk_decode_step: null context or arguments");
     ppk::run_attention(ctx, static_cast<hipStream_t>(stream), args->attn, args);
+  });
+}
+
+int32_t ppk_float_attention_plan(ppk_context* ctx, const PpkFloatAttentionArgs* args, uint32_t* split_tokens,
+                                 uint32_t* nsplits, uint64_t* workspace_bytes) {
+  if (workspace_bytes) *workspace_bytes = 0;
+  return call([&] {
+    ppk::require(args != nullptr, "ppk_float_attention_plan: null arguments");
+    const ppk::AttentionPlan plan = ppk::plan_float_attention(ctx, *args);
+    if (split_tokens) *split_tokens = plan.split;
+    if (nsplits) *nsplits = plan.ngroups;
+    if (workspace_bytes) *workspace_bytes = plan.workspace_bytes;
+  });
+}
+
+int32_t ppk_float_decode_attention(ppk_context* ctx, void* stream, const PpkFloatAttentionArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_float_decode_attention: null context or arguments");
+    ppk::run_float_attention(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_float_attention_prepare(ppk_context* ctx) {
+  return call([&] {
+    ppk::require(ctx != nullptr, "ppk_float_attention_prepare: null context");
+    ppk::float_attention_self_check(ctx);
   });
 }
 

@@ -37,6 +37,9 @@ enum Fn : int {
   kDecode64, kDecode128, kDecode256,
   kDecodeBf16h64, kDecodeBf16h128, kDecodeBf16h256,
   kMerge64, kMerge128, kMerge256,
+  kFDecodeBf16_64, kFDecodeBf16_128, kFDecodeBf16_256,
+  kFDecodeF32_64, kFDecodeF32_128, kFDecodeF32_256,
+  kFMerge64, kFMerge128, kFMerge256,
   kFnCount
 };
 
@@ -86,7 +89,12 @@ struct AttentionPlan {
   uint32_t lds_bytes = 0;
   uint64_t y_bytes = 0, mz_bytes = 0, workspace_bytes = 0;
 };
+// Split policy shared by both attention paths: span history tokens per row,
+// tpl tokens per wave-wide load, token_bytes of K+V (+scales) per token.
+AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim);
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
+AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttentionArgs& a);
 
 void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a);
 void run_append(ppk_context* ctx, hipStream_t stream, const PpkAppendArgs& a);
@@ -94,8 +102,11 @@ void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArg
 // step == nullptr: attention only; otherwise the fused decode step.
 void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a,
                    const PpkDecodeStepArgs* step = nullptr);
+void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a);
 
 // int8_kv_ops::prepare known-answer checks (int8_kv_ops.cpp).
 void prepare_self_check(ppk_context* ctx);
+// hip_attention::validate_split_k known-answer checks (fused_attention.cpp).
+void float_attention_self_check(ppk_context* ctx);
 
 }  // namespace ppk

@@ -82,4 +82,31 @@ struct MergeArgs {
   uint32_t pad;
 };
 
+// Float-KV decode attention: the same block geometry over unquantised bf16 or
+// f32 K/V. Row r attends its first n = lengths ? lengths[r / heads] : size
+// tokens (the current token is already stored); no separate current token.
+// ngroups > 1 leaves partial records for the float merge kernel, laid out as
+// for DecodeArgs.
+struct FloatDecodeArgs {
+  const void* q;            // row r at q + r * q_stride elements
+  const void* k;            // row r at k + r * k_stride elements, tokens D apart
+  const void* v;
+  const uint32_t* lengths;  // [rows / heads], or nullptr
+  float* part_y;
+  float* part_mz;
+  void* out;                // [rows, D]
+  uint64_t q_stride, k_stride, v_stride;
+  uint32_t rows, heads, size, split_tokens, ngroups;
+  uint32_t q_dtype, out_dtype;
+  float scale_log2;         // softmax_scale * log2(e)
+};
+
+struct FloatMergeArgs {
+  const uint32_t* lengths;  // [rows / heads], or nullptr
+  const float* part_y;
+  const float* part_mz;
+  void* out;                // [rows, D]
+  uint32_t rows, heads, size, split_tokens, nsplits, out_dtype;
+};
+
 }  // namespace ppk

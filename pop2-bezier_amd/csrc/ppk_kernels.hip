@@ -6,6 +6,8 @@
 //   ppk_dequantize                     codes * scales -> f32/bf16/f16
 //   ppk_decode[_bf16h]_d{..}           decode attention (+ fused append, + in-block merge)
 //   ppk_attn_merge_d{..}               cross-group merge + current token
+//   ppk_fdecode_{bf16,f32}_d{..}       decode attention over float (bf16/f32) K/V
+//   ppk_fmerge_d{..}                   cross-group merge of the float path
 //
 // Semantics follow app/src/model/int8_kv_ops.rs:11-40 and
 // app/src/model/int8_kv.cu:8-59; the design (wave-per-row quantize, one-wave
@@ -607,6 +609,275 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Float-KV decode attention: the reference's non-int8 decode path
+// (app/src/model/decode_attention.hip:9-66, fused_attention.rs:8-30) on the
+// block geometry of the int8 kernel. K/V are stored bf16 or f32; row r attends
+// its first n = lengths ? lengths[r / heads] : size tokens (the current token
+// is already in the store) and gives NaN if n == 0 or n > size.
+//
+// Lane layout: a lane holds one 16-byte chunk of a token, EPC = 8 (bf16) or 4
+// (f32) channels; LPT = D / EPC lanes share a token and a wave-wide dwordx4
+// load moves TPL = 64 / LPT whole tokens (1 KiB). Scores go to LDS in the
+// log2 domain, exactly as in the int8 kernel, and phase V weights each token's
+// chunk by p = 2^(s - m) broadcast from the lane that owns the token.
+// ---------------------------------------------------------------------------
+template <int LPT>
+__device__ __forceinline__ float token_sum(float x) {
+  if constexpr (LPT <= 16) {
+    return group_sum<LPT>(x);
+  } else {
+    x = group_sum<16>(x);
+    x += __shfl_xor(x, 16);
+    if constexpr (LPT >= 64) x += __shfl_xor(x, 32);
+    return x;
+  }
+}
+
+template <bool BF16KV>
+__device__ __forceinline__ void unpack_chunk(const u4& r, float (&x)[BF16KV ? 8 : 4]) {
+  if constexpr (BF16KV) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      x[2 * w] = __uint_as_float(r[w] << 16);
+      x[2 * w + 1] = __uint_as_float(r[w] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) x[w] = __uint_as_float(r[w]);
+  }
+}
+
+template <int D, bool BF16KV>
+struct FloatGeom {
+  static constexpr int kElemBytes = BF16KV ? 2 : 4;
+  static constexpr int kEpc = ppk::kLaneBytes / kElemBytes;  // channels per lane
+  static constexpr int kLpt = D / kEpc;                       // lanes per token
+  static constexpr int kTpl = ppk::kWave / kLpt;              // tokens per wave load
+  static constexpr int kTokenBytes = D * kElemBytes;
+  static_assert(kLpt >= 4 && kLpt <= ppk::kWave, "token must span 4..64 lanes");
+};
+
+template <int D, bool BF16KV, int U>
+__device__ __forceinline__ void load_fbatch(const char* base, uint32_t t0, uint32_t n, int j, u4 (&raw)[U]) {
+  using G = FloatGeom<D, BF16KV>;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t tc = min((t0 + u) * G::kTpl + j, n - 1);  // clamp: always in bounds
+    raw[u] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(base + size_t(tc) * G::kTokenBytes));
+  }
+}
+
+template <int D, bool BF16KV, int U>
+__device__ __forceinline__ float fscore_batch(const u4 (&raw)[U], uint32_t t0, uint32_t n, int j, int c,
+                                              const float (&qr)[FloatGeom<D, BF16KV>::kEpc], float sl2,
+                                              float* s_lds, float mloc) {
+  using G = FloatGeom<D, BF16KV>;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t tok = (t0 + u) * G::kTpl + j;
+    float x[G::kEpc];
+    unpack_chunk<BF16KV>(raw[u], x);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < G::kEpc; ++e) d = fmaf(qr[e], x[e], d);
+    float sc = token_sum<G::kLpt>(d) * sl2;
+    sc = tok < n ? sc : -INFINITY;
+    mloc = fmaxf(mloc, sc);
+    if (c == 0 && tok < n) s_lds[tok] = sc;
+  }
+  return mloc;
+}
+
+template <int D, bool BF16KV, int U>
+__device__ __forceinline__ void faccumulate_batch(const u4 (&raw)[U], uint32_t t0, uint32_t n, int j, int lane,
+                                                  float m, const float* s_lds, float& z,
+                                                  float (&acc)[FloatGeom<D, BF16KV>::kEpc]) {
+  using G = FloatGeom<D, BF16KV>;
+  constexpr int TPB = U * G::kTpl;  // tokens per batch (<= 64)
+  static_assert(TPB <= ppk::kWave, "one token per lane per batch");
+  const uint32_t tl = t0 * G::kTpl + uint32_t(lane % TPB);
+  const float e = __builtin_amdgcn_exp2f(s_lds[min(tl, n - 1)] - m);
+  const float pr = (tl < n && lane < TPB) ? e : 0.f;
+  z += pr;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float wgt = __shfl(pr, u * G::kTpl + j);
+    float x[G::kEpc];
+    unpack_chunk<BF16KV>(raw[u], x);
+#pragma unroll
+    for (int e = 0; e < G::kEpc; ++e) acc[e] = fmaf(wgt, x[e], acc[e]);
+  }
+}
+
+template <int D, bool BF16KV>
+struct FloatWavePartial {
+  float m, z;
+  float acc[FloatGeom<D, BF16KV>::kEpc];  // valid in the lanes of token slot j == 0
+};
+
+// One wave streams n tokens of a row from `begin`: phase K scores into LDS,
+// phase V accumulation; A/B batches ping-pong, and the last phase-K
+// iteration already fetches the first V batch.
+template <int D, bool BF16KV>
+__device__ __forceinline__ void fwave_attention(const ppk::FloatDecodeArgs& a, uint32_t row, uint32_t begin,
+                                                uint32_t n, const float (&qr)[FloatGeom<D, BF16KV>::kEpc],
+                                                float* s_lds, int lane, FloatWavePartial<D, BF16KV>& out) {
+  using G = FloatGeom<D, BF16KV>;
+  constexpr int U = 4;
+  const int j = lane / G::kLpt;
+  const int c = lane % G::kLpt;
+  out.m = -INFINITY;
+  out.z = 0.f;
+#pragma unroll
+  for (int i = 0; i < G::kEpc; ++i) out.acc[i] = 0.f;
+  if (n == 0) return;  // uniform per wave
+
+  const char* kb = static_cast<const char*>(a.k) +
+                   (size_t(row) * a.k_stride + size_t(begin) * D) * G::kElemBytes + size_t(c) * ppk::kLaneBytes;
+  const char* vb = static_cast<const char*>(a.v) +
+                   (size_t(row) * a.v_stride + size_t(begin) * D) * G::kElemBytes + size_t(c) * ppk::kLaneBytes;
+  const uint32_t ntiles = (n + G::kTpl - 1) / G::kTpl;
+  const float sl2 = a.scale_log2;
+
+  u4 ra[U], rb[U];
+  float mloc = -INFINITY;
+  load_fbatch<D, BF16KV, U>(kb, 0, n, j, ra);
+  for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
+    load_fbatch<D, BF16KV, U>(kb, t0 + U, n, j, rb);
+    mloc = fscore_batch<D, BF16KV, U>(ra, t0, n, j, c, qr, sl2, s_lds, mloc);
+    const bool last = t0 + 2 * U >= ntiles;
+    load_fbatch<D, BF16KV, U>(last ? vb : kb, last ? 0u : t0 + 2 * U, n, j, ra);
+    mloc = fscore_batch<D, BF16KV, U>(rb, t0 + U, n, j, c, qr, sl2, s_lds, mloc);
+  }
+  float m = mloc;
+#pragma unroll
+  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  __builtin_amdgcn_wave_barrier();
+
+  float z = 0.f;
+  for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
+    load_fbatch<D, BF16KV, U>(vb, t0 + U, n, j, rb);
+    faccumulate_batch<D, BF16KV, U>(ra, t0, n, j, lane, m, s_lds, z, out.acc);
+    load_fbatch<D, BF16KV, U>(vb, t0 + 2 * U, n, j, ra);
+    faccumulate_batch<D, BF16KV, U>(rb, t0 + U, n, j, lane, m, s_lds, z, out.acc);
+  }
+  z = wave_sum(z);
+#pragma unroll
+  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < G::kEpc; ++i) out.acc[i] += __shfl_xor(out.acc[i], o);
+  }
+  out.m = m;
+  out.z = z;
+}
+
+__device__ __forceinline__ uint32_t float_row_length(const uint32_t* lengths, uint32_t row, uint32_t heads,
+                                                     uint32_t size) {
+  return lengths ? lengths[row / heads] : size;
+}
+
+template <int D, bool BF16KV>
+__device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
+  using G = FloatGeom<D, BF16KV>;
+  constexpr int EPL = D / ppk::kWave;
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int W = blockDim.x >> 6;
+  const int c = lane % G::kLpt;
+  const uint32_t row = blockIdx.x / a.ngroups;
+  const uint32_t group = blockIdx.x - row * a.ngroups;
+  const uint32_t S = a.split_tokens;
+  const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
+  const bool valid = len > 0 && len <= a.size && uint64_t(len) <= uint64_t(a.ngroups) * W * S;
+
+  float qr[G::kEpc];
+  load_vec<G::kEpc>(a.q, size_t(row) * a.q_stride + size_t(c) * G::kEpc, a.q_dtype, qr);
+  const uint32_t begin = (group * W + wave) * S;
+  const uint32_t n = (valid && begin < len) ? min(S, len - begin) : 0u;
+  FloatWavePartial<D, BF16KV> part;
+  fwave_attention<D, BF16KV>(a, row, begin, n, qr, lds + size_t(wave) * S, lane, part);
+
+  // Combine the block's waves through LDS: record of wave w at mrg + w * R
+  // holds m, z, 2 pad floats, y[D] (16-byte aligned).
+  constexpr int R = D + 4;
+  __syncthreads();
+  float* mrg = lds;
+  if (lane < G::kLpt) {
+    f4* o = reinterpret_cast<f4*>(mrg + wave * R + 4 + c * G::kEpc);
+#pragma unroll
+    for (int w = 0; w < G::kEpc / 4; ++w)
+      o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
+  }
+  if (lane == 0) {
+    mrg[wave * R] = part.m;
+    mrg[wave * R + 1] = part.z;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  float m = -INFINITY;
+  for (int w = 0; w < W; ++w) m = fmaxf(m, mrg[w * R]);
+  float y[EPL], zsum = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) y[e] = 0.f;
+  for (int w = 0; w < W; ++w) {
+    const float wt = mrg[w * R] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mrg[w * R] - m);
+    zsum = fmaf(wt, mrg[w * R + 1], zsum);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) y[e] = fmaf(wt, mrg[w * R + 4 + lane * EPL + e], y[e]);
+  }
+  if (a.ngroups == 1) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const float o = (valid && zsum > 0.f) ? y[e] / zsum : __builtin_nanf("");
+      store_elem(a.out, size_t(row) * D + size_t(lane) * EPL + e, a.out_dtype, o);
+    }
+  } else {
+    const size_t rec = size_t(row) * a.ngroups + group;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) a.part_y[rec * D + size_t(lane) * EPL + e] = y[e];
+    if (lane == 0) {
+      a.part_mz[rec * 2] = m;
+      a.part_mz[rec * 2 + 1] = zsum;
+    }
+  }
+}
+
+// Cross-group merge of the float path (pp_attention_merge,
+// decode_attention.hip:55-66): one wave per row, log-sum-exp weights, NaN for
+// invalid rows or a non-positive total weight.
+template <int D>
+__device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
+  constexpr int EPL = D / ppk::kWave;
+  const int lane = threadIdx.x;
+  const uint32_t row = blockIdx.x;
+  const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
+  const bool valid = len > 0 && len <= a.size && uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
+  const float* mz = a.part_mz + size_t(row) * a.nsplits * 2;
+  const float* py = a.part_y + size_t(row) * a.nsplits * D + size_t(lane) * EPL;
+  float m = -INFINITY;
+  for (uint32_t s = lane; s < a.nsplits; s += ppk::kWave) m = fmaxf(m, mz[2 * s]);
+  m = wave_max(m);
+  float y[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) y[e] = 0.f;
+  float zsum = 0.f;
+  for (uint32_t s = 0; s < a.nsplits; ++s) {
+    const float w = mz[2 * s] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mz[2 * s] - m);
+    zsum = fmaf(w, mz[2 * s + 1], zsum);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) y[e] = fmaf(w, py[size_t(s) * D + e], y[e]);
+  }
+  const size_t base = size_t(row) * D + size_t(lane) * EPL;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const float o = (valid && zsum > 0.f) ? y[e] / zsum : __builtin_nanf("");
+    store_elem(a.out, base + e, a.out_dtype, o);
+  }
+}
+
 }  // namespace
 
 #define PPK_QUANTIZE(D)                                                                \
@@ -632,3 +903,17 @@ extern "C" __global__ __launch_bounds__(256) void ppk_dequantize(ppk::Dequantize
 PPK_ATTN(64)
 PPK_ATTN(128)
 PPK_ATTN(256)
+
+#define PPK_FLOAT_ATTN(D)                                                                        \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_fdecode_bf16_d##D(ppk::FloatDecodeArgs a) { \
+    fdecode_body<D, true>(a);                                                                    \
+  }                                                                                              \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_fdecode_f32_d##D(ppk::FloatDecodeArgs a) {  \
+    fdecode_body<D, false>(a);                                                                   \
+  }                                                                                              \
+  extern "C" __global__ __launch_bounds__(64) void ppk_fmerge_d##D(ppk::FloatMergeArgs a) {      \
+    fmerge_body<D>(a);                                                                           \
+  }
+PPK_FLOAT_ATTN(64)
+PPK_FLOAT_ATTN(128)
+PPK_FLOAT_ATTN(256)

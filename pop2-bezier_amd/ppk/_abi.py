@@ -17,8 +17,8 @@ PPK_OK, PPK_PRECONDITION, PPK_INVALID_OUTPUT, PPK_EXECUTION_UNCERTAIN = 0, 1, 2,
 PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
 PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW = 1, 2
 PPK_ATTN_BF16_HISTORY = 1
-(PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE,
- PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_COUNT) = range(6)
+(PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE,
+ PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_COUNT) = range(8)
 
 _u32, _u64, _ptr, _f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_float
 
@@ -54,6 +54,15 @@ class PpkDecodeStepArgs(ctypes.Structure):
                 ("attn", PpkAttentionArgs)]
 
 
+class PpkFloatAttentionArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("kv_dtype", _u32), ("q_dtype", _u32), ("out_dtype", _u32),
+                ("rows", _u32), ("heads", _u32), ("size", _u32), ("head_dim", _u32), ("split_tokens", _u32),
+                ("max_length", _u32), ("softmax_scale", _f32), ("reserved", _u32),
+                ("q_row_stride", _u64), ("k_row_stride", _u64), ("v_row_stride", _u64),
+                ("q", _ptr), ("k", _ptr), ("v", _ptr), ("lengths", _ptr), ("out", _ptr), ("workspace", _ptr),
+                ("workspace_bytes", _u64)]
+
+
 # Every function the header declares: name -> (restype, argtypes).
 FUNCTIONS = {
     "ppk_abi_version": (_u32, []),
@@ -69,6 +78,10 @@ FUNCTIONS = {
                                             ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
     "ppk_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkAttentionArgs)]),
     "ppk_decode_step": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDecodeStepArgs)]),
+    "ppk_float_attention_plan": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkFloatAttentionArgs), ctypes.POINTER(_u32),
+                                                  ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
+    "ppk_float_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatAttentionArgs)]),
+    "ppk_float_attention_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_context_set_profiling": (ctypes.c_int32, [_ptr, ctypes.c_int32]),
     "ppk_context_kernel_stats": (ctypes.c_int32, [_ptr, _u32, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double),

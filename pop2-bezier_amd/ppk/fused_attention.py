@@ -1,0 +1,112 @@
+"""Torch-tensor mirror of the reference's float-KV decode attention.
+
+fused_attention::decode_attention(q, k, v, lengths, heads, split_tokens)
+(app/src/model/fused_attention.rs:8-30, its ROCm branch
+app/src/model/hip_attention.rs:47-113): single-query attention of
+q F32[batch*heads, 1, D] over unquantised bf16/f32 K/V [batch*heads, length, D]
+that already hold the current token, optionally limited per sequence by
+lengths U32[batch]. Every computation runs in the gfx950 kernels behind
+libppk.so (ppk_float_decode_attention); CPU tensors are refused as the
+reference refuses them (fused_attention.rs:28, hip_attention.rs:51-53).
+
+Beyond the reference: head_dim 64/128/256 (reference: 64), any length
+(reference: <= 1024), bf16/f16 q and output dtypes.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _abi
+from ._abi import check, lib
+from .int8_kv_ops import _DTYPES, _HEAD_DIMS, _require, _stream, context
+
+_KV_DTYPES = {torch.bfloat16: _abi.PPK_BF16, torch.float32: _abi.PPK_F32}
+
+
+def decode_attention_args(q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
+                          out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
+                          softmax_scale: float = 0.0) -> tuple[_abi.PpkFloatAttentionArgs, torch.Tensor]:
+    """Validate like fused_attention::decode_attention and build the ABI block (workspace unset)."""
+    _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "fused decode attention requires 3-d q/k/v")
+    rows, query, width = q.shape
+    key_rows, length, key_width = k.shape
+    _require(heads > 0 and rows > 0 and rows % heads == 0 and query == 1 and width in _HEAD_DIMS
+             and key_rows == rows and key_width == width and length > 0 and v.shape == k.shape
+             and q.dtype in _DTYPES and k.dtype in _KV_DTYPES and k.dtype == v.dtype
+             and q.device == k.device == v.device,
+             "fused decode attention requires float[batch*heads,1,D] Q and same-device BF16/F32 K/V")
+    for t in (q, k, v):
+        _require(t.stride(2) == 1 and t.stride(1) == width, "fused attention requires dense width and token strides")
+    if lengths is not None:
+        _require(lengths.dim() == 1 and lengths.shape[0] == rows // heads
+                 and lengths.dtype in (torch.int32, torch.uint32) and lengths.is_contiguous()
+                 and lengths.device == q.device, "fused attention row lengths require same-device U32[batch]")
+    if q.device.type != "cuda":
+        raise RuntimeError("fused decode attention needs a HIP device; use ordinary attention on this backend")
+    if out is None:
+        out = torch.empty((rows, 1, width), dtype=out_dtype, device=q.device)
+    _require(out.numel() == rows * width and out.dtype in _DTYPES and out.is_contiguous() and out.device == q.device,
+             "fused attention output must be a dense float tensor of rows*D elements")
+    a = _abi.PpkFloatAttentionArgs(
+        struct_size=ctypes.sizeof(_abi.PpkFloatAttentionArgs), kv_dtype=_KV_DTYPES[k.dtype],
+        q_dtype=_DTYPES[q.dtype], out_dtype=_DTYPES[out.dtype], rows=rows, heads=heads, size=length,
+        head_dim=width, split_tokens=split_tokens, max_length=max_length, softmax_scale=softmax_scale,
+        q_row_stride=q.stride(0), k_row_stride=k.stride(0), v_row_stride=v.stride(0),
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
+        lengths=lengths.data_ptr() if lengths is not None else None, out=out.data_ptr(), workspace=None,
+        workspace_bytes=0)
+    return a, out
+
+
+def plan(args: _abi.PpkFloatAttentionArgs, ctx: ctypes.c_void_p | None = None) -> tuple[int, int, int]:
+    """(tokens per wave, blocks per row, workspace bytes) the library chooses for args."""
+    split, nsplits, nbytes = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+    check(lib().ppk_float_attention_plan(ctx, ctypes.byref(args), ctypes.byref(split), ctypes.byref(nsplits),
+                                         ctypes.byref(nbytes)), "ppk_float_attention_plan")
+    return split.value, nsplits.value, nbytes.value
+
+
+def decode_attention(q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
+                     out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0) -> torch.Tensor:
+    """fused_attention::decode_attention -> out [rows, 1, D] (float32 by default)."""
+    a, out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length,
+                                   out_dtype=out_dtype, softmax_scale=softmax_scale)
+    ctx = context(q.device)
+    nbytes = plan(a, ctx)[2]
+    # Stream-ordered caching allocator: the block outlives the queued kernels.
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = nbytes
+    check(lib().ppk_float_decode_attention(ctx, _stream(q), ctypes.byref(a)), "ppk_float_decode_attention")
+    return out
+
+
+class FloatDecodeAttention:
+    """A prepared float-KV attention call for fixed buffers: argument block and workspace are built once;
+    __call__ only enqueues the kernels (bench and serving loops, graph capture)."""
+
+    def __init__(self, q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32):
+        self.args, self.out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length,
+                                                    out=out, out_dtype=out_dtype)
+        self.ctx = context(q.device)
+        self.split_tokens, self.ngroups, nbytes = plan(self.args, self.ctx)
+        self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        self.args.workspace = self.workspace.data_ptr()
+        self.args.workspace_bytes = nbytes
+        self._keep = (q, k, v, lengths)
+        self._ref = ctypes.byref(self.args)
+        self._fn = lib().ppk_float_decode_attention
+        self.device = q.device
+
+    def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_float_decode_attention")
+        return self.out
+
+
+def prepare(device: torch.device | int | None = None) -> None:
+    """hip_attention::validate_split_k on the device (raises PpkInvalidOutputError on a mismatch)."""
+    check(lib().ppk_float_attention_prepare(context(device)), "ppk_float_attention_prepare")

@@ -39,7 +39,7 @@ def test_code_object_is_built_for_gfx950():
     blob = open(_abi.HSACO_PATH, "rb").read()
     assert b"gfx950" in blob
     for kernel in (b"ppk_quantize_d128", b"ppk_decode_d128", b"ppk_decode_bf16h_d128", b"ppk_attn_merge_d128",
-                   b"ppk_dequantize"):
+                   b"ppk_dequantize", b"ppk_fdecode_bf16_d64", b"ppk_fdecode_f32_d64", b"ppk_fmerge_d64"):
         assert kernel in blob
 
 
@@ -54,9 +54,9 @@ def c_layout(tmp_path_factory):
     exe = src.with_suffix("")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs,
-                _abi.PpkDecodeStepArgs):
+                _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs):
         name = cls.__name__
-        lines.append(f'printf("{name} size %zu\\n", sizeof({name}));')
+        lines.append(f'printf("{name} __sizeof__ %zu\\n", sizeof({name}));')
         for field, _ in cls._fields_:
             lines.append(f'printf("{name} {field} %zu\\n", offsetof({name}, {field}));')
     lines.append("return 0;}")
@@ -67,10 +67,10 @@ def c_layout(tmp_path_factory):
 
 
 @pytest.mark.parametrize("cls", [_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs,
-                                 _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs])
+                                 _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs])
 def test_struct_layout_matches_c(c_layout, cls):
     name = cls.__name__
-    assert c_layout[(name, "size")] == ctypes.sizeof(cls)
+    assert c_layout[(name, "__sizeof__")] == ctypes.sizeof(cls)
     for field, _ in cls._fields_:
         assert c_layout[(name, field)] == getattr(cls, field).offset, f"{name}.{field}"
 
@@ -121,3 +121,42 @@ def test_null_context_calls_return_status_1():
     step = _abi.PpkDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkDecodeStepArgs), attn=a)
     assert lib.ppk_decode_step(None, None, ctypes.byref(step)) == _abi.PPK_PRECONDITION
     assert lib.ppk_context_release(None) == _abi.PPK_OK
+
+
+def _float_args(**kw) -> _abi.PpkFloatAttentionArgs:
+    a = _abi.PpkFloatAttentionArgs(struct_size=ctypes.sizeof(_abi.PpkFloatAttentionArgs), kv_dtype=_abi.PPK_BF16,
+                                   q_dtype=0, out_dtype=0, rows=512, heads=16, size=8192, head_dim=128,
+                                   split_tokens=0, max_length=0, softmax_scale=0.0)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_float_plan_without_a_device():
+    # Long rows, many of them: one 16-wave block per row, a single launch.
+    assert ppk.fused_attention.plan(_float_args()) == (512, 1, 0)
+    # The reference's graph-decode shape (16 rows of a 1024-token bf16 store, D = 64):
+    # 16 one-wave groups per row cover the CUs; merge workspace y + (m, z) records.
+    split, groups, nbytes = ppk.fused_attention.plan(_float_args(rows=16, size=1024, head_dim=64))
+    assert (split, groups) == (64, 16)
+    assert nbytes == 16 * 16 * 64 * 4 + -(-(16 * 16 * 2 * 4) // 256) * 256
+    # Explicit split: whole wave loads of tokens (f32, D = 128: 2 tokens per 1 KiB load).
+    split, groups, _ = ppk.fused_attention.plan(_float_args(kv_dtype=_abi.PPK_F32, split_tokens=33))
+    assert split == 34 and groups == -(-(-(-8192 // 34)) // 16)
+    # max_length bounds the planned span.
+    assert ppk.fused_attention.plan(_float_args(max_length=1024, lengths=8))[:2] == (64, 1)
+
+
+@pytest.mark.parametrize("bad", [dict(kv_dtype=_abi.PPK_F16), dict(head_dim=96), dict(size=0), dict(rows=30),
+                                 dict(q_dtype=5), dict(out_dtype=9), dict(k_row_stride=8191 * 128),
+                                 dict(v_row_stride=8192 * 128 + 4), dict(max_length=8193),
+                                 dict(max_length=100), dict(softmax_scale=-1.0), dict(struct_size=16)])
+def test_invalid_float_attention_arguments_are_refused_before_launch(bad):
+    with pytest.raises(ppk.PpkPreconditionError):
+        ppk.fused_attention.plan(_float_args(**bad))
+    assert "HIP_PREPARATION" in _abi.lib().ppk_last_error().decode()
+
+
+def test_float_attention_null_context_returns_status_1():
+    a = _float_args()
+    assert _abi.lib().ppk_float_decode_attention(None, None, ctypes.byref(a)) == _abi.PPK_PRECONDITION
