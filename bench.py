@@ -112,6 +112,12 @@ def bench_float(args) -> int:
     q = torch.randn((rows, 1, D), generator=g, device=dev, dtype=torch.float32)
     lengths = torch.full((B,), L, dtype=torch.int32, device=dev)
     call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     torch.cuda.synchronize()
     print("# bench: warmup", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
@@ -143,6 +149,17 @@ def bench_float(args) -> int:
     achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
     kname = f"ppk_fdecode_{args.kv}_d{D}"
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"ppk_fdecode_{args.kv}_d{D}_b{B}_h{H}_ctx{L}_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            with open(tpath) as f:
+                t = json.load(f)
+            if (t.get("split") == call.split_tokens and t.get("workload") == f"B{B}H{H}D{D}L{L}{args.kv}"
+                    and t.get("kernel") == kname):
+                traffic = t.get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
     result = {
         "metric": f"float-KV decode-attention µs/step + achieved HBM GB/s (% of peak), B={B} ctx={L} {args.kv} KV",
         "value": round(step_ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
@@ -155,7 +172,7 @@ def bench_float(args) -> int:
                    "blocks_per_row": call.ngroups, "launches_per_step": 1 if call.ngroups == 1 else 2},
         "step_hbm_gbps": round(step_gbps, 1), "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": kernel_bytes, "avg_launch_us": round(kernel_avg_ms * 1e3, 2),
                      "launches": launches},
     }
