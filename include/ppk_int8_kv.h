@@ -9,7 +9,8 @@
  *   2. split-K single-query decode attention over the int8 arena
  *      (partial kernel + cross-split merge kernel).
  * The same attention kernel design also serves the float (bf16/f32) KV
- * decode path (ppk_float_decode_attention).
+ * decode path (ppk_float_decode_attention); the decode loop's next step, the
+ * CFG + Renyi sampler, is ppk_renyi_sample.
  *
  * Every device buffer is caller-owned; the library never frees or allocates
  * caller memory. All work is stream-ordered on the hipStream_t passed in
@@ -250,6 +251,36 @@ PPK_API int32_t ppk_float_decode_attention(ppk_context* ctx, void* stream, const
    Returns 2 with the failing check in ppk_last_error() on a numeric mismatch. */
 PPK_API int32_t ppk_float_attention_prepare(ppk_context* ctx);
 
+/* CFG + Renyi effective-support sampler, the decode loop's step after
+   attention. Replaces hip_sampling::sample (app/src/inference/hip_sampling.rs:71-106)
+   and kernel pp_hip_renyi_sample (app/src/inference/renyi_sample.hip:23-204).
+   For logical row b (raw rows b*guidance [+1] = conditional [, unconditional]):
+     v_c = guidance == 2 ? u_c + cfg * (c_c - u_c) : c_c      over all choices
+     legal candidates [start_b, start_b + count_b) from bounds[b] = (start, count)
+     H = log Z + max(0, log Z - log Z_alpha) / (alpha - 1), clamped to [0, ln count]
+     support = clamp((u32)(exp(H) + 0.5), 1, count); rank = min((u32)(uniform_b * support), support - 1)
+     token = token_offset + the rank-th legal column by (v descending, column ascending)
+   out = U32 [3, batch]: tokens, valid flags, supports. A non-finite logit
+   anywhere in the head, a uniform outside [0, 1) or bounds outside the head
+   give valid = 0, support = 1 and a placeholder token (the reference's rule).
+   Host checks: guidance 1 or 2 (cfg == 1 for 1), 1 <= choices <= 2048,
+   finite alpha > 1, finite cfg >= 0, token_offset + choices - 1 < 2^32. */
+typedef struct PpkRenyiSampleArgs {
+  uint32_t struct_size;
+  uint32_t batch;          /* logical rows */
+  uint32_t choices;        /* head width, 1..2048 */
+  uint32_t guidance;       /* 1, or 2 for interleaved (conditional, unconditional) rows */
+  float alpha;             /* Renyi order, > 1 */
+  float cfg;               /* guidance scale, >= 0 (1 when guidance == 1) */
+  uint32_t token_offset;   /* added to the selected column */
+  uint32_t reserved;
+  const float* raw;        /* F32 [batch * guidance, choices], contiguous */
+  const float* uniforms;   /* F32 [batch] */
+  const uint32_t* bounds;  /* U32 [batch, 2] */
+  uint32_t* out;           /* U32 [3, batch] */
+} PpkRenyiSampleArgs;
+PPK_API int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiSampleArgs* args);
+
 /* Known-answer self-check on the context's device, the three checks of
    int8_kv_ops::prepare (int8_kv_ops.rs:56-103) plus their fp32-history twins.
    Returns 2 with the failing check in ppk_last_error() on a numeric mismatch. */
@@ -262,7 +293,7 @@ PPK_API int32_t ppk_prepare(ppk_context* ctx);
 enum { PPK_KERNEL_QUANTIZE = 0, PPK_KERNEL_APPEND = 1, PPK_KERNEL_DEQUANTIZE = 2,
        PPK_KERNEL_ATTENTION = 3, /* the decode kernel, with or without the fused append */
        PPK_KERNEL_ATTN_MERGE = 4, PPK_KERNEL_FLOAT_ATTENTION = 5, PPK_KERNEL_FLOAT_MERGE = 6,
-       PPK_KERNEL_COUNT = 7 };
+       PPK_KERNEL_RENYI_SAMPLE = 7, PPK_KERNEL_COUNT = 8 };
 PPK_API int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable);
 PPK_API int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint64_t* launches,
                                  double* total_ms, uint32_t reset);

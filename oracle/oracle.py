@@ -43,6 +43,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_attention_splitk_reference.restype = None
         L.oracle_attention_float.argtypes = [P, P, P, ctypes.c_int, Z, Z, P, Z, Z, Z, Z, ctypes.c_float, P]
         L.oracle_attention_float.restype = None
+        L.oracle_renyi_sample.argtypes = [P, Z, Z, P, P, ctypes.c_float, ctypes.c_float, Z, ctypes.c_uint32,
+                                          ctypes.c_int, P, P, P, P]
+        L.oracle_renyi_sample.restype = ctypes.c_int
         L.cpu_baseline_decode.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, Z, P]
         L.cpu_baseline_decode.restype = ctypes.c_int
         _lib = L
@@ -176,3 +179,28 @@ def attention_float(q, k, v, lengths, heads: int, scale: float | None = None) ->
                                  v.strides[0] // elem, _p(lengths) if lengths is not None else None, rows, heads,
                                  size, d, float(scale), _p(out))
     return out
+
+
+def renyi_sample(raw, uniforms, bounds, alpha: float, cfg: float, guidance: int, offset: int,
+                 cfg_fma: bool = True) -> dict:
+    """CFG + Renyi sampler (see oracle_renyi_sample). raw float32 [batch*guidance, choices];
+    uniforms float32 [batch]; bounds uint32 [batch, 2] = (start, count). Returns a dict of
+    token / valid / support (uint32 [batch]) and margin (float32 [batch]); raises ValueError
+    for metadata the reference rejects."""
+    raw = _c(raw, np.float32)
+    physical, choices = raw.shape
+    uniforms = _c(uniforms, np.float32).reshape(-1)
+    bounds = _c(bounds, np.uint32).reshape(-1, 2)
+    if physical % guidance or uniforms.size != physical // guidance or bounds.shape[0] != physical // guidance:
+        raise ValueError("renyi_sample input lengths differ")
+    batch = physical // guidance
+    token = np.empty(batch, np.uint32)
+    valid = np.empty(batch, np.uint32)
+    support = np.empty(batch, np.uint32)
+    margin = np.empty(batch, np.float32)
+    rc = lib().oracle_renyi_sample(_p(raw), physical, choices, _p(uniforms), _p(bounds), float(alpha), float(cfg),
+                                   guidance, int(offset), int(bool(cfg_fma)), _p(token), _p(valid), _p(support),
+                                   _p(margin))
+    if rc != 0:
+        raise ValueError("invalid reference metadata")
+    return {"token": token, "valid": valid, "support": support, "margin": margin}

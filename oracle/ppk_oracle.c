@@ -425,3 +425,105 @@ void oracle_attention_float(const float* q, const void* k, const void* v, int kv
   }
   free(scores);
 }
+
+/*
+ * CFG + Renyi effective-support sampler, restating the reference's host
+ * validation oracle (app/src/inference/hip_sampling_reference.rs:12-141) of
+ * the kernel pp_hip_renyi_sample (app/src/inference/renyi_sample.hip:23-204):
+ *   value_c = guidance == 2 ? u_c + cfg * (c_c - u_c) : c_c   (every column checked finite)
+ *   legal candidates [start, start + count); m = max; 256 strided partial sums
+ *   of exp(v - m) and exp(alpha (v - m)) reduced by the kernel's tree;
+ *   H = log Z + max(0, log Z - log Z_alpha) / (alpha - 1), clamped to [0, ln count];
+ *   support = clamp((u32)(exp(H) + 0.5), 1, count); rank = min((u32)(uniform * support), support - 1);
+ *   token = offset + the rank-th candidate by (value descending, index ascending).
+ * Invalid rows give (fallback token, valid 0, support 1). With cfg_fma = 1 the
+ * CFG value is fmaf(cfg, c - u, u), the device kernel's contracted form;
+ * cfg_fma = 0 is the host oracle's separately rounded product and sum.
+ * margin[row] (optional) = distance of exp(H) + 0.5 from the nearest integer:
+ * libm and device exp/log may round a row with a tiny margin differently.
+ * Returns 0, or -1 for metadata the reference rejects.
+ */
+static int oracle_before(float a, uint32_t ai, float b, uint32_t bi) { return a > b || (a == b && ai < bi); }
+
+static float* g_sort_values;
+static int oracle_order_cmp(const void* x, const void* y) {
+  const uint32_t a = *(const uint32_t*)x, b = *(const uint32_t*)y;
+  if (oracle_before(g_sort_values[a], a, g_sort_values[b], b)) return -1;
+  if (oracle_before(g_sort_values[b], b, g_sort_values[a], a)) return 1;
+  return 0;
+}
+
+int oracle_renyi_sample(const float* raw, size_t physical_rows, size_t choices, const float* uniforms,
+                        const uint32_t* bounds, float alpha, float cfg, size_t guidance, uint32_t offset,
+                        int cfg_fma, uint32_t* token, uint32_t* valid, uint32_t* support, float* margin) {
+  if (!(guidance == 1 || guidance == 2) || physical_rows == 0 || physical_rows % guidance != 0 || choices < 1 ||
+      choices > 2048 || !isfinite(alpha) || alpha <= 1.f || !isfinite(cfg) || cfg < 0.f ||
+      (guidance == 1 && cfg != 1.f) || (uint64_t)offset + (choices - 1) > 0xffffffffull)
+    return -1;
+  const size_t batch = physical_rows / guidance;
+  float* logits = (float*)malloc(choices * sizeof(float));
+  uint32_t* order = (uint32_t*)malloc(choices * sizeof(uint32_t));
+  for (size_t row = 0; row < batch; ++row) {
+    const uint32_t start = bounds[2 * row], count = bounds[2 * row + 1];
+    const float uniform = uniforms[row];
+    token[row] = offset + (start < choices ? start : 0);
+    valid[row] = 0;
+    support[row] = 1;
+    if (margin) margin[row] = INFINITY;
+    if (!isfinite(uniform) || !(uniform >= 0.f && uniform < 1.f) || count == 0 || start >= choices ||
+        count > choices - start)
+      continue;
+    const float* c = raw + row * guidance * choices;
+    int finite = 1;
+    for (size_t col = 0; col < choices; ++col) {
+      float value = c[col];
+      if (guidance == 2) {
+        const float u = c[choices + col];
+        finite &= isfinite(u);
+        value = cfg_fma ? fmaf(cfg, c[col] - u, u) : u + cfg * (c[col] - u);
+      }
+      finite &= isfinite(c[col]) && isfinite(value);
+      logits[col] = value;
+    }
+    if (!finite) continue;
+    float maximum = -INFINITY;
+    for (uint32_t i = start; i < start + count; ++i) maximum = fmaxf(maximum, logits[i]);
+    float sums[256] = {0}, sums_alpha[256] = {0};
+    for (size_t t = 0; t < 256; ++t)
+      for (size_t k = t; k < count; k += 256) {
+        const float shifted = logits[start + k] - maximum;
+        sums[t] += expf(shifted);
+        sums_alpha[t] += expf(alpha * shifted);
+      }
+    for (size_t step = 128; step > 0; step >>= 1)
+      for (size_t t = 0; t < step; ++t) {
+        sums[t] += sums[t + step];
+        sums_alpha[t] += sums_alpha[t + step];
+      }
+    const float log_z = logf(sums[0]);
+    const float log_za = logf(sums_alpha[0]);
+    const float excess = log_z - log_za;
+    float entropy = log_z + (excess > 0.f ? excess : 0.f) / (alpha - 1.f);
+    if (!isfinite(log_z) || !isfinite(log_za) || !isfinite(entropy)) continue;
+    const float hmax = logf((float)count);
+    if (entropy < 0.f) entropy = 0.f;
+    if (entropy > hmax) entropy = hmax;
+    const float rounded = expf(entropy) + 0.5f;
+    if (margin) margin[row] = fabsf(rounded - nearbyintf(rounded));
+    uint32_t s = rounded >= 4294967295.f ? 0xffffffffu : (uint32_t)rounded;
+    if (s < 1) s = 1;
+    if (s > count) s = count;
+    const float scaled = uniform * (float)s;
+    uint32_t rank = (uint32_t)scaled;
+    if (rank > s - 1) rank = s - 1;
+    for (uint32_t i = 0; i < count; ++i) order[i] = start + i;
+    g_sort_values = logits;
+    qsort(order, count, sizeof(uint32_t), oracle_order_cmp);
+    token[row] = offset + order[rank];
+    valid[row] = 1;
+    support[row] = s;
+  }
+  free(logits);
+  free(order);
+  return 0;
+}

@@ -54,6 +54,7 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_fdecode_bf16_d64", "ppk_fdecode_bf16_d128", "ppk_fdecode_bf16_d256",
     "ppk_fdecode_f32_d64", "ppk_fdecode_f32_d128", "ppk_fdecode_f32_d256",
     "ppk_fmerge_d64", "ppk_fmerge_d128", "ppk_fmerge_d256",
+    "ppk_renyi_sample",
 };
 
 std::string default_code_object() {
@@ -448,6 +449,37 @@ void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAtt
   }
 }
 
+// CFG + Renyi sampler (app/src/inference/hip_sampling.rs:18-69 validation,
+// :150-214 launch): metadata is checked on the host; device values (bounds,
+// uniforms, logits) are judged by the kernel, which marks bad rows valid = 0.
+void run_renyi_sample(ppk_context* ctx, hipStream_t stream, const PpkRenyiSampleArgs& a) {
+  require(a.struct_size >= sizeof(PpkRenyiSampleArgs), "PpkRenyiSampleArgs.struct_size too small");
+  require((a.guidance == 1 || a.guidance == 2) && a.batch > 0 && a.choices >= 1 &&
+              a.choices <= uint32_t(kSamplerMaxChoices),
+          "HIP sampler needs 1/2 guidance rows and a nonempty head of at most 2048 choices");
+  require(a.batch <= 0x7fffffffu, "HIP sampler logical row, uniform or bounds shape mismatch");
+  require(std::isfinite(a.alpha) && a.alpha > 1.f && std::isfinite(a.cfg) && a.cfg >= 0.f &&
+              (a.guidance != 1 || a.cfg == 1.f),
+          "invalid HIP sampler alpha/CFG/guidance combination");
+  require(uint64_t(a.token_offset) + (a.choices - 1) <= 0xffffffffull, "HIP sampler token range overflow");
+  require(a.raw && a.uniforms && a.bounds && a.out, "HIP sampler null pointer");
+  require(aligned(a.raw, 4) && aligned(a.uniforms, 4) && aligned(a.bounds, 4) && aligned(a.out, 4),
+          "HIP sampler operand misaligned");
+  RenyiArgs k{};
+  k.raw = a.raw;
+  k.uniforms = a.uniforms;
+  k.bounds = a.bounds;
+  k.out = a.out;
+  k.batch = a.batch;
+  k.choices = a.choices;
+  k.guidance = a.guidance;
+  k.token_offset = a.token_offset;
+  k.alpha = a.alpha;
+  k.cfg = a.cfg;
+  DeviceGuard guard(ctx->device);
+  launch(ctx, PPK_KERNEL_RENYI_SAMPLE, kRenyiSample, a.batch, kSamplerThreads, 0, stream, k);
+}
+
 }  // namespace ppk
 
 extern "C" {
@@ -574,6 +606,13 @@ int32_t ppk_float_decode_attention(ppk_context* ctx, void* stream, const PpkFloa
   return call([&] {
     ppk::require(ctx && args, "ppk_float_decode_attention: null context or arguments");
     ppk::run_float_attention(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiSampleArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_renyi_sample: null context or arguments");
+    ppk::run_renyi_sample(ctx, static_cast<hipStream_t>(stream), *args);
   });
 }
 

@@ -40,6 +40,7 @@ enum Fn : int {
   kFDecodeBf16_64, kFDecodeBf16_128, kFDecodeBf16_256,
   kFDecodeF32_64, kFDecodeF32_128, kFDecodeF32_256,
   kFMerge64, kFMerge128, kFMerge256,
+  kRenyiSample,
   kFnCount
 };
 
@@ -103,6 +104,7 @@ void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArg
 void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a,
                    const PpkDecodeStepArgs* step = nullptr);
 void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a);
+void run_renyi_sample(ppk_context* ctx, hipStream_t stream, const PpkRenyiSampleArgs& a);
 
 // int8_kv_ops::prepare known-answer checks (int8_kv_ops.cpp).
 void prepare_self_check(ppk_context* ctx);

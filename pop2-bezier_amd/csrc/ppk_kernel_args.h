@@ -109,4 +109,19 @@ struct FloatMergeArgs {
   uint32_t rows, heads, size, split_tokens, nsplits, out_dtype;
 };
 
+// CFG + Renyi effective-support sampler: one 256-thread block per logical row.
+struct RenyiArgs {
+  const float* raw;         // [batch * guidance, choices]; guided rows interleave (conditional, unconditional)
+  const float* uniforms;    // [batch]
+  const uint32_t* bounds;   // [batch, 2] = (start, count) of the legal range
+  uint32_t* out;            // [3, batch]: token, valid, support
+  uint32_t batch, choices, guidance, token_offset;
+  float alpha, cfg;
+};
+
+// Threads per sampler block: the partial-sum layout (256 strided partials and
+// their tree) is part of the sampler's arithmetic contract.
+constexpr int kSamplerThreads = 256;
+constexpr int kSamplerMaxChoices = 2048;
+
 }  // namespace ppk

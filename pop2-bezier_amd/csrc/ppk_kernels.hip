@@ -8,6 +8,7 @@
 //   ppk_attn_merge_d{..}               cross-group merge + current token
 //   ppk_fdecode_{bf16,f32}_d{..}       decode attention over float (bf16/f32) K/V
 //   ppk_fmerge_d{..}                   cross-group merge of the float path
+//   ppk_renyi_sample                   CFG + Renyi effective-support sampler
 //
 // Semantics follow app/src/model/int8_kv_ops.rs:11-40 and
 // app/src/model/int8_kv.cu:8-59; the design (wave-per-row quantize, one-wave
@@ -878,6 +879,254 @@ __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// CFG + Renyi effective-support sampler (app/src/inference/renyi_sample.hip:23-204,
+// hip_sampling.rs:89-105). Per logical row: v = u + cfg (c - u) over the whole
+// head (every column must be finite), legal candidates [start, start + count),
+// H = log Z + max(0, log Z - log Z_alpha) / (alpha - 1) clamped to [0, ln count],
+// support = clamp((u32)(exp(H) + 0.5), 1, count), rank = min((u32)(uniform *
+// support), support - 1), token = the rank-th candidate by (value descending,
+// index ascending).
+//
+// The arithmetic that decides support keeps the reference's order: 256
+// strided partial sums of exp(v - m) and exp(alpha (v - m)) in candidate
+// order, then the halving tree (steps 128, 64 through LDS, 32..1 by
+// shuffles within one wave: the same pairs added in the same order), with
+// the device expf/logf. The candidate selection is this file's own: the
+// reference sorts the whole legal range (a bitonic network of ~66 barrier
+// phases at 2048 candidates); here a 4-pass radix select over a 32-bit
+// order-preserving key of the value finds the selected value and a ballot
+// count orders equal values by index, which names the same candidate.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool finite_bits(float x) { return (__float_as_uint(x) & 0x7fffffffu) < 0x7f800000u; }
+__device__ __forceinline__ bool sample_before(float a, uint32_t ai, float b, uint32_t bi) {
+  return a > b || (a == b && ai < bi);
+}
+// Ascending key order = descending value order; -0 and +0 share a key (they
+// compare equal, so their order is by index).
+__device__ __forceinline__ uint32_t descending_key(float v) {
+  const uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
+  const uint32_t ascending = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ~ascending;
+}
+
+__device__ __forceinline__ void write_sample(const ppk::RenyiArgs& a, uint32_t row, uint32_t token, uint32_t valid,
+                                             uint32_t support) {
+  a.out[row] = token;
+  a.out[size_t(a.batch) + row] = valid;
+  a.out[2 * size_t(a.batch) + row] = support;
+}
+
+__device__ __forceinline__ void renyi_sample_body(const ppk::RenyiArgs& a) {
+  constexpr int T = ppk::kSamplerThreads;
+  constexpr int PER = ppk::kSamplerMaxChoices / T;  // candidates per thread
+  __shared__ float s_vals[ppk::kSamplerMaxChoices];
+  __shared__ float s_sum[T], s_sum_a[T];
+  __shared__ float s_wmax[T / 64];
+  __shared__ uint32_t s_wid[T / 64], s_wbad[T / 64];
+  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_wtotal[T / 64];
+  __shared__ uint64_t s_ballot[PER][T / 64];
+  __shared__ uint32_t s_state[4];  // support, rank, invalid, selected bin / below
+
+  const uint32_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const uint32_t start = a.bounds[2 * row];
+  const uint32_t count = a.bounds[2 * row + 1];
+  const float uniform = a.uniforms[row];
+  // Every thread evaluates the same metadata, so these exits are uniform.
+  if (!finite_bits(uniform) || uniform < 0.f || uniform >= 1.f || start >= a.choices || count == 0 ||
+      count > a.choices - start) {
+    if (t == 0) write_sample(a, row, a.token_offset + (start < a.choices ? start : 0u), 0, 1);
+    return;
+  }
+
+  // Whole head: CFG combine and finiteness; legal values to LDS; arg-max.
+  const float* c_row = a.raw + size_t(row) * a.guidance * a.choices;
+  float lmax = -INFINITY;
+  uint32_t lid = 0xffffffffu, lbad = 0;
+  for (uint32_t col = t; col < a.choices; col += T) {
+    const float c = c_row[col];
+    float value = c;
+    bool finite = finite_bits(c);
+    if (a.guidance == 2) {
+      const float u = c_row[a.choices + col];
+      finite = finite && finite_bits(u);
+      value = u + a.cfg * (c - u);
+    }
+    finite = finite && finite_bits(value);
+    lbad |= finite ? 0u : 1u;
+    if (!finite) value = 0.f;
+    if (col >= start && col - start < count) {
+      s_vals[col - start] = value;
+      if (sample_before(value, col, lmax, lid)) {
+        lmax = value;
+        lid = col;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    const float ov = __shfl_xor(lmax, o);
+    const uint32_t oi = __shfl_xor(lid, o);
+    if (sample_before(ov, oi, lmax, lid)) {
+      lmax = ov;
+      lid = oi;
+    }
+    lbad |= __shfl_xor(lbad, o);
+  }
+  if (lane == 0) {
+    s_wmax[wave] = lmax;
+    s_wid[wave] = lid;
+    s_wbad[wave] = lbad;
+  }
+  __syncthreads();
+  float maximum = s_wmax[0];
+  uint32_t maximum_id = s_wid[0], bad = s_wbad[0];
+#pragma unroll
+  for (int w = 1; w < T / 64; ++w) {
+    if (sample_before(s_wmax[w], s_wid[w], maximum, maximum_id)) {
+      maximum = s_wmax[w];
+      maximum_id = s_wid[w];
+    }
+    bad |= s_wbad[w];
+  }
+  if (bad) {
+    if (t == 0) write_sample(a, row, a.token_offset + start, 0, 1);
+    return;
+  }
+
+  // Strided partial sums in candidate order, then the halving tree.
+  float vals[PER];
+  float sum = 0.f, sum_a = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t ci = uint32_t(t) + uint32_t(k) * T;
+    vals[k] = ci < count ? s_vals[ci] : 0.f;
+    if (ci < count) {
+      const float shifted = vals[k] - maximum;
+      sum += expf(shifted);
+      sum_a += expf(a.alpha * shifted);
+    }
+  }
+  s_sum[t] = sum;
+  s_sum_a[t] = sum_a;
+  __syncthreads();
+  if (t < 128) {
+    s_sum[t] += s_sum[t + 128];
+    s_sum_a[t] += s_sum_a[t + 128];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float z = s_sum[lane] + s_sum[lane + 64];
+    float za = s_sum_a[lane] + s_sum_a[lane + 64];
+#pragma unroll
+    for (int o = 32; o; o >>= 1) {
+      z += __shfl_down(z, o);
+      za += __shfl_down(za, o);
+    }
+    if (lane == 0) {
+      const float log_z = logf(z);
+      const float log_za = logf(za);
+      float correction = log_z - log_za;
+      if (correction < 0.0f) correction = 0.0f;
+      float entropy = log_z + correction / (a.alpha - 1.0f);
+      uint32_t invalid = !finite_bits(log_z) || !finite_bits(log_za) || !finite_bits(entropy);
+      uint32_t support = 1, rank = 0;
+      if (!invalid) {
+        const float maximum_entropy = logf((float)count);
+        if (entropy < 0.0f) entropy = 0.0f;
+        if (entropy > maximum_entropy) entropy = maximum_entropy;
+        const float rounded = expf(entropy) + 0.5f;
+        support = (uint32_t)rounded;
+        if (support < 1) support = 1;
+        if (support > count) support = count;
+        rank = (uint32_t)(uniform * (float)support);
+        if (rank >= support) rank = support - 1;
+      }
+      s_state[0] = support;
+      s_state[1] = rank;
+      s_state[2] = invalid;
+    }
+  }
+  __syncthreads();
+  const uint32_t support = s_state[0];
+  uint32_t r = s_state[1];
+  if (s_state[2]) {
+    if (t == 0) write_sample(a, row, a.token_offset + start, 0, 1);
+    return;
+  }
+  if (r == 0) {
+    if (t == 0) write_sample(a, row, a.token_offset + maximum_id, 1, support);
+    return;
+  }
+
+  // Radix select, 8 key bits per pass from the top: after four passes the
+  // prefix is the selected value's key and r its rank among equal values.
+  uint32_t keys[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) keys[k] = descending_key(vals[k]);
+  uint32_t prefix = 0, pmask = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    s_hist[t] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const uint32_t ci = uint32_t(t) + uint32_t(k) * T;
+      if (ci < count && (keys[k] & pmask) == prefix) atomicAdd(&s_hist[(keys[k] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    const uint32_t h = s_hist[t];
+    uint32_t incl = h;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(incl, o);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) s_wtotal[wave] = incl;
+    __syncthreads();
+    uint32_t below = incl - h;
+    for (int w = 0; w < wave; ++w) below += s_wtotal[w];
+    if (h > 0 && below <= r && r < below + h) {
+      s_state[3] = uint32_t(t);
+      s_hist[0] = below;  // every thread has read its own bin already
+    }
+    __syncthreads();
+    const uint32_t bin = s_state[3];
+    r -= s_hist[0];
+    prefix |= bin << shift;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+
+  // Among candidates with the selected key, the r-th by ascending index.
+  // Candidate ci = t + 256 k: index order is (k, wave, lane) order. The
+  // selection always names one candidate (r stays below the count of keys
+  // matching the prefix); the record written first only keeps the row's
+  // output defined should it not.
+  if (t == 0) write_sample(a, row, a.token_offset + start, 0, 1);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t ci = uint32_t(t) + uint32_t(k) * T;
+    const uint64_t b = __ballot(ci < count && keys[k] == prefix);
+    if (lane == 0) s_ballot[k][wave] = b;
+  }
+  __syncthreads();
+  uint32_t before_k = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t ci = uint32_t(t) + uint32_t(k) * T;
+    if (ci < count && keys[k] == prefix) {
+      uint32_t pos = before_k + uint32_t(__popcll(s_ballot[k][wave] & ((uint64_t(1) << lane) - 1)));
+      for (int w = 0; w < wave; ++w) pos += uint32_t(__popcll(s_ballot[k][w]));
+      if (pos == r) write_sample(a, row, a.token_offset + start + ci, 1, support);
+    }
+#pragma unroll
+    for (int w = 0; w < T / 64; ++w) before_k += uint32_t(__popcll(s_ballot[k][w]));
+  }
+}
+
 }  // namespace
 
 #define PPK_QUANTIZE(D)                                                                \
@@ -917,3 +1166,5 @@ PPK_ATTN(256)
 PPK_FLOAT_ATTN(64)
 PPK_FLOAT_ATTN(128)
 PPK_FLOAT_ATTN(256)
+
+extern "C" __global__ __launch_bounds__(256) void ppk_renyi_sample(ppk::RenyiArgs a) { renyi_sample_body(a); }

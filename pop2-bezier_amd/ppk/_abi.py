@@ -18,7 +18,7 @@ PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
 PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW = 1, 2
 PPK_ATTN_BF16_HISTORY = 1
 (PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE,
- PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_COUNT) = range(8)
+ PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_RENYI_SAMPLE, PPK_KERNEL_COUNT) = range(9)
 
 _u32, _u64, _ptr, _f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_float
 
@@ -63,6 +63,12 @@ class PpkFloatAttentionArgs(ctypes.Structure):
                 ("workspace_bytes", _u64)]
 
 
+class PpkRenyiSampleArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("batch", _u32), ("choices", _u32), ("guidance", _u32), ("alpha", _f32),
+                ("cfg", _f32), ("token_offset", _u32), ("reserved", _u32), ("raw", _ptr), ("uniforms", _ptr),
+                ("bounds", _ptr), ("out", _ptr)]
+
+
 # Every function the header declares: name -> (restype, argtypes).
 FUNCTIONS = {
     "ppk_abi_version": (_u32, []),
@@ -82,6 +88,7 @@ FUNCTIONS = {
                                                   ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
     "ppk_float_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatAttentionArgs)]),
     "ppk_float_attention_prepare": (ctypes.c_int32, [_ptr]),
+    "ppk_renyi_sample": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkRenyiSampleArgs)]),
     "ppk_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_context_set_profiling": (ctypes.c_int32, [_ptr, ctypes.c_int32]),
     "ppk_context_kernel_stats": (ctypes.c_int32, [_ptr, _u32, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double),

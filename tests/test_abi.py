@@ -39,7 +39,8 @@ def test_code_object_is_built_for_gfx950():
     blob = open(_abi.HSACO_PATH, "rb").read()
     assert b"gfx950" in blob
     for kernel in (b"ppk_quantize_d128", b"ppk_decode_d128", b"ppk_decode_bf16h_d128", b"ppk_attn_merge_d128",
-                   b"ppk_dequantize", b"ppk_fdecode_bf16_d64", b"ppk_fdecode_f32_d64", b"ppk_fmerge_d64"):
+                   b"ppk_dequantize", b"ppk_fdecode_bf16_d64", b"ppk_fdecode_f32_d64", b"ppk_fmerge_d64",
+                   b"ppk_renyi_sample"):
         assert kernel in blob
 
 
@@ -54,7 +55,7 @@ def c_layout(tmp_path_factory):
     exe = src.with_suffix("")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs,
-                _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs):
+                _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs, _abi.PpkRenyiSampleArgs):
         name = cls.__name__
         lines.append(f'printf("{name} __sizeof__ %zu\\n", sizeof({name}));')
         for field, _ in cls._fields_:
@@ -67,7 +68,8 @@ def c_layout(tmp_path_factory):
 
 
 @pytest.mark.parametrize("cls", [_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs,
-                                 _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs])
+                                 _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs,
+                                 _abi.PpkRenyiSampleArgs])
 def test_struct_layout_matches_c(c_layout, cls):
     name = cls.__name__
     assert c_layout[(name, "__sizeof__")] == ctypes.sizeof(cls)
@@ -160,3 +162,44 @@ def test_invalid_float_attention_arguments_are_refused_before_launch(bad):
 def test_float_attention_null_context_returns_status_1():
     a = _float_args()
     assert _abi.lib().ppk_float_decode_attention(None, None, ctypes.byref(a)) == _abi.PPK_PRECONDITION
+
+
+def _sample_args(**kw) -> _abi.PpkRenyiSampleArgs:
+    a = _abi.PpkRenyiSampleArgs(struct_size=ctypes.sizeof(_abi.PpkRenyiSampleArgs), batch=2, choices=128,
+                                guidance=1, alpha=3.5, cfg=1.0, token_offset=100, raw=8, uniforms=8, bounds=8, out=8)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("bad", [dict(alpha=1.0), dict(alpha=0.0), dict(alpha=float("nan")), dict(alpha=float("inf")),
+                                 dict(cfg=-1.0), dict(cfg=float("nan")), dict(cfg=float("inf")), dict(cfg=2.0),
+                                 dict(guidance=3), dict(token_offset=2**32 - 1), dict(choices=2049),
+                                 dict(choices=0), dict(batch=0), dict(raw=None), dict(out=6),
+                                 dict(struct_size=8)])
+def test_invalid_sampler_metadata_is_refused_before_launch(bad):
+    """hip_sampling.rs:209-245 (validates_metadata_and_refuses_host_mathematics,
+    supports_cfg_pairs_offsets_and_rejects_wrong_shapes): the same rules, at the C-ABI."""
+    # A stand-in context pointer: every case fails validation, which precedes any use of the context.
+    a = _sample_args(**bad)
+    assert _abi.lib().ppk_renyi_sample(ctypes.c_void_p(16), None, ctypes.byref(a)) == _abi.PPK_PRECONDITION
+    msg = _abi.lib().ppk_last_error().decode()
+    assert msg.startswith("HIP_PREPARATION") and "null context" not in msg
+
+
+def test_sampler_python_mirror_refuses_cpu_tensors_and_bad_shapes():
+    import torch
+
+    raw = torch.zeros((4, 270))
+    u = torch.zeros((2, 1))
+    b = torch.zeros((2, 2), dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="no CPU/CUDA fallback"):
+        ppk.sampling.sample(raw, u, b, 3.5, 2.5, 2, 2048)
+    with pytest.raises(ValueError):
+        ppk.sampling.sample(torch.zeros((4, 2049)), u, b, 4.0, 2.0, 2, 0)
+    with pytest.raises(ValueError):
+        ppk.sampling.sample(raw.to(torch.bfloat16), u, b, 4.0, 2.0, 2, 0)
+    with pytest.raises(ValueError):
+        ppk.sampling.sample(raw, torch.zeros((2, 2))[:, :1], b, 4.0, 2.0, 2, 0)
+    with pytest.raises(ValueError):
+        ppk.sampling.sample(raw, u, b, 4.0, 2.0, 1, 0)

@@ -1,0 +1,168 @@
+"""GPU parity of the CFG + Renyi sampler (ppk_renyi_sample).
+
+Bars:
+* against the reference's own kernel pp_hip_renyi_sample, built unchanged
+  from its source into oracle/_ref with the same device flags: token, valid
+  and support identical on every row (integer outputs, bit-exact);
+* against the C oracle (the reference's host validation oracle restated, with
+  the device's contracted CFG product): identical on every row whose
+  exp(H) + 0.5 lies at least 1e-4 from an integer; nearer rows may round to a
+  neighbouring support, as the reference's oracle notes for libm vs device
+  exp/log (hip_sampling_reference.rs:1-3), and must then be consistent with
+  the support the kernel chose;
+* the reference's known answers (hip_sampling_reference.rs:143-205).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import ppk
+import refkernels
+from helpers import SEED
+
+pytestmark = pytest.mark.gpu
+F32_MAX = np.finfo(np.float32).max
+
+
+def run(device, raw, uniforms, bounds, alpha, cfg, guidance, offset):
+    raw_t = torch.from_numpy(np.ascontiguousarray(raw, np.float32)).to(device)
+    u_t = torch.from_numpy(np.ascontiguousarray(uniforms, np.float32).reshape(-1, 1)).to(device)
+    b_t = torch.from_numpy(np.ascontiguousarray(bounds, np.uint32).reshape(-1, 2).view(np.int32)).to(device)
+    tok, val, sup = ppk.sampling.sample(raw_t, u_t, b_t, alpha, cfg, guidance, offset)
+    torch.cuda.synchronize()
+    as_u32 = lambda t: t.reshape(-1).cpu().numpy().view(np.uint32)
+    return {"token": as_u32(tok), "valid": as_u32(val), "support": as_u32(sup)}, (raw_t, u_t, b_t)
+
+
+def random_problem(rng, batch, choices, guidance, kind="normal"):
+    scale = rng.uniform(0.05, 8.0, (batch * guidance, 1))
+    raw = rng.standard_normal((batch * guidance, choices)) * scale
+    if kind == "ties":
+        raw = np.round(raw * 2) / 2  # many exactly equal logits, signed zeros included
+        raw[:, ::7] = -0.0
+    raw = raw.astype(np.float32)
+    uniforms = rng.uniform(0, 1, batch).astype(np.float32)
+    uniforms[::11] = np.float32(0.99999994)
+    uniforms[5::13] = 0.0
+    starts = rng.integers(0, max(choices // 3, 1), batch)
+    counts = rng.integers(1, choices - starts + 1)
+    counts[::9] = choices - starts[::9]
+    return raw, uniforms, np.stack([starts, counts], 1).astype(np.uint32)
+
+
+def check_against_oracle(got, ref, what):
+    exact = ref["margin"] >= 1e-4
+    for key in ("token", "valid", "support"):
+        bad = np.nonzero((got[key] != ref[key]) & exact)[0]
+        assert bad.size == 0, f"{what}: {key} differs at rows {bad[:8]} (gpu {got[key][bad[:8]]}, oracle {ref[key][bad[:8]]})"
+    near = ~exact
+    assert np.all(np.abs(got["support"][near].astype(np.int64) - ref["support"][near].astype(np.int64)) <= 1)
+    return int(exact.sum())
+
+
+@pytest.mark.parametrize("guidance", [1, 2])
+@pytest.mark.parametrize("choices", [1, 37, 256, 700, 2048])
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_matches_oracle(device, guidance, choices, kind):
+    rng = np.random.default_rng(SEED + choices * 3 + guidance + (kind == "ties"))
+    batch = 96
+    raw, u, b = random_problem(rng, batch, choices, guidance, kind)
+    alpha, cfg = 3.5, (2.5 if guidance == 2 else 1.0)
+    got, _ = run(device, raw, u, b, alpha, cfg, guidance, 11)
+    ref = oracle.renyi_sample(raw, u, b, alpha, cfg, guidance, 11, cfg_fma=True)
+    assert check_against_oracle(got, ref, f"{kind} g{guidance} c{choices}") >= batch * 0.9
+    assert np.all(got["valid"] == 1)
+
+
+@pytest.mark.parametrize("alpha", [1.25, 4.0, 32.0])
+def test_alpha_range_matches_oracle(device, alpha):
+    rng = np.random.default_rng(SEED + int(alpha * 4))
+    raw, u, b = random_problem(rng, 64, 1024, 2)
+    got, _ = run(device, raw, u, b, alpha, 1.7, 2, 0)
+    check_against_oracle(got, oracle.renyi_sample(raw, u, b, alpha, 1.7, 2, 0), f"alpha {alpha}")
+
+
+def test_reference_known_answers(device):
+    """hip_sampling_reference.rs:147-204 on the device kernel."""
+    for count in [1, 2, 127, 128, 255, 256, 270, 1024, 2048]:
+        for alpha in [1.25, 3.5, 4.0, 7.0, 32.0]:
+            u = np.array([0.0, 0.25, 0.75, np.float32(0.99999994)], np.float32)
+            got, _ = run(device, np.zeros((4, count), np.float32), u, np.tile([0, count], (4, 1)), alpha, 1.0, 1, 100)
+            expect = [100 + min(int(u[r] * np.float32(count)), count - 1) for r in range(4)]
+            assert list(got["token"]) == expect and all(got["valid"] == 1) and all(got["support"] == count)
+    raw = np.array([0, 1, 2, 3, 1, 1, 1, 1, 9, 8, 7, 6, 1, 1, 1, 1], np.float32).reshape(4, 4)
+    got, _ = run(device, raw, np.zeros(2, np.float32), np.array([[1, 2], [2, 2]]), 4.0, 2.5, 2, 2048)
+    assert list(got["token"]) == [2050, 2050] and list(got["valid"]) == [1, 1]
+    for value in [np.nan, np.inf, -np.inf]:
+        got, _ = run(device, np.array([[1, 2, value]], np.float32), np.zeros(1), np.array([[0, 2]]), 4.0, 1.0, 1, 0)
+        assert (got["token"][0], got["valid"][0], got["support"][0]) == (0, 0, 1)
+    for uu in [1.0, -0.1, np.nan, np.inf]:
+        got, _ = run(device, np.array([[1, 2]], np.float32), np.array([uu]), np.array([[0, 2]]), 4.0, 1.0, 1, 0)
+        assert got["valid"][0] == 0
+    got, _ = run(device, np.array([[F32_MAX], [-F32_MAX]], np.float32), np.zeros(1), np.array([[0, 1]]), 4.0, 2.0, 2, 0)
+    assert got["valid"][0] == 0
+    got, _ = run(device, np.zeros((1, 2), np.float32), np.zeros(1), np.array([[2, 1]]), 4.0, 1.0, 1, 0)
+    assert (got["token"][0], got["valid"][0], got["support"][0]) == (0, 0, 1)
+
+
+def test_invalid_rows_do_not_disturb_valid_rows(device):
+    rng = np.random.default_rng(SEED + 77)
+    raw, u, b = random_problem(rng, 40, 300, 2)
+    raw[2 * 3, 299] = np.nan           # row 3: NaN outside its legal range still invalidates it
+    u[7] = 1.0                         # row 7: uniform out of range
+    b[9] = [300, 1]                    # row 9: start beyond the head
+    b[11] = [10, 291]                  # row 11: count runs past the head
+    b[13] = [5, 0]                     # row 13: empty range
+    got, _ = run(device, raw, u, b, 4.0, 2.0, 2, 5)
+    ref = oracle.renyi_sample(raw, u, b, 4.0, 2.0, 2, 5)
+    check_against_oracle(got, ref, "mixed rows")
+    for row, token in [(3, 5 + int(b[3, 0])), (7, 5 + int(b[7, 0])), (9, 5), (11, 15), (13, 10)]:
+        assert (got["token"][row], got["valid"][row], got["support"][row]) == (token, 0, 1), row
+
+
+def test_bit_identical_to_reference_kernel(device):
+    """The reference's pp_hip_renyi_sample, built from its source, on the same device buffers."""
+    rng = np.random.default_rng(SEED + 99)
+    total = 0
+    for guidance in (1, 2):
+        for choices in (1, 64, 333, 1024, 2048):
+            for kind in ("normal", "ties"):
+                raw, u, b = random_problem(rng, 128, choices, guidance, kind)
+                if choices > 3:
+                    raw[guidance * 5, 2] = np.inf  # one invalid row
+                    u[6] = np.nan
+                alpha, cfg = float(rng.uniform(1.1, 12.0)), (float(rng.uniform(0, 4)) if guidance == 2 else 1.0)
+                got, (raw_t, u_t, b_t) = run(device, raw, u, b, alpha, cfg, guidance, 3)
+                ref = refkernels.renyi_sample(raw_t, u_t, b_t, alpha, cfg, guidance, 3)
+                torch.cuda.synchronize()
+                ref = ref.cpu().numpy().view(np.uint32)
+                for i, key in enumerate(("token", "valid", "support")):
+                    bad = np.nonzero(got[key] != ref[i])[0]
+                    assert bad.size == 0, (guidance, choices, kind, key, bad[:8], got[key][bad[:8]], ref[i][bad[:8]])
+                total += len(u)
+    assert total == 2 * 5 * 2 * 128
+
+
+def test_graph_replay(device):
+    rng = np.random.default_rng(SEED + 5)
+    raw, u, b = random_problem(rng, 32, 2048, 2)
+    _, (raw_t, u_t, b_t) = run(device, raw, u, b, 4.0, 2.0, 2, 0)
+    call = ppk.RenyiSampler(raw_t, u_t, b_t, 4.0, 2.0, 2, 0)
+    eager = call().clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        call(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            call(s)
+    for _ in range(3):
+        call.out.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(call.out, eager)
