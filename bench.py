@@ -35,6 +35,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--split", type=int, default=0, help="tokens per split (0 = library policy)")
     p.add_argument("--kv", choices=("int8", "bf16", "f32"), default="int8",
                    help="int8 (default, the headline workload) or the float-KV decode path over a bf16/f32 store")
+    p.add_argument("--sampler", action="store_true",
+                   help="time the CFG + Renyi sampler instead (batch = --batch, --choices, --guidance)")
+    p.add_argument("--choices", type=int, default=2048)
+    p.add_argument("--guidance", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=64, help="head rows timed for the CPU baseline sample")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -205,6 +209,78 @@ def bench_float(args) -> int:
     return 0
 
 
+def bench_sampler(args) -> int:
+    """The CFG + Renyi sampler (ppk_renyi_sample): one step = one call over `batch` logical rows of
+    guidance x choices fp32 logits, every row's whole head legal."""
+    import numpy as np
+    import torch
+    import ppk
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, G, C = args.batch, args.guidance, args.choices
+    cfg = 2.0 if G == 2 else 1.0
+    rng = np.random.default_rng(SEED)
+    raw_h = (rng.standard_normal((B * G, C)) * 3).astype(np.float32)
+    u_h = rng.uniform(0, 1, B).astype(np.float32)
+    bounds_h = np.tile(np.array([0, C], np.uint32), (B, 1))
+    raw = torch.from_numpy(raw_h).to(dev)
+    u = torch.from_numpy(u_h.reshape(B, 1)).to(dev)
+    bounds = torch.from_numpy(bounds_h.view(np.int32)).to(dev)
+    call = ppk.RenyiSampler(raw, u, bounds, 4.0, cfg, G, 0)
+    for _ in range(args.warmup):
+        call()
+    stream = torch.cuda.current_stream(dev)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(args.steps):
+        call()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t0.elapsed_time(t1) / args.steps
+    ppk.kernel_stats(ppk.PPK_KERNEL_RENYI_SAMPLE, reset=True)
+    ppk.set_profiling(True)
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_RENYI_SAMPLE, reset=True)
+    kernel_avg_ms = kernel_ms / max(launches, 1)
+    kernel_bytes = B * G * C * 4 + B * 4 + B * 8 + 3 * B * 4
+    achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
+    result = {
+        "metric": f"CFG + Renyi sampler µs/call, batch={B} guidance={G} choices={C}", "value": round(step_ms * 1e3, 2),
+        "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0, 9) logits, uniforms U[0,1), whole head legal; alpha 4)",
+        "config": {"workload": "CFG + Renyi sampler (ppk_renyi_sample, the reference's hip_sampling::sample)",
+                   "batch": B, "guidance": G, "choices": C, "alpha": 4.0, "cfg": cfg},
+        "roofline": {"bound": "latency (hbm bytes shown)", "kernel": "ppk_renyi_sample", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 5),
+                     "traffic": None, "algorithmic_bytes_per_launch": kernel_bytes,
+                     "avg_launch_us": round(kernel_avg_ms * 1e3, 2), "launches": launches},
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle  # noqa: E402  (CPU baseline leg only)
+
+        reps, t_start = 0, time.perf_counter()
+        while True:
+            oracle.renyi_sample(raw_h, u_h, bounds_h, 4.0, cfg, G, 0, cfg_fma=False)
+            reps += 1
+            el = time.perf_counter() - t_start
+            if el >= args.cpu_seconds or reps >= 100000:
+                break
+        result["cpu_baseline"] = {"value": round(el / reps * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
+                                  "sample": f"the whole batch ({B} rows), oracle_renyi_sample (the reference's host "
+                                            f"oracle restated in C), {reps} reps in {el:.1f} s"}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -212,6 +288,8 @@ def main() -> int:
                                    "sequence or head with no collective on the hot path (see DESIGN.md)",
                           "n_gpus": args.gpus}))
         return 2
+    if args.sampler:
+        return bench_sampler(args)
     if args.kv != "int8":
         return bench_float(args)
     import torch

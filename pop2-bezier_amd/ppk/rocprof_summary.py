@@ -41,11 +41,11 @@ def trace(args) -> None:
     disp = _rows(_one(args.dir, "kernel_trace.csv"))
     lines = [f"# rocprofv3 kernel trace: {args.title}", "", "Command (from the repository root):", "",
              f"    {args.command}", "", "Summarised with:", "", f"    {_self_command()}", "",
-             "## Per-kernel durations (ppk kernels, all dispatches)", "",
+             f"## Per-kernel durations (kernels matching `{args.kernel_regex}`, all dispatches)", "",
              "| kernel | calls | avg µs | min µs | max µs | total ms |", "|---|---|---|---|---|---|"]
     for r in sorted(stats, key=lambda r: -float(r.get("totaldurationns", 0))):
         name = r.get("name", "")
-        if not name.startswith("ppk_"):
+        if not re.search(args.kernel_regex, name):
             continue
         lines.append(f"| {name} | {r['calls']} | {float(r['averagens']) / 1e3:.2f} | {float(r['minns']) / 1e3:.2f} | "
                      f"{float(r['maxns']) / 1e3:.2f} | {float(r['totaldurationns']) / 1e6:.3f} |")
@@ -144,6 +144,7 @@ def main(argv=None) -> int:
     t.add_argument("--command", required=True)
     t.add_argument("--title", default="decode step")
     t.add_argument("--anchor", default="ppk_decode")
+    t.add_argument("--kernel-regex", default="^ppk_", help="kernels listed in the duration table")
     t.add_argument("--steps", type=int, default=100)
     f = sub.add_parser("traffic")
     f.add_argument("fetch_dir")
