@@ -37,6 +37,11 @@ def parse() -> argparse.Namespace:
                    help="int8 (default, the headline workload) or the float-KV decode path over a bf16/f32 store")
     p.add_argument("--sampler", action="store_true",
                    help="time the CFG + Renyi sampler instead (batch = --batch, --choices, --guidance)")
+    p.add_argument("--arena", action="store_true",
+                   help="time the KV arena manager: joining prefilled caches into batch arenas, then decode rounds "
+                        "of one-token appends over --layers layers with a shared write plan")
+    p.add_argument("--layers", type=int, default=24)
+    p.add_argument("--prefill", type=int, default=1000)
     p.add_argument("--choices", type=int, default=2048)
     p.add_argument("--guidance", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -281,6 +286,142 @@ def bench_sampler(args) -> int:
     return 0
 
 
+def bench_arena(args) -> int:
+    """KV arena manager (ppk_kv_query_batch): B sequences x `layers` int8 caches prefilled with `prefill`
+    tokens each (single-sequence arenas), one joining round that moves every layer's caches into a batch
+    arena (committed prefixes copied once), then `steps` decode rounds of one-token appends per layer with
+    one shared write plan per round."""
+    import numpy as np
+    import torch
+    import ppk
+    from ppk.kv_arena import LayerCache, WritePlan
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, Lyr, T0 = args.batch, args.heads, args.head_dim, args.layers, args.prefill
+    print(f"# bench: arena B={B} H={H} D={D} layers={Lyr} prefill={T0}", file=sys.stderr, flush=True)
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    prefill = torch.randn((H, T0, D), generator=g, device=dev, dtype=torch.bfloat16)
+    layers = []
+    for _ in range(Lyr):
+        caches = [LayerCache("int8", H, D, max_context=8192) for _ in range(B)]
+        for c in caches:
+            c.query(prefill, prefill, 0, True)
+        layers.append(caches)
+    torch.cuda.synchronize()
+    kv = torch.randn((B, H, 1, D), generator=g, device=dev, dtype=torch.bfloat16)
+
+    # Joining round: every layer's caches move into a new batch arena.
+    ppk.kernel_stats(ppk.PPK_KERNEL_COPY, reset=True)
+    ppk.set_profiling(True)
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    past = [T0] * B
+    plan = WritePlan(past, H, D)
+    for caches in layers:
+        LayerCache.query_batch(caches, kv, kv, past, True, plan)
+    e1.record()
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    copy_launches, copy_ms = ppk.kernel_stats(ppk.PPK_KERNEL_COPY, reset=True)
+    past = [p + 1 for p in past]
+    join_ms = e0.elapsed_time(e1)
+    join_host_ms = (time.perf_counter() - t0) * 1e3
+    # Copied bytes: committed K/V codes + scales of every row, read once and written once.
+    join_bytes = 2 * Lyr * B * H * T0 * (2 * D + 8)
+
+    # Steady decode rounds (warmup, then timed): per round one write plan and
+    # one ppk_kv_query_batch per layer, called through the C-ABI with argument
+    # blocks built once (the per-layer cost a native caller pays).
+    import ctypes
+    from ppk import _abi
+
+    lib = _abi.lib()
+    ctx = ppk.context(dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    handles = [(ctypes.c_void_p * B)(*[c.handle.value for c in caches]) for caches in layers]
+    write = _abi.PpkKvWrite(struct_size=ctypes.sizeof(_abi.PpkKvWrite), src_dtype=_abi.PPK_BF16, tokens=1,
+                            commit=1, k=kv.data_ptr(), v=kv.data_ptr())
+    view = _abi.PpkKvView(struct_size=ctypes.sizeof(_abi.PpkKvView))
+    fn = lib.ppk_kv_query_batch
+
+    def round_():
+        nonlocal past
+        lens = (ctypes.c_uint32 * B)(*past)
+        plan = ctypes.c_void_p()
+        _abi.check(lib.ppk_write_plan_create(ctx, stream, lens, B, H, D, ctypes.byref(plan)), "plan")
+        for h in handles:
+            st = fn(ctx, stream, h, B, lens, ctypes.byref(write), plan, ctypes.byref(view))
+            if st:
+                _abi.check(st, "ppk_kv_query_batch")
+        lib.ppk_write_plan_release(plan)
+        past = [p + 1 for p in past]
+
+    for _ in range(args.warmup):
+        round_()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        round_()
+    e1.record()
+    torch.cuda.synchronize()
+    round_ms = e0.elapsed_time(e1) / args.steps
+    host_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ppk.kernel_stats(ppk.PPK_KERNEL_APPEND, reset=True)
+    ppk.set_profiling(True)
+    round_()
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_APPEND, reset=True)
+    append_us = kernel_ms / max(launches, 1) * 1e3
+    arena_ids = {c.info().arena_id for caches in layers for c in caches}
+    append_bytes = 2 * B * H * D * 2 + 2 * B * H * (D + 4)
+    result = {
+        "metric": f"KV arena decode round µs (append of one token per sequence into {Lyr} layers' batch arenas)",
+        "value": round(round_ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(round_ms, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded bf16 prefill and tokens on the device)",
+        "config": {"workload": "KV arena manager (ppk_kv_query_batch with a shared ppk_write_plan per round)",
+                   "batch": B, "heads": H, "head_dim": D, "layers": Lyr, "prefill": T0,
+                   "arenas_after_join": len(arena_ids)},
+        "host_us_per_round": round(host_ms * 1e3, 1),
+        "append_kernel_us": round(append_us, 2),
+        "join": {"ms": round(join_ms, 3), "host_ms": round(join_host_ms, 2), "copied_bytes": join_bytes,
+                 "copy_launches": copy_launches, "copy_kernel_ms": round(copy_ms, 3)},
+        "roofline": {"bound": "hbm", "kernel": "ppk_copy2d_batch (prefix copies at join)",
+                     "achieved": round(join_bytes / (copy_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(join_bytes / (copy_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "append_bytes_per_layer": append_bytes},
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle  # noqa: E402  (CPU baseline leg only)
+
+        cap = 2048
+        codes = np.zeros((B * H, cap, D), np.uint8)
+        scales = np.zeros((B * H, cap), np.float32)
+        src = kv.float().cpu().numpy()
+        past_h = np.full(B, T0, np.uint32)
+        reps, t_start = 0, time.perf_counter()
+        while True:
+            for _ in range(2 * Lyr):  # K and V of every layer
+                oracle.append(src, past_h, codes, scales)
+            reps += 1
+            el = time.perf_counter() - t_start
+            if el >= args.cpu_seconds or reps >= 10000:
+                break
+        result["cpu_baseline"] = {"value": round(el / reps * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
+                                  "sample": f"one decode round: {2 * Lyr} quantize-appends of [B={B}, H={H}, 1, "
+                                            f"D={D}] (oracle_append), {reps} reps in {el:.1f} s"}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -290,6 +431,8 @@ def main() -> int:
         return 2
     if args.sampler:
         return bench_sampler(args)
+    if args.arena:
+        return bench_arena(args)
     if args.kv != "int8":
         return bench_float(args)
     import torch

@@ -281,6 +281,122 @@ typedef struct PpkRenyiSampleArgs {
 } PpkRenyiSampleArgs;
 PPK_API int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiSampleArgs* args);
 
+/* ---------------------------------------------------------------------------
+   KV arenas: per-(sequence, layer) caches over shared device arenas, with
+   copy-on-write snapshots, slot reuse and one write plan shared by every
+   layer of a decode round. Replaces LayerCache (app/src/model/cache.rs:40-531),
+   Int8LayerCache's commit path (app/src/model/int8_cache.rs:292-359) and
+   BatchWritePlan (app/src/model/write_plan.rs:12-102).
+
+   A cache is one sequence's K/V history for one layer: heads rows of
+   capacity token slots, each slot head_dim values (int8 codes + one f32 scale
+   per slot for PPK_KV_INT8, raw bf16/f16/f32 otherwise). Rules kept from the
+   reference:
+   * capacity starts at min_capacity (64) and doubles up to max_context (1024 in
+     the reference, MAX_CONTEXT, app/src/model/mod.rs:55);
+   * ppk_kv_cache_clone is a snapshot sharing storage; a write through a cache
+     whose storage is shared (or too small) first copies the committed prefix
+     (never uncommitted scratch) into storage of its own;
+   * commit = 0 writes scratch at slot `past` without advancing the length;
+     truncation is metadata only;
+   * ppk_kv_query_batch writes one token per sequence into one batch arena
+     [batch * heads, capacity, head_dim], reusing the arena the caches already
+     share when every row is provably theirs alone (no live snapshot of a
+     replaced slot, same row order, same capacity), otherwise moving every row
+     into a fresh arena (committed prefixes copied once);
+   * every shape, length and plan check completes before any device write.
+   The context must outlive its caches and plans. Calls that touch caches
+   sharing an arena must be serialised by the caller, on one stream; storage
+   is released stream-ordered on the stream that last wrote it. */
+enum { PPK_KV_INT8 = 0, PPK_KV_BF16 = 1, PPK_KV_F16 = 2, PPK_KV_F32 = 3 };
+
+typedef struct ppk_kv_cache ppk_kv_cache;
+typedef struct ppk_write_plan ppk_write_plan;
+
+typedef struct PpkKvConfig {
+  uint32_t struct_size;
+  uint32_t kind;          /* PPK_KV_* */
+  uint32_t heads;
+  uint32_t head_dim;      /* 64/128/256 for PPK_KV_INT8; any >= 1 for float kinds */
+  uint32_t max_context;   /* 0 = 1024 (the reference's MAX_CONTEXT) */
+  uint32_t min_capacity;  /* 0 = 64 (the reference's MIN_CAPACITY) */
+} PpkKvConfig;
+
+/* Device view of cache storage. For a single cache: rows = heads, the
+   cache's own row block; for a batch: rows = batch * heads, the whole arena,
+   with past[b] (the slot just written) and lengths[b] = past[b] + 1 as device
+   U32[batch] vectors ready for ppk_decode_attention (past) and
+   ppk_float_decode_attention (lengths). Pointers stay valid until the next
+   write through any cache of the arena or the arena's release. */
+typedef struct PpkKvView {
+  uint32_t struct_size;
+  uint32_t kind;
+  uint32_t rows;
+  uint32_t capacity;      /* slots per row: the row stride is capacity * head_dim elements */
+  uint32_t head_dim;
+  uint32_t length;        /* slots holding data: end of the write (single) or max(past) + 1 (batch); committed length (ppk_kv_cache_view) */
+  uint32_t batch;         /* 0 for a single-cache view */
+  uint32_t reserved;
+  void* k;                /* [rows, capacity, head_dim]: codes (u8) or floats */
+  void* v;
+  float* k_scales;        /* [rows, capacity] (PPK_KV_INT8), else NULL */
+  float* v_scales;
+  const uint32_t* past;   /* batch views: device U32[batch] */
+  const uint32_t* lengths;/* batch views: device U32[batch] */
+} PpkKvView;
+
+typedef struct PpkKvInfo {
+  uint32_t struct_size;
+  uint32_t length;        /* committed tokens */
+  uint32_t capacity;      /* 0 when no storage */
+  uint32_t grouped;       /* 1 when the storage is a row of a batch arena */
+  uint32_t slot;          /* row (sequence) index in its arena */
+  uint32_t shared;        /* 1 when another cache (a snapshot) shares the storage */
+  uint64_t reserved_bytes;/* device bytes of this cache's rows (reserve included) */
+  uint64_t storage_id;    /* identity of the storage owner (changes on copy-on-write) */
+  uint64_t arena_id;      /* identity of the arena */
+  uint64_t arena_copied_rows;   /* sequences whose committed history was copied into this arena */
+  uint64_t arena_offset_uploads;/* device offset vectors uploaded by this arena (writes without a plan) */
+} PpkKvInfo;
+
+/* Source of a write: K and V [heads, tokens, head_dim] (single) or
+   [batch, heads, 1, head_dim] (batch), dense, in src_dtype. INT8 caches
+   quantise the source (any of f32/bf16/f16) as ppk_quantize does; float
+   caches take the storage dtype only, as the reference's query does. */
+typedef struct PpkKvWrite {
+  uint32_t struct_size;
+  uint32_t src_dtype;     /* PPK_F32 / PPK_BF16 / PPK_F16 */
+  uint32_t tokens;        /* single writes; 1 for batch writes */
+  uint32_t commit;        /* 0 = scratch write at slot past, length unchanged */
+  const void* k;
+  const void* v;
+} PpkKvWrite;
+
+PPK_API int32_t ppk_kv_cache_create(ppk_context* ctx, const PpkKvConfig* config, ppk_kv_cache** out);
+PPK_API int32_t ppk_kv_cache_clone(const ppk_kv_cache* cache, ppk_kv_cache** out);
+PPK_API int32_t ppk_kv_cache_release(ppk_kv_cache* cache);
+PPK_API int32_t ppk_kv_cache_info(const ppk_kv_cache* cache, PpkKvInfo* out);
+/* LayerCache::truncate_committed: new_len <= length; storage untouched. */
+PPK_API int32_t ppk_kv_cache_truncate(ppk_kv_cache* cache, uint32_t new_len);
+/* The cache's own rows, length = committed tokens (LayerCache::key / value / arena). */
+PPK_API int32_t ppk_kv_cache_view(const ppk_kv_cache* cache, PpkKvView* out);
+/* LayerCache::query / Int8LayerCache::query: write tokens at slot past
+   (past must equal the committed length), growing or detaching first. */
+PPK_API int32_t ppk_kv_query(ppk_context* ctx, void* stream, ppk_kv_cache* cache, uint32_t past,
+                             const PpkKvWrite* write, PpkKvView* out);
+/* BatchWritePlan::new: the write offsets of one decode round as a device
+   vector (uploaded on stream), shared by every layer's ppk_kv_query_batch. */
+PPK_API int32_t ppk_write_plan_create(ppk_context* ctx, void* stream, const uint32_t* past_lens, uint32_t batch,
+                                      uint32_t heads, uint32_t head_dim, ppk_write_plan** out);
+PPK_API int32_t ppk_write_plan_release(ppk_write_plan* plan);
+/* LayerCache::query_batch_with_plan / Int8LayerCache::query_batch: one token
+   per sequence at slot past_lens[b] (= each cache's committed length). A plan
+   (optional) must match past_lens, heads and head_dim (checked on the host,
+   no device read). */
+PPK_API int32_t ppk_kv_query_batch(ppk_context* ctx, void* stream, ppk_kv_cache* const* caches, uint32_t batch,
+                                   const uint32_t* past_lens, const PpkKvWrite* write, const ppk_write_plan* plan,
+                                   PpkKvView* out);
+
 /* Known-answer self-check on the context's device, the three checks of
    int8_kv_ops::prepare (int8_kv_ops.rs:56-103) plus their fp32-history twins.
    Returns 2 with the failing check in ppk_last_error() on a numeric mismatch. */
@@ -288,12 +404,15 @@ PPK_API int32_t ppk_prepare(ppk_context* ctx);
 
 /* Tracing: when enabled, the library brackets every launch of the named kernel
    with HIP events on the launch stream; stats resolve them (blocking on the
-   recorded events only). Kernel ids below. The reference keeps launch counters
-   only (app/src/model/hip_kernel.rs:8-21). */
+   recorded events only) and report the number of traced launches and their
+   total time. Kernel ids below. The reference keeps launch counters only
+   (app/src/model/hip_kernel.rs:8-21). */
 enum { PPK_KERNEL_QUANTIZE = 0, PPK_KERNEL_APPEND = 1, PPK_KERNEL_DEQUANTIZE = 2,
        PPK_KERNEL_ATTENTION = 3, /* the decode kernel, with or without the fused append */
        PPK_KERNEL_ATTN_MERGE = 4, PPK_KERNEL_FLOAT_ATTENTION = 5, PPK_KERNEL_FLOAT_MERGE = 6,
-       PPK_KERNEL_RENYI_SAMPLE = 7, PPK_KERNEL_COUNT = 8 };
+       PPK_KERNEL_RENYI_SAMPLE = 7,
+       PPK_KERNEL_COPY = 8, /* arena prefix copies (joins, growth, copy-on-write) */
+       PPK_KERNEL_COUNT = 9 };
 PPK_API int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable);
 PPK_API int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint64_t* launches,
                                  double* total_ms, uint32_t reset);

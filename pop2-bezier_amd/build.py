@@ -55,7 +55,7 @@ def build(verbose: bool = True) -> dict:
             CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
             f"-I{os.path.join(ROOT, 'include')}", f"-I{ROCM}/include",
             os.path.join(CSRC, "ppk_abi.cpp"), os.path.join(CSRC, "int8_kv_ops.cpp"),
-            os.path.join(CSRC, "fused_attention.cpp"),
+            os.path.join(CSRC, "fused_attention.cpp"), os.path.join(CSRC, "kv_arena.cpp"),
             "-o", tmp_lib, f"-L{ROCM}/lib", f"-Wl,-rpath,{ROCM}/lib", "-lamdhip64", "-ldl",
         ],
         verbose,

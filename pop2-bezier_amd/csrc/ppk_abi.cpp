@@ -55,6 +55,8 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_fdecode_f32_d64", "ppk_fdecode_f32_d128", "ppk_fdecode_f32_d256",
     "ppk_fmerge_d64", "ppk_fmerge_d128", "ppk_fmerge_d256",
     "ppk_renyi_sample",
+    "ppk_kv_scatter_u16", "ppk_kv_scatter_u4", "ppk_kv_scatter_u2",
+    "ppk_copy2d_batch",
 };
 
 std::string default_code_object() {
@@ -86,7 +88,7 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 template <class Args>
 void launch(ppk_context* ctx, int prof_kernel, ppk::Fn fn, uint32_t grid, uint32_t block, uint32_t lds,
-            hipStream_t stream, Args& args) {
+            hipStream_t stream, Args& args, uint32_t grid_y = 1) {
   void* params[] = {&args};
   ppk::EventPair ev;
   bool traced = false;
@@ -104,16 +106,13 @@ void launch(ppk_context* ctx, int prof_kernel, ppk::Fn fn, uint32_t grid, uint32
   if (traced && hipEventRecord(ev.start, stream) != hipSuccess)
     throw ppk::UncertainError(std::string("event record before ") + kFnNames[fn]);
   const hipError_t st =
-      hipModuleLaunchKernel(ctx->fn[fn], grid, 1, 1, block, 1, 1, lds, stream, params, nullptr);
+      hipModuleLaunchKernel(ctx->fn[fn], grid, grid_y, 1, block, 1, 1, lds, stream, params, nullptr);
   if (st != hipSuccess) throw ppk::UncertainError(std::string(kFnNames[fn]) + ": " + hipGetErrorString(st));
   if (traced) {
     if (hipEventRecord(ev.stop, stream) != hipSuccess)
       throw ppk::UncertainError(std::string("event record after ") + kFnNames[fn]);
     std::lock_guard<std::mutex> lock(ctx->prof_mutex);
     ctx->pending[prof_kernel].push_back(ev);
-  } else {
-    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
-    ctx->launches[prof_kernel] += 1;
   }
 }
 
@@ -480,6 +479,93 @@ void run_renyi_sample(ppk_context* ctx, hipStream_t stream, const PpkRenyiSample
   launch(ctx, PPK_KERNEL_RENYI_SAMPLE, kRenyiSample, a.batch, kSamplerThreads, 0, stream, k);
 }
 
+void run_arena_write(ppk_context* ctx, hipStream_t stream, const ArenaWrite& w) {
+  const uint64_t rows = w.sequences * w.heads;
+  DeviceGuard guard(ctx->device);
+  if (w.elem_bytes == 0) {
+    QuantizeArgs k{};
+    k.src[0] = w.k_src;
+    k.src[1] = w.v_src;
+    k.codes[0] = w.k;
+    k.codes[1] = w.v;
+    k.scales[0] = w.ks;
+    k.scales[1] = w.vs;
+    k.past = w.past;
+    k.rows = rows * w.tokens;
+    k.heads = w.heads;
+    k.tokens = w.tokens;
+    k.capacity = w.capacity;
+    k.src_dtype = w.src_dtype;
+    k.ntensors = 2;
+    k.uniform_past = w.uniform_past;
+    const uint64_t grid = (2 * k.rows + 3) / 4;
+    require(grid <= 0x7fffffffu, "KV append grid too large");
+    launch(ctx, PPK_KERNEL_APPEND, Fn(kQuantize64 + dim_index(w.head_dim)), uint32_t(grid), 256, 0, stream, k);
+    return;
+  }
+  const uint64_t record = uint64_t(w.head_dim) * w.elem_bytes;
+  auto fits = [&](uint64_t unit) {
+    return record % unit == 0 && aligned(w.k_src, unit) && aligned(w.v_src, unit) && aligned(w.k, unit) &&
+           aligned(w.v, unit);
+  };
+  const uint32_t unit = fits(16) ? 16 : fits(4) ? 4 : 2;
+  require(record % unit == 0 && aligned(w.k_src, unit) && aligned(w.v_src, unit), "KV append source misaligned");
+  ScatterArgs a{};
+  a.src[0] = static_cast<const uint8_t*>(w.k_src);
+  a.src[1] = static_cast<const uint8_t*>(w.v_src);
+  a.dst[0] = w.k;
+  a.dst[1] = w.v;
+  a.past = w.past;
+  a.rows = rows;
+  a.heads = w.heads;
+  a.tokens = w.tokens;
+  a.capacity = w.capacity;
+  a.uniform_past = w.uniform_past;
+  a.row_units = uint32_t(record / unit);
+  const uint64_t units = 2 * rows * w.tokens * a.row_units;
+  const uint64_t grid = std::min<uint64_t>((units + 255) / 256, uint64_t(std::max(ctx->cu_count, 1)) * 16);
+  launch(ctx, PPK_KERNEL_APPEND, unit == 16 ? kScatter16 : unit == 4 ? kScatter4 : kScatter2, uint32_t(grid), 256, 0,
+         stream, a);
+}
+
+void run_copy_batch(ppk_context* ctx, hipStream_t stream, const std::vector<CopyDesc>& in) {
+  if (in.empty()) return;
+  // Like-sized rectangles share a launch, so one grid shape fits them all.
+  std::vector<CopyDesc> copies(in);
+  std::stable_sort(copies.begin(), copies.end(), [](const CopyDesc& x, const CopyDesc& y) {
+    return uint64_t(x.height) * x.fill > uint64_t(y.height) * y.fill;
+  });
+  DeviceGuard guard(ctx->device);
+  for (size_t first = 0; first < copies.size(); first += kMaxCopies) {
+    const size_t n = std::min<size_t>(kMaxCopies, copies.size() - first);
+    CopyBatchArgs a{};
+    a.n = uint32_t(n);
+    uint64_t most = 0;
+    for (size_t i = 0; i < n; ++i) {
+      const CopyDesc& c = copies[first + i];
+      require(c.width <= c.fill && c.fill <= c.dpitch && c.fill <= 0xffffffffu && (c.width == 0 || c.width <= c.spitch),
+              "arena copy rectangle out of its rows");
+      uint32_t unit = 16;
+      while (unit > 1 && (c.width % unit || c.fill % unit || c.spitch % unit || c.dpitch % unit ||
+                          !aligned(c.src, unit) || !aligned(c.dst, unit)))
+        unit >>= unit == 16 ? 2 : 1;
+      a.c[i].src = static_cast<const uint8_t*>(c.src);
+      a.c[i].dst = static_cast<uint8_t*>(c.dst);
+      a.c[i].spitch = c.spitch;
+      a.c[i].dpitch = c.dpitch;
+      a.c[i].width = uint32_t(c.width);
+      a.c[i].fill = uint32_t(c.fill);
+      a.c[i].height = c.height;
+      a.c[i].unit = unit;
+      most = std::max<uint64_t>(most, uint64_t(c.height) * (c.fill / unit));
+    }
+    // About sixteen resident blocks per CU over the whole launch, eight units per thread per pass.
+    const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
+    const uint64_t gx = std::max<uint64_t>(1, std::min<uint64_t>((most + 2047) / 2048, (cus * 16 + n - 1) / n));
+    launch(ctx, PPK_KERNEL_COPY, kCopyBatch, uint32_t(gx), 256, 0, stream, a, uint32_t(n));
+  }
+}
+
 }  // namespace ppk
 
 extern "C" {
@@ -613,6 +699,77 @@ int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiSampleArg
   return call([&] {
     ppk::require(ctx && args, "ppk_renyi_sample: null context or arguments");
     ppk::run_renyi_sample(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_kv_cache_create(ppk_context* ctx, const PpkKvConfig* config, ppk_kv_cache** out) {
+  if (out) *out = nullptr;
+  return call([&] {
+    ppk::require(ctx && config && out, "ppk_kv_cache_create: null argument");
+    *out = ppk::kv::create(ctx, *config);
+  });
+}
+
+int32_t ppk_kv_cache_clone(const ppk_kv_cache* cache, ppk_kv_cache** out) {
+  if (out) *out = nullptr;
+  return call([&] {
+    ppk::require(cache && out, "ppk_kv_cache_clone: null argument");
+    *out = ppk::kv::clone(*cache);
+  });
+}
+
+int32_t ppk_kv_cache_release(ppk_kv_cache* cache) {
+  return call([&] { ppk::kv::release(cache); });
+}
+
+int32_t ppk_kv_cache_info(const ppk_kv_cache* cache, PpkKvInfo* out) {
+  return call([&] {
+    ppk::require(cache != nullptr, "ppk_kv_cache_info: null cache");
+    ppk::kv::info(*cache, out);
+  });
+}
+
+int32_t ppk_kv_cache_truncate(ppk_kv_cache* cache, uint32_t new_len) {
+  return call([&] {
+    ppk::require(cache != nullptr, "ppk_kv_cache_truncate: null cache");
+    ppk::kv::truncate(*cache, new_len);
+  });
+}
+
+int32_t ppk_kv_cache_view(const ppk_kv_cache* cache, PpkKvView* out) {
+  return call([&] {
+    ppk::require(cache != nullptr, "ppk_kv_cache_view: null cache");
+    ppk::kv::view(*cache, out);
+  });
+}
+
+int32_t ppk_kv_query(ppk_context* ctx, void* stream, ppk_kv_cache* cache, uint32_t past, const PpkKvWrite* write,
+                     PpkKvView* out) {
+  return call([&] {
+    ppk::require(ctx && cache && write, "ppk_kv_query: null argument");
+    ppk::kv::query(ctx, static_cast<hipStream_t>(stream), *cache, past, *write, out);
+  });
+}
+
+int32_t ppk_write_plan_create(ppk_context* ctx, void* stream, const uint32_t* past_lens, uint32_t batch,
+                              uint32_t heads, uint32_t head_dim, ppk_write_plan** out) {
+  if (out) *out = nullptr;
+  return call([&] {
+    ppk::require(out != nullptr, "ppk_write_plan_create: null output");
+    *out = ppk::kv::plan_create(ctx, static_cast<hipStream_t>(stream), past_lens, batch, heads, head_dim);
+  });
+}
+
+int32_t ppk_write_plan_release(ppk_write_plan* plan) {
+  return call([&] { ppk::kv::plan_release(plan); });
+}
+
+int32_t ppk_kv_query_batch(ppk_context* ctx, void* stream, ppk_kv_cache* const* caches, uint32_t batch,
+                           const uint32_t* past_lens, const PpkKvWrite* write, const ppk_write_plan* plan,
+                           PpkKvView* out) {
+  return call([&] {
+    ppk::require(ctx && write, "ppk_kv_query_batch: null argument");
+    ppk::kv::query_batch(ctx, static_cast<hipStream_t>(stream), caches, batch, past_lens, *write, plan, out);
   });
 }
 

@@ -41,6 +41,8 @@ enum Fn : int {
   kFDecodeF32_64, kFDecodeF32_128, kFDecodeF32_256,
   kFMerge64, kFMerge128, kFMerge256,
   kRenyiSample,
+  kScatter16, kScatter4, kScatter2,
+  kCopyBatch,
   kFnCount
 };
 
@@ -105,6 +107,54 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
                    const PpkDecodeStepArgs* step = nullptr);
 void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a);
 void run_renyi_sample(ppk_context* ctx, hipStream_t stream, const PpkRenyiSampleArgs& a);
+
+// Arena writes for the KV cache manager (kv_arena.cpp). Rows of `heads`
+// per sequence; token t of sequence b lands at slot (past ? past[b] :
+// uniform_past) + t of [rows, capacity, head_dim] storage. The caller has
+// validated every shape; these only build the kernel arguments and launch.
+struct ArenaWrite {
+  const void* k_src = nullptr;
+  const void* v_src = nullptr;
+  uint32_t src_dtype = 0;     // PPK_F32 / PPK_BF16 / PPK_F16
+  uint8_t* k = nullptr;       // codes (int8) or float records
+  uint8_t* v = nullptr;
+  float* ks = nullptr;        // int8 only
+  float* vs = nullptr;
+  const uint32_t* past = nullptr;
+  uint32_t uniform_past = 0;
+  uint64_t sequences = 0;
+  uint32_t heads = 0, tokens = 0, capacity = 0, head_dim = 0;
+  uint32_t elem_bytes = 0;    // 0 = int8 (quantise); else bytes per float element
+};
+void run_arena_write(ppk_context* ctx, hipStream_t stream, const ArenaWrite& w);
+
+// Batched strided copies (one launch per up to kMaxCopies rectangles): each of
+// `height` dst rows (dpitch apart) gets `width` bytes of its src row (spitch
+// apart; src may be null when width is 0), then zeros up to `fill` bytes.
+struct CopyDesc {
+  const void* src = nullptr;
+  void* dst = nullptr;
+  uint64_t spitch = 0, dpitch = 0, width = 0, fill = 0;
+  uint32_t height = 0;
+};
+void run_copy_batch(ppk_context* ctx, hipStream_t stream, const std::vector<CopyDesc>& copies);
+
+// KV cache manager (kv_arena.cpp).
+namespace kv {
+ppk_kv_cache* create(ppk_context* ctx, const PpkKvConfig& cfg);
+void info(const ppk_kv_cache& c, PpkKvInfo* out);
+void view(const ppk_kv_cache& c, PpkKvView* out);
+void truncate(ppk_kv_cache& c, uint32_t new_len);
+void query(ppk_context* ctx, hipStream_t stream, ppk_kv_cache& c, uint32_t past, const PpkKvWrite& w,
+           PpkKvView* out);
+ppk_write_plan* plan_create(ppk_context* ctx, hipStream_t stream, const uint32_t* past_lens, uint32_t batch,
+                            uint32_t heads, uint32_t head_dim);
+void query_batch(ppk_context* ctx, hipStream_t stream, ppk_kv_cache* const* caches, uint32_t batch,
+                 const uint32_t* past_lens, const PpkKvWrite& w, const ppk_write_plan* plan, PpkKvView* out);
+ppk_kv_cache* clone(const ppk_kv_cache& c);
+void release(ppk_kv_cache* c);
+void plan_release(ppk_write_plan* p);
+}  // namespace kv
 
 // int8_kv_ops::prepare known-answer checks (int8_kv_ops.cpp).
 void prepare_self_check(ppk_context* ctx);

@@ -17,14 +17,27 @@ struct QuantizeArgs {
   const void* src[2];       // K and V sources ([rows_per_tensor, D]); src[1] unused if ntensors == 1
   uint8_t* codes[2];        // dense [rows, D] or arena [bh, capacity, D]
   float* scales[2];         // dense [rows] or arena [bh, capacity]
-  const uint32_t* past;     // nullptr = dense mode
+  const uint32_t* past;     // append mode: slot of token 0 of sequence b = past[b]
   uint32_t* flags;          // optional
   uint64_t rows;            // (bh * tokens) rows per tensor
   uint32_t heads;           // append mode: sequence b = bh / heads
   uint32_t tokens;          // append mode: tokens per bh row
-  uint32_t capacity;        // append mode
+  uint32_t capacity;        // 0 = dense mode; > 0 = append mode
   uint32_t src_dtype;       // PPK_F32 / PPK_BF16 / PPK_F16
   uint32_t ntensors;        // 1 or 2
+  uint32_t uniform_past;    // append mode with past == nullptr: slot of token 0 for every row
+};
+
+// Float-store append: copy [rows, tokens, row_bytes] token records of K and V
+// into [rows, capacity, row_bytes] arenas at slot past[row / heads] + t (or
+// uniform_past + t when past is null), in units of the kernel's UNIT bytes.
+struct ScatterArgs {
+  const uint8_t* src[2];
+  uint8_t* dst[2];
+  const uint32_t* past;
+  uint64_t rows;
+  uint32_t heads, tokens, capacity, uniform_past;
+  uint32_t row_units;       // units per token record
   uint32_t pad;
 };
 
@@ -107,6 +120,23 @@ struct FloatMergeArgs {
   const float* part_mz;
   void* out;                // [rows, D]
   uint32_t rows, heads, size, split_tokens, nsplits, out_dtype;
+};
+
+// Batched rectangle copies: block (x, y) serves rectangle y. Each of its
+// `height` destination rows receives `width` bytes copied from the source row
+// followed by zeros up to `fill` bytes (src may be null when width is 0).
+// `unit` bytes (16, 4, 2 or 1) per thread and step, chosen on the host so
+// that width, fill, both pitches and both base addresses are multiples of it.
+struct Copy2D {
+  const uint8_t* src;
+  uint8_t* dst;
+  uint64_t spitch, dpitch;
+  uint32_t width, fill, height, unit;
+};
+constexpr int kMaxCopies = 32;
+struct CopyBatchArgs {
+  uint32_t n, pad;
+  Copy2D c[kMaxCopies];
 };
 
 // CFG + Renyi effective-support sampler: one 256-thread block per logical row.

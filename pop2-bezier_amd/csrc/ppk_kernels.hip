@@ -9,6 +9,8 @@
 //   ppk_fdecode_{bf16,f32}_d{..}       decode attention over float (bf16/f32) K/V
 //   ppk_fmerge_d{..}                   cross-group merge of the float path
 //   ppk_renyi_sample                   CFG + Renyi effective-support sampler
+//   ppk_kv_scatter_u{16,4,2}           float-store append of token records into arena slots
+//   ppk_copy2d_batch                   batched rectangle copies + zero fill (arena joins, growth, copy-on-write)
 //
 // Semantics follow app/src/model/int8_kv_ops.rs:11-40 and
 // app/src/model/int8_kv.cu:8-59; the design (wave-per-row quantize, one-wave
@@ -169,10 +171,10 @@ __device__ __forceinline__ void quantize_body(const ppk::QuantizeArgs& a) {
   const uint64_t r = wave - (tensor ? a.rows : 0);
   const void* src = tensor ? a.src[1] : a.src[0];
   size_t dst = r;
-  if (a.past) {
+  if (a.capacity) {
     const uint64_t bh = r / a.tokens;
     const uint32_t tok = uint32_t(r - bh * a.tokens);
-    const uint64_t slot = uint64_t(a.past[bh / a.heads]) + tok;
+    const uint64_t slot = uint64_t(a.past ? a.past[bh / a.heads] : a.uniform_past) + tok;
     if (slot >= a.capacity) {
       if (lane == 0 && a.flags) atomicOr(a.flags, 2u);
       return;
@@ -1127,6 +1129,91 @@ __device__ __forceinline__ void renyi_sample_body(const ppk::RenyiArgs& a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Float-store append (the in-place slice_set / scatter_set of
+// app/src/model/cache.rs:271-276,437-469): token records of K and V to their
+// arena slots, UNIT bytes per thread and step, grid-stride. Slots at or past
+// capacity are skipped (the host never plans them).
+// ---------------------------------------------------------------------------
+template <int UNIT>
+struct UnitType;
+template <>
+struct UnitType<16> {
+  using T = u4;
+};
+template <>
+struct UnitType<4> {
+  using T = uint32_t;
+};
+template <>
+struct UnitType<2> {
+  using T = uint16_t;
+};
+
+template <int UNIT>
+__device__ __forceinline__ void scatter_body(const ppk::ScatterArgs& a) {
+  using T = typename UnitType<UNIT>::T;
+  const uint64_t per_tensor = a.rows * a.tokens * a.row_units;
+  const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+  for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < 2 * per_tensor; i += stride) {
+    const uint32_t tensor = i >= per_tensor ? 1u : 0u;
+    const uint64_t j = i - (tensor ? per_tensor : 0);
+    const uint64_t rt = j / a.row_units;
+    const uint32_t u = uint32_t(j - rt * a.row_units);
+    const uint64_t r = rt / a.tokens;
+    const uint32_t t = uint32_t(rt - r * a.tokens);
+    const uint64_t slot = uint64_t(a.past ? a.past[r / a.heads] : a.uniform_past) + t;
+    if (slot >= a.capacity) continue;
+    const T* src = reinterpret_cast<const T*>(a.src[tensor]);
+    T* dst = reinterpret_cast<T*>(a.dst[tensor]);
+    dst[(r * a.capacity + slot) * a.row_units + u] = src[rt * a.row_units + u];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Batched rectangle copy with zero fill (arena joins, growth and
+// copy-on-write: every row of a new arena receives its committed prefix and
+// zeros up to its capacity in one launch, instead of a memset of the whole
+// arena plus one runtime copy per plane and sequence). Grid-stride over the
+// rectangle's units, eight in flight per thread.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void copy_rect(const ppk::Copy2D& c, uint32_t unit_bytes) {
+  constexpr int ILP = 8;
+  const uint32_t per_row = c.fill / unit_bytes;
+  const uint32_t copy_cols = c.width / unit_bytes;
+  const uint64_t total = uint64_t(c.height) * per_row;
+  const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+  for (uint64_t base = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; base < total; base += ILP * stride) {
+    T val[ILP];
+    uint64_t row[ILP];
+    uint32_t col[ILP];
+#pragma unroll
+    for (int k = 0; k < ILP; ++k) {
+      const uint64_t i = base + k * stride;
+      row[k] = i / per_row;
+      col[k] = uint32_t(i - row[k] * per_row);
+      val[k] = T{};
+      if (i < total && col[k] < copy_cols)
+        val[k] = __builtin_nontemporal_load(reinterpret_cast<const T*>(c.src + row[k] * c.spitch) + col[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < ILP; ++k)
+      if (base + k * stride < total) reinterpret_cast<T*>(c.dst + row[k] * c.dpitch)[col[k]] = val[k];
+  }
+}
+
+__device__ __forceinline__ void copy_batch_body(const ppk::CopyBatchArgs& a) {
+  if (blockIdx.y >= a.n) return;
+  const ppk::Copy2D& c = a.c[blockIdx.y];
+  switch (c.unit) {  // uniform per block
+    case 16: copy_rect<u4>(c, 16); break;
+    case 4: copy_rect<uint32_t>(c, 4); break;
+    case 2: copy_rect<uint16_t>(c, 2); break;
+    default: copy_rect<uint8_t>(c, 1); break;
+  }
+}
+
 }  // namespace
 
 #define PPK_QUANTIZE(D)                                                                \
@@ -1168,3 +1255,8 @@ PPK_FLOAT_ATTN(128)
 PPK_FLOAT_ATTN(256)
 
 extern "C" __global__ __launch_bounds__(256) void ppk_renyi_sample(ppk::RenyiArgs a) { renyi_sample_body(a); }
+
+extern "C" __global__ __launch_bounds__(256) void ppk_kv_scatter_u16(ppk::ScatterArgs a) { scatter_body<16>(a); }
+extern "C" __global__ __launch_bounds__(256) void ppk_kv_scatter_u4(ppk::ScatterArgs a) { scatter_body<4>(a); }
+extern "C" __global__ __launch_bounds__(256) void ppk_kv_scatter_u2(ppk::ScatterArgs a) { scatter_body<2>(a); }
+extern "C" __global__ __launch_bounds__(256) void ppk_copy2d_batch(ppk::CopyBatchArgs a) { copy_batch_body(a); }

@@ -4,24 +4,25 @@
 The product path is libppk.so (C-ABI, include/ppk_int8_kv.h) plus the gfx950
 code object ppk_kernels.hsaco; this package binds them for torch callers.
 """
-from . import fused_attention, sampling
+from . import fused_attention, kv_arena, sampling
 from ._abi import (PPK_ABI_VERSION, PPK_ATTN_BF16_HISTORY, PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW,
-                   PPK_KERNEL_APPEND, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_ATTENTION, PPK_KERNEL_DEQUANTIZE,
-                   PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_QUANTIZE,
+                   PPK_KERNEL_APPEND, PPK_KERNEL_ATTN_MERGE, PPK_KERNEL_ATTENTION, PPK_KERNEL_COPY,
+                   PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_QUANTIZE,
                    PPK_KERNEL_RENYI_SAMPLE, PpkError,
                    PpkExecutionUncertainError, PpkInvalidOutputError, PpkPreconditionError)
 from .fused_attention import FloatDecodeAttention
+from .kv_arena import LayerCache, WritePlan
 from .sampling import RenyiSampler
 from .int8_kv_ops import (AppendKV, DecodeAttention, DecodeStep, append, attention, context, decode_step,
                           dequantize, kernel_stats, prepare, quantize, set_profiling)
 
 __all__ = [
     "PPK_ABI_VERSION", "PPK_ATTN_BF16_HISTORY", "PPK_FLAG_NONFINITE", "PPK_FLAG_OVERFLOW",
-    "PPK_KERNEL_APPEND", "PPK_KERNEL_ATTN_MERGE", "PPK_KERNEL_ATTENTION", "PPK_KERNEL_DEQUANTIZE",
+    "PPK_KERNEL_APPEND", "PPK_KERNEL_ATTN_MERGE", "PPK_KERNEL_ATTENTION", "PPK_KERNEL_COPY", "PPK_KERNEL_DEQUANTIZE",
     "PPK_KERNEL_FLOAT_ATTENTION", "PPK_KERNEL_FLOAT_MERGE", "PPK_KERNEL_QUANTIZE", "PPK_KERNEL_RENYI_SAMPLE",
     "PpkError", "PpkExecutionUncertainError", "PpkInvalidOutputError", "PpkPreconditionError",
-    "AppendKV", "DecodeAttention", "DecodeStep", "FloatDecodeAttention", "RenyiSampler", "fused_attention",
-    "sampling",
+    "AppendKV", "DecodeAttention", "DecodeStep", "FloatDecodeAttention", "LayerCache", "RenyiSampler", "WritePlan",
+    "fused_attention", "kv_arena", "sampling",
     "append", "attention", "context", "decode_step", "dequantize", "kernel_stats", "prepare", "quantize",
     "set_profiling",
 ]

@@ -18,7 +18,8 @@ PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
 PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW = 1, 2
 PPK_ATTN_BF16_HISTORY = 1
 (PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE,
- PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_RENYI_SAMPLE, PPK_KERNEL_COUNT) = range(9)
+ PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_RENYI_SAMPLE, PPK_KERNEL_COPY,
+ PPK_KERNEL_COUNT) = range(10)
 
 _u32, _u64, _ptr, _f32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_float
 
@@ -69,6 +70,31 @@ class PpkRenyiSampleArgs(ctypes.Structure):
                 ("bounds", _ptr), ("out", _ptr)]
 
 
+PPK_KV_INT8, PPK_KV_BF16, PPK_KV_F16, PPK_KV_F32 = 0, 1, 2, 3
+
+
+class PpkKvConfig(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("kind", _u32), ("heads", _u32), ("head_dim", _u32), ("max_context", _u32),
+                ("min_capacity", _u32)]
+
+
+class PpkKvView(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("kind", _u32), ("rows", _u32), ("capacity", _u32), ("head_dim", _u32),
+                ("length", _u32), ("batch", _u32), ("reserved", _u32), ("k", _ptr), ("v", _ptr),
+                ("k_scales", _ptr), ("v_scales", _ptr), ("past", _ptr), ("lengths", _ptr)]
+
+
+class PpkKvInfo(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("length", _u32), ("capacity", _u32), ("grouped", _u32), ("slot", _u32),
+                ("shared", _u32), ("reserved_bytes", _u64), ("storage_id", _u64), ("arena_id", _u64),
+                ("arena_copied_rows", _u64), ("arena_offset_uploads", _u64)]
+
+
+class PpkKvWrite(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("src_dtype", _u32), ("tokens", _u32), ("commit", _u32), ("k", _ptr),
+                ("v", _ptr)]
+
+
 # Every function the header declares: name -> (restype, argtypes).
 FUNCTIONS = {
     "ppk_abi_version": (_u32, []),
@@ -89,6 +115,18 @@ FUNCTIONS = {
     "ppk_float_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatAttentionArgs)]),
     "ppk_float_attention_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_renyi_sample": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkRenyiSampleArgs)]),
+    "ppk_kv_cache_create": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkKvConfig), ctypes.POINTER(_ptr)]),
+    "ppk_kv_cache_clone": (ctypes.c_int32, [_ptr, ctypes.POINTER(_ptr)]),
+    "ppk_kv_cache_release": (ctypes.c_int32, [_ptr]),
+    "ppk_kv_cache_info": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkKvInfo)]),
+    "ppk_kv_cache_truncate": (ctypes.c_int32, [_ptr, _u32]),
+    "ppk_kv_cache_view": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkKvView)]),
+    "ppk_kv_query": (ctypes.c_int32, [_ptr, _ptr, _ptr, _u32, ctypes.POINTER(PpkKvWrite), ctypes.POINTER(PpkKvView)]),
+    "ppk_write_plan_create": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(_u32), _u32, _u32, _u32,
+                                               ctypes.POINTER(_ptr)]),
+    "ppk_write_plan_release": (ctypes.c_int32, [_ptr]),
+    "ppk_kv_query_batch": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(_ptr), _u32, ctypes.POINTER(_u32),
+                                            ctypes.POINTER(PpkKvWrite), _ptr, ctypes.POINTER(PpkKvView)]),
     "ppk_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_context_set_profiling": (ctypes.c_int32, [_ptr, ctypes.c_int32]),
     "ppk_context_kernel_stats": (ctypes.c_int32, [_ptr, _u32, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double),

@@ -1,0 +1,173 @@
+"""Torch-facing mirror of the reference's KV cache layer over the C-ABI arena
+manager (include/ppk_int8_kv.h, ppk_kv_*).
+
+LayerCache follows app/src/model/cache.rs:40-531 (query, query_batch[_with_plan],
+clone = snapshot, truncate_committed, key/value, len) with int8 storage as
+Int8LayerCache (app/src/model/int8_cache.rs:292-359); WritePlan follows
+BatchWritePlan (app/src/model/write_plan.rs:12-102). Storage lives in
+device arenas owned by libppk; views are returned as the C view block plus
+`read()`, which copies a view's rows into a new torch tensor.
+"""
+from __future__ import annotations
+
+import ctypes
+import sys
+
+import torch
+
+from . import _abi
+from ._abi import check, lib
+from .int8_kv_ops import _DTYPES, _stream, context
+
+KINDS = {"int8": _abi.PPK_KV_INT8, torch.bfloat16: _abi.PPK_KV_BF16, torch.float16: _abi.PPK_KV_F16,
+         torch.float32: _abi.PPK_KV_F32}
+_KIND_DTYPE = {_abi.PPK_KV_INT8: torch.uint8, _abi.PPK_KV_BF16: torch.bfloat16, _abi.PPK_KV_F16: torch.float16,
+               _abi.PPK_KV_F32: torch.float32}
+_hip = None
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime already loaded by torch and libppk (one SONAME, one instance)."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipMemcpy2DAsync.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
+                                          ctypes.c_size_t, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+        _hip.hipMemcpy2DAsync.restype = ctypes.c_int
+    return _hip
+
+
+def _write(k: torch.Tensor, v: torch.Tensor, tokens: int, commit: bool) -> _abi.PpkKvWrite:
+    if k.dtype not in _DTYPES or v.dtype != k.dtype or k.shape != v.shape or not (k.is_cuda and v.is_cuda):
+        raise ValueError("K/V query precision, shape or device mismatch")
+    return _abi.PpkKvWrite(struct_size=ctypes.sizeof(_abi.PpkKvWrite), src_dtype=_DTYPES[k.dtype], tokens=tokens,
+                           commit=int(bool(commit)), k=k.data_ptr(), v=v.data_ptr())
+
+
+def read(view: _abi.PpkKvView, which: str = "k", tokens: int | None = None,
+         device: torch.device | None = None) -> torch.Tensor:
+    """Copy of a view's [rows, tokens, head_dim] values (`k` / `v`) or [rows, tokens] scales
+    (`k_scales` / `v_scales`); tokens defaults to the view's length."""
+    n = view.length if tokens is None else tokens
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    src = getattr(view, which)
+    if which in ("k", "v"):
+        dtype = _KIND_DTYPE[view.kind]
+        shape, inner = (view.rows, n, view.head_dim), view.head_dim
+    else:
+        dtype, shape, inner = torch.float32, (view.rows, n), 1
+    out = torch.empty(shape, dtype=dtype, device=device)
+    if out.numel() == 0 or not src:
+        return out
+    eb = out.element_size()
+    st = _hip_runtime().hipMemcpy2DAsync(out.data_ptr(), n * inner * eb, src, view.capacity * inner * eb,
+                                         n * inner * eb, view.rows, 3, _stream(out))
+    if st != 0:
+        raise RuntimeError(f"hipMemcpy2DAsync failed with {st}")
+    return out
+
+
+class LayerCache:
+    """One sequence's K/V history for one layer (cache.rs LayerCache / int8_cache.rs Int8LayerCache)."""
+
+    def __init__(self, kind, heads: int, head_dim: int, *, max_context: int = 0, min_capacity: int = 0,
+                 device: torch.device | int | None = None, _handle: ctypes.c_void_p | None = None):
+        self.kind = KINDS[kind] if not isinstance(kind, int) else kind
+        self.heads, self.head_dim = heads, head_dim
+        self.ctx = context(device)
+        self.device = device
+        if _handle is not None:
+            self.handle = _handle
+        else:
+            cfg = _abi.PpkKvConfig(struct_size=ctypes.sizeof(_abi.PpkKvConfig), kind=self.kind, heads=heads,
+                                   head_dim=head_dim, max_context=max_context, min_capacity=min_capacity)
+            self.handle = ctypes.c_void_p()
+            check(lib().ppk_kv_cache_create(self.ctx, ctypes.byref(cfg), ctypes.byref(self.handle)),
+                  "ppk_kv_cache_create")
+
+    def __del__(self):
+        # At interpreter shutdown the HIP runtime may already be gone; the process frees everything.
+        h = getattr(self, "handle", None)
+        if h is not None and h.value and not sys.is_finalizing():
+            lib().ppk_kv_cache_release(h)
+            self.handle = None
+
+    def clone(self) -> "LayerCache":
+        """A snapshot sharing storage; the next write through either side copies first."""
+        h = ctypes.c_void_p()
+        check(lib().ppk_kv_cache_clone(self.handle, ctypes.byref(h)), "ppk_kv_cache_clone")
+        return LayerCache(self.kind, self.heads, self.head_dim, device=self.device, _handle=h)
+
+    def info(self) -> _abi.PpkKvInfo:
+        out = _abi.PpkKvInfo(struct_size=ctypes.sizeof(_abi.PpkKvInfo))
+        check(lib().ppk_kv_cache_info(self.handle, ctypes.byref(out)), "ppk_kv_cache_info")
+        return out
+
+    def __len__(self) -> int:
+        return self.info().length
+
+    def truncate_committed(self, new_len: int) -> None:
+        check(lib().ppk_kv_cache_truncate(self.handle, new_len), "ppk_kv_cache_truncate")
+
+    def view(self) -> _abi.PpkKvView:
+        out = _abi.PpkKvView(struct_size=ctypes.sizeof(_abi.PpkKvView))
+        check(lib().ppk_kv_cache_view(self.handle, ctypes.byref(out)), "ppk_kv_cache_view")
+        return out
+
+    def key(self) -> torch.Tensor | None:
+        """Copy of the committed keys [heads, len, D] (codes for int8), or None when empty."""
+        v = self.view()
+        return read(v, "k") if v.length else None
+
+    def value(self) -> torch.Tensor | None:
+        v = self.view()
+        return read(v, "v") if v.length else None
+
+    def query(self, k: torch.Tensor, v: torch.Tensor, past: int, commit: bool) -> _abi.PpkKvView:
+        """k/v [heads, tokens, D] at slot `past` (= len(self)); returns the view of [0, past + tokens)."""
+        if k.dim() != 3 or k.shape[0] != self.heads or k.shape[2] != self.head_dim:
+            raise ValueError("K/V query shape differs from the cache geometry")
+        k, v = k.contiguous(), v.contiguous()
+        w = _write(k, v, k.shape[1], commit)
+        out = _abi.PpkKvView(struct_size=ctypes.sizeof(_abi.PpkKvView))
+        check(lib().ppk_kv_query(self.ctx, _stream(k), self.handle, past, ctypes.byref(w), ctypes.byref(out)),
+              "ppk_kv_query")
+        return out
+
+    @staticmethod
+    def query_batch(caches: list["LayerCache"], k: torch.Tensor, v: torch.Tensor, past_lens, commit: bool,
+                    plan: "WritePlan | None" = None) -> _abi.PpkKvView:
+        """k/v [B, H, 1, D]: one token per sequence at slot past_lens[b]; returns the arena view
+        [B*H, capacity, D] with length max(past) + 1 and device past / lengths vectors."""
+        b = len(caches)
+        if k.dim() != 4 or k.shape[0] != b or k.shape[2] != 1:
+            raise ValueError("batch KV requires [B,H,1,D] scratch and matching row histories")
+        k, v = k.contiguous(), v.contiguous()
+        w = _write(k, v, 1, commit)
+        handles = (ctypes.c_void_p * b)(*[c.handle.value for c in caches])
+        lens = (ctypes.c_uint32 * b)(*[int(x) for x in past_lens])
+        out = _abi.PpkKvView(struct_size=ctypes.sizeof(_abi.PpkKvView))
+        check(lib().ppk_kv_query_batch(caches[0].ctx, _stream(k), handles, b, lens, ctypes.byref(w),
+                                       plan.handle if plan is not None else None, ctypes.byref(out)),
+              "ppk_kv_query_batch")
+        return out
+
+
+class WritePlan:
+    """BatchWritePlan: one decode round's per-sequence write offsets on the device, shared by every layer."""
+
+    def __init__(self, past_lens, heads: int, head_dim: int, device: torch.device | int | None = None):
+        self.offsets = [int(x) for x in past_lens]
+        b = len(self.offsets)
+        lens = (ctypes.c_uint32 * max(b, 1))(*self.offsets)
+        self.handle = ctypes.c_void_p()
+        dev = device if device is not None else torch.cuda.current_device()
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        check(lib().ppk_write_plan_create(context(dev), stream, lens, b, heads, head_dim, ctypes.byref(self.handle)),
+              "ppk_write_plan_create")
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value and not sys.is_finalizing():
+            lib().ppk_write_plan_release(h)
+            self.handle = None

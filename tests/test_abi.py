@@ -55,7 +55,8 @@ def c_layout(tmp_path_factory):
     exe = src.with_suffix("")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs,
-                _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs, _abi.PpkRenyiSampleArgs):
+                _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs, _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig,
+                _abi.PpkKvView, _abi.PpkKvInfo, _abi.PpkKvWrite):
         name = cls.__name__
         lines.append(f'printf("{name} __sizeof__ %zu\\n", sizeof({name}));')
         for field, _ in cls._fields_:
@@ -69,7 +70,8 @@ def c_layout(tmp_path_factory):
 
 @pytest.mark.parametrize("cls", [_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs,
                                  _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs,
-                                 _abi.PpkRenyiSampleArgs])
+                                 _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig, _abi.PpkKvView, _abi.PpkKvInfo,
+                                 _abi.PpkKvWrite])
 def test_struct_layout_matches_c(c_layout, cls):
     name = cls.__name__
     assert c_layout[(name, "__sizeof__")] == ctypes.sizeof(cls)
@@ -203,3 +205,20 @@ def test_sampler_python_mirror_refuses_cpu_tensors_and_bad_shapes():
         ppk.sampling.sample(raw, torch.zeros((2, 2))[:, :1], b, 4.0, 2.0, 2, 0)
     with pytest.raises(ValueError):
         ppk.sampling.sample(raw, u, b, 4.0, 2.0, 1, 0)
+
+
+def test_kv_arena_entry_points_refuse_null_arguments():
+    lib = _abi.lib()
+    cfg = _abi.PpkKvConfig(struct_size=ctypes.sizeof(_abi.PpkKvConfig), kind=0, heads=2, head_dim=64)
+    out = ctypes.c_void_p(123)
+    assert lib.ppk_kv_cache_create(None, ctypes.byref(cfg), ctypes.byref(out)) == _abi.PPK_PRECONDITION
+    assert out.value is None
+    assert lib.ppk_kv_cache_clone(None, ctypes.byref(out)) == _abi.PPK_PRECONDITION
+    assert lib.ppk_kv_cache_info(None, None) == _abi.PPK_PRECONDITION
+    assert lib.ppk_kv_cache_truncate(None, 0) == _abi.PPK_PRECONDITION
+    w = _abi.PpkKvWrite(struct_size=ctypes.sizeof(_abi.PpkKvWrite))
+    assert lib.ppk_kv_query(None, None, None, 0, ctypes.byref(w), None) == _abi.PPK_PRECONDITION
+    assert lib.ppk_kv_query_batch(None, None, None, 0, None, ctypes.byref(w), None, None) == _abi.PPK_PRECONDITION
+    assert lib.ppk_write_plan_create(None, None, None, 0, 1, 1, ctypes.byref(out)) == _abi.PPK_PRECONDITION
+    assert lib.ppk_kv_cache_release(None) == _abi.PPK_OK
+    assert lib.ppk_write_plan_release(None) == _abi.PPK_OK
