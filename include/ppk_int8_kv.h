@@ -357,6 +357,7 @@ typedef struct PpkKvInfo {
   uint64_t arena_id;      /* identity of the arena */
   uint64_t arena_copied_rows;   /* sequences whose committed history was copied into this arena */
   uint64_t arena_offset_uploads;/* device offset vectors uploaded by this arena (writes without a plan) */
+  uint64_t scale_bytes;   /* of reserved_bytes, the f32 scale planes (int8 caches; int8_cache.rs:291) */
 } PpkKvInfo;
 
 /* Source of a write: K and V [heads, tokens, head_dim] (single) or

@@ -283,6 +283,7 @@ void info(const ppk_kv_cache& c, PpkKvInfo* out) {
   out->slot = c.backing->slot;
   out->shared = c.backing.use_count() > 1 ? 1 : 0;
   out->reserved_bytes = a.slot_bytes();
+  out->scale_bytes = a.kind == PPK_KV_INT8 ? 2 * uint64_t(a.heads) * a.scale_row_bytes() : 0;
   out->storage_id = reinterpret_cast<uintptr_t>(c.backing.get());
   out->arena_id = reinterpret_cast<uintptr_t>(&a);
   std::lock_guard<std::mutex> lock(c.backing->arena->mu);

@@ -87,7 +87,7 @@ class PpkKvView(ctypes.Structure):
 class PpkKvInfo(ctypes.Structure):
     _fields_ = [("struct_size", _u32), ("length", _u32), ("capacity", _u32), ("grouped", _u32), ("slot", _u32),
                 ("shared", _u32), ("reserved_bytes", _u64), ("storage_id", _u64), ("arena_id", _u64),
-                ("arena_copied_rows", _u64), ("arena_offset_uploads", _u64)]
+                ("arena_copied_rows", _u64), ("arena_offset_uploads", _u64), ("scale_bytes", _u64)]
 
 
 class PpkKvWrite(ctypes.Structure):

@@ -134,6 +134,28 @@ class LayerCache:
               "ppk_kv_query")
         return out
 
+    def query_int8_prefill(self, k: torch.Tensor, v: torch.Tensor, past: int, commit: bool
+                           ) -> tuple[torch.Tensor, torch.Tensor]:
+        """LayerCache::query_int8_prefill (cache.rs:133-141, int8_cache.rs:363-371): the committed int8
+        history dequantised through bf16 (ppk_dequantize) and cast to k's dtype, concatenated with the
+        original k/v chunk; the chunk itself is committed (quantised) as query() does. Only prefill
+        uses this transient floating prefix."""
+        from .int8_kv_ops import dequantize
+
+        if self.kind != _abi.PPK_KV_INT8:
+            raise ValueError("query_int8_prefill needs an INT8 cache")
+        view = self.view()
+        prefix = None
+        if view.length:
+            codes_k, codes_v = read(view, "k"), read(view, "v")
+            sk, sv = read(view, "k_scales"), read(view, "v_scales")
+            prefix = (dequantize(codes_k, sk, torch.bfloat16).to(k.dtype),
+                      dequantize(codes_v, sv, torch.bfloat16).to(v.dtype))
+        self.query(k, v, past, commit)
+        if prefix is None:
+            return k, v
+        return torch.cat([prefix[0], k], 1), torch.cat([prefix[1], v], 1)
+
     @staticmethod
     def query_batch(caches: list["LayerCache"], k: torch.Tensor, v: torch.Tensor, past_lens, commit: bool,
                     plan: "WritePlan | None" = None) -> _abi.PpkKvView:
