@@ -89,10 +89,11 @@ def _attn_args(**kw) -> _abi.PpkAttentionArgs:
 
 
 def test_plan_sizes_workspace_without_a_device():
-    # Config 5 on 256 CUs: 16 waves x 512 tokens cover a row, so one block per
-    # row finishes the step in one launch and needs no workspace.
+    # Config 5 on 256 CUs: 4 waves x 2048 tokens cover a row (8 waves per CU over
+    # the launch), so one block per row finishes the step in one launch and needs
+    # no workspace.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args())
-    assert (split, groups, nbytes) == (512, 1, 0)
+    assert (split, groups, nbytes) == (2048, 1, 0)
     # An explicit per-wave split is honoured (rounded up to whole 1 KiB tiles);
     # up to 16 waves per block, so ceil(ceil(8192/104)/16) blocks per row.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
@@ -137,8 +138,8 @@ def _float_args(**kw) -> _abi.PpkFloatAttentionArgs:
 
 
 def test_float_plan_without_a_device():
-    # Long rows, many of them: one 16-wave block per row, a single launch.
-    assert ppk.fused_attention.plan(_float_args()) == (512, 1, 0)
+    # Long rows, many of them: one 4-wave block per row, a single launch.
+    assert ppk.fused_attention.plan(_float_args()) == (2048, 1, 0)
     # The reference's graph-decode shape (16 rows of a 1024-token bf16 store, D = 64):
     # 16 one-wave groups per row cover the CUs; merge workspace y + (m, z) records.
     split, groups, nbytes = ppk.fused_attention.plan(_float_args(rows=16, size=1024, head_dim=64))
@@ -148,7 +149,7 @@ def test_float_plan_without_a_device():
     split, groups, _ = ppk.fused_attention.plan(_float_args(kv_dtype=_abi.PPK_F32, split_tokens=33))
     assert split == 34 and groups == -(-(-(-8192 // 34)) // 16)
     # max_length bounds the planned span.
-    assert ppk.fused_attention.plan(_float_args(max_length=1024, lengths=8))[:2] == (64, 1)
+    assert ppk.fused_attention.plan(_float_args(max_length=1024, lengths=8))[:2] == (256, 1)
 
 
 @pytest.mark.parametrize("bad", [dict(kv_dtype=_abi.PPK_F16), dict(head_dim=96), dict(size=0), dict(rows=30),
