@@ -197,17 +197,18 @@ def bench_float(args) -> int:
         else:
             k_h, v_h = k[:n].cpu().numpy(), v[:n].cpu().numpy()
         q_h = q[:n].cpu().numpy()
+        threads = max(1, min(os.cpu_count() or 1, 16))
         reps, t0 = 0, time.perf_counter()
         while True:
-            oracle.attention_float(q_h, k_h, v_h, None, 1)
+            oracle.cpu_baseline_float(q_h, k_h, v_h, threads)
             reps += 1
             el = time.perf_counter() - t0
             if el >= args.cpu_seconds or reps >= 1000:
                 break
         result["cpu_baseline"] = {
-            "value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/step", "cores": 1, "kind": "port",
-            "sample": f"{n} of {rows} head rows x {L} tokens (oracle_attention_float, f64 scalar), {reps} reps "
-                      f"in {el:.1f} s, scaled x{rows / n:g}"}
+            "value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": f"{n} of {rows} head rows x {L} tokens (Candle's ordinary CPU attention restated in C, "
+                      f"cpu_baseline_float_decode), {reps} reps in {el:.1f} s, scaled x{rows / n:g}"}
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -403,6 +403,28 @@ PPK_API int32_t ppk_kv_query_batch(ppk_context* ctx, void* stream, ppk_kv_cache*
    Returns 2 with the failing check in ppk_last_error() on a numeric mismatch. */
 PPK_API int32_t ppk_prepare(ppk_context* ctx);
 
+/* The int8 KV capability gate: PrimitiveModel::prepare_int8_kv / Int8KvStatus
+   (app/src/model/int8_policy.rs:3-56). Decision order as the reference:
+   not requested -> disabled (status 0); requested but unavailable (head_dim
+   not 64/128/256) -> disabled with the reason (status 0); requested and
+   available -> the known-answer self-check of ppk_prepare runs once per
+   context (its failure is returned with its status: 1, 2 or 3, and the
+   reason says why), then enabled. Bytes per token and head: 2 * head_dim
+   packed (K and V codes), 8 for the two f32 scales. */
+typedef struct PpkInt8KvStatus {
+  uint32_t struct_size;
+  uint32_t requested;
+  uint32_t available;
+  uint32_t ready;
+  uint32_t enabled;
+  uint32_t packed_bytes_per_token_head;
+  uint32_t scale_bytes_per_token_head;
+  uint32_t reserved;
+  char format[64];        /* "INT8 symmetric per-token/head + FP32 scales" when enabled */
+  char reason[256];       /* UTF-8, NUL-terminated */
+} PpkInt8KvStatus;
+PPK_API int32_t ppk_prepare_int8_kv(ppk_context* ctx, uint32_t requested, uint32_t head_dim, PpkInt8KvStatus* out);
+
 /* Tracing: when enabled, the library brackets every launch of the named kernel
    with HIP events on the launch stream; stats resolve them (blocking on the
    recorded events only) and report the number of traced launches and their

@@ -46,6 +46,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_renyi_sample.argtypes = [P, Z, Z, P, P, ctypes.c_float, ctypes.c_float, Z, ctypes.c_uint32,
                                           ctypes.c_int, P, P, P, P]
         L.oracle_renyi_sample.restype = ctypes.c_int
+        L.cpu_baseline_float_decode.argtypes = [P, P, P, ctypes.c_int, Z, Z, Z, ctypes.c_float, Z, P]
+        L.cpu_baseline_float_decode.restype = ctypes.c_int
         L.cpu_baseline_decode.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, Z, P]
         L.cpu_baseline_decode.restype = ctypes.c_int
         _lib = L
@@ -204,3 +206,21 @@ def renyi_sample(raw, uniforms, bounds, alpha: float, cfg: float, guidance: int,
     if rc != 0:
         raise ValueError("invalid reference metadata")
     return {"token": token, "valid": valid, "support": support, "margin": margin}
+
+
+def cpu_baseline_float(q, k, v, threads: int, scale: float | None = None) -> np.ndarray:
+    """Candle's ordinary CPU attention over a dense bf16 (uint16 bits) or f32 store [rows, size, d], f32,
+    parallel over rows (see cpu_baseline_float_decode); float32 [rows, d]."""
+    kv_bf16 = k.dtype == np.uint16
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v, dtype=k.dtype)
+    rows, size, d = k.shape
+    q = _c(q, np.float32).reshape(rows, d)
+    if scale is None:
+        scale = 1.0 / np.sqrt(d)
+    out = np.empty((rows, d), np.float32)
+    rc = lib().cpu_baseline_float_decode(_p(q), k.ctypes.data, v.ctypes.data, int(kv_bf16), rows, size, d,
+                                         float(scale), int(threads), _p(out))
+    if rc != 0:
+        raise RuntimeError("cpu_baseline_float_decode: a worker thread failed to start (ran inline)")
+    return out

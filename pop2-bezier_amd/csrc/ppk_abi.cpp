@@ -788,6 +788,52 @@ int32_t ppk_prepare(ppk_context* ctx) {
   });
 }
 
+int32_t ppk_prepare_int8_kv(ppk_context* ctx, uint32_t requested, uint32_t head_dim, PpkInt8KvStatus* out) {
+  auto text = [](char* dst, size_t cap, const std::string& src) {
+    const size_t n = std::min(cap - 1, src.size());
+    std::memcpy(dst, src.data(), n);
+    dst[n] = '\0';
+  };
+  return call([&] {
+    ppk::require(ctx && out, "ppk_prepare_int8_kv: null argument");
+    ppk::require(out->struct_size >= sizeof(PpkInt8KvStatus), "PpkInt8KvStatus.struct_size too small");
+    const uint32_t size = out->struct_size;
+    std::memset(out, 0, sizeof(PpkInt8KvStatus));
+    out->struct_size = size;
+    out->requested = requested ? 1 : 0;
+    out->available = (head_dim == 64 || head_dim == 128 || head_dim == 256) ? 1 : 0;
+    out->packed_bytes_per_token_head = 2 * head_dim;
+    out->scale_bytes_per_token_head = 8;
+    text(out->format, sizeof(out->format), "BF16/F32");
+    std::lock_guard<std::mutex> lock(ctx->prepare_mutex);
+    out->ready = ctx->int8_ready ? 1 : 0;
+    if (!requested) {
+      text(out->reason, sizeof(out->reason), "int8 KV history disabled; the ordinary floating cache is kept");
+      return;
+    }
+    if (!out->available) {
+      text(out->reason, sizeof(out->reason),
+           "int8 KV history on this backend needs gfx950 and 64/128/256-channel heads; the ordinary floating "
+           "cache is kept");
+      return;
+    }
+    if (!ctx->int8_ready) {
+      try {
+        ppk::prepare_self_check(ctx);
+      } catch (const std::exception& e) {
+        text(out->reason, sizeof(out->reason), std::string("int8 KV preparation incomplete: ") + e.what());
+        throw;
+      }
+      ctx->int8_ready = true;
+      out->ready = 1;
+    }
+    out->enabled = 1;
+    text(out->format, sizeof(out->format), "INT8 symmetric per-token/head + FP32 scales");
+    text(out->reason, sizeof(out->reason),
+         "committed history is int8; the current K/V stay floating; attention dequantises on read");
+  });
+}
+
 int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable) {
   return call([&] {
     ppk::require(ctx != nullptr, "ppk_context_set_profiling: null context");

@@ -59,6 +59,9 @@ struct ppk_context {
   hipFunction_t fn[ppk::kFnCount] = {};
   std::string code_object;
 
+  std::mutex prepare_mutex;
+  bool int8_ready = false;  // ppk_prepare_int8_kv's self-check passed on this context
+
   std::mutex prof_mutex;
   bool profiling = false;
   std::vector<ppk::EventPair> pending[PPK_KERNEL_COUNT];

@@ -14,7 +14,7 @@ from .fused_attention import FloatDecodeAttention
 from .kv_arena import LayerCache, WritePlan
 from .sampling import RenyiSampler
 from .int8_kv_ops import (AppendKV, DecodeAttention, DecodeStep, append, attention, context, decode_step,
-                          dequantize, kernel_stats, prepare, quantize, set_profiling)
+                          dequantize, kernel_stats, prepare, prepare_int8_kv, quantize, set_profiling)
 
 __all__ = [
     "PPK_ABI_VERSION", "PPK_ATTN_BF16_HISTORY", "PPK_FLAG_NONFINITE", "PPK_FLAG_OVERFLOW",
@@ -23,6 +23,7 @@ __all__ = [
     "PpkError", "PpkExecutionUncertainError", "PpkInvalidOutputError", "PpkPreconditionError",
     "AppendKV", "DecodeAttention", "DecodeStep", "FloatDecodeAttention", "LayerCache", "RenyiSampler", "WritePlan",
     "fused_attention", "kv_arena", "sampling",
-    "append", "attention", "context", "decode_step", "dequantize", "kernel_stats", "prepare", "quantize",
+    "append", "attention", "context", "decode_step", "dequantize", "kernel_stats", "prepare", "prepare_int8_kv",
+    "quantize",
     "set_profiling",
 ]

@@ -95,6 +95,12 @@ class PpkKvWrite(ctypes.Structure):
                 ("v", _ptr)]
 
 
+class PpkInt8KvStatus(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("requested", _u32), ("available", _u32), ("ready", _u32), ("enabled", _u32),
+                ("packed_bytes_per_token_head", _u32), ("scale_bytes_per_token_head", _u32), ("reserved", _u32),
+                ("format", ctypes.c_char * 64), ("reason", ctypes.c_char * 256)]
+
+
 # Every function the header declares: name -> (restype, argtypes).
 FUNCTIONS = {
     "ppk_abi_version": (_u32, []),
@@ -128,6 +134,7 @@ FUNCTIONS = {
     "ppk_kv_query_batch": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(_ptr), _u32, ctypes.POINTER(_u32),
                                             ctypes.POINTER(PpkKvWrite), _ptr, ctypes.POINTER(PpkKvView)]),
     "ppk_prepare": (ctypes.c_int32, [_ptr]),
+    "ppk_prepare_int8_kv": (ctypes.c_int32, [_ptr, _u32, _u32, ctypes.POINTER(PpkInt8KvStatus)]),
     "ppk_context_set_profiling": (ctypes.c_int32, [_ptr, ctypes.c_int32]),
     "ppk_context_kernel_stats": (ctypes.c_int32, [_ptr, _u32, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double),
                                                   _u32]),

@@ -303,6 +303,18 @@ def prepare(device: torch.device | int | None = None) -> None:
     check(lib().ppk_prepare(context(device)), "ppk_prepare")
 
 
+def prepare_int8_kv(requested: bool, head_dim: int = 64, device: torch.device | int | None = None) -> dict:
+    """PrimitiveModel::prepare_int8_kv (int8_policy.rs:26-55): the Int8KvStatus fields as a dict. A failed
+    self-check raises (PpkInvalidOutputError etc.) after recording the reason, as the reference returns Err."""
+    st = _abi.PpkInt8KvStatus(struct_size=ctypes.sizeof(_abi.PpkInt8KvStatus))
+    check(lib().ppk_prepare_int8_kv(context(device), int(bool(requested)), head_dim, ctypes.byref(st)),
+          "ppk_prepare_int8_kv")
+    return {"requested": bool(st.requested), "available": bool(st.available), "ready": bool(st.ready),
+            "enabled": bool(st.enabled), "format": st.format.decode(), "reason": st.reason.decode(),
+            "packed_bytes_per_token_head": st.packed_bytes_per_token_head,
+            "scale_bytes_per_token_head": st.scale_bytes_per_token_head}
+
+
 def set_profiling(enable: bool, device: torch.device | int | None = None) -> None:
     check(lib().ppk_context_set_profiling(context(device), int(bool(enable))), "ppk_context_set_profiling")
 

@@ -56,7 +56,7 @@ def c_layout(tmp_path_factory):
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs,
                 _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs, _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig,
-                _abi.PpkKvView, _abi.PpkKvInfo, _abi.PpkKvWrite):
+                _abi.PpkKvView, _abi.PpkKvInfo, _abi.PpkKvWrite, _abi.PpkInt8KvStatus):
         name = cls.__name__
         lines.append(f'printf("{name} __sizeof__ %zu\\n", sizeof({name}));')
         for field, _ in cls._fields_:
@@ -71,7 +71,7 @@ def c_layout(tmp_path_factory):
 @pytest.mark.parametrize("cls", [_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs,
                                  _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs,
                                  _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig, _abi.PpkKvView, _abi.PpkKvInfo,
-                                 _abi.PpkKvWrite])
+                                 _abi.PpkKvWrite, _abi.PpkInt8KvStatus])
 def test_struct_layout_matches_c(c_layout, cls):
     name = cls.__name__
     assert c_layout[(name, "__sizeof__")] == ctypes.sizeof(cls)
@@ -223,3 +223,8 @@ def test_kv_arena_entry_points_refuse_null_arguments():
     assert lib.ppk_write_plan_create(None, None, None, 0, 1, 1, ctypes.byref(out)) == _abi.PPK_PRECONDITION
     assert lib.ppk_kv_cache_release(None) == _abi.PPK_OK
     assert lib.ppk_write_plan_release(None) == _abi.PPK_OK
+
+
+def test_int8_gate_refuses_null_context():
+    st = _abi.PpkInt8KvStatus(struct_size=ctypes.sizeof(_abi.PpkInt8KvStatus))
+    assert _abi.lib().ppk_prepare_int8_kv(None, 1, 64, ctypes.byref(st)) == _abi.PPK_PRECONDITION

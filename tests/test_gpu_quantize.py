@@ -165,3 +165,16 @@ def test_dequantize_matches_oracle(device, d, dt):
         assert np.array_equal(out.view(torch.int16).numpy().view(np.uint16), to_bf16_bits(ref))
     else:
         assert np.array_equal(out.numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
+
+
+def test_int8_capability_gate(device):
+    """prepare_int8_kv (int8_policy.rs:26-55): not requested, unavailable head width, then ready + enabled."""
+    off = ppk.prepare_int8_kv(False, 64, device)
+    assert not off["enabled"] and off["format"] == "BF16/F32" and off["requested"] is False
+    odd = ppk.prepare_int8_kv(True, 96, device)
+    assert odd["requested"] and not odd["available"] and not odd["enabled"]
+    on = ppk.prepare_int8_kv(True, 64, device)
+    assert on["available"] and on["ready"] and on["enabled"] and on["format"].startswith("INT8")
+    assert (on["packed_bytes_per_token_head"], on["scale_bytes_per_token_head"]) == (128, 8)
+    again = ppk.prepare_int8_kv(True, 128, device)
+    assert again["enabled"] and again["packed_bytes_per_token_head"] == 256

@@ -161,3 +161,12 @@ def test_pins_catch_planted_float_attention_mistakes():
     np.testing.assert_allclose(oracle.attention_float(q, k, v, lengths, 2), ref, rtol=1e-12, atol=1e-12)
     for planted in (_planted_row_lengths, _planted_no_scale):
         assert np.max(np.abs(planted(q, k, v, lengths, 2) - ref)) > 1e-3, planted.__name__
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_cpu_baseline_float_matches_oracle(bf16):
+    """The float path's CPU baseline (Candle's ordinary attention restated) agrees with the f64 oracle."""
+    rng = np.random.default_rng(SEED + 21)
+    q, k, v, _, _ = _inputs(rng, 12, 333, 64, bf16)
+    got = oracle.cpu_baseline_float(q, k, v, threads=3)
+    np.testing.assert_allclose(got, oracle.attention_float(q, k, v, None, 1), rtol=1e-4, atol=1e-5)
