@@ -1,0 +1,136 @@
+"""Seeded randomized parity sweep over the whole C-ABI surface (GPU).
+
+Each case draws its geometry, dtypes, lengths, splits and value ranges from a
+seeded generator (the case id is the seed offset, printed on failure) and
+checks the device result against the oracle at the bar of the row it
+belongs to: quantize bit-exact; int8 attention within 2e-3 + 1e-2 |ref|;
+float-KV attention within 1e-4 + 1e-4 |ref|; the sampler bit-identical to
+the reference's own kernel (oracle/_ref). Sizes are bounded so the whole
+sweep runs in seconds.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import ppk
+import refkernels
+from helpers import SEED, assert_close, bf16_bits_to_f32, to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def as_device(x32: np.ndarray, dtype, device):
+    """float32 host values -> device tensor of `dtype` plus the float32 values it holds exactly."""
+    if dtype == torch.float32:
+        return torch.from_numpy(x32).to(device), x32
+    if dtype == torch.float16:
+        h = x32.astype(np.float16)
+        return torch.from_numpy(h).to(device), h.astype(np.float32)
+    bits = to_bf16_bits(x32)
+    return torch.from_numpy(bits.view(np.int16)).to(device).view(torch.bfloat16), bf16_bits_to_f32(bits)
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_quantize_random(device, case):
+    rng = np.random.default_rng(SEED + 1000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    heads, tokens = int(rng.integers(1, 9)), int(rng.integers(1, 700))
+    dtype = DTYPES[case % 3]
+    top = {torch.float32: 6, torch.bfloat16: 3, torch.float16: 2}[dtype]  # 127 * mag stays finite in f16
+    mag = 10.0 ** rng.uniform(-6, top)
+    x = (rng.standard_normal((heads, tokens, d)) * mag).astype(np.float32)
+    x[:, ::17] = 0.0                                   # zero rows
+    x[:, 3::29, 5] = np.float32(mag * 127)             # large entries fix the scale exactly
+    xt, x32 = as_device(x, dtype, device)
+    codes, scales = ppk.quantize(xt)
+    ref_c, ref_s, _ = oracle.quantize(x32)
+    assert np.array_equal(codes.cpu().numpy(), ref_c), f"case {case}"
+    assert np.array_equal(scales.cpu().numpy(), ref_s), f"case {case}"
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_int8_attention_random(device, case):
+    rng = np.random.default_rng(SEED + 2000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    B, H = int(rng.integers(1, 5)), int(rng.integers(1, 9))
+    rows = B * H
+    past = rng.integers(0, 2500, B).astype(np.uint32)
+    past[0] = int(rng.choice([0, int(past[0])]))
+    cap = int(past.max()) + 1 + int(rng.integers(0, 40))
+    hist = rng.standard_normal((rows, cap, d)).astype(np.float32) * np.float32(rng.uniform(0.1, 5))
+    vhist = rng.standard_normal((rows, cap, d)).astype(np.float32)
+    kc, ks, _ = oracle.quantize(hist)
+    vc, vs, _ = oracle.quantize(vhist)
+    q_dt, s_dt, o_dt = DTYPES[case % 3], DTYPES[(case // 3) % 3], DTYPES[(case // 2) % 3]
+    qt, q32 = as_device(rng.standard_normal((rows, 1, d)).astype(np.float32), q_dt, device)
+    skt, sk32 = as_device(rng.standard_normal((rows, 1, d)).astype(np.float32), s_dt, device)
+    svt, sv32 = as_device(rng.standard_normal((rows, 1, d)).astype(np.float32), s_dt, device)
+    split = int(rng.choice([0, 0, int(rng.integers(1, 3000))]))
+    t = lambda a: torch.from_numpy(a).to(device)
+    out = ppk.attention(qt, t(kc), t(vc), t(ks), t(vs), skt, svt, t(past.view(np.int32)), H, split, out_dtype=o_dt)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q32, kc, vc, ks, vs, sk32, sv32, past, H)
+    got = out.float().reshape(rows, d).cpu().numpy()
+    tol = 2e-3 if o_dt == torch.float32 else 8e-3  # a 16-bit output adds its own rounding
+    assert_close(got, ref, atol=tol, rtol=1e-2, what=f"case {case} d{d} B{B} H{H} split {split}")
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_float_attention_random(device, case):
+    rng = np.random.default_rng(SEED + 3000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    B, H = int(rng.integers(1, 5)), int(rng.integers(1, 9))
+    rows = B * H
+    size = int(rng.integers(1, 2000))
+    cap = size + int(rng.integers(0, 3)) * 8
+    kv = torch.bfloat16 if case % 2 else torch.float32
+    k32 = rng.standard_normal((rows, cap, d)).astype(np.float32)
+    v32 = rng.standard_normal((rows, cap, d)).astype(np.float32)
+    if kv == torch.bfloat16:
+        kh, vh = to_bf16_bits(k32), to_bf16_bits(v32)
+        k = torch.from_numpy(kh.view(np.int16)).to(device).view(torch.bfloat16)[:, :size]
+        v = torch.from_numpy(vh.view(np.int16)).to(device).view(torch.bfloat16)[:, :size]
+    else:
+        kh, vh = k32, v32
+        k, v = torch.from_numpy(k32).to(device)[:, :size], torch.from_numpy(v32).to(device)[:, :size]
+    lengths = None
+    if rng.random() < 0.7:
+        lengths = rng.integers(0, size + 2, B).astype(np.uint32)
+    lt = None if lengths is None else torch.from_numpy(lengths.view(np.int32)).to(device)
+    q = rng.standard_normal((rows, 1, d)).astype(np.float32)
+    split = int(rng.choice([0, 0, int(rng.integers(1, 2048))]))
+    out = ppk.fused_attention.decode_attention(torch.from_numpy(q).to(device), k, v, lt, H, split)
+    torch.cuda.synchronize()
+    ref = oracle.attention_float(q, kh[:, :size], vh[:, :size], lengths, H)
+    assert_close(out.reshape(rows, d).cpu().numpy(), ref, atol=1e-4, rtol=1e-4,
+                 what=f"case {case} d{d} B{B} H{H} size {size} split {split}")
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_sampler_random_vs_reference_kernel(device, case):
+    rng = np.random.default_rng(SEED + 4000 + case)
+    guidance = 1 + case % 2
+    batch, choices = int(rng.integers(1, 70)), int(rng.integers(1, 2049))
+    scale = 10.0 ** rng.uniform(-2, 1.5)
+    raw = (rng.standard_normal((batch * guidance, choices)) * scale).astype(np.float32)
+    if case % 3 == 0:
+        raw = np.round(raw)  # heavy ties
+    u = rng.uniform(0, 1, batch).astype(np.float32)
+    starts = rng.integers(0, choices, batch)
+    counts = rng.integers(1, choices - starts + 1)
+    bounds = np.stack([starts, counts], 1).astype(np.uint32)
+    alpha = float(rng.uniform(1.01, 20))
+    cfg = float(rng.uniform(0, 5)) if guidance == 2 else 1.0
+    offset = int(rng.integers(0, 1 << 20))
+    raw_t = torch.from_numpy(raw).to(device)
+    u_t = torch.from_numpy(u.reshape(-1, 1)).to(device)
+    b_t = torch.from_numpy(bounds.view(np.int32)).to(device)
+    tok, val, sup = ppk.sampling.sample(raw_t, u_t, b_t, alpha, cfg, guidance, offset)
+    ref = refkernels.renyi_sample(raw_t, u_t, b_t, alpha, cfg, guidance, offset)
+    torch.cuda.synchronize()
+    got = torch.stack([tok.reshape(-1), val.reshape(-1), sup.reshape(-1)])
+    assert torch.equal(got, ref), f"case {case}: batch {batch} choices {choices} guidance {guidance}"
