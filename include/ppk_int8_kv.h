@@ -307,7 +307,12 @@ PPK_API int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiS
    * every shape, length and plan check completes before any device write.
    The context must outlive its caches and plans. Calls that touch caches
    sharing an arena must be serialised by the caller, on one stream; storage
-   is released stream-ordered on the stream that last wrote it. */
+   is released stream-ordered (hipFreeAsync) on the stream that last wrote or
+   copied it, so that stream must still exist when the last cache or plan
+   using the storage is released, and work reading a view on another stream
+   must be ordered before that release by the caller. Calls that allocate
+   (a first write, growth, copy-on-write, a new batch arena) refuse to run
+   under HIP graph capture. */
 enum { PPK_KV_INT8 = 0, PPK_KV_BF16 = 1, PPK_KV_F16 = 2, PPK_KV_F32 = 3 };
 
 typedef struct ppk_kv_cache ppk_kv_cache;

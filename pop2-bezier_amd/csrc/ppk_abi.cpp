@@ -533,6 +533,10 @@ void run_copy_batch(ppk_context* ctx, hipStream_t stream, const std::vector<Copy
   if (in.empty()) return;
   // Like-sized rectangles share a launch, so one grid shape fits them all.
   std::vector<CopyDesc> copies(in);
+  for (const CopyDesc& c : copies)  // every rectangle checked before the first launch
+    require(c.width <= c.fill && c.fill <= c.dpitch && c.fill <= 0xffffffffu && (c.width == 0 || c.width <= c.spitch) &&
+                (c.width == 0 || c.src) && c.dst,
+            "arena copy rectangle out of its rows");
   std::stable_sort(copies.begin(), copies.end(), [](const CopyDesc& x, const CopyDesc& y) {
     return uint64_t(x.height) * x.fill > uint64_t(y.height) * y.fill;
   });
@@ -544,8 +548,6 @@ void run_copy_batch(ppk_context* ctx, hipStream_t stream, const std::vector<Copy
     uint64_t most = 0;
     for (size_t i = 0; i < n; ++i) {
       const CopyDesc& c = copies[first + i];
-      require(c.width <= c.fill && c.fill <= c.dpitch && c.fill <= 0xffffffffu && (c.width == 0 || c.width <= c.spitch),
-              "arena copy rectangle out of its rows");
       uint32_t unit = 16;
       while (unit > 1 && (c.width % unit || c.fill % unit || c.spitch % unit || c.dpitch % unit ||
                           !aligned(c.src, unit) || !aligned(c.dst, unit)))
