@@ -569,6 +569,48 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
 // combines it with every split's (m, z, y) by log-sum-exp weights, divides.
 // Rows with past > capacity (or beyond the launched coverage) give NaN.
 // ---------------------------------------------------------------------------
+// Log-sum-exp combine of one row's `nsplits` partial records, one wave: the
+// combined max m (at least m0), the sum z of 2^(m_s - m) z_s, and y for this
+// lane's D/64 channels, sum_s 2^(m_s - m) y_s, added in split order. Lane s
+// loads record s's (m, z); the y rows load eight splits at a time with all
+// eight loads issued before the first use, so the chain costs one memory
+// round trip per eight splits instead of one per split.
+template <int D>
+__device__ __forceinline__ void combine_records(const float* mz, const float* py, uint32_t nsplits, int lane,
+                                                float m0, float& m, float& z, float (&y)[D / ppk::kWave]) {
+  constexpr int EPL = D / ppk::kWave;
+  float mm = m0;
+  for (uint32_t s = lane; s < nsplits; s += ppk::kWave) mm = fmaxf(mm, mz[2 * s]);
+  m = wave_max(mm);
+  z = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) y[e] = 0.f;
+  for (uint32_t s0 = 0; s0 < nsplits; s0 += ppk::kWave) {
+    const uint32_t s = s0 + uint32_t(lane);
+    const float ms = s < nsplits ? mz[2 * s] : -INFINITY;
+    const float zs = s < nsplits ? mz[2 * s + 1] : 0.f;
+    const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m);
+    z = fmaf(w, zs, z);
+    const uint32_t cnt = min(uint32_t(ppk::kWave), nsplits - s0);
+    for (uint32_t i = 0; i < cnt; i += 8) {
+      float v[8][EPL];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t si = s0 + min(i + uint32_t(k), cnt - 1);  // clamp: always a loaded record
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[k][e] = py[size_t(si) * D + size_t(lane) * EPL + e];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float wk = i + uint32_t(k) < cnt ? __shfl(w, int(i) + k) : 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) y[e] = fmaf(wk, v[k][e], y[e]);
+      }
+    }
+  }
+  z = wave_sum(z);
+}
+
 template <int D>
 __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   constexpr int EPL = D / ppk::kWave;
@@ -587,22 +629,9 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kv[e], d);
   const float s_cur = wave_sum(d) * a.scale_log2;
 
-  const float* mz = a.part_mz + size_t(row) * a.nsplits * 2;
-  const float* py = a.part_y + size_t(row) * a.nsplits * D + size_t(lane) * EPL;
-  float m = s_cur;
-  for (uint32_t s = lane; s < a.nsplits; s += ppk::kWave) m = fmaxf(m, mz[2 * s]);
-  m = wave_max(m);
-
-  float y[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) y[e] = 0.f;
-  float zsum = 0.f;
-  for (uint32_t s = 0; s < a.nsplits; ++s) {
-    const float w = mz[2 * s] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mz[2 * s] - m);
-    zsum = fmaf(w, mz[2 * s + 1], zsum);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) y[e] = fmaf(w, py[size_t(s) * D + e], y[e]);
-  }
+  float m, zsum, y[EPL];
+  combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
+                     lane, s_cur, m, zsum, y);
   const float wc = __builtin_amdgcn_exp2f(s_cur - m);
   zsum += wc;
 #pragma unroll
@@ -858,21 +887,9 @@ __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
   const uint32_t row = blockIdx.x;
   const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
   const bool valid = len > 0 && len <= a.size && uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
-  const float* mz = a.part_mz + size_t(row) * a.nsplits * 2;
-  const float* py = a.part_y + size_t(row) * a.nsplits * D + size_t(lane) * EPL;
-  float m = -INFINITY;
-  for (uint32_t s = lane; s < a.nsplits; s += ppk::kWave) m = fmaxf(m, mz[2 * s]);
-  m = wave_max(m);
-  float y[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) y[e] = 0.f;
-  float zsum = 0.f;
-  for (uint32_t s = 0; s < a.nsplits; ++s) {
-    const float w = mz[2 * s] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mz[2 * s] - m);
-    zsum = fmaf(w, mz[2 * s + 1], zsum);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) y[e] = fmaf(w, py[size_t(s) * D + e], y[e]);
-  }
+  float m, zsum, y[EPL];
+  combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
+                     lane, -INFINITY, m, zsum, y);
   const size_t base = size_t(row) * D + size_t(lane) * EPL;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
