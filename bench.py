@@ -33,6 +33,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--head-dim", type=int, default=128)
     p.add_argument("--context", type=int, default=8192)
     p.add_argument("--split", type=int, default=0, help="tokens per split (0 = library policy)")
+    p.add_argument("--config", type=int, choices=(1, 2, 3, 4, 5), default=5,
+                   help="BASELINE config: 5 (default) is the headline workload; 1, 3, 4 are the latency-bound "
+                        "decode shapes and 2 the append-only shape, timed warm and cold (HBM) with the same "
+                        "fields")
     p.add_argument("--kv", choices=("int8", "bf16", "f32"), default="int8",
                    help="int8 (default, the headline workload) or the float-KV decode path over a bf16/f32 store")
     p.add_argument("--sampler", action="store_true",
@@ -40,6 +44,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--arena", action="store_true",
                    help="time the KV arena manager: joining prefilled caches into batch arenas, then decode rounds "
                         "of one-token appends over --layers layers with a shared write plan")
+    p.add_argument("--dequantize", choices=("bf16", "f32", "f16"), default=None,
+                   help="time ppk_dequantize (int8 -> DTYPE) over one tensor of the headline history "
+                        "(B*H rows x --context tokens x D)")
     p.add_argument("--layers", type=int, default=24)
     p.add_argument("--prefill", type=int, default=1000)
     p.add_argument("--choices", type=int, default=2048)
@@ -55,19 +62,44 @@ def parse() -> argparse.Namespace:
     return p.parse_args()
 
 
-def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args) -> dict:
-    """The reference's Candle CPU decode (restated in C, oracle/) on a bounded sample of head rows."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _time_cpu(fn, seconds: float, max_reps: int = 1000) -> tuple[int, float]:
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= max_reps:
+            return reps, el
+
+
+def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args, *, threads: int | None = None,
+                 rows: int | None = None, seconds: float | None = None, context: int | None = None,
+                 repeat: int = 1, what: str = "") -> dict:
+    """The reference's Candle CPU decode (restated in C, oracle/) on a bounded sample of head rows.
+
+    The sample is the first `rows` head rows (whole sequences); its time is scaled by total/sampled rows
+    and by `repeat` (identical layers of one step)."""
     import numpy as np
-    import torch
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # noqa: E402  (CPU baseline leg only)
 
     rows_total = q.shape[0]
-    n = min(args.cpu_rows, rows_total)
+    n = min(args.cpu_rows if rows is None else rows, rows_total)
     n -= n % heads
     n = max(n, heads)
-    L = args.context
+    L = args.context if context is None else context
     q_h = q[:n].float().reshape(n, -1).cpu().numpy()
     k_h = kc[:n, :L].cpu().numpy()
     v_h = vc[:n, :L].cpu().numpy()
@@ -76,29 +108,16 @@ def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args) -> dict:
     sk_h = kn.float().reshape(rows_total, -1)[:n].cpu().numpy()
     sv_h = vn.float().reshape(rows_total, -1)[:n].cpu().numpy()
     past_h = past[: n // heads].cpu().numpy().astype(np.uint32)
-    threads = max(1, min(os.cpu_count() or 1, 16))
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.cpu_baseline(q_h, k_h, v_h, ks_h, vs_h, sk_h, sv_h, past_h, heads, threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or reps >= 1000:
-            break
-    per_rep_us = el / reps * 1e6
-    us_per_step = per_rep_us * rows_total / n
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    if threads is None:
+        threads = max(1, min(os.cpu_count() or 1, 16))
+    reps, el = _time_cpu(lambda: oracle.cpu_baseline(q_h, k_h, v_h, ks_h, vs_h, sk_h, sv_h, past_h, heads, threads),
+                         args.cpu_seconds if seconds is None else seconds)
+    scale = rows_total / n * repeat
+    us_per_step = el / reps * 1e6 * scale
     return {"value": round(us_per_step, 1), "unit": "us/step", "cores": threads, "kind": "port",
-            "sample": f"{n} of {rows_total} head rows x {L} tokens (Candle CPU path restated in C, "
-                      f"oracle/ppk_oracle.c cpu_baseline_decode), {reps} reps in {el:.1f} s, scaled x{rows_total / n:g}",
-            "cpu_model": model}
+            "sample": f"{n} of {rows_total} head rows{what} (Candle CPU path restated in C, "
+                      f"oracle/ppk_oracle.c cpu_baseline_decode), {reps} reps in {el:.1f} s, scaled x{scale:g}",
+            "cpu_model": _cpu_model()}
 
 
 def bench_float(args) -> int:
@@ -423,19 +442,394 @@ def bench_arena(args) -> int:
     return 0
 
 
+# latency-bound shapes of the same path (the headline is config 5).
+CONFIGS = {
+    1: {"batch": 1, "heads": 16, "head_dim": 64, "lengths": [512], "layers": 1, "query": "f32",
+        "workload": "BASELINE config 1: decode step (append + attention) over a 512-token int8 history, f32 q/K/V"},
+    3: {"batch": 1, "heads": 16, "head_dim": 128, "lengths": [2048], "layers": 24, "query": "bf16",
+        "workload": "BASELINE config 3: 24 layers x decode step (append + attention + merge) over 2048-token "
+                    "int8 histories, one stream"},
+    4: {"batch": 8, "heads": 16, "head_dim": 128, "lengths": None, "layers": 1, "query": "bf16",
+        "workload": "BASELINE config 4: decode step over ragged int8 histories, lengths ~ U[256, 4096] (seeded)"},
+}
+COLD_BYTES = 1 << 30  # cold runs rotate over at least this much distinct history (>> the 256 MB MALL)
+
+
+def _event_times(fn, steps: int, stream, per_step: bool):
+    """Mean us over `steps` calls bracketed by two events, or the per-call durations with one event
+    between consecutive calls (the event packets then count in every interval)."""
+    import torch
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1 if per_step else 2)]
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for i in range(steps):
+        fn(i)
+        if per_step:
+            ev[i + 1].record(stream)
+    if not per_step:
+        ev[1].record(stream)
+    torch.cuda.synchronize()
+    if per_step:
+        return [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(steps)]
+    return ev[0].elapsed_time(ev[1]) * 1e3 / steps
+
+
+def bench_config(args) -> int:
+    """BASELINE configs 1, 3, 4: decode steps (append of the current token + attention [+ merge]) at the
+    shapes of the reference's decode calls; warm (history resident in cache where it fits) and cold
+    (steps rotate over >= 1 GiB of distinct history copies, so every step reads HBM)."""
+    import statistics
+
+    import numpy as np
+    import torch
+    import ppk
+    from ppk import synthetic
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, layers = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["layers"]
+    if cfg["lengths"] is None:
+        lengths = [int(x) for x in np.random.default_rng(SEED).integers(256, 4097, size=B)]
+    else:
+        lengths = cfg["lengths"] * B
+    rows, L = B * H, max(lengths)
+    cap = L + 1
+    qdt = torch.float32 if cfg["query"] == "f32" else torch.bfloat16
+    qb = 4 if qdt == torch.float32 else 2
+    hist_bytes = sum(lengths) * H * (2 * D + 8)  # per layer: K + V codes and scales of the live history
+    copies = 1 + -(-COLD_BYTES // (hist_bytes * layers))
+    print(f"# bench config {args.config}: B={B} H={H} D={D} lengths={lengths} layers={layers}, "
+          f"{copies} history copies for the cold runs", file=sys.stderr, flush=True)
+
+    # One history per layer, replicated into `copies` distinct arenas.
+    kc = torch.empty((copies, layers, rows, cap, D), dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((copies, layers, rows, cap), dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    for li in range(layers):
+        synthetic.fill_history(kc[0, li], vc[0, li], ks[0, li], vs[0, li], L, H, SEED + 100 * li)
+    for c in range(1, copies):
+        kc[c].copy_(kc[0])
+        vc[c].copy_(vc[0])
+        ks[c].copy_(ks[0])
+        vs[c].copy_(vs[0])
+    g = torch.Generator(device=dev).manual_seed(SEED + 1)
+    q = [torch.randn((rows, 1, D), generator=g, device=dev).to(qdt) for _ in range(layers)]
+    kn = [torch.randn((rows, 1, D), generator=g, device=dev).to(qdt) for _ in range(layers)]
+    vn = [torch.randn((rows, 1, D), generator=g, device=dev).to(qdt) for _ in range(layers)]
+    past = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    out = torch.empty((rows, 1, D), dtype=torch.float32, device=dev)
+    steps = [[ppk.DecodeStep(q[li], kc[c, li], vc[c, li], ks[c, li], vs[c, li], kn[li], vn[li], past, H,
+                             split_tokens=args.split, max_past=L, out=out) for li in range(layers)]
+             for c in range(copies)]
+    split, ngroups = steps[0][0].split_tokens, steps[0][0].ngroups
+    torch.cuda.synchronize()
+
+    def warm(_i):
+        for s in steps[0]:
+            s()
+
+    def cold(i):
+        for s in steps[i % copies]:
+            s()
+
+    stream = torch.cuda.current_stream(dev)
+    print("# bench: warmup", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        warm(i)
+    warm_mean = _event_times(warm, args.steps, stream, per_step=False)
+    warm_each = _event_times(warm, args.steps, stream, per_step=True)
+    for i in range(copies):
+        cold(i)
+    cold_mean = _event_times(lambda i: cold(i + 1), args.steps, stream, per_step=False)
+    cold_each = _event_times(lambda i: cold(i + 1), args.steps, stream, per_step=True)
+
+    # Graph replay of the warm step: the same launches with the host side removed.
+    graph_us = None
+    try:
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            warm(0)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            warm(0)
+        for _ in range(10):
+            graph.replay()
+        graph_us = _event_times(lambda _i: graph.replay(), args.steps, stream, per_step=False)
+        del graph
+    except RuntimeError as e:  # capture unsupported on this stack: report eager numbers only
+        print(f"# bench: graph replay skipped: {e}", file=sys.stderr, flush=True)
+
+    # Roofline of the decode kernel (and the merge kernel when rows span blocks), traced launches, warm.
+    ppk.kernel_stats(ppk.PPK_KERNEL_ATTENTION, reset=True)
+    ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_MERGE, reset=True)
+    ppk.set_profiling(True)
+    for i in range(args.steps):
+        warm(i)
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_ATTENTION, reset=True)
+    m_launches, merge_ms = ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_MERGE, reset=True)
+    kernel_avg_us = kernel_ms / max(launches, 1) * 1e3
+
+    # Algorithmic bytes of one layer: live history + q + current k, v + f32 out + appended codes/scales.
+    layer_bytes = hist_bytes + rows * D * qb + 2 * rows * D * qb + rows * D * 4 + 2 * rows * (D + 4)
+    kernel_bytes = layer_bytes if ngroups == 1 else layer_bytes - rows * D * 4
+    step_bytes = layer_bytes * layers
+    achieved = kernel_bytes / (kernel_avg_us * 1e-6) / 1e9
+    tag = f"c{args.config}_b{B}_h{H}_d{D}"
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"ppk_decode_{tag}_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            with open(tpath) as f:
+                t = json.load(f)
+            if t.get("split") == split and t.get("workload") == tag:
+                traffic = t.get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    result = {
+        "metric": METRIC, "value": round(warm_mean, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(warm_mean / 1e3, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels, quantised on device; "
+                f"{cfg['query']} q and current K/V)",
+        "config": {"workload": cfg["workload"], "batch": B, "heads": H, "head_dim": D, "lengths": lengths,
+                   "layers": layers, "capacity": cap, "kv": "int8 + f32 scales", "query": cfg["query"],
+                   "tokens_per_wave": split, "blocks_per_row": ngroups,
+                   "launches_per_step": layers * (1 if ngroups == 1 else 2)},
+        "median_us": round(statistics.median(warm_each), 2),
+        "cold": {"mean_us": round(cold_mean, 2), "median_us": round(statistics.median(cold_each), 2),
+                 "history_copies": copies, "rotated_bytes": copies * hist_bytes * layers,
+                 "step_hbm_gbps": round(step_bytes / (cold_mean * 1e-6) / 1e9, 1)},
+        "per_step_events_note": "median_us values come from a pass with one event between consecutive steps",
+        "graph_replay_us": None if graph_us is None else round(graph_us, 2),
+        "algorithmic_bytes_per_step": step_bytes,
+        "step_hbm_gbps": round(step_bytes / (warm_mean * 1e-6) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "ppk_decode_d%d" % D, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": kernel_bytes,
+                     "avg_launch_us": round(kernel_avg_us, 2), "launches": launches,
+                     "merge_avg_launch_us": round(merge_ms / m_launches * 1e3, 2) if m_launches else None},
+    }
+    if not args.no_cpu_baseline:
+        print("# bench: cpu baseline", file=sys.stderr, flush=True)
+        a = (q[0], kc[0, 0], vc[0, 0], ks[0, 0], vs[0, 0], kn[0], vn[0], past, H, args)
+        what = f" x {L} tokens" if len(set(lengths)) == 1 else " (ragged)"
+        what += f", one of {layers} identical layers" if layers > 1 else ""
+        result["cpu_baseline"] = cpu_baseline(*a, rows=rows, context=L, repeat=layers, what=what,
+                                              seconds=args.cpu_seconds / 2)
+        result["cpu_baseline_1thread"] = cpu_baseline(*a, threads=1, rows=rows, context=L, repeat=layers, what=what,
+                                                      seconds=args.cpu_seconds / 2)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def bench_append(args) -> int:
+    """append only. One fp16 token of K and V for B=1, H=16, D=128 quantised into
+    slot 1000 of capacity-4096 int8 arenas (ppk_quantize_append); latency-bound, its parity bar is
+    bit-exactness (tests/test_gpu_quantize.py). Warm and cold (rotating arena copies) timings."""
+    import statistics
+
+    import numpy as np
+    import torch
+    import ppk
+    from ppk import synthetic
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, cap, filled = 1, 16, 128, 4096, 1000
+    rows = B * H
+    copies = 1 + -(-COLD_BYTES // (2 * rows * cap * (D + 4)))
+    kc = torch.zeros((copies, rows, cap, D), dtype=torch.uint8, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((copies, rows, cap), dtype=torch.float32, device=dev)
+    vs = torch.zeros_like(ks)
+    synthetic.fill_history(kc[0], vc[0], ks[0], vs[0], filled, H, SEED)
+    kn = synthetic.history_chunk(SEED, 2, 0, rows, H, 0, 1, D, dev, torch.float16).reshape(B, H, 1, D).contiguous()
+    vn = synthetic.history_chunk(SEED, 3, 0, rows, H, 0, 1, D, dev, torch.float16).reshape(B, H, 1, D).contiguous()
+    past = torch.full((B,), filled, dtype=torch.int32, device=dev)
+    calls = [ppk.AppendKV(kn, vn, past, kc[c], vc[c], ks[c], vs[c]) for c in range(copies)]
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    for i in range(args.warmup):
+        calls[0]()
+    warm_mean = _event_times(lambda _i: calls[0](), args.steps, stream, per_step=False)
+    warm_each = _event_times(lambda _i: calls[0](), args.steps, stream, per_step=True)
+    cold_mean = _event_times(lambda i: calls[1 + i % (copies - 1)](), args.steps, stream, per_step=False)
+    ppk.kernel_stats(ppk.PPK_KERNEL_APPEND, reset=True)
+    ppk.set_profiling(True)
+    for _ in range(args.steps):
+        calls[0]()
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_APPEND, reset=True)
+    kernel_avg_us = kernel_ms / max(launches, 1) * 1e3
+    nbytes = 2 * rows * D * 2 + 2 * rows * (D + 4)  # read fp16 K, V; write codes + scales
+    achieved = nbytes / (kernel_avg_us * 1e-6) / 1e9
+    result = {
+        "metric": METRIC, "value": round(warm_mean, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(warm_mean / 1e3, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels, fp16 new K/V)",
+        "config": {"workload": "BASELINE config 2: append only, one fp16 token of K and V into slot 1000 of "
+                               "capacity-4096 int8 arenas (ppk_quantize_append)",
+                   "batch": B, "heads": H, "head_dim": D, "capacity": cap, "slot": filled},
+        "median_us": round(statistics.median(warm_each), 2),
+        "cold": {"mean_us": round(cold_mean, 2), "arena_copies": copies},
+        "roofline": {"bound": "hbm", "kernel": "ppk_quantize_d%d (append)" % D, "achieved": round(achieved, 2),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 6),
+                     "traffic": None, "algorithmic_bytes_per_launch": nbytes,
+                     "avg_launch_us": round(kernel_avg_us, 2), "launches": launches,
+                     "note": "latency-bound: 8.7 KB per launch"},
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle  # noqa: E402  (CPU baseline leg only)
+
+        src = np.stack([kn.float().cpu().numpy(), vn.float().cpu().numpy()])
+        past_h = np.array([filled], np.uint32)
+        arenas = [(kc[0].cpu().numpy(), ks[0].cpu().numpy()), (vc[0].cpu().numpy(), vs[0].cpu().numpy())]
+
+        def cpu_append():
+            for x, (codes, scales) in zip(src, arenas):
+                oracle.append(x, past_h, codes, scales)
+
+        reps, el = _time_cpu(cpu_append, args.cpu_seconds / 2, max_reps=100000)
+        result["cpu_baseline"] = {"value": round(el / reps * 1e6, 2), "unit": "us/step", "cores": 1, "kind": "port",
+                                  "sample": f"the whole append (K and V, 16 rows x {D}), C oracle oracle_append, "
+                                            f"{reps} reps in {el:.1f} s",
+                                  "cpu_model": _cpu_model()}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def bench_dequantize(args) -> int:
+    """Int8 -> bf16/f32/f16 dequantization (ppk_dequantize, the prefill path's `dequantize`) of one history
+    tensor at the headline shape: B*H rows x ctx tokens x D codes + one f32 scale per token."""
+    import ctypes
+    import statistics
+
+    import numpy as np
+    import torch
+    import ppk
+    from ppk import _abi, synthetic
+    from ppk import int8_kv_ops as ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, L = args.batch, args.heads, args.head_dim, args.context
+    rows = B * H
+    dt = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}[args.dequantize]
+    print(f"# bench dequantize: {rows} rows x {L} tokens x {D} -> {args.dequantize}", file=sys.stderr, flush=True)
+    kc = torch.empty((rows, L, D), dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((rows, L), dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    synthetic.fill_history(kc, vc, ks, vs, L, H, SEED)
+    del vc, vs
+    out = torch.empty((rows, L, D), dtype=dt, device=dev)
+    a = _abi.PpkDequantizeArgs(struct_size=ctypes.sizeof(_abi.PpkDequantizeArgs), out_dtype=ops._DTYPES[dt],
+                               codes=kc.data_ptr(), scales=ks.data_ptr(), out=out.data_ptr(), rows=rows * L,
+                               head_dim=D, round_bf16=0)
+    ctx, fn, ref = ops.context(dev), ops.lib().ppk_dequantize, ctypes.byref(a)
+    stream = torch.cuda.current_stream(dev)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        torch.neg(src, out=torch.empty_like(src))
+        torch.cuda.synchronize()
+        del src
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def call(_i=0):
+        ops.check(fn(ctx, sp, ref), "ppk_dequantize")
+
+    for _ in range(args.warmup):
+        call()
+    mean_us = _event_times(call, args.steps, stream, per_step=False)
+    each = _event_times(call, args.steps, stream, per_step=True)
+    ppk.kernel_stats(ppk.PPK_KERNEL_DEQUANTIZE, reset=True)
+    ppk.set_profiling(True)
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_DEQUANTIZE, reset=True)
+    kernel_us = kernel_ms / max(launches, 1) * 1e3
+    nbytes = rows * L * D + rows * L * 4 + rows * L * D * out.element_size()
+    achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"ppk_dequantize_{args.dequantize}_b{B}_h{H}_d{D}_ctx{L}_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            with open(tpath) as f:
+                t = json.load(f)
+            if t.get("workload") == f"B{B}H{H}D{D}L{L}{args.dequantize}":
+                traffic = t.get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    result = {
+        "metric": "int8 -> %s dequantize, us per history tensor + achieved HBM GB/s" % args.dequantize,
+        "value": round(mean_us, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(mean_us / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels, quantised on device)",
+        "config": {"workload": "dequantize one int8 history tensor (ppk_dequantize)", "rows": rows, "tokens": L,
+                   "head_dim": D, "out": args.dequantize},
+        "median_us": round(statistics.median(each), 2),
+        "step_hbm_gbps": round(nbytes / (mean_us * 1e-6) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "ppk_dequantize", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(kernel_us, 2),
+                     "launches": launches},
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle  # noqa: E402  (CPU baseline leg only)
+
+        n = min(rows, 16)
+        c_h, s_h = kc[:n].cpu().numpy(), ks[:n].cpu().numpy()
+        reps, el = _time_cpu(lambda: oracle.dequantize(c_h, s_h, round_bf16=dt == torch.bfloat16), args.cpu_seconds / 2)
+        result["cpu_baseline"] = {"value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/call", "cores": 1,
+                                  "kind": "port",
+                                  "sample": f"{n} of {rows} rows x {L} tokens (C oracle oracle_dequantize, f32 out"
+                                            f"{' rounded to bf16' if dt == torch.bfloat16 else ''}), {reps} reps "
+                                            f"in {el:.1f} s, scaled x{rows / n:g}",
+                                  "cpu_model": _cpu_model()}
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the int8 KV decode path shards by "
-                                   "sequence or head with no collective on the hot path (see DESIGN.md)",
+                                   "sequence or head with no collective on the hot path; run it once per GPU",
                           "n_gpus": args.gpus}))
         return 2
     if args.sampler:
         return bench_sampler(args)
     if args.arena:
         return bench_arena(args)
+    if args.dequantize:
+        return bench_dequantize(args)
     if args.kv != "int8":
         return bench_float(args)
+    if args.config == 2:
+        return bench_append(args)
+    if args.config != 5:
+        return bench_config(args)
     import torch
     import ppk
     from ppk import synthetic
@@ -551,7 +945,9 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         print("# bench: cpu baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, H, args)
+        result["cpu_baseline"] = cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, H, args, what=f" x {L} tokens")
+        result["cpu_baseline_1thread"] = cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, H, args, threads=1,
+                                                      rows=H, seconds=args.cpu_seconds / 2, what=f" x {L} tokens")
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

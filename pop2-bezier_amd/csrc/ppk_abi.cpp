@@ -277,8 +277,13 @@ void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArg
   k.head_dim = a.head_dim;
   k.out_dtype = a.out_dtype;
   k.round_bf16 = a.round_bf16 ? 1u : 0u;
-  const uint64_t chunks = a.rows * (a.head_dim / 16);
-  const uint64_t grid = std::min<uint64_t>((chunks + 255) / 256, uint64_t(std::max(ctx->cu_count, 1)) * 32);
+  // One lane per 16-byte output chunk (8 codes, or 4 for f32) and batches of
+  // 8 chunks per lane: one batch per lane, up to 128 blocks of 256 lanes per
+  // CU, beyond which lanes loop over a grid-stride range.
+  constexpr uint64_t kBlocksPerCu = 128, kChunksPerBatch = 8;
+  const uint64_t chunks = a.rows * a.head_dim / (a.out_dtype == PPK_F32 ? 4 : 8);
+  const uint64_t grid = std::min<uint64_t>((chunks + 256 * kChunksPerBatch - 1) / (256 * kChunksPerBatch),
+                                           uint64_t(std::max(ctx->cu_count, 1)) * kBlocksPerCu);
   DeviceGuard guard(ctx->device);
   launch(ctx, PPK_KERNEL_DEQUANTIZE, kDequantize, uint32_t(grid), 256, 0, stream, k);
 }

@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "ppk_kernel_args.h"
 
 namespace {
@@ -188,39 +190,87 @@ __device__ __forceinline__ void quantize_body(const ppk::QuantizeArgs& a) {
 // ---------------------------------------------------------------------------
 // Dequantize: 16 codes per thread (one dwordx4), grid-stride.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void dequantize_body(const ppk::DequantizeArgs& a) {
+using u2 = uint32_t __attribute__((ext_vector_type(2)));
+
+// Dequantization in units of one 16-byte output chunk: E = 8 codes for a
+// 16-bit output, 4 for f32. Lane l of a wave handles units i, i + stride, ...
+// so every load instruction of a wave reads 64*E consecutive code bytes and
+// every store instruction writes 1 KiB of consecutive output. Each lane keeps
+// two batches of R units: the next batch's loads are issued before the
+// current batch's stores, so a load never waits behind the previous batch's
+// store acknowledgements (loads and stores share one in-order counter). The
+// host sizes the grid for one batch per lane up to 128 blocks per CU (the
+// measured optimum; the grid-stride loop covers larger inputs).
+template <int E, uint32_t OUT, bool ROUND>
+__device__ __forceinline__ void dequantize_units(const ppk::DequantizeArgs& a) {
 #pragma clang fp contract(off)
-  const uint32_t chunks_per_row = a.head_dim / 16;
-  const uint64_t chunks = a.rows * chunks_per_row;
+  constexpr int R = 8;
+  using Raw = typename std::conditional<E == 8, u2, uint32_t>::type;
+  const uint64_t units = a.rows * (a.head_dim / E);
   const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
-  for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < chunks; i += stride) {
-    const uint64_t row = i / chunks_per_row;
-    const u4 raw = *reinterpret_cast<const u4*>(a.codes + i * 16);
-    const float s = a.scales[row];
-    float f[16];
+  const uint32_t row_shift = __builtin_ctz(a.head_dim / E);  // units per token row: a power of two
+  uint64_t base = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (base >= units) return;
+  Raw cur[R], nxt[R];
+  float cs[R], ns[R];
+  auto load = [&](uint64_t b, Raw (&raw)[R], float (&sc)[R]) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float v = sbyte(raw[w], k) * s;
-        f[4 * w + k] = a.round_bf16 ? round_bf16(v) : v;
-      }
-    if (a.out_dtype == kF32) {
-      f4* o = reinterpret_cast<f4*>(static_cast<float*>(a.out) + i * 16);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) o[w] = f4{f[4 * w], f[4 * w + 1], f[4 * w + 2], f[4 * w + 3]};
-    } else {
-      uint32_t h[8];
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        const uint16_t lo = a.out_dtype == kBF16 ? f32_to_bf16_bits(f[2 * w]) : f32_to_f16_bits(f[2 * w]);
-        const uint16_t hi = a.out_dtype == kBF16 ? f32_to_bf16_bits(f[2 * w + 1]) : f32_to_f16_bits(f[2 * w + 1]);
-        h[w] = uint32_t(lo) | (uint32_t(hi) << 16);
-      }
-      u4* o = reinterpret_cast<u4*>(static_cast<uint16_t*>(a.out) + i * 16);
-      o[0] = u4{h[0], h[1], h[2], h[3]};
-      o[1] = u4{h[4], h[5], h[6], h[7]};
+    for (int r = 0; r < R; ++r) {
+      const uint64_t u = min(b + r * stride, units - 1);  // clamp: always in bounds, extra units unused
+      raw[r] = __builtin_nontemporal_load(reinterpret_cast<const Raw*>(a.codes) + u);
+      sc[r] = a.scales[u >> row_shift];
     }
+  };
+  load(base, cur, cs);
+  for (; base < units; base += R * stride) {
+    const bool more = base + R * stride < units;
+    if (more) load(base + R * stride, nxt, ns);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint64_t u = base + r * stride;
+      if (u >= units) break;
+      float f[E];
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        uint32_t w;
+        if constexpr (E == 8) w = cur[r][k / 4];
+        else w = cur[r];
+        const float v = sbyte(w, k % 4) * cs[r];
+        f[k] = ROUND ? round_bf16(v) : v;
+      }
+      if constexpr (E == 4) {
+        __builtin_nontemporal_store(f4{f[0], f[1], f[2], f[3]}, static_cast<f4*>(a.out) + u);
+      } else {
+        uint32_t h[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint16_t lo = OUT == kBF16 ? f32_to_bf16_bits(f[2 * w]) : f32_to_f16_bits(f[2 * w]);
+          const uint16_t hi = OUT == kBF16 ? f32_to_bf16_bits(f[2 * w + 1]) : f32_to_f16_bits(f[2 * w + 1]);
+          h[w] = uint32_t(lo) | (uint32_t(hi) << 16);
+        }
+        __builtin_nontemporal_store(u4{h[0], h[1], h[2], h[3]}, static_cast<u4*>(a.out) + u);
+      }
+    }
+    if (!more) break;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      cur[r] = nxt[r];
+      cs[r] = ns[r];
+    }
+  }
+}
+
+// Output type and the bf16 pre-rounding are fixed per instantiation (a bf16
+// output already rounds to bf16, so it needs no pre-rounding).
+__device__ __forceinline__ void dequantize_body(const ppk::DequantizeArgs& a) {
+  if (a.out_dtype == kF32) {
+    if (a.round_bf16) dequantize_units<4, kF32, true>(a);
+    else dequantize_units<4, kF32, false>(a);
+  } else if (a.out_dtype == kBF16) {
+    dequantize_units<8, kBF16, false>(a);
+  } else {
+    if (a.round_bf16) dequantize_units<8, kF16, true>(a);
+    else dequantize_units<8, kF16, false>(a);
   }
 }
 
@@ -396,6 +446,17 @@ __device__ __forceinline__ void accumulate_batch(const u4 (&raw)[U], float scale
   }
 }
 
+// Log2-domain score of the current token (q . sk * scale), which comes from
+// the scratch copy, not the arena: each lane dots its 16-channel chunk.
+template <int D>
+__device__ __forceinline__ float current_score(const ppk::DecodeArgs& a, const float (&kv)[16],
+                                               const float (&qr)[16]) {
+  float d = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) d = fmaf(qr[i], kv[i], d);
+  return group_sum<D / 16>(d) * a.scale_log2;
+}
+
 // Streams this wave's n tokens (from `begin`) of one row: phase K scores,
 // phase V accumulation. Two batches (A, B) ping-pong so the next batch's loads
 // are always in flight while the current one is consumed; addresses past the
@@ -420,33 +481,59 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   const float* ksb = a.ks + tok0;
   const float* vsb = a.vs + tok0;
   const uint32_t ntiles = (n + TPL - 1) / TPL;
-  QInt qi{};
-  float sl2 = a.scale_log2;
-  if constexpr (!BF16H) {
-    qi = quantize_query<LPT>(qr);
-    sl2 *= qi.unscale;
-  }
-
-  // Batch A of the last phase-K iteration already fetches phase V's first
-  // batch, so the V stream starts without a full memory latency.
   u4 ra[U], rb[U];
   float sa, sb;
   float mloc = -INFINITY;
-  load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
-  for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
-    load_batch<D, U>(kb, ksb, t0 + U, n, j, lane, rb, sb);
-    mloc = score_batch<D, BF16H, U>(ra, sa, t0, n, j, c, qr, qi, sl2, s_lds, mloc);
-    const bool last = t0 + 2 * U >= ntiles;
-    load_batch<D, U>(last ? vb : kb, last ? vsb : ksb, last ? 0u : t0 + 2 * U, n, j, lane, ra, sa);
-    mloc = score_batch<D, BF16H, U>(rb, sb, t0 + U, n, j, c, qr, qi, sl2, s_lds, mloc);
-  }
-  float m = mloc;
+  float m, z = 0.f;
+  QInt qi{};
+  float sl2 = a.scale_log2;
+  if (ntiles <= 2 * U) {
+    // Short stream (at most two batches per phase, e.g. many small splits of
+    // short rows): K and V of the whole wave are requested together, so the
+    // wave waits on one memory round trip instead of a K trip and a V trip.
+    const bool two = ntiles > U;  // uniform per wave
+    u4 va[U], vb2[U];
+    float vsa, vsb2;
+    load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
+    load_batch<D, U>(vb, vsb, 0, n, j, lane, va, vsa);
+    if (two) {
+      load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
+      load_batch<D, U>(vb, vsb, U, n, j, lane, vb2, vsb2);
+    }
+    if constexpr (!BF16H) {
+      qi = quantize_query<LPT>(qr);
+      sl2 *= qi.unscale;
+    }
+    mloc = score_batch<D, BF16H, U>(ra, sa, 0, n, j, c, qr, qi, sl2, s_lds, mloc);
+    if (two) mloc = score_batch<D, BF16H, U>(rb, sb, U, n, j, c, qr, qi, sl2, s_lds, mloc);
+    m = mloc;
 #pragma unroll
-  for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-  __builtin_amdgcn_wave_barrier();
-
-  float z = 0.f;
-  {
+    for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __builtin_amdgcn_wave_barrier();
+    accumulate_batch<D, BF16H, U>(va, vsa, 0, n, j, lane, m, s_lds, z, out.acc);
+    if (two) accumulate_batch<D, BF16H, U>(vb2, vsb2, U, n, j, lane, m, s_lds, z, out.acc);
+  } else {
+    // The first two K batches do not depend on q: issue them before the query
+    // is quantised, so the q load and its reductions overlap the first memory
+    // round trip. Batch A of the last phase-K iteration already fetches phase
+    // V's first batch, so the V stream starts without a full memory latency.
+    load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
+    load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
+    if constexpr (!BF16H) {
+      qi = quantize_query<LPT>(qr);
+      sl2 *= qi.unscale;
+    }
+    for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
+      if (t0 != 0) load_batch<D, U>(kb, ksb, t0 + U, n, j, lane, rb, sb);
+      mloc = score_batch<D, BF16H, U>(ra, sa, t0, n, j, c, qr, qi, sl2, s_lds, mloc);
+      const bool last = t0 + 2 * U >= ntiles;
+      load_batch<D, U>(last ? vb : kb, last ? vsb : ksb, last ? 0u : t0 + 2 * U, n, j, lane, ra, sa);
+      mloc = score_batch<D, BF16H, U>(rb, sb, t0 + U, n, j, c, qr, qi, sl2, s_lds, mloc);
+    }
+    m = mloc;
+#pragma unroll
+    for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __builtin_amdgcn_wave_barrier();
     for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
       load_batch<D, U>(vb, vsb, t0 + U, n, j, lane, rb, sb);
       accumulate_batch<D, BF16H, U>(ra, sa, t0, n, j, lane, m, s_lds, z, out.acc);
@@ -480,7 +567,10 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   const uint32_t p = a.past[row / a.heads];
   const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.ngroups) * W * S;
 
-  // Fused commit of the current token (kernel 1 inside this launch).
+  // Fused commit of the current token (kernel 1 inside this launch). Done
+  // before the stream: deferring it past the stream (its loads issued early)
+  // measured slower at B=32 x 8192 tokens, the commit then adding to the
+  // block's tail instead of overlapping the other waves' ramp-up.
   if (a.append && group == 0) {
     const bool kw = wave == 0, vw = wave == (W > 1 ? 1 : 0);
     if (kw || vw) {
@@ -496,6 +586,18 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
 
   float qr[16];
   load_vec<16>(a.q, size_t(row) * D + size_t(c) * 16, a.q_dtype, qr);
+  // Wave 0 of a block that covers its whole row also folds in the current
+  // token (from the sk/sv scratch): it is scored here, with loads issued
+  // beside q's, so that no memory round trip is left after the stream.
+  const bool final_out = a.ngroups == 1;
+  float s_cur = -INFINITY;
+  float sv[EPL];
+  if (final_out && wave == 0) {
+    float kv[16];
+    load_vec<16>(a.sk, size_t(row) * D + size_t(c) * 16, a.scratch_dtype, kv);
+    load_vec<EPL>(a.sv, size_t(row) * D + size_t(lane) * EPL, a.scratch_dtype, sv);
+    s_cur = current_score<D>(a, kv, qr);
+  }
   const uint32_t begin = (group * W + wave) * S;
   const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
   WavePartial part;
@@ -519,21 +621,6 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   __syncthreads();
   if (wave != 0) return;
 
-  const bool final_out = a.ngroups == 1;
-  float s_cur = -INFINITY;
-  float sv[EPL];
-  if (final_out) {
-    // Current token: each lane dots its 16-channel chunk of q and sk.
-    float qv[16], kv[16];
-    const size_t so = size_t(row) * D + size_t(c) * 16;
-    load_vec<16>(a.q, so, a.q_dtype, qv);
-    load_vec<16>(a.sk, so, a.scratch_dtype, kv);
-    load_vec<EPL>(a.sv, size_t(row) * D + size_t(lane) * EPL, a.scratch_dtype, sv);
-    float d = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) d = fmaf(qv[i], kv[i], d);
-    s_cur = group_sum<LPT>(d) * a.scale_log2;
-  }
   float m = s_cur;
   for (int w = 0; w < W; ++w) m = fmaxf(m, mrg[w * R]);
   float y[EPL], zsum = 0.f;
@@ -575,30 +662,57 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
 // loads record s's (m, z); the y rows load eight splits at a time with all
 // eight loads issued before the first use, so the chain costs one memory
 // round trip per eight splits instead of one per split.
-template <int D>
+template <int D, class CurrentScore>
 __device__ __forceinline__ void combine_records(const float* mz, const float* py, uint32_t nsplits, int lane,
-                                                float m0, float& m, float& z, float (&y)[D / ppk::kWave]) {
+                                                CurrentScore current_score, float& m, float& z,
+                                                float (&y)[D / ppk::kWave]) {
   constexpr int EPL = D / ppk::kWave;
-  float mm = m0;
-  for (uint32_t s = lane; s < nsplits; s += ppk::kWave) mm = fmaxf(mm, mz[2 * s]);
+  // Everything that does not depend on the max is requested first, in one
+  // round trip: the y rows of the first sixteen splits, the (m, z) pairs of
+  // the first 64 splits (kept in registers for the weights), and then
+  // whatever current_score() loads before it returns the extra score that
+  // joins the max (-inf for none).
+  float first[16][EPL];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint32_t si = min(uint32_t(k), nsplits - 1);  // clamp: always a loaded record
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) first[k][e] = py[size_t(si) * D + size_t(lane) * EPL + e];
+  }
+  const uint32_t s_first = min(uint32_t(lane), nsplits - 1);
+  const float m_first = uint32_t(lane) < nsplits ? mz[2 * s_first] : -INFINITY;
+  const float z_first = uint32_t(lane) < nsplits ? mz[2 * s_first + 1] : 0.f;
+  float mm = m_first;
+  for (uint32_t s = lane + ppk::kWave; s < nsplits; s += ppk::kWave) mm = fmaxf(mm, mz[2 * s]);
+  mm = fmaxf(mm, current_score());
   m = wave_max(mm);
   z = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) y[e] = 0.f;
   for (uint32_t s0 = 0; s0 < nsplits; s0 += ppk::kWave) {
     const uint32_t s = s0 + uint32_t(lane);
-    const float ms = s < nsplits ? mz[2 * s] : -INFINITY;
-    const float zs = s < nsplits ? mz[2 * s + 1] : 0.f;
+    float ms = m_first, zs = z_first;
+    if (s0 != 0) {
+      ms = s < nsplits ? mz[2 * s] : -INFINITY;
+      zs = s < nsplits ? mz[2 * s + 1] : 0.f;
+    }
     const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m);
     z = fmaf(w, zs, z);
     const uint32_t cnt = min(uint32_t(ppk::kWave), nsplits - s0);
     for (uint32_t i = 0; i < cnt; i += 8) {
       float v[8][EPL];
+      if (s0 == 0 && i < 16) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t si = s0 + min(i + uint32_t(k), cnt - 1);  // clamp: always a loaded record
+        for (int k = 0; k < 8; ++k)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) v[k][e] = py[size_t(si) * D + size_t(lane) * EPL + e];
+          for (int e = 0; e < EPL; ++e) v[k][e] = i == 0 ? first[k][e] : first[8 + k][e];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t si = s0 + min(i + uint32_t(k), cnt - 1);  // clamp: always a loaded record
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) v[k][e] = py[size_t(si) * D + size_t(lane) * EPL + e];
+        }
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
@@ -619,19 +733,24 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   const uint32_t p = a.past[row / a.heads];
   const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.nsplits) * a.split_tokens;
 
-  float sv[EPL], qv[EPL], kv[EPL];
-  float d = 0.f;
+  float sv[EPL];
+  float s_cur = -INFINITY;
   const size_t base = size_t(row) * D + size_t(lane) * EPL;
-  load_vec<EPL>(a.q, base, a.q_dtype, qv);
-  load_vec<EPL>(a.sk, base, a.scratch_dtype, kv);
-  load_vec<EPL>(a.sv, base, a.scratch_dtype, sv);
+  // The current token (q . sk, and sv): loaded after the records are requested.
+  auto current = [&]() {
+    float qv[EPL], kv[EPL];
+    load_vec<EPL>(a.q, base, a.q_dtype, qv);
+    load_vec<EPL>(a.sk, base, a.scratch_dtype, kv);
+    load_vec<EPL>(a.sv, base, a.scratch_dtype, sv);
+    float d = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kv[e], d);
-  const float s_cur = wave_sum(d) * a.scale_log2;
-
+    for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kv[e], d);
+    s_cur = wave_sum(d) * a.scale_log2;
+    return s_cur;
+  };
   float m, zsum, y[EPL];
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
-                     lane, s_cur, m, zsum, y);
+                     lane, current, m, zsum, y);
   const float wc = __builtin_amdgcn_exp2f(s_cur - m);
   zsum += wc;
 #pragma unroll
@@ -889,7 +1008,7 @@ __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
   const bool valid = len > 0 && len <= a.size && uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
   float m, zsum, y[EPL];
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
-                     lane, -INFINITY, m, zsum, y);
+                     lane, [] { return -INFINITY; }, m, zsum, y);
   const size_t base = size_t(row) * D + size_t(lane) * EPL;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {

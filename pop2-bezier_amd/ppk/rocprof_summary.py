@@ -3,6 +3,10 @@
   python pop2-bezier_amd/ppk/rocprof_summary.py trace DIR --out FILE.md --command "..."
       kernel-trace + stats: per-kernel durations of the ppk kernels, and the
       decode-step period and inter-kernel gaps measured from the dispatch trace.
+  python pop2-bezier_amd/ppk/rocprof_summary.py counters DIR [DIR ...] --kernel-regex RX --out FILE.md
+         --title T --command "..."
+      any --pmc runs: the median per-dispatch value of every counter for each kernel
+      matching RX, plus the L2 hit rate when TCC_HIT_sum and TCC_MISS_sum were read.
   python pop2-bezier_amd/ppk/rocprof_summary.py traffic FETCH_DIR WRITE_DIR --kernel NAME
          --calib-regex REGEX --calib-bytes N --algorithmic-bytes N --workload W --split S
          --out-md FILE.md --out-json FILE.json --command "..."
@@ -124,6 +128,38 @@ def traffic(args) -> None:
     _write(args.out_md, "\n".join(md) + "\n")
 
 
+def counters(args) -> None:
+    kre = re.compile(args.kernel_regex)
+    per: dict[str, dict[str, list[float]]] = {}
+    for d in args.dirs:
+        path = _one(d, "counter_collection.csv")
+        by_dispatch: dict[tuple[int, str], tuple[str, float]] = {}
+        for r in _rows(path):
+            name = r["kernel_name"]
+            if not kre.search(name):
+                continue
+            key = (int(r["dispatch_id"]), r["counter_name"].strip())
+            prev = by_dispatch.get(key, (name, 0.0))[1]
+            by_dispatch[key] = (name, prev + float(r["counter_value"]))
+        for (_, counter), (name, value) in by_dispatch.items():
+            per.setdefault(name, {}).setdefault(counter, []).append(value)
+    if not per:
+        raise SystemExit(f"no dispatches of kernels matching {args.kernel_regex!r}")
+    lines = [f"# rocprofv3 counters: {args.title}", "", "Commands (from the repository root):", "",
+             f"    {args.command}", "", "Summarised with:", "", f"    {_self_command()}", "",
+             "| kernel | counter | dispatches | median per dispatch |", "|---|---|---|---|"]
+    for name in sorted(per):
+        for counter in sorted(per[name]):
+            vals = per[name][counter]
+            lines.append(f"| {name} | {counter} | {len(vals)} | {statistics.median(vals):.6g} |")
+        hit, miss = per[name].get("TCC_HIT_sum"), per[name].get("TCC_MISS_sum")
+        if hit and miss:
+            h, m = statistics.median(hit), statistics.median(miss)
+            lines.append(f"| {name} | L2 hit rate = TCC_HIT / (TCC_HIT + TCC_MISS) | {len(hit)} | "
+                         f"{100.0 * h / max(h + m, 1.0):.2f} % |")
+    _write(args.out, "\n".join(lines) + "\n")
+
+
 def _self_command() -> str:
     return "python3 pop2-bezier_amd/ppk/rocprof_summary.py " + shlex.join(sys.argv[1:])
 
@@ -158,8 +194,14 @@ def main(argv=None) -> int:
     f.add_argument("--out-md", required=True)
     f.add_argument("--out-json", required=True)
     f.add_argument("--command", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("dirs", nargs="+")
+    c.add_argument("--kernel-regex", required=True)
+    c.add_argument("--out", required=True)
+    c.add_argument("--title", required=True)
+    c.add_argument("--command", required=True)
     a = p.parse_args(argv)
-    (trace if a.mode == "trace" else traffic)(a)
+    {"trace": trace, "traffic": traffic, "counters": counters}[a.mode](a)
     return 0
 
 

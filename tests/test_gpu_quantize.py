@@ -167,6 +167,40 @@ def test_dequantize_matches_oracle(device, d, dt):
         assert np.array_equal(out.numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
 
 
+@pytest.mark.parametrize("dt,round_bf16,d", [("f32", 0, 128), ("f32", 1, 256), ("bf16", 0, 64), ("f16", 1, 128)])
+def test_dequantize_grid_stride_sizes(device, dt, round_bf16, d):
+    """Inputs past one batch per lane of the largest grid (two grid-stride passes plus a ragged tail), every
+    output type and the bf16 pre-rounding flag. Reference on the device: int8 code * f32 scale is one exact
+    IEEE product, then torch's round-to-nearest-even conversions (bf16 first when the flag is set)."""
+    import ctypes
+
+    from ppk import _abi
+    from ppk import int8_kv_ops as ops
+
+    out_dt = DTYPES[dt]
+    per_unit = 4 if out_dt == torch.float32 else 8          # codes per 16-byte output chunk
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    units = 2 * cus * 128 * 256 * 8 + 12345                  # 128 blocks/CU x 256 lanes x 8-chunk batches
+    rows = -(-units * per_unit // d)
+    g = torch.Generator(device=device).manual_seed(SEED + 11)
+    codes = torch.randint(0, 256, (rows, d), dtype=torch.uint8, device=device, generator=g)
+    scales = torch.rand((rows,), generator=g, device=device) * 10.0 ** torch.randint(
+        -30, 30, (rows,), generator=g, device=device).float()
+    out = torch.empty((rows, d), dtype=out_dt, device=device)
+    a = _abi.PpkDequantizeArgs(struct_size=ctypes.sizeof(_abi.PpkDequantizeArgs), out_dtype=ops._DTYPES[out_dt],
+                               codes=codes.data_ptr(), scales=scales.data_ptr(), out=out.data_ptr(), rows=rows,
+                               head_dim=d, round_bf16=round_bf16)
+    _abi.check(_abi.lib().ppk_dequantize(ops.context(device), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                                         ctypes.byref(a)), "ppk_dequantize")
+    ref = codes.view(torch.int8).float() * scales[:, None]
+    if round_bf16:
+        ref = ref.to(torch.bfloat16).float()
+    ref = ref.to(out_dt)
+    bits = torch.int32 if out_dt == torch.float32 else torch.int16
+    mismatch = (out.view(bits) != ref.view(bits)).sum().item()
+    assert mismatch == 0, f"{mismatch} of {out.numel()} outputs differ ({dt}, round_bf16={round_bf16}, d={d})"
+
+
 def test_int8_capability_gate(device):
     """prepare_int8_kv (int8_policy.rs:26-55): not requested, unavailable head width, then ready + enabled."""
     off = ppk.prepare_int8_kv(False, 64, device)
