@@ -75,7 +75,12 @@ __device__ __forceinline__ float round_bf16(float x) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return __uint_as_float(u & 0xffff0000u);
 }
+// f32 -> f16, round to nearest even, from a materialised f32 value: the empty
+// asm keeps the backend from folding a producing multiply into one fused
+// multiply-to-f16 (v_fma_mixlo_f16), which rounds once where the reference
+// semantics (an f32 product, then a conversion) round twice.
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+  __asm__("" : "+v"(x));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 

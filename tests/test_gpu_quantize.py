@@ -167,7 +167,8 @@ def test_dequantize_matches_oracle(device, d, dt):
         assert np.array_equal(out.numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
 
 
-@pytest.mark.parametrize("dt,round_bf16,d", [("f32", 0, 128), ("f32", 1, 256), ("bf16", 0, 64), ("f16", 1, 128)])
+@pytest.mark.parametrize("dt,round_bf16,d", [("f32", 0, 128), ("f32", 1, 256), ("bf16", 0, 64), ("f16", 0, 128),
+                                            ("f16", 1, 256)])
 def test_dequantize_grid_stride_sizes(device, dt, round_bf16, d):
     """Inputs past one batch per lane of the largest grid (two grid-stride passes plus a ragged tail), every
     output type and the bf16 pre-rounding flag. Reference on the device: int8 code * f32 scale is one exact

@@ -3,7 +3,7 @@
 Each case draws its geometry, dtypes, lengths, splits and value ranges from a
 seeded generator (the case id is the seed offset, printed on failure) and
 checks the device result against the oracle at the bar of the row it
-belongs to: quantize bit-exact; int8 attention within 2e-3 + 1e-2 |ref|;
+belongs to: quantize and dequantize bit-exact; int8 attention within 2e-3 + 1e-2 |ref|;
 float-KV attention within 1e-4 + 1e-4 |ref|; the sampler bit-identical to
 the reference's own kernel (oracle/_ref). Sizes are bounded so the whole
 sweep runs in seconds.
@@ -50,6 +50,37 @@ def test_quantize_random(device, case):
     ref_c, ref_s, _ = oracle.quantize(x32)
     assert np.array_equal(codes.cpu().numpy(), ref_c), f"case {case}"
     assert np.array_equal(scales.cpu().numpy(), ref_s), f"case {case}"
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_dequantize_random(device, case):
+    import ctypes
+
+    from ppk import _abi
+    from ppk import int8_kv_ops as ops
+
+    rng = np.random.default_rng(SEED + 1500 + case)
+    d = int(rng.choice([64, 128, 256]))
+    rows = int(rng.integers(1, 5000))
+    out_dt = DTYPES[case % 3]
+    round_bf16 = int(rng.integers(0, 2))
+    codes = rng.integers(0, 256, (rows, d), dtype=np.uint8)
+    scales = (rng.random(rows) * 10.0 ** rng.uniform(-20, 20, rows)).astype(np.float32)
+    c_t, s_t = torch.from_numpy(codes).to(device), torch.from_numpy(scales).to(device)
+    out = torch.empty((rows, d), dtype=out_dt, device=device)
+    a = _abi.PpkDequantizeArgs(struct_size=ctypes.sizeof(_abi.PpkDequantizeArgs), out_dtype=ops._DTYPES[out_dt],
+                               codes=c_t.data_ptr(), scales=s_t.data_ptr(), out=out.data_ptr(), rows=rows,
+                               head_dim=d, round_bf16=round_bf16)
+    _abi.check(_abi.lib().ppk_dequantize(ops.context(device), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                                         ctypes.byref(a)), "ppk_dequantize")
+    ref = oracle.dequantize(codes, scales, round_bf16=bool(round_bf16))
+    what = f"case {case}: rows {rows} d {d} {out_dt} round {round_bf16}"
+    if out_dt == torch.float32:
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32)), what
+    elif out_dt == torch.bfloat16:
+        assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), to_bf16_bits(ref)), what
+    else:
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16)), what
 
 
 @pytest.mark.parametrize("case", range(16))
