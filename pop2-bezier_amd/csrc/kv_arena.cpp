@@ -315,12 +315,14 @@ void query(ppk_context* ctx, hipStream_t stream, ppk_kv_cache& c, uint32_t past,
            PpkKvView* out) {
   require(ctx == c.ctx, "KV cache belongs to another context");
   check_write(c.cfg, w);
-  require(past == c.committed, "KV past_len " + std::to_string(past) + " differs from the committed length " +
-                                   std::to_string(c.committed));
+  if (past != c.committed)
+    throw PreconditionError("KV past_len " + std::to_string(past) + " differs from the committed length " +
+                            std::to_string(c.committed));
   require(w.tokens > 0, "KV query dimensions must be nonzero");
   const uint64_t end = uint64_t(past) + w.tokens;
-  require(end <= c.cfg.max_context, "KV capacity is " + std::to_string(c.cfg.max_context) + ", the query needs " +
-                                        std::to_string(end) + "; rebuild the context first");
+  if (end > c.cfg.max_context)
+    throw PreconditionError("KV capacity is " + std::to_string(c.cfg.max_context) + ", the query needs " +
+                            std::to_string(end) + "; rebuild the context first");
   if (out) require(out->struct_size >= sizeof(PpkKvView), "PpkKvView.struct_size too small");
   const uint32_t current = c.backing ? c.backing->arena->capacity : 0;
   const uint32_t capacity = grown_capacity(c.cfg, current, end);

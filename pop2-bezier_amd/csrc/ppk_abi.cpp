@@ -299,8 +299,9 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
           "INT8 attention float operand misaligned");
   if (plan.workspace_bytes) {
     require(a.workspace && aligned(a.workspace, 256), "INT8 attention workspace missing or not 256-byte aligned");
-    require(a.workspace_bytes >= plan.workspace_bytes,
-            "INT8 attention workspace too small: need " + std::to_string(plan.workspace_bytes) + " bytes");
+    if (a.workspace_bytes < plan.workspace_bytes)
+      throw PreconditionError("INT8 attention workspace too small: need " + std::to_string(plan.workspace_bytes) +
+                              " bytes");
   }
   if (step) {
     require(step->struct_size >= sizeof(PpkDecodeStepArgs), "PpkDecodeStepArgs.struct_size too small");
@@ -408,8 +409,9 @@ void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAtt
   require(qs >= a.head_dim, "float attention Q row stride smaller than head_dim");
   if (plan.workspace_bytes) {
     require(a.workspace && aligned(a.workspace, 256), "float attention workspace missing or not 256-byte aligned");
-    require(a.workspace_bytes >= plan.workspace_bytes,
-            "float attention workspace too small: need " + std::to_string(plan.workspace_bytes) + " bytes");
+    if (a.workspace_bytes < plan.workspace_bytes)
+      throw PreconditionError("float attention workspace too small: need " + std::to_string(plan.workspace_bytes) +
+                              " bytes");
   }
   const int di = dim_index(a.head_dim);
   const float scale = a.softmax_scale > 0.f ? a.softmax_scale : 1.0f / std::sqrt(float(a.head_dim));

@@ -28,6 +28,11 @@ struct InvalidOutputError : std::runtime_error {
   explicit InvalidOutputError(const std::string& m) : std::runtime_error("INVALID_OUTPUT: " + m) {}
 };
 
+// Checks on the launch path run hundreds of times per call (per row, per
+// pair of rows): a literal message is only turned into a string on failure.
+inline void require(bool ok, const char* message) {
+  if (!ok) throw PreconditionError(message);
+}
 inline void require(bool ok, const std::string& message) {
   if (!ok) throw PreconditionError(message);
 }
