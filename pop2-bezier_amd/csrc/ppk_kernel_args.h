@@ -52,8 +52,9 @@ struct DequantizeArgs {
   uint32_t pad;
 };
 
-// Decode attention: block (group g, row r) of W = blockDim.x / 64 waves covers
-// history tokens [g*W*S, (g+1)*W*S) of row r, S = split_tokens per wave.
+// Decode attention: block (group g, row r), blockIdx.x = g * rows + r, of
+// W = blockDim.x / 64 waves covers history tokens [g*W*S, (g+1)*W*S) of row r,
+// S = split_tokens per wave.
 // ngroups == 1: the block writes the final output row (current token included).
 // ngroups > 1: it writes a partial record for the merge kernel:
 //   y[D] floats at part_y + (row * ngroups + g) * D

@@ -566,8 +566,11 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   const int wave = threadIdx.x >> 6;
   const int W = blockDim.x >> 6;
   const int c = lane % LPT;
-  const uint32_t row = blockIdx.x / a.ngroups;
-  const uint32_t group = blockIdx.x - row * a.ngroups;
+  // Blocks are numbered group-major: consecutive blocks belong to different
+  // rows, so the empty tail groups of short rows (ragged batches) spread over
+  // the CUs instead of leaving some CUs with only live blocks.
+  const uint32_t row = blockIdx.x % a.rows;
+  const uint32_t group = blockIdx.x / a.rows;
   const uint32_t S = a.split_tokens;
   const uint32_t p = a.past[row / a.heads];
   const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.ngroups) * W * S;
@@ -942,8 +945,11 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
   const int wave = threadIdx.x >> 6;
   const int W = blockDim.x >> 6;
   const int c = lane % G::kLpt;
-  const uint32_t row = blockIdx.x / a.ngroups;
-  const uint32_t group = blockIdx.x - row * a.ngroups;
+  // Blocks are numbered group-major: consecutive blocks belong to different
+  // rows, so the empty tail groups of short rows (ragged batches) spread over
+  // the CUs instead of leaving some CUs with only live blocks.
+  const uint32_t row = blockIdx.x % a.rows;
+  const uint32_t group = blockIdx.x / a.rows;
   const uint32_t S = a.split_tokens;
   const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
   const bool valid = len > 0 && len <= a.size && uint64_t(len) <= uint64_t(a.ngroups) * W * S;
