@@ -62,6 +62,13 @@ def parse() -> argparse.Namespace:
     return p.parse_args()
 
 
+def _host_cpus() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -117,7 +124,7 @@ def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args, *, threads: int |
     return {"value": round(us_per_step, 1), "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{n} of {rows_total} head rows{what} (Candle CPU path restated in C, "
                       f"oracle/ppk_oracle.c cpu_baseline_decode), {reps} reps in {el:.1f} s, scaled x{scale:g}",
-            "cpu_model": _cpu_model()}
+            "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
 
 
 def bench_float(args) -> int:
@@ -227,7 +234,8 @@ def bench_float(args) -> int:
         result["cpu_baseline"] = {
             "value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{n} of {rows} head rows x {L} tokens (Candle's ordinary CPU attention restated in C, "
-                      f"cpu_baseline_float_decode), {reps} reps in {el:.1f} s, scaled x{rows / n:g}"}
+                      f"cpu_baseline_float_decode), {reps} reps in {el:.1f} s, scaled x{rows / n:g}",
+            "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
@@ -299,7 +307,8 @@ def bench_sampler(args) -> int:
                 break
         result["cpu_baseline"] = {"value": round(el / reps * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
                                   "sample": f"the whole batch ({B} rows), oracle_renyi_sample (the reference's host "
-                                            f"oracle restated in C), {reps} reps in {el:.1f} s"}
+                                            f"oracle restated in C), {reps} reps in {el:.1f} s",
+                                  "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
@@ -435,7 +444,8 @@ def bench_arena(args) -> int:
                 break
         result["cpu_baseline"] = {"value": round(el / reps * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
                                   "sample": f"one decode round: {2 * Lyr} quantize-appends of [B={B}, H={H}, 1, "
-                                            f"D={D}] (oracle_append), {reps} reps in {el:.1f} s"}
+                                            f"D={D}] (oracle_append), {reps} reps in {el:.1f} s",
+                                  "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
@@ -707,7 +717,7 @@ def bench_append(args) -> int:
         result["cpu_baseline"] = {"value": round(el / reps * 1e6, 2), "unit": "us/step", "cores": 1, "kind": "port",
                                   "sample": f"the whole append (K and V, 16 rows x {D}), C oracle oracle_append, "
                                             f"{reps} reps in {el:.1f} s",
-                                  "cpu_model": _cpu_model()}
+                                  "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
@@ -804,7 +814,7 @@ def bench_dequantize(args) -> int:
                                   "sample": f"{n} of {rows} rows x {L} tokens (C oracle oracle_dequantize, f32 out"
                                             f"{' rounded to bf16' if dt == torch.bfloat16 else ''}), {reps} reps "
                                             f"in {el:.1f} s, scaled x{rows / n:g}",
-                                  "cpu_model": _cpu_model()}
+                                  "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
@@ -881,6 +891,9 @@ def main() -> int:
     t_end.record(stream)
     torch.cuda.synchronize()
     step_ms = t_start.elapsed_time(t_end) / args.steps
+    # Median from a second pass with an event between consecutive steps.
+    import statistics
+    median_us = statistics.median(_event_times(lambda _i: step(), args.steps, stream, per_step=True))
 
     # Timed region 2 (the roofline): the same K steps with the library's tracer
     # bracketing every launch of the decode kernel with HIP events on the
@@ -935,6 +948,7 @@ def main() -> int:
                    "batch": B, "heads": H, "head_dim": D, "context": L, "capacity": cap, "kv": "int8 + f32 scales",
                    "query": "bf16", "tokens_per_wave": split, "blocks_per_row": step.ngroups,
                    "launches_per_step": 1 if step.ngroups == 1 else 2},
+        "median_us": round(median_us, 2),
         "tokens_per_s": round(B / (step_ms * 1e-3), 1),
         "step_hbm_gbps": round(step_gbps, 1),
         "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
