@@ -131,6 +131,18 @@ def test_split_invariance(device, split):
     assert_close(c.run(split=split), c.reference(), what=f"split {split}")
 
 
+@pytest.mark.parametrize("split", [0, 32])
+def test_long_rows_merge_more_than_64_groups(device, split):
+    """Two rows of 65536 tokens: each row spans hundreds of blocks (the automatic plan's 64-token waves, or
+    the smallest explicit split), so the merge combines more than 64 records per row and takes its second
+    pass over the (m, z) pairs."""
+    c = Case(device, 1, 2, 128, [65536], 65537, seed=SEED + 21)
+    call = ppk.DecodeAttention(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, split)
+    assert call.ngroups > 64
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    assert_close(got, c.reference(), what=f"65536 tokens, split {split}, {call.ngroups} groups")
+
+
 def test_bf16_history_mode_matches_reference_kernel_semantics(device):
     c = Case(device, 2, 2, 64, [300, 41], 301)
     ref = c.reference(history_bf16=True)

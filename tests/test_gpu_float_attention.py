@@ -176,6 +176,17 @@ def test_full_size_bf16_b32_h16_ctx8192_sampled_rows(device):
     del k, v
 
 
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
+def test_long_rows_merge_more_than_64_groups(device, kv):
+    """Two rows of 65000 live tokens: hundreds of blocks per row, so the merge takes its second pass over
+    the (m, z) records beyond the first 64."""
+    c = FloatCase(device, 1, 2, 128, 65536, kv, lengths=[65000], seed=SEED + 22)
+    call = ppk.FloatDecodeAttention(c.q, c.k, c.v, c.lengths_t, c.H)
+    assert call.ngroups > 64
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    assert_close(got, c.reference(), atol=ATOL, rtol=RTOL, what=f"65000 tokens, {call.ngroups} groups")
+
+
 def test_hip_graph_replay(device):
     """A prepared call captured in a HIP graph replays bit-identically to the eager call."""
     c = FloatCase(device, 1, 16, 64, 1024, torch.bfloat16, lengths=[900], seed=SEED + 11)
