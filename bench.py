@@ -47,6 +47,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--dequantize", choices=("bf16", "f32", "f16"), default=None,
                    help="time ppk_dequantize (int8 -> DTYPE) over one tensor of the headline history "
                         "(B*H rows x --context tokens x D)")
+    p.add_argument("--quantize", choices=("bf16", "f32", "f16"), default=None,
+                   help="time ppk_quantize (DTYPE -> int8 codes + scales) over one tensor of the headline "
+                        "history (B*H rows x --context tokens x D)")
     p.add_argument("--layers", type=int, default=24)
     p.add_argument("--prefill", type=int, default=1000)
     p.add_argument("--choices", type=int, default=2048)
@@ -724,6 +727,103 @@ def bench_append(args) -> int:
     return 0
 
 
+def bench_quantize(args) -> int:
+    """Dense quantization (ppk_quantize, the bit-exact contract of int8_kv_ops::quantize) of one history
+    tensor at the headline shape: B*H rows x ctx tokens x D values of DTYPE -> codes + one f32 scale per
+    token row."""
+    import ctypes
+    import statistics
+
+    import torch
+    import ppk
+    from ppk import _abi, synthetic
+    from ppk import int8_kv_ops as ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, D, L = args.batch, args.heads, args.head_dim, args.context
+    rows = B * H
+    dt = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}[args.quantize]
+    print(f"# bench quantize: {rows} rows x {L} tokens x {D} {args.quantize}", file=sys.stderr, flush=True)
+    x = torch.empty((rows, L, D), dtype=dt, device=dev)
+    for r0 in range(0, rows, 16):
+        x[r0:r0 + 16].copy_(synthetic.history_chunk(SEED, 0, r0 // 16, min(16, rows - r0), H, r0, L, D, dev, dt))
+    codes = torch.empty((rows, L, D), dtype=torch.uint8, device=dev)
+    scales = torch.empty((rows, L), dtype=torch.float32, device=dev)
+    a = _abi.PpkQuantizeArgs(struct_size=ctypes.sizeof(_abi.PpkQuantizeArgs), src_dtype=ops._DTYPES[dt],
+                             src=x.data_ptr(), codes=codes.data_ptr(), scales=scales.data_ptr(), rows=rows * L,
+                             head_dim=D, flags=None)
+    ctx, fn, ref = ops.context(dev), ops.lib().ppk_quantize, ctypes.byref(a)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        torch.neg(src, out=torch.empty_like(src))
+        torch.cuda.synchronize()
+        del src
+
+    def call(_i=0):
+        ops.check(fn(ctx, sp, ref), "ppk_quantize")
+
+    for _ in range(args.warmup):
+        call()
+    mean_us = _event_times(call, args.steps, stream, per_step=False)
+    each = _event_times(call, args.steps, stream, per_step=True)
+    ppk.kernel_stats(ppk.PPK_KERNEL_QUANTIZE, reset=True)
+    ppk.set_profiling(True)
+    for _ in range(args.steps):
+        call()
+    torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_QUANTIZE, reset=True)
+    kernel_us = kernel_ms / max(launches, 1) * 1e3
+    nbytes = rows * L * D * x.element_size() + rows * L * D + rows * L * 4
+    achieved = nbytes / (kernel_us * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"ppk_quantize_{args.quantize}_b{B}_h{H}_d{D}_ctx{L}_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            with open(tpath) as f:
+                t = json.load(f)
+            if t.get("workload") == f"B{B}H{H}D{D}L{L}{args.quantize}":
+                traffic = t.get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    result = {
+        "metric": "%s -> int8 quantize, us per history tensor + achieved HBM GB/s" % args.quantize,
+        "value": round(mean_us, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(mean_us / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.quantize, "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels)",
+        "config": {"workload": "quantize one history tensor (ppk_quantize)", "rows": rows, "tokens": L,
+                   "head_dim": D, "src": args.quantize},
+        "median_us": round(statistics.median(each), 2),
+        "step_hbm_gbps": round(nbytes / (mean_us * 1e-6) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "ppk_quantize_d%d" % D, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(kernel_us, 2),
+                     "launches": launches},
+    }
+    if not args.no_cpu_baseline:
+        import numpy as np
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle  # noqa: E402  (CPU baseline leg only)
+
+        n = min(rows, 4)
+        xh = x[:n].float().cpu().numpy()
+        reps, el = _time_cpu(lambda: oracle.quantize(xh), args.cpu_seconds / 2)
+        result["cpu_baseline"] = {"value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/call", "cores": 1,
+                                  "kind": "port",
+                                  "sample": f"{n} of {rows} rows x {L} tokens (C oracle oracle_quantize, the "
+                                            f"reference's CPU branch restated), {reps} reps in {el:.1f} s, "
+                                            f"scaled x{rows / n:g}",
+                                  "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
+        del np
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def bench_dequantize(args) -> int:
     """Int8 -> bf16/f32/f16 dequantization (ppk_dequantize, the prefill path's `dequantize`) of one history
     tensor at the headline shape: B*H rows x ctx tokens x D codes + one f32 scale per token."""
@@ -834,6 +934,8 @@ def main() -> int:
         return bench_arena(args)
     if args.dequantize:
         return bench_dequantize(args)
+    if args.quantize:
+        return bench_quantize(args)
     if args.kv != "int8":
         return bench_float(args)
     if args.config == 2:

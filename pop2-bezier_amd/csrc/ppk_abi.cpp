@@ -57,6 +57,7 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_renyi_sample",
     "ppk_kv_scatter_u16", "ppk_kv_scatter_u4", "ppk_kv_scatter_u2",
     "ppk_copy2d_batch",
+    "ppk_quantize_dense_d64", "ppk_quantize_dense_d128", "ppk_quantize_dense_d256",
 };
 
 std::string default_code_object() {
@@ -221,9 +222,21 @@ void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a
   k.rows = a.rows;
   k.src_dtype = a.src_dtype;
   k.ntensors = 1;
+  DeviceGuard guard(ctx->device);
+  // Streaming kernel: one 16-byte load per lane covers 16 bytes of a row, so
+  // the source must be 16-byte aligned and the codes 8-byte aligned (4 for
+  // f32 sources, 4 codes per lane). Batches of 4 units per lane, one batch
+  // per lane up to 128 blocks of 256 lanes per CU. Other alignments take the
+  // one-wave-per-row kernel.
+  const uint32_t per_lane = a.src_dtype == PPK_F32 ? 4u : 8u;
+  if (aligned(a.src, 16) && aligned(a.codes, per_lane)) {
+    const uint64_t units = a.rows * (a.head_dim / per_lane);
+    const uint64_t grid = std::min<uint64_t>((units + 1023) / 1024, uint64_t(std::max(ctx->cu_count, 1)) * 128);
+    launch(ctx, PPK_KERNEL_QUANTIZE, Fn(kQuantizeDense64 + di), uint32_t(grid), 256, 0, stream, k);
+    return;
+  }
   const uint64_t grid = (a.rows + 3) / 4;
   require(grid <= 0x7fffffffu, "INT8 KV quantize grid too large");
-  DeviceGuard guard(ctx->device);
   launch(ctx, PPK_KERNEL_QUANTIZE, Fn(kQuantize64 + di), uint32_t(grid), 256, 0, stream, k);
 }
 

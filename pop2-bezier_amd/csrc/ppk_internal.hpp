@@ -48,6 +48,7 @@ enum Fn : int {
   kRenyiSample,
   kScatter16, kScatter4, kScatter2,
   kCopyBatch,
+  kQuantizeDense64, kQuantizeDense128, kQuantizeDense256,
   kFnCount
 };
 

@@ -24,6 +24,7 @@
 
 namespace {
 
+using u2 = uint32_t __attribute__((ext_vector_type(2)));
 using u4 = uint32_t __attribute__((ext_vector_type(4)));
 using f4 = float __attribute__((ext_vector_type(4)));
 
@@ -195,8 +196,6 @@ __device__ __forceinline__ void quantize_body(const ppk::QuantizeArgs& a) {
 // ---------------------------------------------------------------------------
 // Dequantize: 16 codes per thread (one dwordx4), grid-stride.
 // ---------------------------------------------------------------------------
-using u2 = uint32_t __attribute__((ext_vector_type(2)));
-
 // Dequantization in units of one 16-byte output chunk: E = 8 codes for a
 // 16-bit output, 4 for f32. Lane l of a wave handles units i, i + stride, ...
 // so every load instruction of a wave reads 64*E consecutive code bytes and
@@ -340,6 +339,99 @@ __device__ __forceinline__ float group_max(float x) {
   if constexpr (LPT >= 8) x = fmaxf(x, dpp_half_mirror(x));
   if constexpr (LPT >= 16) x = fmaxf(x, dpp_mirror(x));
   return x;
+}
+
+// Dense quantization (int8_kv_ops::quantize over [rows, D]) at streaming
+// rates. A row's D values are split over G = D / E lanes, 16 bytes (E values)
+// per lane, so one wave-wide load covers 64 / G whole rows and the row's
+// absmax is a G-lane reduction; each lane then forms its E codes with the
+// same arithmetic as quantize_row (IEEE division, ties-to-even, clamp, NaN
+// quotient -> 0). Lanes hold two batches of R units and issue the next
+// batch's loads before the current batch's stores. Loop control is uniform
+// per wave (rows never straddle waves: G divides 64), so the cross-lane
+// reductions always run with every lane active; units past the end are
+// clamped for loading and masked for storing.
+template <int D, int E, uint32_t DT>
+__device__ __forceinline__ void quantize_dense_units(const ppk::QuantizeArgs& a) {
+#pragma clang fp contract(off)
+  constexpr int G = D / E;
+  constexpr int R = 4;
+  static_assert(64 % G == 0, "a row's lanes stay inside one wave");
+  using Code = typename std::conditional<E == 8, u2, uint32_t>::type;
+  const int lane = threadIdx.x & 63;
+  const uint64_t units = a.rows * G;
+  const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+  uint64_t wave_base = uint64_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u);
+  if (wave_base >= units) return;  // uniform per wave
+  const u4* src = static_cast<const u4*>(a.src[0]);
+  u4 cur[R], nxt[R];
+  auto load = [&](uint64_t wb, u4 (&raw)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint64_t u = min(wb + uint64_t(lane) + r * stride, units - 1);  // clamp: in bounds, masked later
+      raw[r] = __builtin_nontemporal_load(src + u);
+    }
+  };
+  load(wave_base, cur);
+  bool any_bad = false;
+  for (; wave_base < units; wave_base += R * stride) {
+    const bool more = wave_base + R * stride < units;  // uniform per wave
+    if (more) load(wave_base + R * stride, nxt);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint64_t u = wave_base + uint64_t(lane) + r * stride;
+      const bool valid = u < units;
+      float x[E];
+      if constexpr (DT == kF32) {
+#pragma unroll
+        for (int k = 0; k < E; ++k) x[k] = __uint_as_float(cur[r][k]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+          const uint16_t h = uint16_t(cur[r][k / 2] >> (16 * (k % 2)));
+          x[k] = DT == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
+        }
+      }
+      bool finite = true;
+      float amax = 0.f;
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        finite = finite && __builtin_isfinite(x[k]);
+        amax = fmaxf(amax, fabsf(x[k]));
+      }
+      // Row max over the G lanes: DPP within 16-lane rows, shuffles beyond.
+      amax = group_max<(G < 16 ? G : 16)>(amax);
+#pragma unroll
+      for (int o = 16; o < G; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+      const float sc = fmaxf(amax / 127.0f, 1e-12f);
+      uint32_t packed[(E + 3) / 4] = {};
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        const float qf = rintf(x[k] / sc);
+        const int qi = (qf != qf) ? 0 : int(fminf(fmaxf(qf, -127.f), 127.f));
+        packed[k / 4] |= (uint32_t(qi) & 0xffu) << (8 * (k % 4));
+      }
+      if (valid) {
+        Code c;
+        if constexpr (E == 8) c = u2{packed[0], packed[1]};
+        else c = packed[0];
+        __builtin_nontemporal_store(c, reinterpret_cast<Code*>(a.codes[0]) + u);
+        if (lane % G == 0) a.scales[0][u / G] = sc;
+      }
+      any_bad = any_bad || (valid && !finite);
+    }
+    if (!more) break;
+#pragma unroll
+    for (int r = 0; r < R; ++r) cur[r] = nxt[r];
+  }
+  if (a.flags && __any(any_bad) && lane == 0) atomicOr(a.flags, 1u);
+}
+
+template <int D>
+__device__ __forceinline__ void quantize_dense_body(const ppk::QuantizeArgs& a) {
+  if (a.src_dtype == kF32) quantize_dense_units<D, 4, kF32>(a);
+  else if (a.src_dtype == kBF16) quantize_dense_units<D, 8, kBF16>(a);
+  else quantize_dense_units<D, 8, kF16>(a);
 }
 
 template <int LPT>
@@ -1372,6 +1464,15 @@ PPK_QUANTIZE(128)
 PPK_QUANTIZE(256)
 
 extern "C" __global__ __launch_bounds__(256) void ppk_dequantize(ppk::DequantizeArgs a) { dequantize_body(a); }
+extern "C" __global__ __launch_bounds__(256) void ppk_quantize_dense_d64(ppk::QuantizeArgs a) {
+  quantize_dense_body<64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void ppk_quantize_dense_d128(ppk::QuantizeArgs a) {
+  quantize_dense_body<128>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void ppk_quantize_dense_d256(ppk::QuantizeArgs a) {
+  quantize_dense_body<256>(a);
+}
 
 #define PPK_ATTN(D)                                                                          \
   extern "C" __global__ __launch_bounds__(1024) void ppk_decode_d##D(ppk::DecodeArgs a) {     \

@@ -95,6 +95,67 @@ def test_quantize_nonfinite_rows_flagged(device):
     assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
 
 
+def _quantize_raw(device, src_ptr, src_dtype, codes, scales, rows, d):
+    import ctypes
+    a = ppk._abi.PpkQuantizeArgs(struct_size=ctypes.sizeof(ppk._abi.PpkQuantizeArgs), src_dtype=src_dtype,
+                                 src=src_ptr, codes=codes.data_ptr(), scales=scales.data_ptr(), rows=rows,
+                                 head_dim=d, flags=None)
+    ppk._abi.check(ppk._abi.lib().ppk_quantize(ppk.context(device), None, ctypes.byref(a)), "ppk_quantize")
+
+
+@pytest.mark.parametrize("dt,d", [("bf16", 64), ("f32", 128), ("f16", 256)])
+def test_quantize_misaligned_source_matches_oracle(device, dt, d):
+    """A source that is not 16-byte aligned takes the one-wave-per-row kernel; it stays bit-exact."""
+    rng = np.random.default_rng(SEED + 31 + d)
+    x = np.concatenate([kv_values(rng, 1, 8, 65, d).reshape(520, d), _special_rows(d)[0]])
+    rows = x.shape[0]
+    xt, x32 = _to_device(x, DTYPES[dt], device)
+    eb = xt.element_size()
+    big = torch.empty(rows * d + 16 // eb, dtype=xt.dtype, device=device)
+    view = big[4 // eb:4 // eb + rows * d]           # 4 bytes past a 16-byte boundary
+    view.copy_(xt.reshape(-1))
+    codes = torch.empty((rows, d), dtype=torch.uint8, device=device)
+    scales = torch.empty(rows, dtype=torch.float32, device=device)
+    _quantize_raw(device, view.data_ptr(), ppk._abi.PPK_F32 if dt == "f32" else
+                  (ppk._abi.PPK_BF16 if dt == "bf16" else ppk._abi.PPK_F16), codes, scales, rows, d)
+    torch.cuda.synchronize()
+    ref_codes, ref_scales, _ = oracle.quantize(x32)
+    assert np.array_equal(codes.cpu().numpy(), ref_codes.reshape(rows, d))
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.reshape(rows).view(np.uint32))
+
+
+@pytest.mark.parametrize("dt,d", [("bf16", 128), ("f32", 64), ("f16", 256)])
+def test_quantize_streaming_kernel_large_equals_row_kernel(device, dt, d):
+    """Past the largest grid (two grid-stride passes plus a ragged tail, ~1 GB of input, special rows
+    mixed in): the streaming kernel's codes and scales equal the one-wave-per-row kernel's bit for bit."""
+    out_dt = DTYPES[dt]
+    per_lane = 4 if out_dt == torch.float32 else 8
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    units = 2 * cus * 128 * 256 * 4 + 777                  # 128 blocks/CU x 256 lanes x 4-unit batches
+    rows = -(-units * per_lane // d)
+    g = torch.Generator(device=device).manual_seed(SEED + 41)
+    x32 = torch.randn((rows, d), generator=g, device=device) * 3.0
+    x32[::1009] *= 1e30                                    # huge rows
+    x32[3::1013] = 0.0                                     # zero rows
+    x32[5::2003, 7] = float("nan")                         # non-finite rows
+    x32[11::4001] = torch.round(x32[11::4001] * 4) / 4     # quarter steps: exact half-step quotients
+    x = x32.to(out_dt)
+    del x32
+    eb = x.element_size()
+    code = ppk._abi.PPK_F32 if dt == "f32" else (ppk._abi.PPK_BF16 if dt == "bf16" else ppk._abi.PPK_F16)
+    codes, scales = ppk.quantize(x.reshape(1, rows, d))
+    big = torch.empty(rows * d + 16 // eb, dtype=x.dtype, device=device)
+    view = big[4 // eb:4 // eb + rows * d]
+    view.copy_(x.reshape(-1))
+    del x
+    codes_r = torch.empty((rows, d), dtype=torch.uint8, device=device)
+    scales_r = torch.empty(rows, dtype=torch.float32, device=device)
+    _quantize_raw(device, view.data_ptr(), code, codes_r, scales_r, rows, d)
+    torch.cuda.synchronize()
+    assert torch.equal(codes.reshape(rows, d), codes_r)
+    assert torch.equal(scales.reshape(rows).view(torch.int32), scales_r.view(torch.int32))
+
+
 def _arenas(rng, rows, cap, d, filled):
     codes = rng.integers(-127, 128, size=(rows, cap, d)).astype(np.int8).view(np.uint8)
     scales = rng.random((rows, cap), dtype=np.float32) * 0.1
