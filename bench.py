@@ -335,12 +335,22 @@ def bench_arena(args) -> int:
     g = torch.Generator(device=dev).manual_seed(SEED)
     prefill = torch.randn((H, T0, D), generator=g, device=dev, dtype=torch.bfloat16)
     layers = []
+    # Prefill: one multi-token commit per cache (quantize-and-append of H x T0 tokens of K and V).
+    ppk.kernel_stats(ppk.PPK_KERNEL_APPEND, reset=True)
+    ppk.set_profiling(True)
+    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    p0.record()
     for _ in range(Lyr):
         caches = [LayerCache("int8", H, D, max_context=8192) for _ in range(B)]
         for c in caches:
             c.query(prefill, prefill, 0, True)
         layers.append(caches)
+    p1.record()
     torch.cuda.synchronize()
+    ppk.set_profiling(False)
+    pre_launches, pre_ms = ppk.kernel_stats(ppk.PPK_KERNEL_APPEND, reset=True)
+    pre_us = pre_ms / max(pre_launches, 1) * 1e3
+    pre_bytes = 2 * H * T0 * D * prefill.element_size() + 2 * H * T0 * (D + 4)
     kv = torch.randn((B, H, 1, D), generator=g, device=dev, dtype=torch.bfloat16)
 
     # Joining round: every layer's caches move into a new batch arena.
@@ -421,6 +431,9 @@ def bench_arena(args) -> int:
                    "arenas_after_join": len(arena_ids)},
         "host_us_per_round": round(host_ms * 1e3, 1),
         "append_kernel_us": round(append_us, 2),
+        "prefill": {"caches": Lyr * B, "tokens": T0, "ms": round(p0.elapsed_time(p1), 3),
+                    "append_kernel_us": round(pre_us, 2), "append_bytes": pre_bytes,
+                    "append_gbps": round(pre_bytes / (pre_us * 1e-6) / 1e9, 1) if pre_us else None},
         "join": {"ms": round(join_ms, 3), "host_ms": round(join_host_ms, 2), "copied_bytes": join_bytes,
                  "copy_launches": copy_launches, "copy_kernel_ms": round(copy_ms, 3)},
         "roofline": {"bound": "hbm", "kernel": "ppk_copy2d_batch (prefix copies at join)",

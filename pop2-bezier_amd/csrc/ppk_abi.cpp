@@ -58,6 +58,7 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_kv_scatter_u16", "ppk_kv_scatter_u4", "ppk_kv_scatter_u2",
     "ppk_copy2d_batch",
     "ppk_quantize_dense_d64", "ppk_quantize_dense_d128", "ppk_quantize_dense_d256",
+    "ppk_quantize_append_d64", "ppk_quantize_append_d128", "ppk_quantize_append_d256",
 };
 
 std::string default_code_object() {
@@ -204,6 +205,25 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   return plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
 }
 
+// The streaming quantize kernel (dense or append): one 16-byte load per lane
+// covers 16 bytes of a source row, so every source must be 16-byte aligned
+// and every code array aligned to the 8 (4 for f32 sources) codes a lane
+// stores; rows of all tensors are indexed in 32 bits. Batches of 4 units per
+// lane, one batch per lane up to 128 blocks of 256 lanes per CU. Returns
+// false (nothing launched) when the operands do not fit these conditions.
+bool launch_stream_quantize(ppk_context* ctx, hipStream_t stream, int prof_kernel, QuantizeArgs k,
+                            uint32_t head_dim) {
+  const uint32_t per_lane = k.src_dtype == PPK_F32 ? 4u : 8u;
+  for (uint32_t t = 0; t < k.ntensors; ++t)
+    if (!aligned(k.src[t], 16) || !aligned(k.codes[t], per_lane)) return false;
+  if (uint64_t(k.rows) * k.ntensors >= (uint64_t(1) << 32)) return false;
+  const uint64_t units = uint64_t(k.ntensors) * k.rows * (head_dim / per_lane);
+  const uint64_t grid = std::min<uint64_t>((units + 1023) / 1024, uint64_t(std::max(ctx->cu_count, 1)) * 128);
+  const Fn fn = Fn((k.capacity ? kQuantizeAppend64 : kQuantizeDense64) + dim_index(head_dim));
+  launch(ctx, prof_kernel, fn, uint32_t(grid), 256, 0, stream, k);
+  return true;
+}
+
 void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a) {
   require(a.struct_size >= sizeof(PpkQuantizeArgs), "PpkQuantizeArgs.struct_size too small");
   const int di = dim_index(a.head_dim);
@@ -223,18 +243,7 @@ void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a
   k.src_dtype = a.src_dtype;
   k.ntensors = 1;
   DeviceGuard guard(ctx->device);
-  // Streaming kernel: one 16-byte load per lane covers 16 bytes of a row, so
-  // the source must be 16-byte aligned and the codes 8-byte aligned (4 for
-  // f32 sources, 4 codes per lane). Batches of 4 units per lane, one batch
-  // per lane up to 128 blocks of 256 lanes per CU. Other alignments take the
-  // one-wave-per-row kernel.
-  const uint32_t per_lane = a.src_dtype == PPK_F32 ? 4u : 8u;
-  if (aligned(a.src, 16) && aligned(a.codes, per_lane)) {
-    const uint64_t units = a.rows * (a.head_dim / per_lane);
-    const uint64_t grid = std::min<uint64_t>((units + 1023) / 1024, uint64_t(std::max(ctx->cu_count, 1)) * 128);
-    launch(ctx, PPK_KERNEL_QUANTIZE, Fn(kQuantizeDense64 + di), uint32_t(grid), 256, 0, stream, k);
-    return;
-  }
+  if (launch_stream_quantize(ctx, stream, PPK_KERNEL_QUANTIZE, k, a.head_dim)) return;
   const uint64_t grid = (a.rows + 3) / 4;
   require(grid <= 0x7fffffffu, "INT8 KV quantize grid too large");
   launch(ctx, PPK_KERNEL_QUANTIZE, Fn(kQuantize64 + di), uint32_t(grid), 256, 0, stream, k);
@@ -272,6 +281,7 @@ void run_append(ppk_context* ctx, hipStream_t stream, const PpkAppendArgs& a) {
   const uint64_t grid = (2 * rows + 3) / 4;
   require(grid <= 0x7fffffffu, "INT8 append grid too large");
   DeviceGuard guard(ctx->device);
+  if (launch_stream_quantize(ctx, stream, PPK_KERNEL_APPEND, k, a.head_dim)) return;
   launch(ctx, PPK_KERNEL_APPEND, Fn(kQuantize64 + di), uint32_t(grid), 256, 0, stream, k);
 }
 
@@ -521,6 +531,7 @@ void run_arena_write(ppk_context* ctx, hipStream_t stream, const ArenaWrite& w) 
     k.uniform_past = w.uniform_past;
     const uint64_t grid = (2 * k.rows + 3) / 4;
     require(grid <= 0x7fffffffu, "KV append grid too large");
+    if (launch_stream_quantize(ctx, stream, PPK_KERNEL_APPEND, k, w.head_dim)) return;
     launch(ctx, PPK_KERNEL_APPEND, Fn(kQuantize64 + dim_index(w.head_dim)), uint32_t(grid), 256, 0, stream, k);
     return;
   }

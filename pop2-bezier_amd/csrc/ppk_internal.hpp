@@ -49,6 +49,7 @@ enum Fn : int {
   kScatter16, kScatter4, kScatter2,
   kCopyBatch,
   kQuantizeDense64, kQuantizeDense128, kQuantizeDense256,
+  kQuantizeAppend64, kQuantizeAppend128, kQuantizeAppend256,
   kFnCount
 };
 

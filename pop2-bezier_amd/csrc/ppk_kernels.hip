@@ -341,42 +341,54 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
-// Dense quantization (int8_kv_ops::quantize over [rows, D]) at streaming
-// rates. A row's D values are split over G = D / E lanes, 16 bytes (E values)
-// per lane, so one wave-wide load covers 64 / G whole rows and the row's
-// absmax is a G-lane reduction; each lane then forms its E codes with the
-// same arithmetic as quantize_row (IEEE division, ties-to-even, clamp, NaN
-// quotient -> 0). Lanes hold two batches of R units and issue the next
-// batch's loads before the current batch's stores. Loop control is uniform
-// per wave (rows never straddle waves: G divides 64), so the cross-lane
-// reductions always run with every lane active; units past the end are
-// clamped for loading and masked for storing.
-template <int D, int E, uint32_t DT>
-__device__ __forceinline__ void quantize_dense_units(const ppk::QuantizeArgs& a) {
+// Quantization at streaming rates: dense (int8_kv_ops::quantize over [rows,
+// D]) and quantize-and-append into arenas (rows of K and V written at slot
+// past[b] + t). A row's D values are split over G = D / E lanes, 16 bytes (E
+// values) per lane, so one wave-wide load covers 64 / G whole rows and the
+// row's absmax is a G-lane reduction; each lane then forms its E codes with
+// the same arithmetic as quantize_row (IEEE division, ties-to-even, clamp,
+// NaN quotient -> 0). Lanes hold two batches of R units and issue the next
+// batch's loads (and, for appends, the sequences' past entries) before the
+// current batch's stores. Loop control is uniform per wave (rows never
+// straddle waves: G divides 64), so the cross-lane reductions always run
+// with every lane active; units past the end are clamped for loading and
+// masked for storing. The host sends rows * ntensors < 2^32 here.
+template <int D, int E, uint32_t DT, bool ARENA>
+__device__ __forceinline__ void quantize_stream_units(const ppk::QuantizeArgs& a) {
 #pragma clang fp contract(off)
   constexpr int G = D / E;
   constexpr int R = 4;
   static_assert(64 % G == 0, "a row's lanes stay inside one wave");
   using Code = typename std::conditional<E == 8, u2, uint32_t>::type;
   const int lane = threadIdx.x & 63;
-  const uint64_t units = a.rows * G;
+  const uint32_t rows = uint32_t(a.rows);  // per tensor
+  const uint64_t units = uint64_t(a.ntensors) * rows * G;
   const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
   uint64_t wave_base = uint64_t(blockIdx.x) * blockDim.x + (threadIdx.x & ~63u);
   if (wave_base >= units) return;  // uniform per wave
-  const u4* src = static_cast<const u4*>(a.src[0]);
   u4 cur[R], nxt[R];
-  auto load = [&](uint64_t wb, u4 (&raw)[R]) {
+  uint32_t pcur[R], pnxt[R];  // appends: past entry of the unit's sequence
+  auto load = [&](uint64_t wb, u4 (&raw)[R], uint32_t (&pv)[R]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint64_t u = min(wb + uint64_t(lane) + r * stride, units - 1);  // clamp: in bounds, masked later
-      raw[r] = __builtin_nontemporal_load(src + u);
+      if constexpr (ARENA) {
+        const uint32_t ri = uint32_t(u / G);
+        const uint32_t t = ri >= rows ? 1u : 0u;
+        const uint32_t row = ri - t * rows;
+        const u4* src = static_cast<const u4*>(t ? a.src[1] : a.src[0]);
+        raw[r] = __builtin_nontemporal_load(src + uint64_t(row) * G + uint32_t(u % G));
+        pv[r] = a.past ? a.past[(row / a.tokens) / a.heads] : a.uniform_past;
+      } else {
+        raw[r] = __builtin_nontemporal_load(static_cast<const u4*>(a.src[0]) + u);
+      }
     }
   };
-  load(wave_base, cur);
-  bool any_bad = false;
+  load(wave_base, cur, pcur);
+  bool any_bad = false, any_over = false;
   for (; wave_base < units; wave_base += R * stride) {
     const bool more = wave_base + R * stride < units;  // uniform per wave
-    if (more) load(wave_base + R * stride, nxt);
+    if (more) load(wave_base + R * stride, nxt, pnxt);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint64_t u = wave_base + uint64_t(lane) + r * stride;
@@ -411,28 +423,49 @@ __device__ __forceinline__ void quantize_dense_units(const ppk::QuantizeArgs& a)
         const int qi = (qf != qf) ? 0 : int(fminf(fmaxf(qf, -127.f), 127.f));
         packed[k / 4] |= (uint32_t(qi) & 0xffu) << (8 * (k % 4));
       }
-      if (valid) {
-        Code c;
-        if constexpr (E == 8) c = u2{packed[0], packed[1]};
-        else c = packed[0];
+      Code c;
+      if constexpr (E == 8) c = u2{packed[0], packed[1]};
+      else c = packed[0];
+      bool in_arena = true;
+      if constexpr (ARENA) {
+        const uint32_t ri = uint32_t(min(u, units - 1) / G);
+        const uint32_t t = ri >= rows ? 1u : 0u;
+        const uint32_t row = ri - t * rows;
+        const uint32_t bh = row / a.tokens;
+        const uint64_t slot = uint64_t(pcur[r]) + (row - bh * a.tokens);
+        in_arena = slot < a.capacity;
+        const uint64_t dst = uint64_t(bh) * a.capacity + slot;
+        if (valid && in_arena) {
+          __builtin_nontemporal_store(c, reinterpret_cast<Code*>(a.codes[t] + dst * D) + uint32_t(u % G));
+          if (lane % G == 0) a.scales[t][dst] = sc;
+        }
+      } else if (valid) {
         __builtin_nontemporal_store(c, reinterpret_cast<Code*>(a.codes[0]) + u);
         if (lane % G == 0) a.scales[0][u / G] = sc;
       }
       any_bad = any_bad || (valid && !finite);
+      any_over = any_over || (valid && !in_arena);
     }
     if (!more) break;
 #pragma unroll
-    for (int r = 0; r < R; ++r) cur[r] = nxt[r];
+    for (int r = 0; r < R; ++r) {
+      cur[r] = nxt[r];
+      pcur[r] = pnxt[r];
+    }
   }
-  if (a.flags && __any(any_bad) && lane == 0) atomicOr(a.flags, 1u);
+  if (a.flags) {
+    const bool bad = __any(any_bad), over = __any(any_over);
+    if (lane == 0 && (bad || over)) atomicOr(a.flags, (bad ? 1u : 0u) | (over ? 2u : 0u));
+  }
 }
 
-template <int D>
-__device__ __forceinline__ void quantize_dense_body(const ppk::QuantizeArgs& a) {
-  if (a.src_dtype == kF32) quantize_dense_units<D, 4, kF32>(a);
-  else if (a.src_dtype == kBF16) quantize_dense_units<D, 8, kBF16>(a);
-  else quantize_dense_units<D, 8, kF16>(a);
+template <int D, bool ARENA>
+__device__ __forceinline__ void quantize_stream_dtype(const ppk::QuantizeArgs& a) {
+  if (a.src_dtype == kF32) quantize_stream_units<D, 4, kF32, ARENA>(a);
+  else if (a.src_dtype == kBF16) quantize_stream_units<D, 8, kBF16, ARENA>(a);
+  else quantize_stream_units<D, 8, kF16, ARENA>(a);
 }
+
 
 template <int LPT>
 __device__ __forceinline__ QInt quantize_query(const float (&qr)[16]) {
@@ -1464,15 +1497,20 @@ PPK_QUANTIZE(128)
 PPK_QUANTIZE(256)
 
 extern "C" __global__ __launch_bounds__(256) void ppk_dequantize(ppk::DequantizeArgs a) { dequantize_body(a); }
-extern "C" __global__ __launch_bounds__(256) void ppk_quantize_dense_d64(ppk::QuantizeArgs a) {
-  quantize_dense_body<64>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void ppk_quantize_dense_d128(ppk::QuantizeArgs a) {
-  quantize_dense_body<128>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void ppk_quantize_dense_d256(ppk::QuantizeArgs a) {
-  quantize_dense_body<256>(a);
-}
+// Streaming quantize: dense [rows, D] (ppk_quantize) and appends into arenas
+// (ppk_quantize_append, KV arena writes), separate kernels so the dense path
+// keeps its smaller register footprint.
+#define PPK_QSTREAM(D)                                                                              \
+  extern "C" __global__ __launch_bounds__(256) void ppk_quantize_dense_d##D(ppk::QuantizeArgs a) {  \
+    quantize_stream_dtype<D, false>(a);                                                             \
+  }                                                                                                 \
+  extern "C" __global__ __launch_bounds__(256) void ppk_quantize_append_d##D(ppk::QuantizeArgs a) { \
+    quantize_stream_dtype<D, true>(a);                                                              \
+  }
+PPK_QSTREAM(64)
+PPK_QSTREAM(128)
+PPK_QSTREAM(256)
+#undef PPK_QSTREAM
 
 #define PPK_ATTN(D)                                                                          \
   extern "C" __global__ __launch_bounds__(1024) void ppk_decode_d##D(ppk::DecodeArgs a) {     \

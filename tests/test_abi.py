@@ -41,7 +41,8 @@ def test_code_object_is_built_for_gfx950():
     for kernel in (b"ppk_quantize_d128", b"ppk_decode_d128", b"ppk_decode_bf16h_d128", b"ppk_attn_merge_d128",
                    b"ppk_dequantize", b"ppk_fdecode_bf16_d64", b"ppk_fdecode_f32_d64", b"ppk_fmerge_d64",
                    b"ppk_renyi_sample", b"ppk_quantize_dense_d64", b"ppk_quantize_dense_d128",
-                   b"ppk_quantize_dense_d256", b"ppk_kv_scatter_u16", b"ppk_copy2d_batch"):
+                   b"ppk_quantize_dense_d256", b"ppk_quantize_append_d128", b"ppk_kv_scatter_u16",
+                   b"ppk_copy2d_batch"):
         assert kernel in blob
 
 

@@ -156,6 +156,51 @@ def test_quantize_streaming_kernel_large_equals_row_kernel(device, dt, d):
     assert torch.equal(scales.reshape(rows).view(torch.int32), scales_r.view(torch.int32))
 
 
+@pytest.mark.parametrize("dt,d", [("bf16", 128), ("f32", 256), ("f16", 64)])
+def test_append_streaming_kernel_equals_row_kernel(device, dt, d):
+    """A ragged multi-token append (several thousand tokens per row, the last sequence running past the
+    capacity) through the streaming kernel writes the same arenas and flags as the one-wave-per-row
+    kernel, which a source 4 bytes off a 16-byte boundary selects."""
+    import ctypes
+    B, H, T, cap = 5, 16, 3000, 9000
+    out_dt = DTYPES[dt]
+    g = torch.Generator(device=device).manual_seed(SEED + 51)
+    src = (torch.randn((2, B, H, T, d), generator=g, device=device) * 2).to(out_dt)
+    past = torch.tensor([0, 17, 3000, 5999, 7500], dtype=torch.int32, device=device)  # last: 1500 overflow
+    eb = src.element_size()
+    results = []
+    for misaligned in (False, True):
+        kc = torch.full((B * H, cap, d), 0xAB, dtype=torch.uint8, device=device)
+        vc = torch.full_like(kc, 0xCD)
+        ks = torch.full((B * H, cap), -7.0, device=device)
+        vs = torch.full_like(ks, -9.0)
+        flags = torch.zeros(1, dtype=torch.int32, device=device)
+        if misaligned:
+            big = torch.empty(2 * src[0].numel() + 32 // eb, dtype=out_dt, device=device)
+            n = src[0].numel()
+            k_src = big[4 // eb:4 // eb + n]
+            v_src = big[4 // eb + n + 16 // eb:4 // eb + 2 * n + 16 // eb]
+            k_src.copy_(src[0].reshape(-1))
+            v_src.copy_(src[1].reshape(-1))
+            kp, vp = k_src.data_ptr(), v_src.data_ptr()
+        else:
+            kp, vp = src[0].data_ptr(), src[1].data_ptr()
+        a = ppk._abi.PpkAppendArgs(struct_size=ctypes.sizeof(ppk._abi.PpkAppendArgs),
+                                   src_dtype=ppk.int8_kv_ops._DTYPES[out_dt], k_src=kp, v_src=vp,
+                                   past=past.data_ptr(), k_codes=kc.data_ptr(), v_codes=vc.data_ptr(),
+                                   k_scales=ks.data_ptr(), v_scales=vs.data_ptr(), batch=B, heads=H, tokens=T,
+                                   head_dim=d, capacity=cap, flags=flags.data_ptr())
+        ppk._abi.check(ppk._abi.lib().ppk_quantize_append(ppk.context(device), None, ctypes.byref(a)),
+                       "ppk_quantize_append")
+        torch.cuda.synchronize()
+        results.append((kc, vc, ks, vs, flags.item()))
+    (a_k, a_v, a_ks, a_vs, a_f), (b_k, b_v, b_ks, b_vs, b_f) = results
+    assert a_f == b_f and a_f & ppk.PPK_FLAG_OVERFLOW
+    assert torch.equal(a_k, b_k) and torch.equal(a_v, b_v)
+    assert torch.equal(a_ks.view(torch.int32), b_ks.view(torch.int32))
+    assert torch.equal(a_vs.view(torch.int32), b_vs.view(torch.int32))
+
+
 def _arenas(rng, rows, cap, d, filled):
     codes = rng.integers(-127, 128, size=(rows, cap, d)).astype(np.int8).view(np.uint8)
     scales = rng.random((rows, cap), dtype=np.float32) * 0.1
