@@ -218,7 +218,11 @@ bool launch_stream_quantize(ppk_context* ctx, hipStream_t stream, int prof_kerne
     if (!aligned(k.src[t], 16) || !aligned(k.codes[t], per_lane)) return false;
   if (uint64_t(k.rows) * k.ntensors >= (uint64_t(1) << 32)) return false;
   const uint64_t units = uint64_t(k.ntensors) * k.rows * (head_dim / per_lane);
-  const uint64_t grid = std::min<uint64_t>((units + 1023) / 1024, uint64_t(std::max(ctx->cu_count, 1)) * 128);
+  // Below one full block per CU (e.g. a decode round's single-token appends)
+  // the one-wave-per-row kernel spreads the rows wider and finishes sooner.
+  const uint64_t cus = uint64_t(std::max(ctx->cu_count, 1));
+  if (units < cus * 1024) return false;
+  const uint64_t grid = std::min<uint64_t>((units + 1023) / 1024, cus * 128);
   const Fn fn = Fn((k.capacity ? kQuantizeAppend64 : kQuantizeDense64) + dim_index(head_dim));
   launch(ctx, prof_kernel, fn, uint32_t(grid), 256, 0, stream, k);
   return true;

@@ -72,6 +72,26 @@ def test_quantize_special_rows(device, d):
     assert scales[0, 1].item() == 1.0
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_quantize_streaming_kernel_special_rows(device, d, dt):
+    """The special rows, tiled past the size where ppk_quantize takes the streaming kernel (one block of
+    work per CU), bit-exact against the oracle; random rows in between, so rows of every kind share waves."""
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    per_lane = 4 if dt == "f32" else 8
+    need_rows = cus * 1024 * per_lane // d + 64
+    special = _special_rows(d)[0]
+    rng = np.random.default_rng(SEED + 61 + d)
+    filler = kv_values(rng, 1, 1, need_rows, d).reshape(need_rows, d)
+    x = filler.copy()
+    x[::3] = np.resize(special, (len(x[::3]), d))
+    xt, x32 = _to_device(x[None], DTYPES[dt], device)
+    codes, scales = ppk.quantize(xt)
+    ref_codes, ref_scales, _ = oracle.quantize(x32)
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+
+
 def test_quantize_nonfinite_rows_flagged(device):
     d = 128
     x = np.random.default_rng(SEED).standard_normal((1, 4, d)).astype(np.float32)
