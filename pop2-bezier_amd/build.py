@@ -45,23 +45,30 @@ def build(verbose: bool = True) -> dict:
     lib = os.path.join(OUT, "libppk.so")
     tmp_hsaco = hsaco + f".tmp{os.getpid()}"
     tmp_lib = lib + f".tmp{os.getpid()}"
-    _run(
-        [HIPCC, "--genco", f"--offload-arch={ARCH}", *DEVICE_FLAGS, os.path.join(CSRC, "ppk_kernels.hip"), "-o", tmp_hsaco],
-        verbose,
-    )
-    # The shim is host-only code over the HIP runtime API: plain g++.
-    _run(
-        [
-            CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
-            f"-I{os.path.join(ROOT, 'include')}", f"-I{ROCM}/include",
-            os.path.join(CSRC, "ppk_abi.cpp"), os.path.join(CSRC, "int8_kv_ops.cpp"),
-            os.path.join(CSRC, "fused_attention.cpp"), os.path.join(CSRC, "kv_arena.cpp"),
-            "-o", tmp_lib, f"-L{ROCM}/lib", f"-Wl,-rpath,{ROCM}/lib", "-lamdhip64", "-ldl",
-        ],
-        verbose,
-    )
-    os.replace(tmp_hsaco, hsaco)
-    os.replace(tmp_lib, lib)
+    try:
+        _run(
+            [HIPCC, "--genco", f"--offload-arch={ARCH}", *DEVICE_FLAGS, os.path.join(CSRC, "ppk_kernels.hip"), "-o",
+             tmp_hsaco],
+            verbose,
+        )
+        # The shim is host-only code over the HIP runtime API: plain g++.
+        _run(
+            [
+                CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
+                f"-I{os.path.join(ROOT, 'include')}", f"-I{ROCM}/include",
+                os.path.join(CSRC, "ppk_abi.cpp"), os.path.join(CSRC, "int8_kv_ops.cpp"),
+                os.path.join(CSRC, "fused_attention.cpp"), os.path.join(CSRC, "kv_arena.cpp"),
+                "-o", tmp_lib, f"-L{ROCM}/lib", f"-Wl,-rpath,{ROCM}/lib", "-lamdhip64", "-ldl",
+            ],
+            verbose,
+        )
+        # Both outputs replace the previous build together, only once both compiled.
+        os.replace(tmp_hsaco, hsaco)
+        os.replace(tmp_lib, lib)
+    finally:
+        for t in (tmp_hsaco, tmp_lib):
+            if os.path.exists(t):
+                os.remove(t)
     return {"hsaco": hsaco, "lib": lib}
 
 
