@@ -238,12 +238,21 @@ struct ppk_write_plan {
   std::vector<uint32_t> staged;  // past then lengths, the upload source
   uint32_t heads = 0, head_dim = 0;
   uint32_t* dev = nullptr;
+  size_t bytes = 0;
   hipStream_t stream = nullptr;
+  // The device vector goes back to the context's pool (up to 8 kept) for the
+  // next plan on the same stream; beyond that it is freed in stream order.
   ~ppk_write_plan() {
-    if (dev) {
-      ppk::DeviceGuard guard(ctx->device);
-      (void)hipFreeAsync(dev, stream);
+    if (!dev) return;
+    {
+      std::lock_guard<std::mutex> lock(ctx->plan_mutex);
+      if (ctx->plan_pool.size() < 8) {
+        ctx->plan_pool.push_back({dev, bytes, stream});
+        return;
+      }
     }
+    ppk::DeviceGuard guard(ctx->device);
+    (void)hipFreeAsync(dev, stream);
   }
 };
 
@@ -385,10 +394,26 @@ ppk_write_plan* plan_create(ppk_context* ctx, hipStream_t stream, const uint32_t
     plan->staged[batch + b] = past_lens[b] + 1;
   }
   DeviceGuard guard(ctx->device);
-  void* dev = nullptr;
-  const hipError_t st = hipMallocAsync(&dev, align256(2 * size_t(batch) * 4), stream);
-  if (st != hipSuccess) throw PreconditionError(std::string("write plan allocation failed: ") + hipGetErrorString(st));
-  plan->dev = static_cast<uint32_t*>(dev);
+  const size_t bytes = align256(2 * size_t(batch) * 4);
+  {
+    std::lock_guard<std::mutex> lock(ctx->plan_mutex);
+    auto& pool = ctx->plan_pool;
+    for (size_t i = 0; i < pool.size(); ++i)
+      if (pool[i].stream == stream && pool[i].bytes >= bytes) {
+        plan->dev = pool[i].dev;
+        plan->bytes = pool[i].bytes;
+        pool.erase(pool.begin() + std::ptrdiff_t(i));
+        break;
+      }
+  }
+  if (!plan->dev) {
+    void* dev = nullptr;
+    const hipError_t st = hipMallocAsync(&dev, bytes, stream);
+    if (st != hipSuccess)
+      throw PreconditionError(std::string("write plan allocation failed: ") + hipGetErrorString(st));
+    plan->dev = static_cast<uint32_t*>(dev);
+    plan->bytes = bytes;
+  }
   plan->stream = stream;
   check_exec(hipMemcpyAsync(plan->dev, plan->staged.data(), 2 * size_t(batch) * 4, hipMemcpyHostToDevice, stream),
              "hipMemcpyAsync (write plan)");

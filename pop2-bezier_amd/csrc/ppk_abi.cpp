@@ -656,6 +656,8 @@ int32_t ppk_context_release(ppk_context* ctx) {
       (void)hipEventDestroy(ev.start);
       (void)hipEventDestroy(ev.stop);
     }
+    // Recycled write-plan vectors: a synchronous free (their streams may be gone).
+    for (auto& b : ctx->plan_pool) (void)hipFree(b.dev);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
   });
 }

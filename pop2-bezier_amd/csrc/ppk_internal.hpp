@@ -69,6 +69,17 @@ struct ppk_context {
   std::mutex prepare_mutex;
   bool int8_ready = false;  // ppk_prepare_int8_kv's self-check passed on this context
 
+  // Device vectors of released write plans, recycled by the next plan created
+  // on the same stream (stream order puts its upload after the old plan's
+  // readers); an allocation per plan costs ~9 us of host time.
+  struct PlanBuffer {
+    uint32_t* dev = nullptr;
+    size_t bytes = 0;
+    hipStream_t stream = nullptr;
+  };
+  std::mutex plan_mutex;
+  std::vector<PlanBuffer> plan_pool;
+
   std::mutex prof_mutex;
   bool profiling = false;
   std::vector<ppk::EventPair> pending[PPK_KERNEL_COUNT];

@@ -311,6 +311,29 @@ def test_one_write_plan_is_reused_by_thirty_five_layers_without_local_offset_upl
         assert caches[0].info().arena_offset_uploads == 0
 
 
+@pytest.mark.parametrize("batch", [40, 70])
+def test_write_plan_offsets_reach_the_device_for_small_and_large_batches(device, batch):
+    """Plans of up to 64 sequences upload their offsets in a kernel's arguments, larger ones by a copy;
+    either way every sequence's token lands at its own slot (ragged lengths, some empty)."""
+    lengths = [(7 * b) % 13 for b in range(batch)]
+    caches = [LayerCache(F32, 2, 3) for _ in range(batch)]
+    old = []
+    for b, c in enumerate(caches):
+        if lengths[b]:
+            p = data(2, lengths[b], 3, b * 10.0)
+            c.query(p, p, 0, True)
+            old.append(p)
+        else:
+            old.append(None)
+    cur = batch_data(batch, 2, 3, 600.0)
+    view = LayerCache.query_batch(caches, cur, cur, lengths, True, WritePlan(lengths, 2, 3))
+    width = max(lengths) + 1
+    for b in range(batch):
+        visible = rows_of(view, b, 2, width)[:, :lengths[b] + 1]
+        assert torch.equal(visible, cat(old[b], cur[b].reshape(2, 1, 3))), f"sequence {b}"
+        assert len(caches[b]) == lengths[b] + 1
+
+
 def test_wrong_shared_write_plan_is_rejected_before_history_or_scratch_is_touched(device):
     for offsets in ([1, 3], [1, 1]):
         caches = [LayerCache(F32, 2, 3) for _ in range(2)]
