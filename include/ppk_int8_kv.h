@@ -391,7 +391,10 @@ PPK_API int32_t ppk_kv_cache_view(const ppk_kv_cache* cache, PpkKvView* out);
 PPK_API int32_t ppk_kv_query(ppk_context* ctx, void* stream, ppk_kv_cache* cache, uint32_t past,
                              const PpkKvWrite* write, PpkKvView* out);
 /* BatchWritePlan::new: the write offsets of one decode round as a device
-   vector (uploaded on stream), shared by every layer's ppk_kv_query_batch. */
+   vector (uploaded on stream), shared by every layer's ppk_kv_query_batch.
+   Release returns the vector to the context, which hands it to the next plan
+   created on the same stream (stream order keeps the new upload behind the
+   old plan's work); plans are released before their context. */
 PPK_API int32_t ppk_write_plan_create(ppk_context* ctx, void* stream, const uint32_t* past_lens, uint32_t batch,
                                       uint32_t heads, uint32_t head_dim, ppk_write_plan** out);
 PPK_API int32_t ppk_write_plan_release(ppk_write_plan* plan);
