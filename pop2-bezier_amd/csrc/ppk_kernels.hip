@@ -593,7 +593,8 @@ __device__ __forceinline__ float current_score(const ppk::DecodeArgs& a, const f
 // end clamp to the last token and those tokens are masked out.
 template <int D, bool BF16H>
 __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_t row, uint32_t begin, uint32_t n,
-                                               const float (&qr)[16], float* s_lds, int lane, WavePartial& out) {
+                                               uint32_t nspec, const float (&qr)[16], float* s_lds, int lane,
+                                               WavePartial& out) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
   constexpr int U = 4;  // tiles per batch
@@ -603,13 +604,61 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   out.z = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) out.acc[i] = 0.f;
-  if (n == 0) return;  // uniform per wave
 
   const size_t tok0 = size_t(row) * a.capacity + begin;
   const uint8_t* kb = a.k + tok0 * D + size_t(c) * 16;
   const uint8_t* vb = a.v + tok0 * D + size_t(c) * 16;
   const float* ksb = a.ks + tok0;
   const float* vsb = a.vs + tok0;
+  if (nspec > 0 && nspec <= uint32_t(2 * U * TPL)) {
+    // Short window (at most two batches per phase): K and V are requested
+    // before the row's length is known, clamped to the window's slots inside
+    // the arena (always in bounds); slots at or past the length n are masked
+    // below and their scales zeroed, so stale or uninitialised arena memory
+    // never reaches the result.
+    const bool two = nspec > uint32_t(U * TPL);  // uniform per wave
+    u4 ka[U], kb2[U], va[U], vb2[U];
+    float ksa, ksb2, vsa, vsb2;
+    load_batch<D, U>(kb, ksb, 0, nspec, j, lane, ka, ksa);
+    load_batch<D, U>(vb, vsb, 0, nspec, j, lane, va, vsa);
+    if (two) {
+      load_batch<D, U>(kb, ksb, U, nspec, j, lane, kb2, ksb2);
+      load_batch<D, U>(vb, vsb, U, nspec, j, lane, vb2, vsb2);
+    }
+    QInt qi{};
+    float sl2 = a.scale_log2;
+    if constexpr (!BF16H) {
+      qi = quantize_query<LPT>(qr);
+      sl2 *= qi.unscale;
+    }
+    if (n == 0) return;  // uniform per wave
+    const uint32_t tl = uint32_t(lane % (U * TPL));
+    ksa = tl < n ? ksa : 0.f;
+    vsa = tl < n ? vsa : 0.f;
+    float mloc = -INFINITY;
+    mloc = score_batch<D, BF16H, U>(ka, ksa, 0, n, j, c, qr, qi, sl2, s_lds, mloc);
+    if (two) {
+      ksb2 = U * TPL + tl < n ? ksb2 : 0.f;
+      vsb2 = U * TPL + tl < n ? vsb2 : 0.f;
+      mloc = score_batch<D, BF16H, U>(kb2, ksb2, U, n, j, c, qr, qi, sl2, s_lds, mloc);
+    }
+    float m = mloc, z = 0.f;
+#pragma unroll
+    for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __builtin_amdgcn_wave_barrier();
+    accumulate_batch<D, BF16H, U>(va, vsa, 0, n, j, lane, m, s_lds, z, out.acc);
+    if (two) accumulate_batch<D, BF16H, U>(vb2, vsb2, U, n, j, lane, m, s_lds, z, out.acc);
+    z = wave_sum(z);
+#pragma unroll
+    for (int o = LPT; o < ppk::kWave; o <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) out.acc[i] += __shfl_xor(out.acc[i], o);
+    }
+    out.m = m;
+    out.z = z;
+    return;
+  }
+  if (n == 0) return;  // uniform per wave
   const uint32_t ntiles = (n + TPL - 1) / TPL;
   u4 ra[U], rb[U];
   float sa, sb;
@@ -734,7 +783,8 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   const uint32_t begin = (group * W + wave) * S;
   const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
   WavePartial part;
-  wave_attention<D, BF16H>(a, row, begin, n, qr, lds + size_t(wave) * S, lane, part);
+  const uint32_t nspec = begin < a.capacity ? min(S, a.capacity - begin) : 0u;
+  wave_attention<D, BF16H>(a, row, begin, n, nspec, qr, lds + size_t(wave) * S, lane, part);
 
   // Combine the block's waves through LDS (the staging area is reused).
   // Record of wave w at mrg + w * R: m, z, 2 pad floats, y[D] (16-byte aligned).
