@@ -49,7 +49,10 @@ size_t oracle_quantize(const float* x, size_t rows, size_t d, uint8_t* codes, fl
     float amax = 0.0f;
     int finite = 1;
     for (size_t i = 0; i < d; ++i) {
-      amax = fmaxf(amax, fabsf(row[i]));
+      /* f32::max skips a NaN argument of either kind; glibc's fmaxf returns
+       * NaN for a signalling one, so the fold is written as a comparison. */
+      const float a = fabsf(row[i]);
+      if (a > amax) amax = a;
       if (!isfinite(row[i])) finite = 0;
     }
     bad += finite ? 0 : 1;

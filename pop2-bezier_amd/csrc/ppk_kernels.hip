@@ -125,6 +125,21 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Largest |x| of a lane's values with f32::max / fmaxf semantics (NaNs of
+// either kind skipped); the result is >= +0 and never NaN. Written on the bit
+// patterns: the hardware float max quiets a signalling NaN and returns it,
+// which would drop the max of the values before it.
+template <int N>
+__device__ __forceinline__ float lane_absmax(const float (&x)[N]) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const uint32_t a = __float_as_uint(x[k]) & 0x7fffffffu;
+    m = max(m, a > 0x7f800000u ? 0u : a);
+  }
+  return __uint_as_float(m);
+}
+
 // ---------------------------------------------------------------------------
 // Kernel 1: quantize (dense) / quantize-and-append (arena).
 // One wave per (tensor, row); D/64 channels per lane.
@@ -144,13 +159,9 @@ __device__ __forceinline__ void quantize_row(const void* src, size_t src_row, ui
   float x[EPL];
   load_vec<EPL>(src, src_row * D + size_t(lane) * EPL, dtype, x);
   bool finite = true;
-  float amax = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    finite = finite && __builtin_isfinite(x[e]);
-    amax = fmaxf(amax, fabsf(x[e]));
-  }
-  amax = wave_max(amax);
+  for (int e = 0; e < EPL; ++e) finite = finite && __builtin_isfinite(x[e]);
+  const float amax = wave_max(lane_absmax(x));
   const float s = fmaxf(amax / 127.0f, 1e-12f);
   uint32_t packed = 0;
 #pragma unroll
@@ -341,6 +352,23 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
+// Max over G consecutive lanes (G a power of two <= 64) of values that are
+// >= +0 and never NaN: such floats order like their bit patterns, so the
+// reduction runs as unsigned integer max (the DPP move folds into the max,
+// and no NaN canonicalisation is needed).
+template <int G>
+__device__ __forceinline__ float group_max_nonneg(float x) {
+  uint32_t b = __float_as_uint(x);
+  auto step = [&](uint32_t o) { b = max(b, o); };
+  step(uint32_t(__builtin_amdgcn_mov_dpp(int(b), 0xB1, 0xF, 0xF, true)));
+  step(uint32_t(__builtin_amdgcn_mov_dpp(int(b), 0x4E, 0xF, 0xF, true)));
+  if constexpr (G >= 8) step(uint32_t(__builtin_amdgcn_mov_dpp(int(b), 0x141, 0xF, 0xF, true)));
+  if constexpr (G >= 16) step(uint32_t(__builtin_amdgcn_mov_dpp(int(b), 0x140, 0xF, 0xF, true)));
+#pragma unroll
+  for (int o = 16; o < G; o <<= 1) step(uint32_t(__shfl_xor(int(b), o)));
+  return __uint_as_float(b);
+}
+
 // Quantization at streaming rates: dense (int8_kv_ops::quantize over [rows,
 // D]) and quantize-and-append into arenas (rows of K and V written at slot
 // past[b] + t). A row's D values are split over G = D / E lanes, 16 bytes (E
@@ -404,24 +432,61 @@ __device__ __forceinline__ void quantize_stream_units(const ppk::QuantizeArgs& a
           x[k] = DT == kBF16 ? bf16_to_f32(h) : f16_to_f32(h);
         }
       }
-      bool finite = true;
-      float amax = 0.f;
+      // Fast row max: the float max chain is exact unless the lane holds a
+      // NaN (a signalling one can drop the values before it); such a lane
+      // then has a NaN product below, and the wave recomputes.
+      float m = 0.f;
+#pragma unroll
+      for (int k = 0; k < E; ++k) m = fmaxf(m, fabsf(x[k]));
+      float sc = fmaxf(group_max_nonneg<G>(m) / 127.0f, 1e-12f);
+      // Rounded quotients from a product with the hardware reciprocal (at
+      // most 1 ulp off 1/sc): for finite x, |x·r - RN(x/sc)| <= 2.7e-5 since
+      // |x/sc| <= 127·(1 + 2^-24), so a product farther than 2^-14 from every
+      // half-integer rounds to the same integer as the correctly rounded
+      // quotient. A product within that band, or a non-finite one (x or sc
+      // non-finite), marks its lane for the division. A product outside the
+      // band is also below 127.5 in magnitude, so its rounded value needs no
+      // clamp; the division path keeps the clamp.
+      const float rcp = __builtin_amdgcn_rcpf(sc);
+      int qi[E];
+      bool near[E], any_near = false;
 #pragma unroll
       for (int k = 0; k < E; ++k) {
-        finite = finite && __builtin_isfinite(x[k]);
-        amax = fmaxf(amax, fabsf(x[k]));
+        const float p = x[k] * rcp;
+        const float n = rintf(p);
+        near[k] = !(fabsf(p - n) < 0.5f - 0x1p-14f);
+        any_near = any_near || near[k];
+        qi[k] = int(n);
       }
-      // Row max over the G lanes: DPP within 16-lane rows, shuffles beyond.
-      amax = group_max<(G < 16 ? G : 16)>(amax);
+      auto exact = [&](int k) {
+        const float t = rintf(x[k] / sc);
+        qi[k] = t != t ? 0 : int(__builtin_amdgcn_fmed3f(t, -127.f, 127.f));  // NaN quotient -> code 0
+      };
+      bool finite = true;
+      if (__any(any_near)) {  // wave-uniform
 #pragma unroll
-      for (int o = 16; o < G; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-      const float sc = fmaxf(amax / 127.0f, 1e-12f);
-      uint32_t packed[(E + 3) / 4] = {};
+        for (int k = 0; k < E; ++k) finite = finite && __builtin_isfinite(x[k]);
+        if (__any(!finite)) {
+          // A non-finite input may have spoilt the fast max of its row: the
+          // wave recomputes every row it holds with the NaN-skipping max and
+          // the division (the reduction needs all lanes).
+          sc = fmaxf(group_max_nonneg<G>(lane_absmax(x)) / 127.0f, 1e-12f);
 #pragma unroll
-      for (int k = 0; k < E; ++k) {
-        const float qf = rintf(x[k] / sc);
-        const int qi = (qf != qf) ? 0 : int(fminf(fmaxf(qf, -127.f), 127.f));
-        packed[k / 4] |= (uint32_t(qi) & 0xffu) << (8 * (k % 4));
+          for (int k = 0; k < E; ++k) exact(k);
+        } else {
+          // Finite rows: the scale stands; only the flagged values divide.
+#pragma unroll
+          for (int k = 0; k < E; ++k)
+            if (near[k]) exact(k);
+        }
+      }
+      uint32_t packed[(E + 3) / 4];
+#pragma unroll
+      for (int w = 0; w < E / 4; ++w) {
+        // v_perm: bytes 0 of (a, b) and of (c, d), then the two byte pairs.
+        const uint32_t ab = __builtin_amdgcn_perm(uint32_t(qi[4 * w + 1]), uint32_t(qi[4 * w]), 0x0c0c0400u);
+        const uint32_t cd = __builtin_amdgcn_perm(uint32_t(qi[4 * w + 3]), uint32_t(qi[4 * w + 2]), 0x0c0c0400u);
+        packed[w] = __builtin_amdgcn_perm(cd, ab, 0x05040100u);
       }
       Code c;
       if constexpr (E == 8) c = u2{packed[0], packed[1]};

@@ -92,6 +92,49 @@ def test_quantize_streaming_kernel_special_rows(device, d, dt):
     assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
 
 
+@pytest.mark.parametrize("kernel", ["row", "streaming"])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_quantize_signalling_nan_skipped_by_absmax(device, dt, kernel):
+    """Signalling NaNs (either sign) next to the row's largest value: the absmax skips them as Rust's
+    f32::max fold does (int8_kv_ops.rs:17), so the other values keep their codes and NaNs code to 0."""
+    d = 128
+    if kernel == "row":
+        rows = 96
+    else:
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        rows = cus * 1024 * (4 if dt == "f32" else 8) // d + 64
+    rng = np.random.default_rng(SEED + 71)
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    x[:, 1] = 40.0 * np.sign(x[:, 1] + 0.5)               # the row max, in the first lane's 16 bytes
+    if dt == "bf16":
+        bits = to_bf16_bits(x)
+        snan = (np.uint16(0x7F81), np.uint16(0xFF81))
+    elif dt == "f16":
+        bits = x.astype(np.float16).view(np.uint16)
+        snan = (np.uint16(0x7C01), np.uint16(0xFC01))
+    else:
+        bits = x.view(np.uint32).copy()
+        snan = (np.uint32(0x7F800001), np.uint32(0xFF800001))
+    bits[0::3, 0] = snan[0]                                # same lane as the max
+    bits[1::3, 2] = snan[1]
+    bits[2::5, d - 1] = snan[0]                            # another lane
+    bits[7::11, :] = snan[1]                               # whole rows
+    if dt == "bf16":
+        xt = torch.from_numpy(bits.view(np.int16)).to(device).view(torch.bfloat16)
+        x32 = (bits.astype(np.uint32) << 16).view(np.float32)
+    elif dt == "f16":
+        xt = torch.from_numpy(bits.view(np.float16)).to(device)
+        x32 = bits.view(np.float16).astype(np.float32)
+    else:
+        xt = torch.from_numpy(bits.view(np.float32)).to(device)
+        x32 = bits.view(np.float32)
+    codes, scales = ppk.quantize(xt.reshape(1, rows, d))
+    ref_codes, ref_scales, _ = oracle.quantize(x32.reshape(1, rows, d))
+    assert np.array_equal(codes.cpu().numpy(), ref_codes)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+    assert float(ref_scales[0, 0]) == np.float32(40.0) / np.float32(127.0)  # the NaN did not hide the max
+
+
 def test_quantize_nonfinite_rows_flagged(device):
     d = 128
     x = np.random.default_rng(SEED).standard_normal((1, 4, d)).astype(np.float32)

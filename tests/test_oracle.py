@@ -107,6 +107,27 @@ def test_quantize_nonfinite_rows_are_counted():
     assert scales[2] == np.inf and not codes[2].any()
 
 
+def test_quantize_absmax_skips_nans_of_both_kinds():
+    """int8_kv_ops.rs:17 folds |x| with f32::max, which returns the other argument whenever one is NaN,
+    quiet or signalling: the scale is max(nanmax|x| / 127, 1e-12) and the NaNs code to 0."""
+    x = np.random.default_rng(SEED).standard_normal((6, 64)).astype(np.float32)
+    x[:, 5] = 40.0
+    bits = x.view(np.uint32)
+    bits[0, 0] = 0x7F800001   # signalling NaN before the max
+    bits[1, 9] = 0xFF800001   # negative signalling NaN after it
+    bits[2, 63] = 0x7FA00000  # signalling NaN last
+    bits[3, 7] = 0x7FC00000   # quiet NaN
+    bits[4, :] = 0xFF800001   # all NaN -> scale 1e-12
+    codes, scales, bad = oracle.quantize(x)
+    assert bad == 5
+    amax = np.fmax.reduce(np.abs(x), axis=1, initial=np.float32(0))  # fmax skips NaN
+    want = np.maximum(amax / np.float32(127.0), np.float32(1e-12))
+    assert np.array_equal(scales, want.astype(np.float32))
+    assert scales[0] == np.float32(40.0) / np.float32(127.0) and scales[4] == np.float32(1e-12)
+    assert codes[0, 0] == 0 and codes[1, 9] == 0 and not codes[4].any()
+    assert codes[0, 5] == 127
+
+
 def _planted_reciprocal(x):
     """The AMD variant's rule (kv_int8.cpp:51): absmax * (1/127) instead of absmax / 127."""
     amax = np.max(np.abs(x), axis=-1)
