@@ -384,6 +384,23 @@ PPK_API int32_t ppk_kv_cache_release(ppk_kv_cache* cache);
 PPK_API int32_t ppk_kv_cache_info(const ppk_kv_cache* cache, PpkKvInfo* out);
 /* LayerCache::truncate_committed: new_len <= length; storage untouched. */
 PPK_API int32_t ppk_kv_cache_truncate(ppk_kv_cache* cache, uint32_t new_len);
+/* LayerCache::adopt_graph_view (app/src/model/cache.rs:55-64): a cache over
+   caller-owned f32 K and V, each [heads, capacity, head_dim] (a graph decode
+   session's buffers, config->kind = PPK_KV_F32), holding committed_len tokens.
+   The library never frees or reallocates that memory; it must stay valid
+   while the cache or a snapshot of it lives. Writes that fit go into it in
+   place; growth, a write through a shared snapshot, or a batch write moves
+   the cache into storage of its own (committed prefix copied). PpkKvInfo's
+   storage_id is the graph storage identity (cache.rs:51-53). Errors:
+   "invalid graph KV view" (not f32, null or misaligned, K and V overlapping,
+   committed_len > capacity, capacity > max_context). */
+PPK_API int32_t ppk_kv_cache_adopt(ppk_context* ctx, const PpkKvConfig* config, void* k, void* v,
+                                   uint32_t capacity, uint32_t committed_len, ppk_kv_cache** out);
+/* LayerCache::advance_graph_length (cache.rs:66-73): metadata-only commit of
+   the slot a graph wrote; requires length == previous, next == previous + 1
+   and next <= capacity ("graph KV commit length differs from validated host
+   state"). */
+PPK_API int32_t ppk_kv_cache_advance(ppk_kv_cache* cache, uint32_t previous, uint32_t next);
 /* The cache's own rows, length = committed tokens (LayerCache::key / value / arena). */
 PPK_API int32_t ppk_kv_cache_view(const ppk_kv_cache* cache, PpkKvView* out);
 /* LayerCache::query / Int8LayerCache::query: write tokens at slot past

@@ -42,6 +42,7 @@ struct Arena {
   ppk_context* ctx = nullptr;
   uint32_t kind = 0, heads = 0, head_dim = 0, capacity = 0, batch = 0;
   bool grouped = false;
+  bool external = false;  // K and V are caller-owned (an adopted graph view): never freed here
   void* base = nullptr;
   size_t bytes = 0;
   uint8_t* k = nullptr;
@@ -66,9 +67,18 @@ struct Arena {
   size_t slot_bytes() const {
     return 2 * size_t(heads) * (row_bytes() + (kind == PPK_KV_INT8 ? scale_row_bytes() : 0));
   }
+  size_t plane_bytes() const { return size_t(batch) * heads * row_bytes(); }
+  // Whether [p, p + n) overlaps the arena's storage: the whole allocation,
+  // or for an external arena its K and V planes.
   bool contains(const void* p, size_t n) const {
-    const auto a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(base);
-    return a < b + bytes && b < a + n;
+    auto hit = [&](const void* lo, size_t len) {
+      const auto a = reinterpret_cast<uintptr_t>(p), b = reinterpret_cast<uintptr_t>(lo);
+      return len > 0 && n > 0 && a < b + len && b < a + n;
+    };
+    return external ? hit(k, plane_bytes()) || hit(v, plane_bytes()) : hit(base, bytes);
+  }
+  bool overlaps(const Arena& o) const {
+    return o.external ? contains(o.k, o.plane_bytes()) || contains(o.v, o.plane_bytes()) : contains(o.base, o.bytes);
   }
 
   ~Arena() {
@@ -319,6 +329,47 @@ void truncate(ppk_kv_cache& c, uint32_t new_len) {
   c.committed = new_len;
 }
 
+// LayerCache::adopt_graph_view (cache.rs:55-64): caller-owned f32 K and V of
+// [heads, capacity, head_dim] become the storage of a new cache holding
+// committed_len tokens. Writes that fit go into that memory in place; growth
+// or copy-on-write moves the cache into storage of its own, as for any cache.
+ppk_kv_cache* adopt(ppk_context* ctx, const PpkKvConfig& in, void* k, void* v, uint32_t capacity,
+                    uint32_t committed_len) {
+  require(in.struct_size >= sizeof(PpkKvConfig), "PpkKvConfig.struct_size too small");
+  require(in.kind == PPK_KV_F32 && in.heads > 0 && in.head_dim > 0, "invalid graph KV view");
+  std::unique_ptr<ppk_kv_cache> c(create(ctx, in));
+  const PpkKvConfig& cfg = c->cfg;
+  const size_t plane = size_t(cfg.heads) * capacity * cfg.head_dim * 4;
+  const auto kp = reinterpret_cast<uintptr_t>(k), vp = reinterpret_cast<uintptr_t>(v);
+  require(k && v && kp % 4 == 0 && vp % 4 == 0 && committed_len <= capacity && capacity <= cfg.max_context &&
+              (plane == 0 || kp + plane <= vp || vp + plane <= kp),
+          "invalid graph KV view");
+  auto a = std::make_shared<Arena>();
+  a->ctx = ctx;
+  a->kind = cfg.kind;
+  a->heads = cfg.heads;
+  a->head_dim = cfg.head_dim;
+  a->capacity = capacity;
+  a->batch = 1;
+  a->external = true;
+  a->k = static_cast<uint8_t*>(k);
+  a->v = static_cast<uint8_t*>(v);
+  auto backing = std::make_shared<Backing>();
+  backing->arena = std::move(a);
+  c->backing = std::move(backing);
+  c->committed = committed_len;
+  return c.release();
+}
+
+// LayerCache::advance_graph_length (cache.rs:66-73): the graph wrote slot
+// `previous`; the committed length moves by exactly one, metadata only.
+void advance(ppk_kv_cache& c, uint32_t previous, uint32_t next) {
+  require(c.committed == previous && uint64_t(next) == uint64_t(previous) + 1 && c.backing &&
+              next <= c.backing->arena->capacity,
+          "graph KV commit length differs from validated host state");
+  c.committed = next;
+}
+
 // LayerCache::query (cache.rs:194-283), Int8LayerCache::query (int8_cache.rs:313-323).
 void query(ppk_context* ctx, hipStream_t stream, ppk_kv_cache& c, uint32_t past, const PpkKvWrite& w,
            PpkKvView* out) {
@@ -337,8 +388,11 @@ void query(ppk_context* ctx, hipStream_t stream, ppk_kv_cache& c, uint32_t past,
   const uint32_t capacity = grown_capacity(c.cfg, current, end);
   // Validation done; device work from here on.
   DeviceGuard guard(ctx->device);
+  // Shared with a snapshot (Arc::strong_count > 1, cache.rs:249-251): counted
+  // before `target` takes its own reference.
+  const bool shared = c.backing && c.backing.use_count() > 1;
   std::shared_ptr<Backing> target = c.backing;
-  if (!target || capacity > current || target.use_count() > 1) {
+  if (!target || capacity > current || shared) {
     auto arena = make_arena(ctx, stream, c.cfg, capacity, 1, false);
     auto fresh = std::make_shared<Backing>();
     fresh->arena = arena;
@@ -445,7 +499,10 @@ std::shared_ptr<Arena> reusable_arena(ppk_kv_cache* const* caches, uint32_t batc
         if (!registered) return nullptr;
         continue;
       }
-      if (backing->arena->capacity != capacity) return nullptr;
+      // Only an independent same-capacity row may take an orphaned slot; a
+      // view that aliases the candidate's storage (an adopted graph view over
+      // its rows) may not (cache.rs:513-519).
+      if (backing->arena->capacity != capacity || candidate->overlaps(*backing->arena)) return nullptr;
     }
     if (!candidate->owners[row].expired()) return nullptr;
     changed.push_back(row);

@@ -776,6 +776,22 @@ int32_t ppk_kv_cache_truncate(ppk_kv_cache* cache, uint32_t new_len) {
   });
 }
 
+int32_t ppk_kv_cache_adopt(ppk_context* ctx, const PpkKvConfig* config, void* k, void* v, uint32_t capacity,
+                           uint32_t committed_len, ppk_kv_cache** out) {
+  if (out) *out = nullptr;
+  return call([&] {
+    ppk::require(ctx && config && out, "ppk_kv_cache_adopt: null argument");
+    *out = ppk::kv::adopt(ctx, *config, k, v, capacity, committed_len);
+  });
+}
+
+int32_t ppk_kv_cache_advance(ppk_kv_cache* cache, uint32_t previous, uint32_t next) {
+  return call([&] {
+    ppk::require(cache != nullptr, "ppk_kv_cache_advance: null cache");
+    ppk::kv::advance(*cache, previous, next);
+  });
+}
+
 int32_t ppk_kv_cache_view(const ppk_kv_cache* cache, PpkKvView* out) {
   return call([&] {
     ppk::require(cache != nullptr, "ppk_kv_cache_view: null cache");

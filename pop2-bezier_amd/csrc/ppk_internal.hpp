@@ -166,6 +166,9 @@ ppk_kv_cache* create(ppk_context* ctx, const PpkKvConfig& cfg);
 void info(const ppk_kv_cache& c, PpkKvInfo* out);
 void view(const ppk_kv_cache& c, PpkKvView* out);
 void truncate(ppk_kv_cache& c, uint32_t new_len);
+ppk_kv_cache* adopt(ppk_context* ctx, const PpkKvConfig& cfg, void* k, void* v, uint32_t capacity,
+                    uint32_t committed_len);
+void advance(ppk_kv_cache& c, uint32_t previous, uint32_t next);
 void query(ppk_context* ctx, hipStream_t stream, ppk_kv_cache& c, uint32_t past, const PpkKvWrite& w,
            PpkKvView* out);
 ppk_write_plan* plan_create(ppk_context* ctx, hipStream_t stream, const uint32_t* past_lens, uint32_t batch,

@@ -126,6 +126,9 @@ FUNCTIONS = {
     "ppk_kv_cache_release": (ctypes.c_int32, [_ptr]),
     "ppk_kv_cache_info": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkKvInfo)]),
     "ppk_kv_cache_truncate": (ctypes.c_int32, [_ptr, _u32]),
+    "ppk_kv_cache_adopt": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkKvConfig), _ptr, _ptr, _u32, _u32,
+                                            ctypes.POINTER(_ptr)]),
+    "ppk_kv_cache_advance": (ctypes.c_int32, [_ptr, _u32, _u32]),
     "ppk_kv_cache_view": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkKvView)]),
     "ppk_kv_query": (ctypes.c_int32, [_ptr, _ptr, _ptr, _u32, ctypes.POINTER(PpkKvWrite), ctypes.POINTER(PpkKvView)]),
     "ppk_write_plan_create": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(_u32), _u32, _u32, _u32,

@@ -96,7 +96,43 @@ class LayerCache:
         """A snapshot sharing storage; the next write through either side copies first."""
         h = ctypes.c_void_p()
         check(lib().ppk_kv_cache_clone(self.handle, ctypes.byref(h)), "ppk_kv_cache_clone")
-        return LayerCache(self.kind, self.heads, self.head_dim, device=self.device, _handle=h)
+        out = LayerCache(self.kind, self.heads, self.head_dim, device=self.device, _handle=h)
+        out._adopted = getattr(self, "_adopted", None)  # adopted memory stays referenced by every snapshot
+        return out
+
+    @staticmethod
+    def adopt_graph_view(key: torch.Tensor, value: torch.Tensor, capacity: int, committed_len: int,
+                         *, max_context: int = 0) -> "LayerCache":
+        """LayerCache::adopt_graph_view (cache.rs:55-64): a cache over f32 K/V [heads, capacity, D] that
+        the caller owns (a graph decode session's buffers), holding committed_len tokens. The tensors stay
+        referenced by the cache; the library writes into them in place while writes fit."""
+        if (key.dim() != 3 or value.shape != key.shape or key.shape[1] != capacity or key.dtype != torch.float32
+                or value.dtype != key.dtype or key.device != value.device or not key.is_cuda
+                or not (key.is_contiguous() and value.is_contiguous()) or 0 in (key.shape[0], key.shape[2])):
+            raise ValueError("invalid graph KV view")
+        return LayerCache._adopt(key.data_ptr(), value.data_ptr(), key.shape[0], key.shape[2], capacity,
+                                 committed_len, max_context=max_context, device=key.device, keep=(key, value))
+
+    @staticmethod
+    def _adopt(k_ptr: int, v_ptr: int, heads: int, head_dim: int, capacity: int, committed_len: int, *,
+               max_context: int = 0, device=None, keep=()) -> "LayerCache":
+        """ppk_kv_cache_adopt over raw device addresses; `keep` holds whatever owns that memory."""
+        cfg = _abi.PpkKvConfig(struct_size=ctypes.sizeof(_abi.PpkKvConfig), kind=_abi.PPK_KV_F32, heads=heads,
+                               head_dim=head_dim, max_context=max_context, min_capacity=0)
+        h = ctypes.c_void_p()
+        check(lib().ppk_kv_cache_adopt(context(device), ctypes.byref(cfg), k_ptr, v_ptr, capacity, committed_len,
+                                       ctypes.byref(h)), "ppk_kv_cache_adopt")
+        out = LayerCache(_abi.PPK_KV_F32, heads, head_dim, device=device, _handle=h)
+        out._adopted = keep
+        return out
+
+    def advance_graph_length(self, previous: int, next_len: int) -> None:
+        """LayerCache::advance_graph_length (cache.rs:66-73): commit the slot a graph wrote."""
+        check(lib().ppk_kv_cache_advance(self.handle, previous, next_len), "ppk_kv_cache_advance")
+
+    def graph_storage_identity(self) -> int | None:
+        """LayerCache::graph_storage_identity (cache.rs:51-53): identity of the storage owner, None without storage."""
+        return self.info().storage_id or None
 
     def info(self) -> _abi.PpkKvInfo:
         out = _abi.PpkKvInfo(struct_size=ctypes.sizeof(_abi.PpkKvInfo))

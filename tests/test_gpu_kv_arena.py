@@ -84,8 +84,11 @@ def test_capacity_grows_by_powers_of_two_without_losing_committed_prefix(device)
         k, v = data(2, n, 3, step * 1000.0), data(2, n, 3, step * 1000.0 + 500)
         ek, ev = cat(old_k, k), cat(old_v, v)
         prev = len(c)
+        before = c.info()
         view = c.query(k, v, prev, True)
         assert c.info().capacity == cap and len(c) == prev + n
+        # A sole owner writes in place while the capacity holds (cache.rs:249-266): same storage, no copy.
+        assert (c.info().storage_id == before.storage_id) == (before.capacity == cap), step
         assert torch.equal(read(view, "k"), ek) and torch.equal(read(view, "v"), ev)
         old_k, old_v = ek, ev
     assert len(c) == 1024
@@ -493,6 +496,89 @@ def test_unsafe_reuse_falls_back_to_a_new_arena(device, case):
     assert caches[0].info().arena_id != arena, case
     if snapshot is not None:
         assert torch.equal(snapshot.key(), saved)
+
+
+def test_adopted_alias_of_the_batch_arena_keeps_the_safe_fallback(device):
+    """cache.rs:664-681, case 3: row 1 replaced by a graph view adopted over the batch arena's own rows
+    of that slot; the next batch write must not reuse the arena (the view aliases it) and still carries
+    the adopted history."""
+    caches = grouped_rows()
+    arena = caches[0].info().arena_id
+    own = caches[1].view()
+    history = caches[1].key().clone()
+    assert torch.equal(history, data(2, 3, 3, 10.0))
+    old = caches[1]
+    caches[1] = LayerCache._adopt(own.k, own.v, 2, 3, own.capacity, 3, device=device, keep=(caches[0],))
+    del old                                            # its slot is orphaned; the memory stays (caches[0])
+    assert caches[1].info().arena_id != arena and len(caches[1]) == 3
+    cur = batch_data(3, 2, 3, 500.0)
+    view = LayerCache.query_batch(caches, cur, cur, [3, 3, 3], True)
+    assert caches[0].info().arena_id != arena
+    assert caches[1].info().arena_id == caches[0].info().arena_id
+    assert torch.equal(rows_of(view, 1, 2, 4), cat(history, cur[1]))
+    assert torch.equal(rows_of(view, 0, 2, 4), cat(data(2, 3, 3, 0.0), cur[0]))
+
+
+def test_adopted_graph_view_commits_in_place_and_advances_by_one(device):
+    """graph_decode.rs:335-383 over cache.rs:55-73: the first graph commit adopts the graph's f32 buffers
+    with the new length, later commits advance it by exactly one; the identity follows the storage."""
+    heads, cap, d = 2, 64, 4
+    key = torch.zeros(heads, cap, d, device=device)
+    value = torch.zeros_like(key)
+    key[:, :3], value[:, :3] = data(heads, 3, d, 1.0), data(heads, 3, d, 2.0)
+    c = LayerCache.adopt_graph_view(key, value, cap, 3)
+    ident = c.graph_storage_identity()
+    assert ident is not None and len(c) == 3
+    assert c.info().reserved_bytes == 2 * key.numel() * 4 and c.info().capacity == cap
+    assert torch.equal(c.key(), key[:, :3]) and torch.equal(c.value(), value[:, :3])
+    key[:, 3], value[:, 3] = 7.0, 8.0                  # the graph wrote slot 3
+    c.advance_graph_length(3, 4)
+    assert len(c) == 4 and c.graph_storage_identity() == ident and torch.equal(c.key(), key[:, :4])
+    for prev, nxt in ((3, 4), (4, 6), (4, 4), (5, 6)):
+        expect_status(_abi.PPK_PRECONDITION, lambda: c.advance_graph_length(prev, nxt))
+    assert len(c) == 4
+    nxt = data(heads, 1, d, 50.0)
+    c.query(nxt, nxt, 4, True)                         # fits: written into the adopted memory in place
+    torch.cuda.synchronize()
+    assert c.graph_storage_identity() == ident and torch.equal(key[:, 4:5], nxt)
+    snap = c.clone()
+    saved = key.clone()
+    s2 = data(heads, 1, d, 60.0)
+    snap.query(s2, s2, 5, True)                        # shared: the snapshot copies first
+    torch.cuda.synchronize()
+    assert snap.graph_storage_identity() != ident and torch.equal(key, saved)
+    assert torch.equal(snap.key(), torch.cat([saved[:, :5], s2], 1)) and len(c) == 5
+    c.truncate_committed(2)
+    assert c.graph_storage_identity() == ident
+    grow = data(heads, 70, d, 90.0)
+    c.query(grow, grow, 2, True)                       # past the adopted capacity: own storage
+    torch.cuda.synchronize()
+    assert c.graph_storage_identity() != ident and c.info().capacity == 128 and torch.equal(key, saved)
+    assert torch.equal(c.key(), torch.cat([saved[:, :2], grow], 1))
+    full = LayerCache.adopt_graph_view(key, value, cap, cap)
+    expect_status(_abi.PPK_PRECONDITION, lambda: full.advance_graph_length(cap, cap + 1))
+
+
+def test_adopt_graph_view_rejects_invalid_views(device):
+    """cache.rs:55-63: shape, dtype, length and capacity checks fail with "invalid graph KV view"."""
+    key = torch.zeros(2, 8, 4, device=device)
+    value = torch.zeros_like(key)
+    k, v = key.data_ptr(), value.data_ptr()
+    for bad in (dict(committed_len=9), dict(max_context=4), dict(v_ptr=k + 16), dict(k_ptr=k + 2),
+                dict(k_ptr=0), dict(heads=0)):
+        args = dict(k_ptr=k, v_ptr=v, heads=2, head_dim=4, capacity=8, committed_len=3, max_context=0)
+        args.update(bad)
+        with pytest.raises(ppk.PpkError, match="invalid graph KV view"):
+            LayerCache._adopt(args["k_ptr"], args["v_ptr"], args["heads"], args["head_dim"], args["capacity"],
+                              args["committed_len"], max_context=args["max_context"], device=device)
+    cfg = _abi.PpkKvConfig(struct_size=ctypes.sizeof(_abi.PpkKvConfig), kind=_abi.PPK_KV_BF16, heads=2, head_dim=4)
+    h = ctypes.c_void_p()
+    status = _abi.lib().ppk_kv_cache_adopt(ppk.context(device), ctypes.byref(cfg), k, v, 8, 3, ctypes.byref(h))
+    assert status == _abi.PPK_PRECONDITION and not h.value
+    assert b"invalid graph KV view" in _abi.lib().ppk_last_error()
+    for kk, vv in ((key.half(), value.half()), (key[:, :4], value[:, :4]), (key, value[:1])):
+        with pytest.raises(ValueError, match="invalid graph KV view"):
+            LayerCache.adopt_graph_view(kk, vv, 8, 0)
 
 
 def test_truncate_is_metadata_only_and_append_preserves_longer_snapshots(device):
