@@ -1561,32 +1561,39 @@ __device__ __forceinline__ void scatter_body(const ppk::ScatterArgs& a) {
 // Batched rectangle copy with zero fill (arena joins, growth and
 // copy-on-write: every row of a new arena receives its committed prefix and
 // zeros up to its capacity in one launch, instead of a memset of the whole
-// arena plus one runtime copy per plane and sequence). Grid-stride over the
-// rectangle's units, eight in flight per thread.
+// arena plus one runtime copy per plane and sequence). Blocks stride over
+// tiles of one row each, eight units in flight per thread.
 // ---------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void copy_rect(const ppk::Copy2D& c, uint32_t unit_bytes) {
-  constexpr int ILP = 8;
+  constexpr uint32_t ILP = 8;
   const uint32_t per_row = c.fill / unit_bytes;
   const uint32_t copy_cols = c.width / unit_bytes;
-  const uint64_t total = uint64_t(c.height) * per_row;
-  const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
-  for (uint64_t base = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; base < total; base += ILP * stride) {
+  if (per_row == 0) return;
+  // Tiles of up to ILP * blockDim.x units of one row: a block finds its tile's
+  // row and first column with one (block-uniform) division, and each lane's
+  // columns follow by addition, so no unit pays an integer division.
+  const uint32_t tile = min(per_row, ILP * blockDim.x);
+  const uint32_t tiles_per_row = (per_row + tile - 1) / tile;
+  const uint64_t tiles = uint64_t(c.height) * tiles_per_row;
+  for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+    const uint64_t row = t / tiles_per_row;
+    const uint32_t col0 = uint32_t(t - row * tiles_per_row) * tile;
+    const uint32_t end = min(col0 + tile, per_row);
+    const T* src = reinterpret_cast<const T*>(c.src + row * c.spitch);
+    T* dst = reinterpret_cast<T*>(c.dst + row * c.dpitch);
     T val[ILP];
-    uint64_t row[ILP];
-    uint32_t col[ILP];
 #pragma unroll
-    for (int k = 0; k < ILP; ++k) {
-      const uint64_t i = base + k * stride;
-      row[k] = i / per_row;
-      col[k] = uint32_t(i - row[k] * per_row);
+    for (uint32_t k = 0; k < ILP; ++k) {
+      const uint32_t col = col0 + k * blockDim.x + threadIdx.x;
       val[k] = T{};
-      if (i < total && col[k] < copy_cols)
-        val[k] = __builtin_nontemporal_load(reinterpret_cast<const T*>(c.src + row[k] * c.spitch) + col[k]);
+      if (col < end && col < copy_cols) val[k] = __builtin_nontemporal_load(src + col);
     }
 #pragma unroll
-    for (int k = 0; k < ILP; ++k)
-      if (base + k * stride < total) reinterpret_cast<T*>(c.dst + row[k] * c.dpitch)[col[k]] = val[k];
+    for (uint32_t k = 0; k < ILP; ++k) {
+      const uint32_t col = col0 + k * blockDim.x + threadIdx.x;
+      if (col < end) dst[col] = val[k];
+    }
   }
 }
 
