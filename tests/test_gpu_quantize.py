@@ -92,6 +92,34 @@ def test_quantize_streaming_kernel_special_rows(device, d, dt):
     assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
 
 
+def test_streaming_quantize_quotients_next_to_half_integers(device):
+    """f32 rows whose quotients x / s lie within 0-3 ulps of a half-integer on either side (and exactly on
+    one), at the streaming kernel's size: the codes decided near a tie equal the oracle's bit for bit."""
+    d = 128
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    rows = cus * 1024 * 4 // d + 64
+    rng = np.random.default_rng(SEED + 81)
+    amax = (np.float32(127.0) * np.float32(2.0) ** rng.integers(-20, 20, rows).astype(np.float32)
+            * (1 + rng.random(rows, dtype=np.float32))).astype(np.float32)
+    s = np.maximum(amax / np.float32(127.0), np.float32(1e-12)).astype(np.float32)
+    half = rng.integers(-127, 127, (rows, d)).astype(np.float32) + np.float32(0.5)
+    x = (half * s[:, None]).astype(np.float32)
+    steps = rng.integers(-3, 4, (rows, d))
+    toward = np.where(steps > 0, np.float32(np.inf), np.float32(-np.inf))
+    for k in range(1, 4):
+        x = np.where(np.abs(steps) >= k, np.nextafter(x, toward).astype(np.float32), x)
+    x[:, 0] = amax
+    x[:, 1] = -amax * np.float32(0.5)                       # a quotient next to -63.5
+    xt = torch.from_numpy(x).to(device)
+    codes, scales = ppk.quantize(xt.reshape(1, rows, d))
+    ref_codes, ref_scales, _ = oracle.quantize(x.reshape(1, rows, d))
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), ref_scales.view(np.uint32))
+    got = codes.cpu().numpy()
+    assert np.array_equal(got, ref_codes), f"{int((got != ref_codes).sum())} codes differ"
+    q = x / s[:, None]                                      # share of values that sit within the band
+    assert np.mean(np.abs(np.abs(q - np.rint(q)) - 0.5) < 2.0 ** -14) > 0.5
+
+
 @pytest.mark.parametrize("kernel", ["row", "streaming"])
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 def test_quantize_signalling_nan_skipped_by_absmax(device, dt, kernel):
