@@ -235,3 +235,29 @@ def test_kv_arena_entry_points_refuse_null_arguments():
 def test_int8_gate_refuses_null_context():
     st = _abi.PpkInt8KvStatus(struct_size=ctypes.sizeof(_abi.PpkInt8KvStatus))
     assert _abi.lib().ppk_prepare_int8_kv(None, 1, 64, ctypes.byref(st)) == _abi.PPK_PRECONDITION
+
+
+def test_error_text_is_thread_local():
+    """Two threads failing different checks concurrently each read back their own message
+    (the reference keeps its last error per thread, painter_ffi.cpp:12,18-19). Host-only calls."""
+    import threading
+
+    lib = _abi.lib()
+    bad = {"max_past": "max_past exceeds capacity", "q_dtype": "dtype must be f32, bf16 or f16"}
+    seen = {k: set() for k in bad}
+
+    def worker(field):
+        a = _abi.PpkAttentionArgs(struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), rows=16, heads=16,
+                                  capacity=64, head_dim=64)
+        setattr(a, field, 1000 if field == "max_past" else 7)
+        for _ in range(2000):
+            assert lib.ppk_attention_plan(None, ctypes.byref(a), None, None, None) == _abi.PPK_PRECONDITION
+            seen[field].add(lib.ppk_last_error().decode())
+
+    threads = [threading.Thread(target=worker, args=(f,)) for f in bad]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for field, texts in seen.items():
+        assert len(texts) == 1 and bad[field] in next(iter(texts)), (field, texts)
