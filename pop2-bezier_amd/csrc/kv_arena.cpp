@@ -113,7 +113,7 @@ std::shared_ptr<Arena> make_arena(ppk_context* ctx, hipStream_t stream, const Pp
   const size_t offs = grouped ? align256(size_t(batch) * 2 * 4) : 0;
   a->bytes = 2 * plane + 2 * splane + offs;
   ppk::DeviceGuard guard(ctx->device);
-  const hipError_t st = hipMallocAsync(&a->base, a->bytes, stream);
+  const hipError_t st = hipMallocFromPoolAsync(&a->base, a->bytes, ctx->mem_pool, stream);
   if (st != hipSuccess) {
     a->base = nullptr;
     throw PreconditionError(std::string("KV arena allocation of ") + std::to_string(a->bytes) +
@@ -176,7 +176,8 @@ struct SourceSnapshot {
   SourceSnapshot(const void* k_src, const void* v_src, size_t n, const Arena& dst, hipStream_t s)
       : k(k_src), v(v_src), stream(s) {
     if (!dst.contains(k_src, n) && !dst.contains(v_src, n)) return;
-    check_exec(hipMallocAsync(&tmp, 2 * align256(n), s), "hipMallocAsync (aliased source)");
+    check_exec(hipMallocFromPoolAsync(&tmp, 2 * align256(n), dst.ctx->mem_pool, s),
+               "hipMallocFromPoolAsync (aliased source)");
     uint8_t* t = static_cast<uint8_t*>(tmp);
     check_exec(hipMemcpyAsync(t, k_src, n, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (aliased K)");
     check_exec(hipMemcpyAsync(t + align256(n), v_src, n, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (aliased V)");
@@ -462,7 +463,7 @@ ppk_write_plan* plan_create(ppk_context* ctx, hipStream_t stream, const uint32_t
   }
   if (!plan->dev) {
     void* dev = nullptr;
-    const hipError_t st = hipMallocAsync(&dev, bytes, stream);
+    const hipError_t st = hipMallocFromPoolAsync(&dev, bytes, ctx->mem_pool, stream);
     if (st != hipSuccess)
       throw PreconditionError(std::string("write plan allocation failed: ") + hipGetErrorString(st));
     plan->dev = static_cast<uint32_t*>(dev);

@@ -638,6 +638,18 @@ int32_t ppk_context_create(int32_t device, const char* code_object_path, ppk_con
         throw ppk::PreconditionError(std::string("kernel symbol missing: ") + kFnNames[i]);
       }
     }
+    hipMemPoolProps props{};
+    props.allocType = hipMemAllocationTypePinned;
+    props.handleTypes = hipMemHandleTypeNone;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = device;
+    uint64_t keep = UINT64_MAX;
+    if (hipMemPoolCreate(&ctx->mem_pool, &props) != hipSuccess ||
+        hipMemPoolSetAttribute(ctx->mem_pool, hipMemPoolAttrReleaseThreshold, &keep) != hipSuccess) {
+      if (ctx->mem_pool) (void)hipMemPoolDestroy(ctx->mem_pool);
+      (void)hipModuleUnload(ctx->module);
+      throw ppk::PreconditionError("device memory pool set-up failed");
+    }
     *out = ctx.release();
   });
 }
@@ -658,6 +670,7 @@ int32_t ppk_context_release(ppk_context* ctx) {
     }
     // Recycled write-plan vectors: a synchronous free (their streams may be gone).
     for (auto& b : ctx->plan_pool) (void)hipFree(b.dev);
+    if (ctx->mem_pool) (void)hipMemPoolDestroy(ctx->mem_pool);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
   });
 }

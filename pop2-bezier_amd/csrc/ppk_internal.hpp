@@ -80,6 +80,14 @@ struct ppk_context {
   std::mutex plan_mutex;
   std::vector<PlanBuffer> plan_pool;
 
+  // Stream-ordered pool for everything the library allocates (arenas, plan
+  // vectors, aliased-source copies), kept apart from the runtime's default
+  // pool and set to hold freed memory: within a join, the single-sequence
+  // arenas a layer frees are reused for the next layer's batch arena instead
+  // of mapping new pages (a 24-layer join of B = 32: 212 -> 19 ms of host
+  // time). Released at ppk_context_release.
+  hipMemPool_t mem_pool = nullptr;
+
   std::mutex prof_mutex;
   bool profiling = false;
   std::vector<ppk::EventPair> pending[PPK_KERNEL_COUNT];
