@@ -313,9 +313,9 @@ PPK_API int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiS
    must be ordered before that release by the caller. Calls that allocate
    (a first write, growth, copy-on-write, a new batch arena) refuse to run
    under HIP graph capture. Arenas and plan vectors come from a memory pool
-   owned by the context, which keeps freed memory mapped for the library's
-   next allocations (not the runtime's default pool) and returns it at
-   ppk_context_release. */
+   owned by the context (not the runtime's default pool); the storage of
+   released caches is kept by the context (up to 32 GiB) for the next arena
+   of the same size on the same stream, and returned at ppk_context_release. */
 enum { PPK_KV_INT8 = 0, PPK_KV_BF16 = 1, PPK_KV_F16 = 2, PPK_KV_F32 = 3 };
 
 typedef struct ppk_kv_cache ppk_kv_cache;

@@ -82,10 +82,17 @@ struct Arena {
   }
 
   ~Arena() {
-    if (base) {
-      ppk::DeviceGuard guard(ctx->device);
-      (void)hipFreeAsync(base, last_stream);
+    if (!base) return;
+    {
+      std::lock_guard<std::mutex> lock(ctx->block_mutex);
+      if (ctx->block_cache_bytes + bytes <= ppk_context::kBlockCacheBytes) {
+        ctx->block_cache.push_back({base, bytes, last_stream});
+        ctx->block_cache_bytes += bytes;
+        return;
+      }
     }
+    ppk::DeviceGuard guard(ctx->device);
+    (void)hipFreeAsync(base, last_stream);
   }
 };
 
@@ -113,11 +120,25 @@ std::shared_ptr<Arena> make_arena(ppk_context* ctx, hipStream_t stream, const Pp
   const size_t offs = grouped ? align256(size_t(batch) * 2 * 4) : 0;
   a->bytes = 2 * plane + 2 * splane + offs;
   ppk::DeviceGuard guard(ctx->device);
-  const hipError_t st = hipMallocFromPoolAsync(&a->base, a->bytes, ctx->mem_pool, stream);
-  if (st != hipSuccess) {
-    a->base = nullptr;
-    throw PreconditionError(std::string("KV arena allocation of ") + std::to_string(a->bytes) +
-                            " bytes failed: " + hipGetErrorString(st));
+  {
+    // A released arena of the same size last used on this stream.
+    std::lock_guard<std::mutex> lock(ctx->block_mutex);
+    auto& cache = ctx->block_cache;
+    for (size_t i = cache.size(); i-- > 0;)
+      if (cache[i].bytes == a->bytes && cache[i].stream == stream) {
+        a->base = cache[i].ptr;
+        ctx->block_cache_bytes -= cache[i].bytes;
+        cache.erase(cache.begin() + std::ptrdiff_t(i));
+        break;
+      }
+  }
+  if (!a->base) {
+    const hipError_t st = hipMallocFromPoolAsync(&a->base, a->bytes, ctx->mem_pool, stream);
+    if (st != hipSuccess) {
+      a->base = nullptr;
+      throw PreconditionError(std::string("KV arena allocation of ") + std::to_string(a->bytes) +
+                              " bytes failed: " + hipGetErrorString(st));
+    }
   }
   a->last_stream = stream;
   uint8_t* p = static_cast<uint8_t*>(a->base);

@@ -670,6 +670,7 @@ int32_t ppk_context_release(ppk_context* ctx) {
     }
     // Recycled write-plan vectors: a synchronous free (their streams may be gone).
     for (auto& b : ctx->plan_pool) (void)hipFree(b.dev);
+    for (auto& b : ctx->block_cache) (void)hipFree(b.ptr);  // released arenas kept for reuse
     if (ctx->mem_pool) (void)hipMemPoolDestroy(ctx->mem_pool);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
   });

@@ -80,13 +80,27 @@ struct ppk_context {
   std::mutex plan_mutex;
   std::vector<PlanBuffer> plan_pool;
 
-  // Stream-ordered pool for everything the library allocates (arenas, plan
-  // vectors, aliased-source copies), kept apart from the runtime's default
-  // pool and set to hold freed memory: within a join, the single-sequence
-  // arenas a layer frees are reused for the next layer's batch arena instead
-  // of mapping new pages (a 24-layer join of B = 32: 212 -> 19 ms of host
-  // time). Released at ppk_context_release.
+  // Stream-ordered pool for what the library allocates (arenas, plan
+  // vectors, aliased-source copies), apart from the runtime's default pool.
+  // Released at ppk_context_release.
   hipMemPool_t mem_pool = nullptr;
+
+  // Arena blocks whose caches were released, kept for the next arena of the
+  // same size on the same stream (stream order puts the new writes after the
+  // old readers). The runtime pool hands freed memory back at every stream
+  // synchronisation whatever its release threshold, and a 24-layer join of
+  // B = 32 that took its batch arenas from the runtime spent 160-210 ms
+  // allocating; with released blocks kept here it takes 2-3 ms (1.8 ms of it
+  // the copy kernel). Bounded by kBlockCacheBytes; freed at release.
+  struct CachedBlock {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipStream_t stream = nullptr;
+  };
+  static constexpr size_t kBlockCacheBytes = size_t(32) << 30;
+  std::mutex block_mutex;
+  std::vector<CachedBlock> block_cache;
+  size_t block_cache_bytes = 0;
 
   std::mutex prof_mutex;
   bool profiling = false;
