@@ -581,6 +581,39 @@ def test_adopt_graph_view_rejects_invalid_views(device):
             LayerCache.adopt_graph_view(kk, vv, 8, 0)
 
 
+@pytest.mark.parametrize("kind", [F32, "int8"])
+def test_reused_storage_of_released_caches_reads_as_zeros_past_the_new_history(device, kind):
+    """Storage of released caches is reused for the next arena of the same size: the new cache sees only
+    its own history and zeros in every other slot (the reference's Tensor::zeros, cache.rs:241-247),
+    never the released cache's data; single caches and a batch arena alike."""
+    d = 64
+    old = [LayerCache(kind, 2, d) for _ in range(3)]
+    for c in old:
+        p = data(2, 50, d, 7.0)
+        c.query(p, p, 0, True)
+    LayerCache.query_batch(old, batch_data(3, 2, d, 9.0), batch_data(3, 2, d, 9.0), [50, 50, 50], True)
+    old_single = LayerCache(kind, 2, d)
+    old_single.query(data(2, 60, d, 3.0), data(2, 60, d, 3.0), 0, True)
+    ptrs = {old[0].view().k, old_single.view().k}
+    del old, old_single
+    fresh = [LayerCache(kind, 2, d) for _ in range(3)]
+    for c in fresh:
+        p = data(2, 5, d, 100.0)
+        c.query(p, p, 0, True)
+    view = LayerCache.query_batch(fresh, batch_data(3, 2, d, 200.0), batch_data(3, 2, d, 200.0), [5, 5, 5], True)
+    single = LayerCache(kind, 2, d)
+    sview = single.query(data(2, 4, d, 300.0), data(2, 4, d, 300.0), 0, True)
+    torch.cuda.synchronize()
+    assert ptrs & {view.k, sview.k}, "no released storage was reused"
+    for v, used in ((view, 6), (sview, 4)):
+        full = read(v, "k", v.capacity)
+        assert not full[:, used:].any(), "stale data past the new history"
+        if kind == "int8":
+            assert not read(v, "k_scales", v.capacity)[:, used:].any()
+    if kind == F32:
+        assert torch.equal(rows_of(view, 1, 2, 6), cat(data(2, 5, d, 100.0), batch_data(3, 2, d, 200.0)[1]))
+
+
 def test_truncate_is_metadata_only_and_append_preserves_longer_snapshots(device):
     cache = grouped_rows()[0]
     snapshot = cache.clone()
