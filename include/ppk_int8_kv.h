@@ -315,7 +315,8 @@ PPK_API int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiS
    under HIP graph capture. Arenas and plan vectors come from a memory pool
    owned by the context (not the runtime's default pool); the storage of
    released caches is kept by the context (up to 32 GiB) for the next arena
-   of the same size on the same stream, and returned at ppk_context_release. */
+   of the same size (the reusing stream first waits for an event recorded
+   on the stream that last used it), and returned at ppk_context_release. */
 enum { PPK_KV_INT8 = 0, PPK_KV_BF16 = 1, PPK_KV_F16 = 2, PPK_KV_F32 = 3 };
 
 typedef struct ppk_kv_cache ppk_kv_cache;

@@ -83,15 +83,27 @@ struct Arena {
 
   ~Arena() {
     if (!base) return;
+    ppk::DeviceGuard guard(ctx->device);
     {
       std::lock_guard<std::mutex> lock(ctx->block_mutex);
+      hipEvent_t ev = nullptr;
       if (ctx->block_cache_bytes + bytes <= ppk_context::kBlockCacheBytes) {
-        ctx->block_cache.push_back({base, bytes, last_stream});
-        ctx->block_cache_bytes += bytes;
-        return;
+        if (!ctx->spare_events.empty()) {
+          ev = ctx->spare_events.back();
+          ctx->spare_events.pop_back();
+        } else if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+          ev = nullptr;
+        }
+      }
+      if (ev) {
+        if (hipEventRecord(ev, last_stream) == hipSuccess) {
+          ctx->block_cache.push_back({base, bytes, ev});
+          ctx->block_cache_bytes += bytes;
+          return;
+        }
+        (void)hipEventDestroy(ev);
       }
     }
-    ppk::DeviceGuard guard(ctx->device);
     (void)hipFreeAsync(base, last_stream);
   }
 };
@@ -121,11 +133,14 @@ std::shared_ptr<Arena> make_arena(ppk_context* ctx, hipStream_t stream, const Pp
   a->bytes = 2 * plane + 2 * splane + offs;
   ppk::DeviceGuard guard(ctx->device);
   {
-    // A released arena of the same size last used on this stream.
+    // A released arena of the same size; this stream first waits for the
+    // block's last use.
     std::lock_guard<std::mutex> lock(ctx->block_mutex);
     auto& cache = ctx->block_cache;
     for (size_t i = cache.size(); i-- > 0;)
-      if (cache[i].bytes == a->bytes && cache[i].stream == stream) {
+      if (cache[i].bytes == a->bytes) {
+        if (hipStreamWaitEvent(stream, cache[i].released, 0) != hipSuccess) break;  // allocate instead
+        ctx->spare_events.push_back(cache[i].released);
         a->base = cache[i].ptr;
         ctx->block_cache_bytes -= cache[i].bytes;
         cache.erase(cache.begin() + std::ptrdiff_t(i));

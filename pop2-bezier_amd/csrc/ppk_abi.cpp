@@ -670,7 +670,12 @@ int32_t ppk_context_release(ppk_context* ctx) {
     }
     // Recycled write-plan vectors: a synchronous free (their streams may be gone).
     for (auto& b : ctx->plan_pool) (void)hipFree(b.dev);
-    for (auto& b : ctx->block_cache) (void)hipFree(b.ptr);  // released arenas kept for reuse
+    for (auto& b : ctx->block_cache) {  // released arenas kept for reuse
+      (void)hipEventSynchronize(b.released);
+      (void)hipEventDestroy(b.released);
+      (void)hipFree(b.ptr);
+    }
+    for (hipEvent_t ev : ctx->spare_events) (void)hipEventDestroy(ev);
     if (ctx->mem_pool) (void)hipMemPoolDestroy(ctx->mem_pool);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
   });

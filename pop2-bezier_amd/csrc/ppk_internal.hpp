@@ -86,21 +86,24 @@ struct ppk_context {
   hipMemPool_t mem_pool = nullptr;
 
   // Arena blocks whose caches were released, kept for the next arena of the
-  // same size on the same stream (stream order puts the new writes after the
-  // old readers). The runtime pool hands freed memory back at every stream
-  // synchronisation whatever its release threshold, and a 24-layer join of
-  // B = 32 that took its batch arenas from the runtime spent 160-210 ms
-  // allocating; with released blocks kept here it takes 2-3 ms (1.8 ms of it
-  // the copy kernel). Bounded by kBlockCacheBytes; freed at release.
+  // same size: an event recorded on the stream that last used a block is
+  // waited for by the stream that reuses it, so the new writes follow the old
+  // readers on any stream. The runtime pool hands freed memory back at every
+  // stream synchronisation whatever its release threshold, and a 24-layer
+  // join of B = 32 that took its batch arenas from the runtime spent
+  // 160-210 ms allocating; with released blocks kept here it takes 2-3 ms
+  // (1.8 ms of it the copy kernel). Bounded by kBlockCacheBytes; freed at
+  // release.
   struct CachedBlock {
     void* ptr = nullptr;
     size_t bytes = 0;
-    hipStream_t stream = nullptr;
+    hipEvent_t released = nullptr;  // recorded after the block's last use
   };
   static constexpr size_t kBlockCacheBytes = size_t(32) << 30;
   std::mutex block_mutex;
   std::vector<CachedBlock> block_cache;
   size_t block_cache_bytes = 0;
+  std::vector<hipEvent_t> spare_events;  // events of reused blocks, recorded again by later releases
 
   std::mutex prof_mutex;
   bool profiling = false;
