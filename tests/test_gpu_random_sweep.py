@@ -165,3 +165,43 @@ def test_sampler_random_vs_reference_kernel(device, case):
     torch.cuda.synchronize()
     got = torch.stack([tok.reshape(-1), val.reshape(-1), sup.reshape(-1)])
     assert torch.equal(got, ref), f"case {case}: batch {batch} choices {choices} guidance {guidance}"
+
+
+@pytest.mark.parametrize("case", range(32))
+def test_decode_step_random(device, case):
+    """ppk_decode_step (append of the current token + attention in one call) at random geometry, lengths
+    (empty rows, short windows, full rows), splits, dtypes and max_past: output against the oracle at the
+    attention bar, slot past[b] holding the oracle's codes of the current token (nothing at a full row,
+    which is flagged), every other arena byte untouched."""
+    from test_gpu_attention import Case
+
+    rng = np.random.default_rng(SEED + 5000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    B, H = int(rng.integers(1, 6)), int(rng.integers(1, 9))
+    cap = int(rng.choice([int(rng.integers(1, 80)), int(rng.integers(80, 3000))]))
+    lengths = [int(rng.choice([0, cap, int(rng.integers(0, cap + 1)), int(rng.integers(0, min(cap, 40) + 1))]))
+               for _ in range(B)]
+    q_dt, s_dt = DTYPES[case % 3], DTYPES[(case // 3) % 3]
+    c = Case(device, B, H, d, lengths, cap, q_dtype=q_dt, scratch_dtype=s_dt, seed=SEED + 5100 + case)
+    ref = c.reference()
+    before = [t.clone() for t in (c.kc, c.vc, c.ks, c.vs)]
+    split = int(rng.choice([0, 0, int(rng.integers(1, 3000))]))
+    max_past = int(rng.choice([0, max(lengths)]))
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, split_tokens=split, flags=flags,
+                          max_past=max_past)
+    torch.cuda.synchronize()
+    what = f"case {case}: d{d} B{B} H{H} cap {cap} lengths {lengths} split {split} max_past {max_past}"
+    assert_close(out.reshape(c.rows, d).cpu().numpy(), ref, atol=2e-3, rtol=1e-2, what=what)
+    codes, scales, _ = oracle.quantize(c.sk32.reshape(c.rows, 1, d))
+    vcodes, vscales, _ = oracle.quantize(c.sv32.reshape(c.rows, 1, d))
+    exp = [t.cpu().numpy() for t in before]
+    for r in range(c.rows):
+        p = lengths[r // H]
+        if p < cap:
+            exp[0][r, p], exp[2][r, p] = codes[r, 0], scales[r, 0]
+            exp[1][r, p], exp[3][r, p] = vcodes[r, 0], vscales[r, 0]
+    for got, want, name in zip((c.kc, c.vc, c.ks, c.vs), exp, ("k", "v", "ks", "vs")):
+        np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"{name} arena, {what}")
+    assert bool(flags.item() & ppk.PPK_FLAG_OVERFLOW) == (cap in lengths), what
+    assert not flags.item() & ppk.PPK_FLAG_NONFINITE, what
