@@ -183,15 +183,16 @@ def test_decode_step_random(device, case):
                for _ in range(B)]
     q_dt, s_dt = DTYPES[case % 3], DTYPES[(case // 3) % 3]
     c = Case(device, B, H, d, lengths, cap, q_dtype=q_dt, scratch_dtype=s_dt, seed=SEED + 5100 + case)
-    ref = c.reference()
+    bf16h = case % 4 == 3  # the reference-exact mode (history rounded through bf16, int8_kv.cu:26)
+    ref = c.reference(history_bf16=bf16h)
     before = [t.clone() for t in (c.kc, c.vc, c.ks, c.vs)]
     split = int(rng.choice([0, 0, int(rng.integers(1, 3000))]))
     max_past = int(rng.choice([0, max(lengths)]))
     flags = torch.zeros(1, dtype=torch.int32, device=device)
     out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, split_tokens=split, flags=flags,
-                          max_past=max_past)
+                          max_past=max_past, bf16_history=bf16h)
     torch.cuda.synchronize()
-    what = f"case {case}: d{d} B{B} H{H} cap {cap} lengths {lengths} split {split} max_past {max_past}"
+    what = f"case {case}: d{d} B{B} H{H} cap {cap} lengths {lengths} split {split} max_past {max_past} bf16h {bf16h}"
     assert_close(out.reshape(c.rows, d).cpu().numpy(), ref, atol=2e-3, rtol=1e-2, what=what)
     codes, scales, _ = oracle.quantize(c.sk32.reshape(c.rows, 1, d))
     vcodes, vscales, _ = oracle.quantize(c.sv32.reshape(c.rows, 1, d))
