@@ -206,3 +206,42 @@ def test_decode_step_random(device, case):
         np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=f"{name} arena, {what}")
     assert bool(flags.item() & ppk.PPK_FLAG_OVERFLOW) == (cap in lengths), what
     assert not flags.item() & ppk.PPK_FLAG_NONFINITE, what
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_append_random(device, case):
+    """ppk_quantize_append: ragged multi-token appends of K and V [B, H, T, D] at random pasts (some running
+    past the capacity) into pre-filled arenas, bit-exact against the oracle's append (slots written,
+    slots past the capacity skipped and flagged, everything else untouched). Sizes cover the
+    one-wave-per-row kernel and the streaming kernel."""
+    rng = np.random.default_rng(SEED + 6000 + case)
+    d = int(rng.choice([64, 128, 256]))
+    B, H = int(rng.integers(1, 5)), int(rng.integers(1, 9))
+    T = int(rng.choice([1, int(rng.integers(2, 40)), int(rng.integers(200, 3000))]))
+    cap = int(rng.integers(T, 2 * T + 64))
+    past = rng.integers(0, cap + 1, B).astype(np.uint32)
+    past[0] = min(int(past[0]), cap - T)                      # one sequence that fits
+    dt = DTYPES[case % 3]
+    top = {torch.float32: 4, torch.bfloat16: 3, torch.float16: 2}[dt]
+    x32 = (rng.standard_normal((2, B, H, T, d)) * 10.0 ** rng.uniform(-3, top)).astype(np.float32)
+    kt, k32 = as_device(x32[0], dt, device)
+    vt, v32 = as_device(x32[1], dt, device)
+    rows = B * H
+    kc0 = rng.integers(0, 256, (rows, cap, d), dtype=np.uint8)
+    vc0 = rng.integers(0, 256, (rows, cap, d), dtype=np.uint8)
+    ks0 = rng.standard_normal((rows, cap)).astype(np.float32)
+    vs0 = rng.standard_normal((rows, cap)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a.copy()).to(device)  # noqa: E731
+    kc, vc, ks, vs = t(kc0), t(vc0), t(ks0), t(vs0)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    ppk.int8_kv_ops.append(kt.contiguous(), vt.contiguous(), t(past.view(np.int32)), kc, vc, ks, vs, flags=flags)
+    torch.cuda.synchronize()
+    ek, eks, ev, evs = kc0.copy(), ks0.copy(), vc0.copy(), vs0.copy()
+    oracle.append(k32, past, ek, eks)
+    oracle.append(v32, past, ev, evs)
+    what = f"case {case}: d{d} B{B} H{H} T{T} cap {cap} past {past.tolist()} {dt}"
+    assert np.array_equal(kc.cpu().numpy(), ek) and np.array_equal(vc.cpu().numpy(), ev), what
+    assert np.array_equal(ks.cpu().numpy().view(np.uint32), eks.view(np.uint32)), what
+    assert np.array_equal(vs.cpu().numpy().view(np.uint32), evs.view(np.uint32)), what
+    overflow = bool((past.astype(np.int64) + T > cap).any())
+    assert bool(flags.item() & ppk.PPK_FLAG_OVERFLOW) == overflow, what
