@@ -83,6 +83,13 @@ PPK_API const char* ppk_last_error(void);
    app/src/model/hip_kernel.rs:99-149 with an ahead-of-time code object. */
 PPK_API int32_t ppk_context_create(int32_t device, const char* code_object_path, ppk_context** out);
 PPK_API int32_t ppk_context_release(ppk_context* ctx);
+/* No counterpart in the reference: returns to the device the storage of
+   released KV caches that the context keeps for reuse (see the KV arena
+   notes below) and the unused memory of its pool, once the work that last
+   used it has finished. For long-lived callers that need that memory
+   elsewhere. *released_bytes (may be NULL) receives the bytes of kept
+   storage freed. Caches and plans stay valid. */
+PPK_API int32_t ppk_context_trim(ppk_context* ctx, uint64_t* released_bytes);
 
 /* Dense quantize: src[rows, tokens, D] -> codes[rows, tokens, D], scales[rows, tokens].
    Replaces int8_kv_ops::quantize (app/src/model/int8_kv_ops.rs:11-29), i.e. the

@@ -654,6 +654,30 @@ int32_t ppk_context_create(int32_t device, const char* code_object_path, ppk_con
   });
 }
 
+int32_t ppk_context_trim(ppk_context* ctx, uint64_t* released_bytes) {
+  if (released_bytes) *released_bytes = 0;
+  return call([&] {
+    ppk::require(ctx != nullptr, "ppk_context_trim: null context");
+    ppk::DeviceGuard guard(ctx->device);
+    std::vector<ppk_context::CachedBlock> blocks;
+    {
+      std::lock_guard<std::mutex> lock(ctx->block_mutex);
+      blocks.swap(ctx->block_cache);
+      ctx->block_cache_bytes = 0;
+    }
+    uint64_t freed = 0;
+    for (auto& b : blocks) {
+      (void)hipEventSynchronize(b.released);  // the block's last use has finished
+      (void)hipFree(b.ptr);
+      freed += b.bytes;
+      std::lock_guard<std::mutex> lock(ctx->block_mutex);
+      ctx->spare_events.push_back(b.released);
+    }
+    if (ctx->mem_pool) (void)hipMemPoolTrimTo(ctx->mem_pool, 0);
+    if (released_bytes) *released_bytes = freed;
+  });
+}
+
 int32_t ppk_context_release(ppk_context* ctx) {
   return call([&] {
     if (!ctx) return;

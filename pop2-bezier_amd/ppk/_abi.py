@@ -107,6 +107,7 @@ FUNCTIONS = {
     "ppk_last_error": (ctypes.c_char_p, []),
     "ppk_context_create": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_char_p, ctypes.POINTER(_ptr)]),
     "ppk_context_release": (ctypes.c_int32, [_ptr]),
+    "ppk_context_trim": (ctypes.c_int32, [_ptr, ctypes.POINTER(_u64)]),
     "ppk_quantize": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkQuantizeArgs)]),
     "ppk_quantize_append": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkAppendArgs)]),
     "ppk_dequantize": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDequantizeArgs)]),

@@ -211,6 +211,14 @@ class LayerCache:
         return out
 
 
+def trim(device: torch.device | int | None = None) -> int:
+    """ppk_context_trim: free the storage of released caches that the device's context keeps for reuse
+    (and the unused memory of its pool); returns the bytes of kept storage freed."""
+    released = ctypes.c_uint64()
+    check(lib().ppk_context_trim(context(device), ctypes.byref(released)), "ppk_context_trim")
+    return released.value
+
+
 class WritePlan:
     """BatchWritePlan: one decode round's per-sequence write offsets on the device, shared by every layer."""
 

@@ -224,6 +224,9 @@ def test_kv_arena_entry_points_refuse_null_arguments():
     assert lib.ppk_kv_cache_adopt(None, ctypes.byref(cfg), 256, 4096, 8, 0, ctypes.byref(out)) == _abi.PPK_PRECONDITION
     assert out.value is None
     assert lib.ppk_kv_cache_advance(None, 0, 1) == _abi.PPK_PRECONDITION
+    released = ctypes.c_uint64(7)
+    assert lib.ppk_context_trim(None, ctypes.byref(released)) == _abi.PPK_PRECONDITION
+    assert released.value == 0
     w = _abi.PpkKvWrite(struct_size=ctypes.sizeof(_abi.PpkKvWrite))
     assert lib.ppk_kv_query(None, None, None, 0, ctypes.byref(w), None) == _abi.PPK_PRECONDITION
     assert lib.ppk_kv_query_batch(None, None, None, 0, None, ctypes.byref(w), None, None) == _abi.PPK_PRECONDITION

@@ -614,6 +614,29 @@ def test_reused_storage_of_released_caches_reads_as_zeros_past_the_new_history(d
         assert torch.equal(rows_of(view, 1, 2, 6), cat(data(2, 5, d, 100.0), batch_data(3, 2, d, 200.0)[1]))
 
 
+def test_context_trim_returns_kept_storage_and_caches_stay_valid(device):
+    """ppk_context_trim (no counterpart in the reference): the storage of released caches that the context
+    keeps for reuse is freed once, live caches keep their contents, and new caches allocate as before."""
+    ctx = ppk.context(device)
+    trimmed = ctypes.c_uint64()
+    _abi.check(_abi.lib().ppk_context_trim(ctx, ctypes.byref(trimmed)), "ppk_context_trim")  # start empty
+    keep = LayerCache(F32, 2, 16)
+    keep.query(data(2, 40, 16, 1.0), data(2, 40, 16, 1.0), 0, True)
+    gone = [LayerCache(F32, 2, 16) for _ in range(3)]
+    for c in gone:
+        c.query(data(2, 30, 16, 5.0), data(2, 30, 16, 5.0), 0, True)
+    reserved = sum(c.info().reserved_bytes for c in gone)
+    del gone, c
+    _abi.check(_abi.lib().ppk_context_trim(ctx, ctypes.byref(trimmed)), "ppk_context_trim")
+    assert trimmed.value >= reserved
+    _abi.check(_abi.lib().ppk_context_trim(ctx, ctypes.byref(trimmed)), "ppk_context_trim")
+    assert trimmed.value == 0
+    assert torch.equal(keep.key(), data(2, 40, 16, 1.0))
+    fresh = LayerCache(F32, 2, 16)
+    fresh.query(data(2, 3, 16, 9.0), data(2, 3, 16, 9.0), 0, True)
+    assert torch.equal(fresh.key(), data(2, 3, 16, 9.0))
+
+
 def test_truncate_is_metadata_only_and_append_preserves_longer_snapshots(device):
     cache = grouped_rows()[0]
     snapshot = cache.clone()
