@@ -160,10 +160,12 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
   if (!explicit_split && rows < cus && row_bytes > (128u << 10)) {
     // Few, long rows: one block per row would leave most CUs idle (a CU
     // alone streams only a few tens of GB/s). Split rows into blocks of about
-    // 64 KiB of history, then shrink blocks until the launch covers every CU;
-    // the merge kernel joins the groups.
+    // 256 KiB of history, then shrink blocks until the launch covers every CU;
+    // the merge kernel joins the groups. (Config 4 against a 64 KiB target:
+    // three-wave blocks and 4 records per row instead of one-wave blocks and
+    // 12, 2 % faster warm and cold.)
     const uint64_t wave_bytes = uint64_t(split) * token_bytes;
-    uint64_t w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (64u << 10) / wave_bytes));
+    uint64_t w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / wave_bytes));
     while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) --w;
     max_waves = w;
   }
