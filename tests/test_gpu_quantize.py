@@ -24,7 +24,10 @@ def _to_device(x32: np.ndarray, dtype: torch.dtype, device) -> tuple[torch.Tenso
     if dtype == torch.float32:
         return torch.from_numpy(np.ascontiguousarray(x32)).to(device), x32
     if dtype == torch.float16:
-        h = x32.astype(np.float16)
+        # Special rows hold values past f16's range: they become ±inf, a
+        # non-finite f16 input, which the oracle sees as well.
+        with np.errstate(over="ignore"):
+            h = x32.astype(np.float16)
         return torch.from_numpy(h).to(device), h.astype(np.float32)
     bits = to_bf16_bits(x32)
     t = torch.from_numpy(bits.view(np.int16)).to(device).view(torch.bfloat16)

@@ -80,7 +80,11 @@ def test_dequantize_random(device, case):
     elif out_dt == torch.bfloat16:
         assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), to_bf16_bits(ref)), what
     else:
-        assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16)), what
+        # Scales up to 1e20 put values past f16's range: the expected result is
+        # the round-to-nearest cast, ±inf there, as the kernel's conversion gives.
+        with np.errstate(over="ignore"):
+            want = ref.astype(np.float16)
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want.view(np.uint16)), what
 
 
 @pytest.mark.parametrize("case", range(16))
