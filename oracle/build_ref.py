@@ -7,7 +7,9 @@ TEST INFRASTRUCTURE ONLY: tests/ use these as a second checker beside the C
 oracle. Nothing is copied from the reference into the repository; outputs go
 to oracle/_ref/ (git-ignored, carried to the GPU box with the tree). Both
 sources include only <hip/hip_runtime.h> and <math.h>; they are built with
-the same device flags as this repository's kernels.
+the reference's own compile flags (FLAGS of app/src/model/hip_kernel.rs:46:
+--genco -O3 -std=c++17 -ffp-contract=off), plus the flag that keeps packed
+fp32 VALU forms out of every code object run on this pool.
 
   python oracle/build_ref.py [--reference /root/reference]
 """
@@ -21,7 +23,9 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "_ref")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
-DEVICE_FLAGS = ["-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# The reference's FLAGS (hip_kernel.rs:46); --genco and the target are added below.
+REFERENCE_FLAGS = ["-O3", "-std=c++17", "-ffp-contract=off"]
+DEVICE_FLAGS = [*REFERENCE_FLAGS, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 SOURCES = {
     "decode_attention.hsaco": "app/src/model/decode_attention.hip",
     "renyi_sample.hsaco": "app/src/inference/renyi_sample.hip",

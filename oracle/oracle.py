@@ -184,11 +184,12 @@ def attention_float(q, k, v, lengths, heads: int, scale: float | None = None) ->
 
 
 def renyi_sample(raw, uniforms, bounds, alpha: float, cfg: float, guidance: int, offset: int,
-                 cfg_fma: bool = True) -> dict:
+                 cfg_fma: bool = False) -> dict:
     """CFG + Renyi sampler (see oracle_renyi_sample). raw float32 [batch*guidance, choices];
     uniforms float32 [batch]; bounds uint32 [batch, 2] = (start, count). Returns a dict of
     token / valid / support (uint32 [batch]) and margin (float32 [batch]); raises ValueError
-    for metadata the reference rejects."""
+    for metadata the reference rejects. cfg_fma=False is the reference's separately rounded CFG value;
+    True (a fused multiply-add) exists only for tests that show a case separates the two forms."""
     raw = _c(raw, np.float32)
     physical, choices = raw.shape
     uniforms = _c(uniforms, np.float32).reshape(-1)

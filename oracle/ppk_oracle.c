@@ -439,9 +439,12 @@ void oracle_attention_float(const float* q, const void* k, const void* v, int kv
  *   H = log Z + max(0, log Z - log Z_alpha) / (alpha - 1), clamped to [0, ln count];
  *   support = clamp((u32)(exp(H) + 0.5), 1, count); rank = min((u32)(uniform * support), support - 1);
  *   token = offset + the rank-th candidate by (value descending, index ascending).
- * Invalid rows give (fallback token, valid 0, support 1). With cfg_fma = 1 the
- * CFG value is fmaf(cfg, c - u, u), the device kernel's contracted form;
- * cfg_fma = 0 is the host oracle's separately rounded product and sum.
+ * Invalid rows give (fallback token, valid 0, support 1). cfg_fma = 0 is the
+ * reference's form: a separately rounded product and sum, as its host oracle
+ * computes it (hip_sampling_reference.rs:73) and as its kernel is compiled
+ * (-ffp-contract=off, app/src/model/hip_kernel.rs:46). cfg_fma = 1 gives
+ * fmaf(cfg, c - u, u), a contracted form no reference build produces; tests
+ * use it only to show that a case tells the two forms apart.
  * margin[row] (optional) = distance of exp(H) + 0.5 from the nearest integer:
  * libm and device exp/log may round a row with a tiny margin differently.
  * Returns 0, or -1 for metadata the reference rejects.

@@ -1307,6 +1307,12 @@ __device__ __forceinline__ void write_sample(const ppk::RenyiArgs& a, uint32_t r
 }
 
 __device__ __forceinline__ void renyi_sample_body(const ppk::RenyiArgs& a) {
+  // Every float operation rounds on its own, as the reference kernel is built
+  // (-ffp-contract=off, app/src/model/hip_kernel.rs:46) and as its host oracle
+  // evaluates (app/src/inference/hip_sampling_reference.rs:73): the CFG value
+  // u + cfg * (c - u) is a rounded product and then a rounded sum, never one
+  // fused multiply-add, whose 1-ulp differences can reorder candidates.
+#pragma clang fp contract(off)
   constexpr int T = ppk::kSamplerThreads;
   constexpr int PER = ppk::kSamplerMaxChoices / T;  // candidates per thread
   __shared__ float s_vals[ppk::kSamplerMaxChoices];

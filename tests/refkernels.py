@@ -14,6 +14,10 @@ REF = os.path.join(ROOT, "oracle", "_ref")
 _lib = None
 
 
+def available() -> bool:
+    return os.path.exists(os.path.join(REF, "libppk_ref.so"))
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:

@@ -2,10 +2,12 @@
 
 Bars:
 * against the reference's own kernel pp_hip_renyi_sample, built unchanged
-  from its source into oracle/_ref with the same device flags: token, valid
-  and support identical on every row (integer outputs, bit-exact);
-* against the C oracle (the reference's host validation oracle restated, with
-  the device's contracted CFG product): identical on every row whose
+  from its source into oracle/_ref with the reference's own compile flags
+  (-ffp-contract=off, app/src/model/hip_kernel.rs:46): token, valid and
+  support identical on every row (integer outputs, bit-exact);
+* against the C oracle (the reference's host validation oracle restated, the
+  CFG value a separately rounded product and sum as in
+  hip_sampling_reference.rs:73): identical on every row whose
   exp(H) + 0.5 lies at least 1e-4 from an integer; nearer rows may round to a
   neighbouring support, as the reference's oracle notes for libm vs device
   exp/log (hip_sampling_reference.rs:1-3), and must then be consistent with
@@ -72,7 +74,7 @@ def test_matches_oracle(device, guidance, choices, kind):
     raw, u, b = random_problem(rng, batch, choices, guidance, kind)
     alpha, cfg = 3.5, (2.5 if guidance == 2 else 1.0)
     got, _ = run(device, raw, u, b, alpha, cfg, guidance, 11)
-    ref = oracle.renyi_sample(raw, u, b, alpha, cfg, guidance, 11, cfg_fma=True)
+    ref = oracle.renyi_sample(raw, u, b, alpha, cfg, guidance, 11)
     assert check_against_oracle(got, ref, f"{kind} g{guidance} c{choices}") >= batch * 0.9
     assert np.all(got["valid"] == 1)
 
@@ -106,6 +108,45 @@ def test_reference_known_answers(device):
     assert got["valid"][0] == 0
     got, _ = run(device, np.zeros((1, 2), np.float32), np.zeros(1), np.array([[2, 1]]), 4.0, 1.0, 1, 0)
     assert (got["token"][0], got["valid"][0], got["support"][0]) == (0, 0, 1)
+
+
+# CFG inputs whose value u + cfg * (c - u) at cfg = 2.5 differs by one ulp
+# between the separately rounded form (the reference: 2.920362949...) and a
+# fused multiply-add (2.920363187...).
+CFG_SPLIT_U = np.float32(0.8192756772041321)
+CFG_SPLIT_C = np.float32(1.6597106456756592)
+
+
+def cfg_rounding_problem():
+    """Two rows over the same head: column 0 holds exactly the separately rounded value of column 1
+    (c = u = that value), columns 2 and 3 sit far below. Row 0 takes rank 0 (uniform 0), row 1 rank 1 of a
+    support of 2 (uniform 0.75). Separately rounded, columns 0 and 1 tie and order by index; fused,
+    column 1 leads."""
+    cfg = np.float32(2.5)
+    tie = np.float32(CFG_SPLIT_U + np.float32(cfg * np.float32(CFG_SPLIT_C - CFG_SPLIT_U)))
+    cond = np.array([tie, CFG_SPLIT_C, -30.0, -30.0], np.float32)
+    uncond = np.array([tie, CFG_SPLIT_U, -30.0, -30.0], np.float32)
+    raw = np.stack([cond, uncond, cond, uncond]).astype(np.float32)
+    uniforms = np.array([0.0, 0.75], np.float32)
+    bounds = np.array([[0, 4], [0, 4]], np.uint32)
+    return raw, uniforms, bounds, float(cfg)
+
+
+def test_cfg_value_rounds_twice_like_the_reference(device):
+    """hip_sampling_reference.rs:73 and renyi_sample.hip:85 under -ffp-contract=off: the CFG value is a
+    rounded product, then a rounded sum. The case picks different tokens under a fused multiply-add."""
+    raw, u, b, cfg = cfg_rounding_problem()
+    ref = oracle.renyi_sample(raw, u, b, 4.0, cfg, 2, 9)
+    fused = oracle.renyi_sample(raw, u, b, 4.0, cfg, 2, 9, cfg_fma=True)
+    assert list(ref["token"]) == [9, 10] and list(ref["support"]) == [2, 2]
+    assert list(fused["token"]) == [10, 9], "the case must separate the two roundings"
+    got, (raw_t, u_t, b_t) = run(device, raw, u, b, 4.0, cfg, 2, 9)
+    for key in ("token", "valid", "support"):
+        assert list(got[key]) == list(ref[key]), (key, got[key], ref[key])
+    if refkernels.available():
+        r = refkernels.renyi_sample(raw_t, u_t, b_t, 4.0, cfg, 2, 9)
+        torch.cuda.synchronize()
+        assert list(r.cpu().numpy().view(np.uint32)[0]) == [9, 10]
 
 
 def test_invalid_rows_do_not_disturb_valid_rows(device):

@@ -44,6 +44,26 @@ def test_reference_known_answer_guided_rows_and_legal_ranges():
         assert list(r["token"]) == [2050, 2050] and list(r["valid"]) == [1, 1]
 
 
+def test_cfg_value_is_a_rounded_product_then_a_rounded_sum():
+    """hip_sampling_reference.rs:73 (Rust never contracts) and renyi_sample.hip:85 built with
+    -ffp-contract=off (hip_kernel.rs:46): numpy's float32 u + cfg * (c - u) rounds after each operation.
+    Column 0 holds that value exactly; column 1 computes it from (c, u). A fused multiply-add makes
+    column 1 one ulp larger, so the two forms pick different tokens."""
+    cfg = np.float32(2.5)
+    u1, c1 = np.float32(0.8192756772041321), np.float32(1.6597106456756592)
+    tie = np.float32(u1 + np.float32(cfg * np.float32(c1 - u1)))
+    assert tie == np.float32(2.920362949371338)
+    cond = np.array([tie, c1, -30.0, -30.0], np.float32)
+    uncond = np.array([tie, u1, -30.0, -30.0], np.float32)
+    raw = np.stack([cond, uncond, cond, uncond])
+    uniforms = np.array([0.0, 0.75], np.float32)
+    bounds = np.array([[0, 4], [0, 4]], np.uint32)
+    r = oracle.renyi_sample(raw, uniforms, bounds, 4.0, float(cfg), 2, 0)
+    assert list(r["token"]) == [0, 1] and list(r["support"]) == [2, 2]  # tie broken by index
+    f = oracle.renyi_sample(raw, uniforms, bounds, 4.0, float(cfg), 2, 0, cfg_fma=True)
+    assert list(f["token"]) == [1, 0]
+
+
 def test_reference_known_answer_invalid_inputs():
     """hip_sampling_reference.rs:181-204: every raw logit is checked, bad uniforms, CFG overflow, bad bounds."""
     for value in [np.nan, np.inf, -np.inf]:
