@@ -1,13 +1,13 @@
 """Reduce rocprofv3 CSV output to the short summaries kept under profiles/.
 
-  python pop2-bezier_amd/ppk/rocprof_summary.py trace DIR --out FILE.md --command "..."
+  python rocprof_summary.py trace DIR --out FILE.md --command "..."
       kernel-trace + stats: per-kernel durations of the ppk kernels, and the
       decode-step period and inter-kernel gaps measured from the dispatch trace.
-  python pop2-bezier_amd/ppk/rocprof_summary.py counters DIR [DIR ...] --kernel-regex RX --out FILE.md
+  python rocprof_summary.py counters DIR [DIR ...] --kernel-regex RX --out FILE.md
          --title T --command "..."
       any --pmc runs: the median per-dispatch value of every counter for each kernel
       matching RX, plus the L2 hit rate when TCC_HIT_sum and TCC_MISS_sum were read.
-  python pop2-bezier_amd/ppk/rocprof_summary.py traffic FETCH_DIR WRITE_DIR --kernel NAME
+  python rocprof_summary.py traffic FETCH_DIR WRITE_DIR --kernel NAME
          --calib-regex REGEX --calib-bytes N --algorithmic-bytes N --workload W --split S
          --out-md FILE.md --out-json FILE.json --command "..."
       --pmc FETCH_SIZE / WRITE_SIZE: HBM KiB per dispatch of one kernel, scaled by
@@ -161,7 +161,7 @@ def counters(args) -> None:
 
 
 def _self_command() -> str:
-    return "python3 pop2-bezier_amd/ppk/rocprof_summary.py " + shlex.join(sys.argv[1:])
+    return "python3 rocprof_summary.py " + shlex.join(sys.argv[1:])
 
 
 def _write(path: str, text: str) -> None:
