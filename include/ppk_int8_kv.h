@@ -210,6 +210,21 @@ typedef struct PpkDecodeStepArgs {
 } PpkDecodeStepArgs;
 PPK_API int32_t ppk_decode_step(ppk_context* ctx, void* stream, const PpkDecodeStepArgs* args);
 
+/* No counterpart in the reference. ppk_decode_step for callers that cannot
+   allocate device memory (code under HIP graph capture, tight serving loops,
+   harnesses that forbid hipMalloc): the same launches and results, but the
+   partial records of rows that span several blocks go to a library-owned
+   device array of PPK_NOALLOC_SCRATCH_BYTES per GPU (held from the first
+   context on that GPU until the process ends) instead of attn.workspace,
+   which is ignored. A plan that needs more (ppk_attention_plan's
+   workspace_bytes) returns status 1 with nothing enqueued. Calls no
+   hipMalloc / hipFree and never traces (ppk_context_set_profiling is ignored
+   here). Every call on one GPU shares that GPU's array, which keeps the last
+   call's records: calls that overlap in time on one GPU (two streams, two
+   threads, two contexts) race and must be serialised by the caller. */
+#define PPK_NOALLOC_SCRATCH_BYTES (8u << 20)
+PPK_API int32_t ppk_decode_step_noalloc(ppk_context* ctx, void* stream, const PpkDecodeStepArgs* args);
+
 /* Float-KV decode attention: the non-int8 decode path over unquantised bf16
    or f32 K/V, where the current token is already stored. For row r
    (sequence b = r / heads):

@@ -2,7 +2,9 @@
 
 Outputs (next to the Python package, git-ignored, shipped with the tree):
   ppk/ppk_kernels.hsaco  gfx950 code object with every kernel (hipcc --genco)
-  ppk/libppk.so          C-ABI shim + int8_kv_ops host mirror (include/ppk_int8_kv.h)
+  ppk/libppk.so          C-ABI shim + int8_kv_ops host mirror (include/ppk_int8_kv.h), with
+                         the no-alloc entry point's device scratch array (csrc/ppk_scratch.hip,
+                         compiled by hipcc for gfx950 and linked in)
 
 Usage: python pop2-bezier_amd/build.py
 """
@@ -45,10 +47,18 @@ def build(verbose: bool = True) -> dict:
     lib = os.path.join(OUT, "libppk.so")
     tmp_hsaco = hsaco + f".tmp{os.getpid()}"
     tmp_lib = lib + f".tmp{os.getpid()}"
+    tmp_obj = os.path.join(OUT, f"ppk_scratch.o.tmp{os.getpid()}")
     try:
         _run(
             [HIPCC, "--genco", f"--offload-arch={ARCH}", *DEVICE_FLAGS, os.path.join(CSRC, "ppk_kernels.hip"), "-o",
              tmp_hsaco],
+            verbose,
+        )
+        # The device scratch array of the no-alloc entry point lives in the
+        # library itself (a __device__ variable in a HIP translation unit).
+        _run(
+            [HIPCC, "-c", "-fPIC", f"--offload-arch={ARCH}", *DEVICE_FLAGS, "-fvisibility=hidden",
+             f"-I{os.path.join(ROOT, 'include')}", os.path.join(CSRC, "ppk_scratch.hip"), "-o", tmp_obj],
             verbose,
         )
         # The shim is host-only code over the HIP runtime API: plain g++.
@@ -57,7 +67,7 @@ def build(verbose: bool = True) -> dict:
                 CXX, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
                 f"-I{os.path.join(ROOT, 'include')}", f"-I{ROCM}/include",
                 os.path.join(CSRC, "ppk_abi.cpp"), os.path.join(CSRC, "int8_kv_ops.cpp"),
-                os.path.join(CSRC, "fused_attention.cpp"), os.path.join(CSRC, "kv_arena.cpp"),
+                os.path.join(CSRC, "fused_attention.cpp"), os.path.join(CSRC, "kv_arena.cpp"), tmp_obj,
                 "-o", tmp_lib, f"-L{ROCM}/lib", f"-Wl,-rpath,{ROCM}/lib", "-lamdhip64", "-ldl",
             ],
             verbose,
@@ -66,7 +76,7 @@ def build(verbose: bool = True) -> dict:
         os.replace(tmp_hsaco, hsaco)
         os.replace(tmp_lib, lib)
     finally:
-        for t in (tmp_hsaco, tmp_lib):
+        for t in (tmp_hsaco, tmp_lib, tmp_obj):
             if os.path.exists(t):
                 os.remove(t)
     return {"hsaco": hsaco, "lib": lib}

@@ -90,11 +90,11 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 template <class Args>
 void launch(ppk_context* ctx, int prof_kernel, ppk::Fn fn, uint32_t grid, uint32_t block, uint32_t lds,
-            hipStream_t stream, Args& args, uint32_t grid_y = 1) {
+            hipStream_t stream, Args& args, uint32_t grid_y = 1, bool traceable = true) {
   void* params[] = {&args};
   ppk::EventPair ev;
   bool traced = false;
-  if (ctx->profiling) {
+  if (traceable && ctx->profiling) {
     std::lock_guard<std::mutex> lock(ctx->prof_mutex);
     if (ctx->pool.empty()) {
       if (hipEventCreate(&ev.start) != hipSuccess || hipEventCreate(&ev.stop) != hipSuccess)
@@ -317,7 +317,8 @@ void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArg
   launch(ctx, PPK_KERNEL_DEQUANTIZE, kDequantize, uint32_t(grid), 256, 0, stream, k);
 }
 
-void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a, const PpkDecodeStepArgs* step) {
+void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a, const PpkDecodeStepArgs* step,
+                   void* scratch, uint64_t scratch_bytes) {
   const AttentionPlan plan = plan_attention(ctx, a);
   require(a.q && a.k_codes && a.v_codes && a.k_scales && a.v_scales && a.sk && a.sv && a.past && a.out,
           "INT8 attention null pointer");
@@ -326,7 +327,13 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   require(aligned(a.q, dtype_bytes(a.q_dtype)) && aligned(a.sk, dtype_bytes(a.scratch_dtype)) &&
               aligned(a.sv, dtype_bytes(a.scratch_dtype)) && aligned(a.out, dtype_bytes(a.out_dtype)),
           "INT8 attention float operand misaligned");
-  if (plan.workspace_bytes) {
+  void* workspace = a.workspace;
+  if (scratch) {
+    if (plan.workspace_bytes > scratch_bytes)
+      throw PreconditionError("INT8 decode step needs " + std::to_string(plan.workspace_bytes) +
+                              " bytes of workspace; the no-alloc scratch holds " + std::to_string(scratch_bytes));
+    workspace = scratch;
+  } else if (plan.workspace_bytes) {
     require(a.workspace && aligned(a.workspace, 256), "INT8 attention workspace missing or not 256-byte aligned");
     if (a.workspace_bytes < plan.workspace_bytes)
       throw PreconditionError("INT8 attention workspace too small: need " + std::to_string(plan.workspace_bytes) +
@@ -354,8 +361,8 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   d.sk = a.sk;
   d.sv = a.sv;
   d.past = a.past;
-  d.part_y = plan.workspace_bytes ? static_cast<float*>(a.workspace) : nullptr;
-  d.part_mz = plan.workspace_bytes ? reinterpret_cast<float*>(static_cast<char*>(a.workspace) + plan.y_bytes) : nullptr;
+  d.part_y = plan.workspace_bytes ? static_cast<float*>(workspace) : nullptr;
+  d.part_mz = plan.workspace_bytes ? reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.y_bytes) : nullptr;
   d.out = a.out;
   if (step) {
     d.k_new = step->k_new;
@@ -377,7 +384,9 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
   const Fn decode = Fn((bf16h ? kDecodeBf16h64 : kDecode64) + di);
   DeviceGuard guard(ctx->device);
-  launch(ctx, PPK_KERNEL_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d);
+  const bool traceable = scratch == nullptr;
+  launch(ctx, PPK_KERNEL_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d, 1,
+         traceable);
   if (plan.ngroups > 1) {
     MergeArgs m{};
     m.q = a.q;
@@ -396,7 +405,7 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
     m.scratch_dtype = a.scratch_dtype;
     m.out_dtype = a.out_dtype;
     m.scale_log2 = scale_log2;
-    launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMerge64 + di), a.rows, 64, 0, stream, m);
+    launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMerge64 + di), a.rows, 64, 0, stream, m, 1, traceable);
   }
 }
 
@@ -640,6 +649,14 @@ int32_t ppk_context_create(int32_t device, const char* code_object_path, ppk_con
         throw ppk::PreconditionError(std::string("kernel symbol missing: ") + kFnNames[i]);
       }
     }
+    // The no-alloc entry point's scratch: this GPU's device address, looked
+    // up once per device (a failure only disables that entry point).
+    try {
+      ctx->scratch = ppk::scratch_lookup(device);
+    } catch (const std::exception& e) {
+      ctx->scratch = nullptr;
+      ctx->scratch_error = e.what();
+    }
     hipMemPoolProps props{};
     props.allocType = hipMemAllocationTypePinned;
     props.handleTypes = hipMemHandleTypeNone;
@@ -758,6 +775,14 @@ int32_t ppk_decode_step(ppk_context* ctx, void* stream, const PpkDecodeStepArgs*
   return call([&] {
     ppk::require(ctx && args, "ppk_decode_step: null context or arguments");
     ppk::run_attention(ctx, static_cast<hipStream_t>(stream), args->attn, args);
+  });
+}
+
+int32_t ppk_decode_step_noalloc(ppk_context* ctx, void* stream, const PpkDecodeStepArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_decode_step_noalloc: null context or arguments");
+    if (!ctx->scratch) throw ppk::PreconditionError("no-alloc scratch unavailable on this device: " + ctx->scratch_error);
+    ppk::run_attention(ctx, static_cast<hipStream_t>(stream), args->attn, args, ctx->scratch, ppk::kScratchBytes);
   });
 }
 

@@ -57,6 +57,9 @@ struct EventPair {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 
+// Bytes of the per-GPU device array behind ppk_decode_step_noalloc (ppk_scratch.hip).
+constexpr size_t kScratchBytes = PPK_NOALLOC_SCRATCH_BYTES;
+
 }  // namespace ppk
 
 struct ppk_context {
@@ -68,6 +71,11 @@ struct ppk_context {
 
   std::mutex prepare_mutex;
   bool int8_ready = false;  // ppk_prepare_int8_kv's self-check passed on this context
+
+  // Device address of this GPU's copy of the no-alloc scratch array, looked up
+  // at context creation (nullptr with the reason in scratch_error if that failed).
+  void* scratch = nullptr;
+  std::string scratch_error;
 
   // Device vectors of released write plans, recycled by the next plan created
   // on the same stream (stream order puts its upload after the old plan's
@@ -149,8 +157,17 @@ void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a
 void run_append(ppk_context* ctx, hipStream_t stream, const PpkAppendArgs& a);
 void run_dequantize(ppk_context* ctx, hipStream_t stream, const PpkDequantizeArgs& a);
 // step == nullptr: attention only; otherwise the fused decode step.
+// scratch != nullptr: the partial records go to that device buffer of
+// scratch_bytes (the no-alloc entry point) instead of a.workspace, which is
+// then ignored, and no launch is traced (tracing creates events).
 void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs& a,
-                   const PpkDecodeStepArgs* step = nullptr);
+                   const PpkDecodeStepArgs* step = nullptr, void* scratch = nullptr, uint64_t scratch_bytes = 0);
+
+// Device address of the current process's no-alloc scratch array on `device`
+// (ppk_scratch.hip): looked up once per device with that device current,
+// then served from a per-device table. Throws PreconditionError if the
+// lookup failed.
+void* scratch_lookup(int device);
 void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a);
 void run_renyi_sample(ppk_context* ctx, hipStream_t stream, const PpkRenyiSampleArgs& a);
 

@@ -17,6 +17,7 @@ PPK_OK, PPK_PRECONDITION, PPK_INVALID_OUTPUT, PPK_EXECUTION_UNCERTAIN = 0, 1, 2,
 PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
 PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW = 1, 2
 PPK_ATTN_BF16_HISTORY = 1
+PPK_NOALLOC_SCRATCH_BYTES = 8 << 20
 (PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE,
  PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_RENYI_SAMPLE, PPK_KERNEL_COPY,
  PPK_KERNEL_COUNT) = range(10)
@@ -117,6 +118,7 @@ FUNCTIONS = {
                                             ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
     "ppk_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkAttentionArgs)]),
     "ppk_decode_step": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDecodeStepArgs)]),
+    "ppk_decode_step_noalloc": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDecodeStepArgs)]),
     "ppk_float_attention_plan": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkFloatAttentionArgs), ctypes.POINTER(_u32),
                                                   ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
     "ppk_float_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatAttentionArgs)]),
@@ -184,6 +186,11 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(f"libppk ABI {L.ppk_abi_version()} != expected {PPK_ABI_VERSION}")
         _lib = L
     return _lib
+
+
+def last_error() -> str:
+    """ppk_last_error() of the calling thread."""
+    return (lib().ppk_last_error() or b"").decode("utf-8", "replace")
 
 
 def check(status: int, what: str) -> None:
