@@ -39,6 +39,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_append.restype = Z
         L.oracle_attention.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, ctypes.c_int, P]
         L.oracle_attention.restype = None
+        L.oracle_attention_mt.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, ctypes.c_int, Z, P]
+        L.oracle_attention_mt.restype = ctypes.c_int
         L.oracle_attention_splitk_reference.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, Z, P]
         L.oracle_attention_splitk_reference.restype = None
         L.oracle_attention_float.argtypes = [P, P, P, ctypes.c_int, Z, Z, P, Z, Z, Z, Z, ctypes.c_float, P]
@@ -100,8 +102,9 @@ def append(src: np.ndarray, past: np.ndarray, codes: np.ndarray, scales: np.ndar
 
 
 def attention(q, k, v, ks, vs, sk, sv, past, heads: int, scale: float | None = None,
-              history_bf16: bool = False) -> np.ndarray:
-    """f64 decode attention (see oracle_attention); returns float64 [rows, d]."""
+              history_bf16: bool = False, threads: int | None = None) -> np.ndarray:
+    """f64 decode attention (see oracle_attention); returns float64 [rows, d]. Rows are shared out over
+    `threads` POSIX threads (default: the usable cores, at most 16); the result does not depend on it."""
     k = _c(k, np.uint8)
     v = _c(v, np.uint8)
     rows, cap, d = k.shape
@@ -114,9 +117,11 @@ def attention(q, k, v, ks, vs, sk, sv, past, heads: int, scale: float | None = N
     assert past.size == rows // heads and rows % heads == 0
     if scale is None:
         scale = 1.0 / np.sqrt(d)
+    if threads is None:
+        threads = max(1, min(len(os.sched_getaffinity(0)), 16))
     out = np.empty((rows, d), np.float64)
-    lib().oracle_attention(_p(q), _p(k), _p(v), _p(ks), _p(vs), _p(sk), _p(sv), _p(past), rows, heads, cap, d,
-                           float(scale), int(bool(history_bf16)), _p(out))
+    lib().oracle_attention_mt(_p(q), _p(k), _p(v), _p(ks), _p(vs), _p(sk), _p(sv), _p(past), rows, heads, cap, d,
+                              float(scale), int(bool(history_bf16)), int(threads), _p(out))
     return out
 
 

@@ -128,14 +128,23 @@ size_t oracle_append(const float* src, size_t batch, size_t heads, size_t tokens
  * dequantize to F32) or its bf16 rounding (history_bf16 = 1; pp_i8_load,
  * int8_kv.cu:23-27). p > capacity yields NaN (:33,51,58).
  */
-void oracle_attention(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
-                      const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
-                      size_t capacity, size_t d, float scale, int history_bf16, double* out) {
+typedef struct {
+  const float *q, *ks, *vs, *sk, *sv;
+  const uint8_t *k, *v;
+  const uint32_t* past;
+  size_t r0, r1, heads, capacity, d;
+  float scale;
+  int history_bf16;
+  double* out;
+} AttentionJob;
+
+static void attention_rows(const AttentionJob* j) {
+  const size_t capacity = j->capacity, d = j->d;
   double* scores = NULL;
   size_t cap_scores = 0;
-  for (size_t r = 0; r < rows; ++r) {
-    const uint32_t p = past[r / heads];
-    double* o = out + r * d;
+  for (size_t r = j->r0; r < j->r1; ++r) {
+    const uint32_t p = j->past[r / j->heads];
+    double* o = j->out + r * d;
     if (p > capacity) {
       for (size_t i = 0; i < d; ++i) o[i] = NAN;
       continue;
@@ -144,20 +153,20 @@ void oracle_attention(const float* q, const uint8_t* k, const uint8_t* v, const 
       cap_scores = (size_t)p + 1;
       scores = (double*)realloc(scores, cap_scores * sizeof(double));
     }
-    const float* qr = q + r * d;
+    const float* qr = j->q + r * d;
     double mx = -INFINITY;
     for (size_t t = 0; t <= p; ++t) {
       double acc = 0.0;
       for (size_t i = 0; i < d; ++i) {
         float kv;
-        if (t == p) kv = sk[r * d + i];
+        if (t == p) kv = j->sk[r * d + i];
         else {
-          kv = (float)(int8_t)k[(r * capacity + t) * d + i] * ks[r * capacity + t];
-          if (history_bf16) kv = round_bf16(kv);
+          kv = (float)(int8_t)j->k[(r * capacity + t) * d + i] * j->ks[r * capacity + t];
+          if (j->history_bf16) kv = round_bf16(kv);
         }
         acc += (double)qr[i] * (double)kv;
       }
-      scores[t] = acc * (double)scale;
+      scores[t] = acc * (double)j->scale;
       if (scores[t] > mx) mx = scores[t];
     }
     double z = 0.0;
@@ -170,10 +179,10 @@ void oracle_attention(const float* q, const uint8_t* k, const uint8_t* v, const 
       const double w = scores[t];
       for (size_t i = 0; i < d; ++i) {
         float vv;
-        if (t == p) vv = sv[r * d + i];
+        if (t == p) vv = j->sv[r * d + i];
         else {
-          vv = (float)(int8_t)v[(r * capacity + t) * d + i] * vs[r * capacity + t];
-          if (history_bf16) vv = round_bf16(vv);
+          vv = (float)(int8_t)j->v[(r * capacity + t) * d + i] * j->vs[r * capacity + t];
+          if (j->history_bf16) vv = round_bf16(vv);
         }
         o[i] += w * (double)vv;
       }
@@ -181,6 +190,50 @@ void oracle_attention(const float* q, const uint8_t* k, const uint8_t* v, const 
     for (size_t i = 0; i < d; ++i) o[i] /= z;
   }
   free(scores);
+}
+
+static void* attention_worker(void* job) {
+  attention_rows((const AttentionJob*)job);
+  return NULL;
+}
+
+/* The same computation with the rows shared out over `threads` POSIX threads
+   (contiguous row ranges, each row computed exactly as above, so the result
+   does not depend on the thread count). Returns 0, or -1 if a thread could
+   not be started (its rows were then computed on the calling thread). */
+int oracle_attention_mt(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
+                        const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
+                        size_t capacity, size_t d, float scale, int history_bf16, size_t threads, double* out) {
+  if (threads < 1) threads = 1;
+  if (threads > rows) threads = rows ? rows : 1;
+  AttentionJob* jobs = (AttentionJob*)malloc(threads * sizeof(AttentionJob));
+  pthread_t* tid = (pthread_t*)malloc(threads * sizeof(pthread_t));
+  int* started = (int*)calloc(threads, sizeof(int));
+  int rc = 0;
+  for (size_t t = 0; t < threads; ++t) {
+    AttentionJob j = {q, ks, vs, sk, sv, k, v, past, rows * t / threads, rows * (t + 1) / threads,
+                      heads, capacity, d, scale, history_bf16, out};
+    jobs[t] = j;
+    if (t + 1 < threads && pthread_create(&tid[t], NULL, attention_worker, &jobs[t]) == 0) started[t] = 1;
+  }
+  for (size_t t = 0; t < threads; ++t) {
+    if (started[t]) continue;
+    if (t + 1 < threads) rc = -1;
+    attention_rows(&jobs[t]);
+  }
+  for (size_t t = 0; t < threads; ++t)
+    if (started[t]) pthread_join(tid[t], NULL);
+  free(started);
+  free(tid);
+  free(jobs);
+  return rc;
+}
+
+void oracle_attention(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
+                      const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
+                      size_t capacity, size_t d, float scale, int history_bf16, double* out) {
+  AttentionJob j = {q, ks, vs, sk, sv, k, v, past, 0, rows, heads, capacity, d, scale, history_bf16, out};
+  attention_rows(&j);
 }
 
 /*

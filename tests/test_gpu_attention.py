@@ -1,7 +1,8 @@
 """GPU parity of kernel 2 (split-K decode attention + merge) against the f64 oracle.
 
-Tolerance: |gpu - oracle| <= 2e-3 + 1e-2 * |oracle| (
-max-abs 2e-3, relative 1e-2 vs the fp32-dequantised attention). The
+Bar (vs the fp32-dequantised attention): max |gpu - oracle|
+<= 2e-3 and, separately, max |gpu - oracle| / |oracle| <= 1e-2 over elements
+with |oracle| >= 1e-3 (helpers.assert_close prints both maxima). The
 bf16-history mode reproduces pp_i8_load (app/src/model/int8_kv.cu:23-27) and is
 held to the reference's own self-check tolerance, 2e-5 absolute
 (app/src/model/int8_kv_ops.rs:73,101).
@@ -159,9 +160,8 @@ def test_operand_and_output_dtypes(device, q_dtype, out_dtype):
     if out_dtype == torch.float32:
         assert_close(got, ref, what="f32 out")
     else:
-        # Output rounding adds at most half an ulp of the narrow type.
-        eps = 2.0 ** -8 if out_dtype == torch.bfloat16 else 2.0 ** -11
-        assert_close(got, ref, atol=2e-3, rtol=1e-2 + eps, what=f"{out_dtype} out")
+        # The 16-bit output's own rounding (half an ulp at |ref|) is the type's, not the kernel's.
+        assert_close(got, ref, what=f"{out_dtype} out", out_dtype="bf16" if out_dtype == torch.bfloat16 else "f16")
 
 
 def test_softmax_scale_override(device):
@@ -304,9 +304,9 @@ def test_golden_config2_append(device):
         assert np.array_equal(ds.cpu().numpy().view(np.uint32), exp_s.view(np.uint32))
 
 
-def test_config5_full_size_sampled_rows_and_properties(device):
+def test_config5_full_size_all_rows_and_properties(device):
     """BASELINE config 5 at full size (B=32, H=16, D=128, 8192 int8 tokens, heavy-tailed K/V, bf16 q):
-    sampled rows against the oracle, the whole append bit-exact, and plan invariance over all rows."""
+    all 512 rows of both plans against the oracle, the whole append bit-exact, plan invariance."""
     from ppk import synthetic
 
     B, H, D, L = 32, 16, 128, 8192
@@ -334,16 +334,13 @@ def test_config5_full_size_sampled_rows_and_properties(device):
         c, s, _ = oracle.quantize(src.float().reshape(rows, 1, D).cpu().numpy())
         assert np.array_equal(codes[:, L:L + 1].cpu().numpy(), c)
         assert np.array_equal(scales[:, L:L + 1].cpu().numpy().view(np.uint32), s.view(np.uint32))
-    # Sampled rows (first, last, heavy-tailed heads, a spread) against the f64 oracle.
-    sample = sorted({0, 1, 15, 16, 255, 256, 511} | set(np.random.default_rng(seed).choice(rows, 17, replace=False)))
-    idx = torch.tensor(sample, device=device)
-    r_q = q.float().reshape(rows, D)[idx].cpu().numpy()
-    r_k, r_v = kc[idx, :L].cpu().numpy(), vc[idx, :L].cpu().numpy()
-    r_ks, r_vs = ks[idx, :L].cpu().numpy(), vs[idx, :L].cpu().numpy()
-    r_sk = kn.float().reshape(rows, D)[idx].cpu().numpy()
-    r_sv = vn.float().reshape(rows, D)[idx].cpu().numpy()
-    ref = oracle.attention(r_q, r_k, r_v, r_ks, r_vs, r_sk, r_sv, np.full(len(sample), L, np.uint32), 1)
-    assert_close(got[sample], ref, what="config 5 sampled rows")
+    # Every one of the 512 rows against the f64 oracle (threaded over the host's cores).
+    ref = oracle.attention(q.float().reshape(rows, D).cpu().numpy(), kc[:, :L].cpu().numpy(),
+                           vc[:, :L].cpu().numpy(), ks[:, :L].cpu().numpy(), vs[:, :L].cpu().numpy(),
+                           kn.float().reshape(rows, D).cpu().numpy(), vn.float().reshape(rows, D).cpu().numpy(),
+                           np.full(B, L, np.uint32), H)
+    assert_close(got, ref, what="config 5, all 512 rows")
+    assert_close(got_split, ref, what="config 5 split-K plan, all 512 rows")
     # The history codes of the first sampled chunk are the oracle's quantisation of its source values.
     src = synthetic.history_chunk(seed, 0, 0, 16, H, 0, L, D, device).float().cpu().numpy()
     c, s, _ = oracle.quantize(src)

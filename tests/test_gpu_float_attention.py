@@ -1,10 +1,10 @@
 """GPU parity of the float-KV decode attention (ppk_float_decode_attention)
 against the f64 oracle (oracle_attention_float).
 
-Tolerance: |gpu - oracle| <= 1e-4 + 1e-4 * |oracle|. The 1e-4 absolute bound
-is the reference's own acceptance bar for this kernel pair
-(hip_attention::validate_split_k, app/src/model/hip_attention.rs:36-41);
-fp32 accumulation over up to 8192 tokens stays well inside it.
+Bar: max |gpu - oracle| <= 1e-4, the reference's own acceptance bar for this
+kernel pair (hip_attention::validate_split_k, app/src/model/hip_attention.rs:36-41),
+and max relative error <= 1e-2 over |oracle| >= 1e-3, each checked on its own;
+fp32 accumulation over up to 8192 tokens stays well inside both.
 """
 from __future__ import annotations
 
@@ -17,7 +17,7 @@ import ppk
 from helpers import SEED, assert_close, bf16_bits_to_f32, to_bf16_bits
 
 pytestmark = pytest.mark.gpu
-ATOL = RTOL = 1e-4
+ATOL, RTOL = 1e-4, 1e-2
 
 
 class FloatCase:

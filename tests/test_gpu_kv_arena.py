@@ -760,4 +760,4 @@ def test_float_arena_view_feeds_float_attention(device):
         full = torch.cat([model[b], cur[b].reshape(H, 1, D)], 1)
         kh[b * H:(b + 1) * H, :lens[b] + 1] = full.view(torch.int16).cpu().numpy().view(np.uint16)
     ref = oracle.attention_float(q.cpu().numpy(), kh, kh, np.array(lens, np.uint32) + 1, H)
-    assert_close(out.reshape(B * H, D).cpu().numpy(), ref, atol=1e-4, rtol=1e-4, what="float arena attention")
+    assert_close(out.reshape(B * H, D).cpu().numpy(), ref, atol=1e-4, rtol=1e-2, what="float arena attention")

@@ -230,6 +230,18 @@ def test_attention_matches_independent_numpy(bf16):
     np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
 
 
+def test_threaded_attention_is_the_single_thread_result():
+    """oracle_attention_mt shares rows over threads; each row is computed exactly as by one thread."""
+    rng = np.random.default_rng(SEED + 31)
+    rows, heads, cap, d = 24, 4, 70, 64
+    args = _problem(rng, rows, heads, cap, d, [0, 3, 69, 71, 40, 12])
+    one = oracle.attention(*args, heads, threads=1)
+    for threads in (2, 5, 24, 64):
+        many = oracle.attention(*args, heads, threads=threads)
+        assert np.array_equal(np.isnan(one), np.isnan(many))
+        assert np.array_equal(one[~np.isnan(one)].view(np.uint64), many[~np.isnan(many)].view(np.uint64))
+
+
 def test_attention_brute_force_tiny():
     """Plain Python loops with math.exp on a 2-row, 3-token, 64-channel problem."""
     rng = np.random.default_rng(SEED + 4)
