@@ -54,6 +54,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--prefill", type=int, default=1000)
     p.add_argument("--choices", type=int, default=2048)
     p.add_argument("--guidance", type=int, default=2)
+    p.add_argument("--device-lengths", action="store_true",
+                   help="configs 1, 3, 4: pass the lengths on the device only (no host copy), i.e. the per-row plan")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=64, help="head rows timed for the CPU baseline sample")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -571,10 +573,19 @@ def bench_config(args) -> int:
     vn = [torch.randn((rows, 1, D), generator=g, device=dev).to(qdt) for _ in range(layers)]
     past = torch.tensor(lengths, dtype=torch.int32, device=dev)
     out = torch.empty((rows, 1, D), dtype=torch.float32, device=dev)
+    # The caller's host copy of the lengths (the reference builds past on the host, batch.rs:152-161)
+    # lets the library balance a ragged batch; --device-lengths times the plan without it.
+    host = None if args.device_lengths else lengths
     steps = [[ppk.DecodeStep(q[li], kc[c, li], vc[c, li], ks[c, li], vs[c, li], kn[li], vn[li], past, H,
-                             split_tokens=args.split, max_past=L, out=out) for li in range(layers)]
+                             split_tokens=args.split, max_past=L, out=out, past_host=host) for li in range(layers)]
              for c in range(copies)]
     split, ngroups = steps[0][0].split_tokens, steps[0][0].ngroups
+    # The balanced plan is taken when the host lengths are given and rows would span blocks otherwise.
+    per_row = ppk.DecodeStep(q[0], kc[0, 0], vc[0, 0], ks[0, 0], vs[0, 0], kn[0], vn[0], past, H,
+                             split_tokens=args.split, max_past=L, out=out)
+    balanced = host is not None and (split, ngroups) != (per_row.split_tokens, per_row.ngroups)
+    launches = 1 if ngroups == 1 else 2
+    del per_row
     torch.cuda.synchronize()
 
     def warm(_i):
@@ -652,8 +663,9 @@ def bench_config(args) -> int:
                 f"{cfg['query']} q and current K/V)",
         "config": {"workload": cfg["workload"], "batch": B, "heads": H, "head_dim": D, "lengths": lengths,
                    "layers": layers, "capacity": cap, "kv": "int8 + f32 scales", "query": cfg["query"],
-                   "tokens_per_wave": split, "blocks_per_row": ngroups,
-                   "launches_per_step": layers * (1 if ngroups == 1 else 2)},
+                   "plan": "balanced work list (host lengths)" if balanced else "per-row blocks",
+                   "tokens_per_wave": split, ("units_per_row_max" if balanced else "blocks_per_row"): ngroups,
+                   "launches_per_step": layers * launches},
         "median_us": round(statistics.median(warm_each), 2),
         "cold": {"mean_us": round(cold_mean, 2), "median_us": round(statistics.median(cold_each), 2),
                  "history_copies": copies, "rotated_bytes": copies * hist_bytes * layers,
@@ -662,7 +674,8 @@ def bench_config(args) -> int:
         "graph_replay_us": None if graph_us is None else round(graph_us, 2),
         "algorithmic_bytes_per_step": step_bytes,
         "step_hbm_gbps": round(step_bytes / (warm_mean * 1e-6) / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": "ppk_decode_d%d" % D, "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": ("ppk_decode_flat_d%d" if balanced else "ppk_decode_d%d") % D,
+                     "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "algorithmic_bytes_per_launch": kernel_bytes,
                      "avg_launch_us": round(kernel_avg_us, 2), "launches": launches,

@@ -57,7 +57,8 @@ enum { PPK_F32 = 0, PPK_BF16 = 1, PPK_F16 = 2 };
 /* Device-side status bits written by the quantize kernels when a flag word is supplied. */
 enum {
   PPK_FLAG_NONFINITE = 1u, /* an input row held NaN or +-Inf (reference CPU path rejects these, int8_kv_ops.rs:16) */
-  PPK_FLAG_OVERFLOW = 2u   /* past[b] + tokens > capacity: that row was not written */
+  PPK_FLAG_OVERFLOW = 2u,  /* past[b] + tokens > capacity: that row was not written */
+  PPK_FLAG_STALE_LENGTHS = 4u /* attention: a device past[b] differed from PpkAttentionArgs.past_host[b]; its rows gave NaN */
 };
 
 /* Attention flags. */
@@ -179,6 +180,15 @@ typedef struct PpkAttentionArgs {
   void* out;               /* [rows, D] */
   void* workspace;         /* ppk_attention_workspace_bytes() bytes, 256-byte aligned (may be NULL if 0) */
   uint64_t workspace_bytes;
+  /* Optional (NULL, or absent when struct_size ends before it): a host copy
+     of past[], the lengths the caller built before copying them to the
+     device (app/src/model/batch.rs:152-161). With it the library balances a
+     ragged batch: the plan, the workspace size and the work each wave takes
+     follow the actual lengths. Each device past[b] is still read and
+     compared; a sequence whose device value differs gives NaN rows (and
+     PPK_FLAG_STALE_LENGTHS in a decode step's flags), never a wrong result.
+     Only read during the call (a captured graph keeps the plan it saw). */
+  const uint32_t* past_host;
 } PpkAttentionArgs;
 PPK_API int32_t ppk_attention_workspace_bytes(ppk_context* ctx, const PpkAttentionArgs* args, uint64_t* bytes);
 /* The launch plan the library would use for args: history tokens per wave,

@@ -7,6 +7,8 @@
 // validation of every span before the first enqueue (app/src/model/hip_attention.rs:63-88).
 #include <dlfcn.h>
 
+#include <cstddef>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -59,6 +61,9 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_copy2d_batch",
     "ppk_quantize_dense_d64", "ppk_quantize_dense_d128", "ppk_quantize_dense_d256",
     "ppk_quantize_append_d64", "ppk_quantize_append_d128", "ppk_quantize_append_d256",
+    "ppk_decode_flat_d64", "ppk_decode_flat_d128", "ppk_decode_flat_d256",
+    "ppk_decode_flat_bf16h_d64", "ppk_decode_flat_bf16h_d128", "ppk_decode_flat_bf16h_d256",
+    "ppk_attn_merge_flat_d64", "ppk_attn_merge_flat_d128", "ppk_attn_merge_flat_d256",
 };
 
 std::string default_code_object() {
@@ -189,8 +194,15 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
   return plan;
 }
 
+// The attention argument block up to workspace_bytes is required; past_host
+// (added later) is read only when struct_size covers it.
+constexpr size_t kAttentionArgsMin = offsetof(PpkAttentionArgs, past_host);
+const uint32_t* host_lengths(const PpkAttentionArgs& a) {
+  return a.struct_size >= offsetof(PpkAttentionArgs, past_host) + sizeof(a.past_host) ? a.past_host : nullptr;
+}
+
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) {
-  require(a.struct_size >= sizeof(PpkAttentionArgs), "PpkAttentionArgs.struct_size too small");
+  require(a.struct_size >= kAttentionArgsMin, "PpkAttentionArgs.struct_size too small");
   dim_index(a.head_dim);
   require(valid_dtype(a.q_dtype) && valid_dtype(a.scratch_dtype) && valid_dtype(a.out_dtype),
           "INT8 attention dtype must be f32, bf16 or f16");
@@ -204,7 +216,95 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   const uint32_t tpl = 64u / (a.head_dim / 16u);
   const uint64_t span = a.max_past ? a.max_past : a.capacity;
   // Per history token: K and V codes plus two fp32 scales.
-  return plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
+  AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
+  // With the host's lengths of a ragged batch, the balanced plan gives every
+  // wave the same share of the live history. Measured on MI355X (B x H=16 x
+  // D=128, per step, per-row -> balanced): 4 sequences of 8192 tokens beside
+  // 28 of 512, 75 -> 43 us; B=16 of 256..16384 tokens, 103 -> 89 us; B=32 of
+  // 256..8192, 111 -> 103 us; B=64 of 64..4096, 113 -> 106 us; config 4 and
+  // config 3 within 2 %. Uniform lengths keep the per-row plan (B=32 x 8192:
+  // one launch, 166 us, against 171 us balanced).
+  const uint32_t* host = host_lengths(a);
+  const uint32_t batch = a.rows / a.heads;
+  const uint64_t flat_waves = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * kFlatWavesPerCu;
+  if (host && a.split_tokens == 0 && batch <= uint32_t(kFlatMaxBatch) && 2 * uint64_t(a.rows) <= flat_waves) {
+    uint64_t sum = 0, most = 0;
+    for (uint32_t b = 0; b < batch; ++b) {
+      const uint64_t live = (host[b] <= a.capacity && host[b] <= span) ? host[b] : 0;
+      sum += live;
+      most = std::max(most, live);
+    }
+    if (most * batch * 10 > sum * 11)  // the longest row beyond 1.1 x the mean
+      plan = plan_flat(ctx, a, uint32_t(span));
+  }
+  return plan;
+}
+
+// Balanced plan (ragged batches with host lengths): eight waves per CU, all
+// resident; units of at most Q tokens of one row, Q the least share (>= 64)
+// for which the units, sum over rows of max(1, ceil(len / Q)), fit the
+// waves; waves 0 .. 2 rows - 1 also append the current tokens (so waves >= 2
+// rows).
+// Record slots per row = the most units of any row (none when every row is
+// one unit: then the decode launch writes every output and no merge runs).
+AttentionPlan plan_flat(const ppk_context* ctx, const PpkAttentionArgs& a, uint32_t span) {
+  constexpr uint32_t kWavesPerBlock = 4, kMinUnit = 64;
+  AttentionPlan plan;
+  plan.head_dim = a.head_dim;
+  plan.flat = true;
+  plan.waves = kWavesPerBlock;
+  plan.span = span;
+  const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
+  plan.blocks = uint32_t(cus * kFlatWavesPerCu / kWavesPerBlock);
+  const uint64_t waves = uint64_t(plan.blocks) * kWavesPerBlock;
+  const uint32_t* host = host_lengths(a);
+  FlatTable& t = plan.table;
+  t.batch = a.rows / a.heads;
+  uint64_t total = 0;
+  for (uint32_t b = 0; b < t.batch; ++b) {
+    t.past[b] = host[b];
+    t.len[b] = (host[b] <= a.capacity && host[b] <= span) ? host[b] : 0u;
+    total += uint64_t(t.len[b]) * a.heads;
+  }
+  // The least share whose units fit the waves: units(Q) = sum over rows of
+  // max(1, ceil(len / Q)) falls as Q grows, and Q = ceil(T / (waves - rows))
+  // always fits (units <= T / Q + rows), so a binary search between 64 and it.
+  auto units_for = [&](uint64_t q) {
+    uint64_t u = 0;
+    for (uint32_t b = 0; b < t.batch; ++b) u += uint64_t(a.heads) * std::max<uint64_t>(1, (t.len[b] + q - 1) / q);
+    return u;
+  };
+  const uint64_t spare = waves - a.rows;  // the caller keeps rows <= waves / 2
+  uint64_t lo = kMinUnit, hi = std::max<uint64_t>((total + spare - 1) / spare, kMinUnit);
+  while (lo < hi) {
+    const uint64_t mid = (lo + hi) / 2;
+    if (units_for(mid) <= waves) hi = mid;
+    else lo = mid + 1;
+  }
+  t.share = uint32_t(lo);
+  uint64_t first = 0;
+  uint32_t most = 1;
+  for (uint32_t b = 0; b < uint32_t(kFlatMaxBatch); ++b) {
+    if (b >= t.batch) {
+      t.first[b] = 0xffffffffu;
+      continue;
+    }
+    t.units[b] = std::max<uint32_t>(1, (t.len[b] + t.share - 1) / t.share);
+    t.first[b] = uint32_t(first);
+    first += uint64_t(t.units[b]) * a.heads;
+    most = std::max(most, t.units[b]);
+  }
+  require(first <= waves, "balanced plan: units exceed the launched waves");
+  t.units_total = uint32_t(first);
+  plan.split = t.share;
+  plan.ngroups = most;
+  plan.lds_bytes = 0;
+  if (most > 1) {
+    plan.y_bytes = (uint64_t(a.rows) * most * a.head_dim * 4 + 255) / 256 * 256;
+    plan.mz_bytes = (uint64_t(a.rows) * most * 2 * 4 + 255) / 256 * 256;
+  }
+  plan.workspace_bytes = plan.y_bytes + plan.mz_bytes;
+  return plan;
 }
 
 // The streaming quantize kernel (dense or append): one 16-byte load per lane
@@ -340,7 +440,8 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
                               " bytes");
   }
   if (step) {
-    require(step->struct_size >= sizeof(PpkDecodeStepArgs), "PpkDecodeStepArgs.struct_size too small");
+    require(step->struct_size >= offsetof(PpkDecodeStepArgs, attn) + kAttentionArgsMin,
+            "PpkDecodeStepArgs.struct_size too small");
     require(valid_dtype(step->new_dtype), "INT8 decode step new-token dtype must be f32, bf16 or f16");
     require(step->k_new && step->v_new, "INT8 decode step null new-token pointer");
     require(aligned(step->k_new, dtype_bytes(step->new_dtype)) && aligned(step->v_new, dtype_bytes(step->new_dtype)) &&
@@ -382,9 +483,40 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   d.scale_log2 = scale_log2;
 
   const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
+  const bool traceable = scratch == nullptr;
+  if (plan.flat) {
+    d.span = plan.span;
+    DecodeFlatArgs f{};
+    f.d = d;
+    f.t = plan.table;
+    const Fn flat = Fn((bf16h ? kDecodeFlatBf16h64 : kDecodeFlat64) + di);
+    DeviceGuard guard(ctx->device);
+    launch(ctx, PPK_KERNEL_ATTENTION, flat, plan.blocks, 64 * plan.waves, 0, stream, f, 1, traceable);
+    if (plan.ngroups < 2) return;  // every row was one unit: the decode launch wrote them all
+    MergeFlatArgs m{};
+    m.m.q = a.q;
+    m.m.sk = a.sk;
+    m.m.sv = a.sv;
+    m.m.past = a.past;
+    m.m.part_y = d.part_y;
+    m.m.part_mz = d.part_mz;
+    m.m.out = a.out;
+    m.m.rows = a.rows;
+    m.m.heads = a.heads;
+    m.m.capacity = a.capacity;
+    m.m.split_tokens = plan.split;
+    m.m.nsplits = plan.ngroups;
+    m.m.q_dtype = a.q_dtype;
+    m.m.scratch_dtype = a.scratch_dtype;
+    m.m.out_dtype = a.out_dtype;
+    m.m.scale_log2 = scale_log2;
+    m.m.span = plan.span;
+    m.t = plan.table;
+    launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMergeFlat64 + di), a.rows, 64, 0, stream, m, 1, traceable);
+    return;
+  }
   const Fn decode = Fn((bf16h ? kDecodeBf16h64 : kDecode64) + di);
   DeviceGuard guard(ctx->device);
-  const bool traceable = scratch == nullptr;
   launch(ctx, PPK_KERNEL_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d, 1,
          traceable);
   if (plan.ngroups > 1) {

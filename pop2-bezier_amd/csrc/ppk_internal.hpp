@@ -50,6 +50,9 @@ enum Fn : int {
   kCopyBatch,
   kQuantizeDense64, kQuantizeDense128, kQuantizeDense256,
   kQuantizeAppend64, kQuantizeAppend128, kQuantizeAppend256,
+  kDecodeFlat64, kDecodeFlat128, kDecodeFlat256,
+  kDecodeFlatBf16h64, kDecodeFlatBf16h128, kDecodeFlatBf16h256,
+  kMergeFlat64, kMergeFlat128, kMergeFlat256,
   kFnCount
 };
 
@@ -59,6 +62,9 @@ struct EventPair {
 
 // Bytes of the per-GPU device array behind ppk_decode_step_noalloc (ppk_scratch.hip).
 constexpr size_t kScratchBytes = PPK_NOALLOC_SCRATCH_BYTES;
+// Waves per CU of the balanced plan's launch (all resident: the decode_flat
+// kernels hold at most 256 VGPRs).
+constexpr uint32_t kFlatWavesPerCu = 8;
 
 }  // namespace ppk
 
@@ -140,17 +146,26 @@ class DeviceGuard {
 // enqueue; launch throws UncertainError once a launch has been attempted.
 struct AttentionPlan {
   uint32_t head_dim = 0;
-  uint32_t split = 0;    // history tokens per wave
+  uint32_t split = 0;    // history tokens per wave (flat: most tokens a wave streams per piece)
   uint32_t waves = 0;    // waves per block
-  uint32_t ngroups = 0;  // blocks per row; 1 = final output in the same launch
+  uint32_t ngroups = 0;  // blocks per row; 1 = final output in the same launch (flat: record slots per row)
   uint32_t lds_bytes = 0;
   uint64_t y_bytes = 0, mz_bytes = 0, workspace_bytes = 0;
+  // Balanced work list (int8 attention over a ragged batch whose host
+  // lengths are known, see FlatTable); ngroups = record slots per row, 1 when
+  // every row is a single unit (then no merge launch).
+  bool flat = false;
+  uint32_t blocks = 0;   // flat: blocks launched
+  uint32_t span = 0;     // flat: rows with past beyond it give NaN
+  FlatTable table{};
 };
 // Split policy shared by both attention paths: span history tokens per row,
 // tpl tokens per wave-wide load, token_bytes of K+V (+scales) per token.
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
                         uint32_t tpl, uint64_t token_bytes, uint32_t head_dim);
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
+// The balanced plan of the int8 decode from the host lengths (at most 64 sequences).
+AttentionPlan plan_flat(const ppk_context* ctx, const PpkAttentionArgs& a, uint32_t span);
 AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttentionArgs& a);
 
 void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a);

@@ -79,7 +79,7 @@ struct DecodeArgs {
   uint32_t rows, heads, capacity, split_tokens, ngroups;
   uint32_t q_dtype, scratch_dtype, out_dtype, new_dtype, append;
   float scale_log2;         // softmax_scale * log2(e)
-  uint32_t pad;
+  uint32_t span;            // rows with past[b] > span give NaN (balanced plan)
 };
 
 struct MergeArgs {
@@ -93,7 +93,39 @@ struct MergeArgs {
   uint32_t rows, heads, capacity, split_tokens, nsplits;
   uint32_t q_dtype, scratch_dtype, out_dtype;
   float scale_log2;
+  uint32_t span;            // rows with past[b] > span give NaN (balanced plan)
+};
+
+// Balanced work list of a ragged batch (the ppk_decode_flat kernels), built
+// on the host from the caller's host copy of the lengths: the live history
+// of row r = b * heads + h is len[b] tokens (past[b] when it is at most
+// min(capacity, span), else none), cut into units[b] = max(1, ceil(len[b] /
+// share)) units of at most `share` tokens inside the row; units are numbered
+// row after row from first[b] (first[] is nondecreasing and holds
+// 0xffffffff past the batch). Wave i takes unit i. A row of one unit is
+// finished by its wave; unit s of a longer row leaves the record at slot s
+// of the row's ngroups slots (y at part_y + (row * ngroups + s) * D, (m, z)
+// at part_mz + (row * ngroups + s) * 2) for the balanced merge kernel.
+// past[] is compared with the device's past: a sequence whose values differ
+// gives NaN rows.
+constexpr int kFlatMaxBatch = 64;
+struct FlatTable {
+  uint32_t batch;                  // sequences
+  uint32_t share;                  // most tokens of a unit
+  uint32_t units_total;            // units over all rows
   uint32_t pad;
+  uint32_t past[kFlatMaxBatch];    // the host's past[b]
+  uint32_t len[kFlatMaxBatch];     // live history tokens of each row of sequence b
+  uint32_t units[kFlatMaxBatch];   // units per row of sequence b
+  uint32_t first[kFlatMaxBatch];   // index of sequence b's first unit
+};
+struct DecodeFlatArgs {
+  DecodeArgs d;             // ngroups = record slots per row
+  FlatTable t;
+};
+struct MergeFlatArgs {
+  MergeArgs m;              // nsplits = record slots per row
+  FlatTable t;
 };
 
 // Float-KV decode attention: the same block geometry over unquantised bf16 or

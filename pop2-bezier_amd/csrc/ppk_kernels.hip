@@ -6,6 +6,8 @@
 //   ppk_dequantize                     codes * scales -> f32/bf16/f16
 //   ppk_decode[_bf16h]_d{..}           decode attention (+ fused append, + in-block merge)
 //   ppk_attn_merge_d{..}               cross-group merge + current token
+//   ppk_decode_flat[_bf16h]_d{..}      decode attention over a balanced work list (ragged batches, + fused append)
+//   ppk_attn_merge_flat_d{..}          merge of the balanced work list's records + current token
 //   ppk_fdecode_{bf16,f32}_d{..}       decode attention over float (bf16/f32) K/V
 //   ppk_fmerge_d{..}                   cross-group merge of the float path
 //   ppk_renyi_sample                   CFG + Renyi effective-support sampler
@@ -148,16 +150,14 @@ __device__ __forceinline__ float lane_absmax(const float (&x)[N]) {
 // NaN quotients become code 0 (as a float->int conversion of NaN does on
 // the reference GPU path); the absmax ignores NaN like fmaxf / f32::max.
 // ---------------------------------------------------------------------------
-// Quantise one row of D values (src[src_row*D ...]) into codes[0..D) and
-// *scale; the whole wave participates. Returns true if the row held a
-// non-finite value (reported through flags when given).
+// Quantise one row of D values into codes[0..D) and *scale; the whole wave
+// participates, lane l holding elements l*D/64 ... (l+1)*D/64 - 1 of the
+// row. A non-finite value is reported through flags when given.
 template <int D>
-__device__ __forceinline__ void quantize_row(const void* src, size_t src_row, uint32_t dtype, uint8_t* codes,
-                                             float* scale, uint32_t* flags, int lane) {
+__device__ __forceinline__ void quantize_values(const float (&x)[D / ppk::kWave], uint8_t* codes, float* scale,
+                                                uint32_t* flags, int lane) {
 #pragma clang fp contract(off)
   constexpr int EPL = D / ppk::kWave;
-  float x[EPL];
-  load_vec<EPL>(src, src_row * D + size_t(lane) * EPL, dtype, x);
   bool finite = true;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) finite = finite && __builtin_isfinite(x[e]);
@@ -179,6 +179,16 @@ __device__ __forceinline__ void quantize_row(const void* src, size_t src_row, ui
     const bool any_bad = __any(!finite);
     if (any_bad && lane == 0) atomicOr(flags, 1u);
   }
+}
+
+// The same for row src_row of src[rows, D] in dtype.
+template <int D>
+__device__ __forceinline__ void quantize_row(const void* src, size_t src_row, uint32_t dtype, uint8_t* codes,
+                                             float* scale, uint32_t* flags, int lane) {
+  constexpr int EPL = D / ppk::kWave;
+  float x[EPL];
+  load_vec<EPL>(src, src_row * D + size_t(lane) * EPL, dtype, x);
+  quantize_values<D>(x, codes, scale, flags, lane);
 }
 
 template <int D>
@@ -1009,6 +1019,320 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
 }
 
 // ---------------------------------------------------------------------------
+// Kernel 2c: decode attention over a balanced work list (ragged batches). The
+// per-row plan above gives every row the same number of blocks, sized for
+// the longest row, so in a ragged batch the CUs holding long rows run on
+// while the others idle. Here the host, from its copy of the lengths, cuts
+// the live history into units of at most Q tokens, each inside one row (row
+// r of len_r tokens is max(1, ceil(len_r / Q)) units, Q = max(ceil(T /
+// (waves - rows)), 64) for T live tokens in all, so the units fit the
+// waves: sum <= T / Q + rows <= waves), and wave i takes unit i: no unit
+// exceeds the mean share by more than waves / (waves - rows). The table
+// travels in the kernel arguments, so every wave issues all of its loads at
+// once, the device lengths among them (they are compared with the table
+// before anything is written). A row of one unit is finished by its wave
+// (current token included); the units of a longer row leave log-sum-exp
+// records that the balanced merge kernel joins.
+//
+// A unit is streamed as (K, V) pairs of batches through a window of two
+// pairs in registers with an online softmax (running max per token group,
+// one rescale per batch). Measured against four pairs and one, and against
+// the per-row kernel's two-phase stream inside the same assignment, on
+// configs 3 and 4 and ragged batches of 16 to 64 sequences: two pairs and the
+// two-phase stream tie, four pairs is 2-12 % slower.
+// ---------------------------------------------------------------------------
+// One (K, V) batch pair of a unit under the online softmax. Token group j
+// (the LPT lanes holding one token of each tile) keeps its own running max m,
+// sum z and 16-channel accumulator: the batch's four scores are formed, the
+// state is rescaled once to the new max, then each tile's V codes are added
+// with weight 2^(s - m) * vscale.
+template <int D, bool BF16H>
+__device__ __forceinline__ void online_pair(const u4 (&kraw)[4], const u4 (&vraw)[4], float ks_lane, float vs_lane,
+                                            uint32_t t0, uint32_t n, int j, const float (&qr)[16], const QInt& qi,
+                                            float sl2, float& m, float& z, float (&acc)[16]) {
+  constexpr int LPT = D / 16;
+  constexpr int TPL = ppk::kWave / LPT;
+  float s[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t tok = (t0 + u) * TPL + j;
+    const float kscale = __shfl(ks_lane, u * TPL + j);
+    float sc;
+    if constexpr (BF16H) {
+      float d = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d = fmaf(qr[4 * w + k], round_bf16(sbyte(kraw[u][w], k) * kscale), d);
+      sc = group_sum<LPT>(d) * sl2;
+    } else {
+      int sh = 0, sm = 0, slo = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        sh = __builtin_amdgcn_sdot4(int(kraw[u][w]), qi.hi[w], sh, false);
+        sm = __builtin_amdgcn_sdot4(int(kraw[u][w]), qi.mid[w], sm, false);
+        slo = __builtin_amdgcn_sdot4(int(kraw[u][w]), qi.lo[w], slo, false);
+      }
+      const float f = fmaf(float(sh), 16384.f, fmaf(float(sm), 128.f, float(slo)));
+      sc = group_sum<LPT>(f) * (kscale * sl2);
+    }
+    s[u] = tok < n ? sc : -INFINITY;
+  }
+  const float mb = fmaxf(fmaxf(m, fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
+  const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mb);
+  z *= f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] *= f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float pr = s[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[u] - mb);
+    z += pr;
+    const float vscale = __shfl(vs_lane, u * TPL + j);
+    if constexpr (BF16H) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[4 * w + k] = fmaf(pr, round_bf16(sbyte(vraw[u][w], k) * vscale), acc[4 * w + k]);
+    } else {
+      const float wgt = pr * vscale;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[4 * w + k] = fmaf(wgt, sbyte(vraw[u][w], k), acc[4 * w + k]);
+    }
+  }
+  m = mb;
+}
+
+// Streams tokens [begin, begin + n) of one row (n >= 1) through the window
+// of two (K, V) pairs; returns the wave's partial (m, z in every lane, the
+// 16-channel sums in lanes j == 0), as wave_attention does. early() runs
+// once the window's first loads are in flight (work whose own loads were
+// issued before, so that waiting for them does not hold the window back).
+template <int D, bool BF16H, class Early>
+__device__ __forceinline__ void wave_attention_window(const ppk::DecodeArgs& a, uint32_t row, uint32_t begin,
+                                                      uint32_t n, const float (&qr)[16], int lane,
+                                                      WavePartial& out, Early early) {
+  constexpr int LPT = D / 16;
+  constexpr int TPL = ppk::kWave / LPT;
+  constexpr int U = 4, NP = 2;
+  const int j = lane / LPT;
+  const int c = lane % LPT;
+  const size_t tok0 = size_t(row) * a.capacity + begin;
+  const uint8_t* kb = a.k + tok0 * D + size_t(c) * 16;
+  const uint8_t* vb = a.v + tok0 * D + size_t(c) * 16;
+  const float* ksb = a.ks + tok0;
+  const float* vsb = a.vs + tok0;
+  const uint32_t nb = (n + U * TPL - 1) / (U * TPL);  // batches per phase
+  u4 kr[NP][U], vr[NP][U];
+  float ksl[NP], vsl[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    if (uint32_t(p) < nb) {  // uniform per wave
+      load_batch<D, U>(kb, ksb, uint32_t(p) * U, n, j, lane, kr[p], ksl[p]);
+      load_batch<D, U>(vb, vsb, uint32_t(p) * U, n, j, lane, vr[p], vsl[p]);
+    }
+  }
+  QInt qi{};
+  float sl2 = a.scale_log2;
+  if constexpr (!BF16H) {
+    qi = quantize_query<LPT>(qr);
+    sl2 *= qi.unscale;
+  }
+  early();
+  float m = -INFINITY, z = 0.f, acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (uint32_t b0 = 0; b0 < nb; b0 += NP) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const uint32_t bi = b0 + uint32_t(p);
+      if (bi < nb) {  // uniform per wave
+        // Scales of tokens at or past n are never used (their scores are -inf).
+        online_pair<D, BF16H>(kr[p], vr[p], ksl[p], vsl[p], bi * U, n, j, qr, qi, sl2, m, z, acc);
+        if (bi + NP < nb) {
+          load_batch<D, U>(kb, ksb, (bi + NP) * U, n, j, lane, kr[p], ksl[p]);
+          load_batch<D, U>(vb, vsb, (bi + NP) * U, n, j, lane, vr[p], vsl[p]);
+        }
+      }
+    }
+  }
+  // Join the token groups: common max, then sums across groups.
+  float mm = m;
+#pragma unroll
+  for (int o = LPT; o < ppk::kWave; o <<= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+  const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
+  z *= w;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] *= w;
+#pragma unroll
+  for (int o = LPT; o < ppk::kWave; o <<= 1) {
+    z += __shfl_xor(z, o);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] += __shfl_xor(acc[i], o);
+  }
+  out.m = mm;
+  out.z = z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) out.acc[i] = acc[i];
+}
+
+// The table's sequence holding unit `unit` (< units_total): the last b with
+// first[b] <= unit. A uniform binary search over the kernel arguments.
+__device__ __forceinline__ uint32_t flat_sequence(const ppk::FlatTable& t, uint32_t unit) {
+  uint32_t lo = 0, hi = t.batch - 1;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi + 1) / 2;
+    if (t.first[mid] <= unit) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <int D, bool BF16H>
+__device__ __forceinline__ void decode_flat_body(const ppk::DecodeFlatArgs& fa) {
+  const ppk::DecodeArgs& a = fa.d;
+  const ppk::FlatTable& t = fa.t;
+  constexpr int LPT = D / 16;
+  constexpr int EPL = D / ppk::kWave;
+  const int lane = threadIdx.x & 63;
+  const uint32_t W = blockDim.x >> 6;
+  const uint32_t wid = blockIdx.x * W + (threadIdx.x >> 6);
+  const int c = lane % LPT;
+  const int j = lane / LPT;
+
+  // Append job (a decode step): wave q < 2 rows quantises tensor q & 1 of
+  // row q >> 1 into slot past[b] (the device value) of the arenas. Its loads
+  // are issued first, beside everything else this wave reads.
+  const bool append = a.append && wid < 2 * a.rows;  // uniform per wave (the host keeps waves >= 2 rows)
+  const uint32_t arow = wid >> 1;
+  float ax[EPL];
+  uint32_t ap = 0;
+  if (append) {
+    ap = a.past[arow / a.heads];
+    load_vec<EPL>((wid & 1u) ? a.v_new : a.k_new, size_t(arow) * D + size_t(lane) * EPL, a.new_dtype, ax);
+  }
+  const bool work = wid < t.units_total;  // uniform per wave
+  uint32_t b = 0, units = 1, len = 0, row = 0, slot = 0, t0 = 0, n = 0, pdev = 0;
+  float qr[16], kv[16], sv[16];
+  if (work) {
+    b = flat_sequence(t, wid);
+    units = t.units[b];
+    len = t.len[b];
+    const uint32_t k = wid - t.first[b];
+    const uint32_t h = k / units;
+    slot = k - h * units;
+    row = b * a.heads + h;
+    t0 = slot * t.share;
+    n = len > t0 ? min(t.share, len - t0) : 0u;
+    pdev = a.past[b];
+    if (n > 0) load_vec<16>(a.q, size_t(row) * D + size_t(c) * 16, a.q_dtype, qr);
+    if (units == 1) {  // the whole row: its current token too
+      if (n > 0) load_vec<16>(a.sk, size_t(row) * D + size_t(c) * 16, a.scratch_dtype, kv);
+      load_vec<16>(a.sv, size_t(row) * D + size_t(c) * 16, a.scratch_dtype, sv);
+    }
+  }
+  auto commit = [&]() {
+    if (!append) return;
+    if (ap >= a.capacity) {
+      if (lane == 0 && a.flags) atomicOr(a.flags, 2u);
+    } else {
+      const size_t dst = size_t(arow) * a.capacity + ap;
+      if (wid & 1u) quantize_values<D>(ax, a.v + dst * D, a.vs + dst, a.flags, lane);
+      else quantize_values<D>(ax, a.k + dst * D, a.ks + dst, a.flags, lane);
+    }
+  };
+  if (!work) {
+    commit();
+    return;
+  }
+  // The row is valid when the host's length is in range and the device agrees.
+  const uint32_t phost = t.past[b];
+  const bool host_ok = phost <= a.capacity && phost <= a.span;
+  WavePartial part;
+  part.m = -INFINITY;
+  part.z = 0.f;
+  float s_cur = -INFINITY;
+  if (n > 0) {
+    auto early = [&]() {  // with the unit's first loads in flight
+      commit();
+      if (units == 1) s_cur = current_score<D>(a, kv, qr);
+    };
+    wave_attention_window<D, BF16H>(a, row, t0, n, qr, lane, part, early);
+  } else {
+    commit();
+  }
+  const bool fresh = pdev == phost;
+  if (!fresh && lane == 0 && a.flags) atomicOr(a.flags, 4u);
+  if (units == 1) {
+    const bool valid = fresh && host_ok;
+    const float m = fmaxf(part.m, s_cur);
+    const float wp = n > 0 ? __builtin_amdgcn_exp2f(part.m - m) : 0.f;
+    const float wc = n > 0 ? __builtin_amdgcn_exp2f(s_cur - m) : 1.f;
+    const float zsum = n > 0 ? fmaf(wp, part.z, wc) : 1.f;
+    if (j == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float o = valid ? fmaf(wc, sv[i], n > 0 ? wp * part.acc[i] : 0.f) / zsum : __builtin_nanf("");
+        store_elem(a.out, size_t(row) * D + size_t(c) * 16 + i, a.out_dtype, o);
+      }
+    }
+  } else if (slot < a.ngroups) {  // always, by the host's count of slots
+    const size_t rec = size_t(row) * a.ngroups + slot;
+    if (j == 0) {
+      f4* o = reinterpret_cast<f4*>(a.part_y + rec * D + size_t(c) * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
+    }
+    if (lane == 0) {
+      a.part_mz[rec * 2] = part.m;
+      a.part_mz[rec * 2 + 1] = part.z;
+    }
+  }
+}
+
+// Balanced merge: one wave per row of two or more units (the others were
+// written by the decode launch): joins the row's records and the current
+// token, or gives NaN when the row is invalid or the device length differs
+// from the table's.
+template <int D>
+__device__ __forceinline__ void attn_merge_flat_body(const ppk::MergeFlatArgs& fa) {
+  const ppk::MergeArgs& a = fa.m;
+  const ppk::FlatTable& t = fa.t;
+  constexpr int EPL = D / ppk::kWave;
+  const int lane = threadIdx.x;
+  const uint32_t row = blockIdx.x;
+  const uint32_t b = row / a.heads;
+  const uint32_t units = t.units[b];
+  if (units < 2) return;  // uniform per wave
+  const uint32_t phost = t.past[b];
+  const uint32_t pdev = a.past[b];
+  const size_t base = size_t(row) * D + size_t(lane) * EPL;
+  float sv[EPL];
+  float s_cur = -INFINITY;
+  auto current = [&]() {
+    float qv[EPL], kv[EPL];
+    load_vec<EPL>(a.q, base, a.q_dtype, qv);
+    load_vec<EPL>(a.sk, base, a.scratch_dtype, kv);
+    load_vec<EPL>(a.sv, base, a.scratch_dtype, sv);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kv[e], d);
+    s_cur = wave_sum(d) * a.scale_log2;
+    return s_cur;
+  };
+  float m, zsum, y[EPL];
+  combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D,
+                     min(units, a.nsplits), lane, current, m, zsum, y);
+  const bool valid = pdev == phost && phost <= a.capacity && phost <= a.span;
+  const float wc = __builtin_amdgcn_exp2f(s_cur - m);
+  zsum += wc;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e)
+    store_elem(a.out, base + e, a.out_dtype, valid ? fmaf(wc, sv[e], y[e]) / zsum : __builtin_nanf(""));
+}
+
+// ---------------------------------------------------------------------------
 // Float-KV decode attention: the reference's non-int8 decode path
 // (app/src/model/decode_attention.hip:9-66, fused_attention.rs:8-30) on the
 // block geometry of the int8 kernel. K/V are stored bf16 or f32; row r attends
@@ -1653,6 +1977,22 @@ PPK_QSTREAM(256)
 PPK_ATTN(64)
 PPK_ATTN(128)
 PPK_ATTN(256)
+
+// Flat work list kernels: up to 256 VGPRs, i.e. 8 resident waves per CU (the host launches 8).
+#define PPK_ATTN_FLAT(D)                                                                                \
+  extern "C" __global__ __launch_bounds__(512) void ppk_decode_flat_d##D(ppk::DecodeFlatArgs a) {      \
+    decode_flat_body<D, false>(a);                                                                      \
+  }                                                                                                     \
+  extern "C" __global__ __launch_bounds__(512) void ppk_decode_flat_bf16h_d##D(ppk::DecodeFlatArgs a) { \
+    decode_flat_body<D, true>(a);                                                                       \
+  }                                                                                                     \
+  extern "C" __global__ __launch_bounds__(64) void ppk_attn_merge_flat_d##D(ppk::MergeFlatArgs a) {   \
+    attn_merge_flat_body<D>(a);                                                                         \
+  }
+PPK_ATTN_FLAT(64)
+PPK_ATTN_FLAT(128)
+PPK_ATTN_FLAT(256)
+#undef PPK_ATTN_FLAT
 
 #define PPK_FLOAT_ATTN(D)                                                                        \
   extern "C" __global__ __launch_bounds__(1024) void ppk_fdecode_bf16_d##D(ppk::FloatDecodeArgs a) { \

@@ -15,7 +15,7 @@ HSACO_PATH = os.path.join(HERE, "ppk_kernels.hsaco")
 PPK_ABI_VERSION = 1
 PPK_OK, PPK_PRECONDITION, PPK_INVALID_OUTPUT, PPK_EXECUTION_UNCERTAIN = 0, 1, 2, 3
 PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
-PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW = 1, 2
+PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW, PPK_FLAG_STALE_LENGTHS = 1, 2, 4
 PPK_ATTN_BF16_HISTORY = 1
 PPK_NOALLOC_SCRATCH_BYTES = 8 << 20
 (PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE,
@@ -48,7 +48,7 @@ class PpkAttentionArgs(ctypes.Structure):
                 ("split_tokens", _u32), ("max_past", _u32), ("softmax_scale", _f32),
                 ("q", _ptr), ("k_codes", _ptr), ("v_codes", _ptr), ("k_scales", _ptr), ("v_scales", _ptr),
                 ("sk", _ptr), ("sv", _ptr), ("past", _ptr), ("out", _ptr), ("workspace", _ptr),
-                ("workspace_bytes", _u64)]
+                ("workspace_bytes", _u64), ("past_host", _ptr)]
 
 
 class PpkDecodeStepArgs(ctypes.Structure):

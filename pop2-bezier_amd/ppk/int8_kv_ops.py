@@ -126,8 +126,9 @@ def append(k_new: torch.Tensor, v_new: torch.Tensor, past: torch.Tensor, k_codes
 
 def attention_args(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *, bf16_history: bool = False,
                    max_past: int = 0, out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-                   softmax_scale: float = 0.0) -> tuple[_abi.PpkAttentionArgs, torch.Tensor]:
-    """Validate like int8_kv_ops::attention and build the ABI argument block (workspace unset)."""
+                   softmax_scale: float = 0.0, past_host=None) -> tuple[_abi.PpkAttentionArgs, torch.Tensor]:
+    """Validate like int8_kv_ops::attention and build the ABI argument block (workspace unset). past_host: an
+    optional host copy of `past` (a sequence of ints), with which the library balances ragged batches."""
     rows, capacity = _geometry(k)
     d = k.shape[2]
     _require(heads > 0 and rows % heads == 0 and v.shape == k.shape and v.is_contiguous()
@@ -152,7 +153,12 @@ def attention_args(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int 
         heads=heads, capacity=capacity, head_dim=d, split_tokens=split_tokens, max_past=max_past,
         softmax_scale=softmax_scale, q=q.data_ptr(), k_codes=k.data_ptr(), v_codes=v.data_ptr(),
         k_scales=ks.data_ptr(), v_scales=vs.data_ptr(), sk=sk.data_ptr(), sv=sv.data_ptr(), past=past.data_ptr(),
-        out=out.data_ptr(), workspace=None, workspace_bytes=0)
+        out=out.data_ptr(), workspace=None, workspace_bytes=0, past_host=None)
+    if past_host is not None:
+        host = [int(x) for x in past_host]
+        _require(len(host) == rows // heads and all(0 <= x < 2 ** 32 for x in host), "INT8 attention lengths differ")
+        a._past_host = (ctypes.c_uint32 * len(host))(*host)  # kept alive with the argument block
+        a.past_host = ctypes.cast(a._past_host, ctypes.c_void_p).value
     return a, out
 
 
@@ -173,11 +179,12 @@ def plan(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = None) -> tup
 
 
 def attention(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *, bf16_history: bool = False,
-              max_past: int = 0, out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0) -> torch.Tensor:
+              max_past: int = 0, out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0,
+              past_host=None) -> torch.Tensor:
     """int8_kv_ops::attention: q/sk/sv [rows,1,D], k/v uint8 [rows,cap,D], ks/vs f32 [rows,cap],
-    past U32 [rows/heads] -> out [rows,1,D] (float32 by default)."""
+    past U32 [rows/heads] -> out [rows,1,D] (float32 by default). past_host: optional host copy of past."""
     a, out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
-                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale)
+                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale, past_host=past_host)
     ctx = context(q.device)
     nbytes = workspace_bytes(a, ctx)
     # The caching allocator is stream-ordered: the block is not reused before
@@ -192,12 +199,12 @@ def attention(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, 
 def decode_step(q, k, v, ks, vs, sk, sv, past, heads: int, k_new: torch.Tensor | None = None,
                 v_new: torch.Tensor | None = None, split_tokens: int = 0, *, flags: torch.Tensor | None = None,
                 bf16_history: bool = False, max_past: int = 0, out_dtype: torch.dtype = torch.float32,
-                softmax_scale: float = 0.0) -> torch.Tensor:
+                softmax_scale: float = 0.0, past_host=None) -> torch.Tensor:
     """Commit + attend in one call: quantise k_new/v_new [rows, D] (default: sk/sv) into slot past[b] of the
     arenas, then attention over [0, past[b]) plus the current token, as forward_embedding's commit path does
     (query_int8 then int8_kv_ops::attention, app/src/model/mod.rs:699-705)."""
     a, out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
-                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale)
+                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale, past_host=past_host)
     step = _step_args(a, sk if k_new is None else k_new, sv if v_new is None else v_new, flags, k.shape[2])
     ctx = context(q.device)
     nbytes = workspace_bytes(a, ctx)
@@ -215,9 +222,11 @@ def _step_args(a: _abi.PpkAttentionArgs, k_new: torch.Tensor, v_new: torch.Tenso
              "INT8 decode step new token must be float[rows,D]")
     if flags is not None:
         _require(flags.dtype in (torch.int32, torch.uint32) and flags.numel() >= 1, "flags must be one 32-bit word")
-    return _abi.PpkDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkDecodeStepArgs), new_dtype=_DTYPES[k_new.dtype],
+    step = _abi.PpkDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkDecodeStepArgs), new_dtype=_DTYPES[k_new.dtype],
                                   k_new=k_new.data_ptr(), v_new=v_new.data_ptr(),
                                   flags=flags.data_ptr() if flags is not None else None, attn=a)
+    step._past_host = getattr(a, "_past_host", None)  # the copied block points at it
+    return step
 
 
 class DecodeAttention:
@@ -226,10 +235,10 @@ class DecodeAttention:
 
     def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *,
                  bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
-                 out_dtype: torch.dtype = torch.float32):
+                 out_dtype: torch.dtype = torch.float32, past_host=None):
         self.args, self.out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens,
                                              bf16_history=bf16_history, max_past=max_past, out=out,
-                                             out_dtype=out_dtype)
+                                             out_dtype=out_dtype, past_host=past_host)
         self.ctx = context(q.device)
         self.split_tokens, self.ngroups, nbytes = plan(self.args, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
@@ -252,9 +261,9 @@ class DecodeStep:
 
     def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, k_new=None, v_new=None, split_tokens: int = 0, *,
                  flags=None, bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
-                 out_dtype: torch.dtype = torch.float32):
+                 out_dtype: torch.dtype = torch.float32, past_host=None):
         a, self.out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
-                                     max_past=max_past, out=out, out_dtype=out_dtype)
+                                     max_past=max_past, out=out, out_dtype=out_dtype, past_host=past_host)
         k_new = sk if k_new is None else k_new
         v_new = sv if v_new is None else v_new
         self.args = _step_args(a, k_new, v_new, flags, k.shape[2])

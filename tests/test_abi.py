@@ -8,10 +8,12 @@ import os
 import re
 import subprocess
 
+import numpy as np
 import pytest
 
 import ppk
 from ppk import _abi
+from helpers import SEED
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "ppk_int8_kv.h")
@@ -85,8 +87,12 @@ def _attn_args(**kw) -> _abi.PpkAttentionArgs:
     a = _abi.PpkAttentionArgs(struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), q_dtype=0, scratch_dtype=0,
                               out_dtype=0, flags=0, rows=512, heads=16, capacity=8193, head_dim=128,
                               split_tokens=0, max_past=8192, softmax_scale=0.0)
+    host = kw.pop("past_host", None)
     for k, v in kw.items():
         setattr(a, k, v)
+    if host is not None:
+        a._past_host = (ctypes.c_uint32 * len(host))(*[int(x) for x in host])
+        a.past_host = ctypes.cast(a._past_host, ctypes.c_void_p).value
     return a
 
 
@@ -105,8 +111,73 @@ def test_plan_sizes_workspace_without_a_device():
     # joined by the merge kernel.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048))
     assert split == 64 and groups == 16 and nbytes == 16 * 16 * 128 * 4 + 16 * 16 * 2 * 4
+    # Uniform host lengths keep the per-row plan.
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048, past_host=[2048])) == \
+        (split, groups, nbytes)
+    # Ragged host lengths (longest row beyond 1.1 x the mean): the balanced plan over 2048 waves (8 per CU);
+    # the least unit (>= 64 tokens) whose units fit is 64, so rows of 2048 tokens are 32 units (record slots).
+    split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(rows=16, heads=8, capacity=2049, max_past=2048,
+                                                            past_host=[2048, 1000]))
+    assert split == 64 and groups == 32 and nbytes == 16 * 32 * 128 * 4 + 16 * 32 * 2 * 4
+    # Short ragged rows with host lengths: every row one unit, so no records and no merge launch.
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900,
+                                           past_host=[10, 0, 60, 64])) == (64, 1, 0)
     # Few short rows (config 1 shape): one block per row, one launch.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=513, max_past=512, head_dim=64)) == (64, 1, 0)
+
+
+def _flat_units(past, heads, rows, capacity, span, waves, min_unit=64):
+    """Units per row of the balanced plan from the host lengths: live length past[b] (0 beyond
+    min(capacity, span)), a row of len tokens is max(1, ceil(len / Q)) units of at most Q tokens, Q the least
+    share >= 64 whose units fit the waves (found here by a linear scan); returns (units per row, Q)."""
+    lens = [p if p <= capacity and p <= span else 0 for p in past]
+    share = min_unit
+    while sum(heads * max(1, -(-length // share)) for length in lens) > waves:
+        share += 1
+    return [max(1, -(-length // share)) for length in lens for _ in range(heads)], share
+
+
+@pytest.mark.parametrize("heads,d", [(16, 128), (1, 64), (4, 256), (8, 128)])
+def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
+    """Ragged batches of up to 64 sequences (zero, tiny, capacity-long and past-capacity rows) with host
+    lengths: the balanced plan is taken when the longest live row exceeds 1.1 x the mean (and rows fit half
+    the waves); its units cover every live token, never outnumber the launched waves (2048 on the 256 CUs
+    assumed without a context), and the record slots per row are the most units of any row."""
+    rng = np.random.default_rng(SEED + heads + d)
+    checked = 0
+    for trial in range(500):
+        batch = int(rng.integers(1, 65))
+        cap = int(rng.choice([64, 700, 4096, 30000]))
+        span = int(rng.choice([cap, max(1, cap // 3)]))
+        kind = trial % 4
+        if kind == 0:
+            past = rng.integers(0, span + 1, batch)
+        elif kind == 1:  # one long row among empty ones
+            past = np.zeros(batch, np.int64)
+            past[int(rng.integers(batch))] = span
+        elif kind == 2:  # all at the span, one past the capacity
+            past = np.full(batch, span)
+            past[0] = cap + 1
+        else:  # tiny rows and a few long ones
+            past = rng.integers(0, 3, batch)
+            past[rng.integers(0, batch, 3)] = span
+        rows = batch * heads
+        a = _attn_args(rows=rows, heads=heads, capacity=cap, max_past=span, head_dim=d, past_host=past)
+        per_row = ppk.int8_kv_ops.plan(_attn_args(rows=rows, heads=heads, capacity=cap, max_past=span, head_dim=d))
+        split, groups, nbytes = ppk.int8_kv_ops.plan(a)
+        live = [int(p) if p <= min(cap, span) else 0 for p in past]
+        if 2 * rows > 2048 or max(live) * batch * 10 <= sum(live) * 11:  # too many rows, or not ragged
+            assert (split, groups, nbytes) == per_row
+            continue
+        units, share = _flat_units([int(p) for p in past], heads, rows, cap, span, 2048)
+        assert split == share and groups == max(units)
+        assert sum(units) <= 2048, "every unit has a wave"
+        for p, u in zip(np.repeat(past, heads), units):
+            live = int(p) if p <= min(cap, span) else 0
+            assert u * share >= live and (u - 1) * share < max(live, 1)
+        assert nbytes == (0 if groups == 1 else rows * groups * d * 4 + -(-(rows * groups * 8) // 256) * 256)
+        checked += 1
+    assert checked > 60
 
 
 @pytest.mark.parametrize("bad", [dict(head_dim=96), dict(rows=30, heads=16), dict(heads=0), dict(capacity=0),

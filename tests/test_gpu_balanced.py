@@ -1,0 +1,187 @@
+"""GPU parity of the balanced plan for ragged batches (ppk_decode_flat + ppk_attn_merge_flat).
+
+The plan is taken when the caller passes its host copy of the lengths
+(PpkAttentionArgs.past_host) and rows would otherwise span several blocks.
+Bars as for the per-row plan (tests/test_gpu_attention.py): against the f64
+oracle, max abs error <= 2e-3 and max relative error <= 1e-2 (|oracle| >=
+1e-3); the bf16-history mode within 2e-5 absolute; appended codes and scales
+bit-exact; rows whose device length is invalid, or differs from the host
+copy, give NaN.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import ppk
+from helpers import SEED, assert_close
+from test_gpu_attention import Case
+
+pytestmark = pytest.mark.gpu
+
+
+def _plan(c: Case, past_host, max_past=0, **kw):
+    a, _ = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H,
+                                          max_past=max_past, past_host=past_host, **kw)
+    return ppk.int8_kv_ops.plan(a, ppk.context(c.q.device))
+
+
+def test_config4_ragged_balanced(device):
+    """BASELINE config 4 (B=8, H=16, D=128, lengths U[256, 4096], bf16 q) through the balanced plan."""
+    lengths = [int(x) for x in np.random.default_rng(SEED).integers(256, 4097, size=8)]
+    c = Case(device, 8, 16, 128, lengths, max(lengths) + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    split, slots, _ = _plan(c, lengths, max_past=max(lengths))
+    assert slots > 1, "config 4 rows span several units"
+    ref = c.reference()
+    assert_close(c.run(past_host=lengths, max_past=max(lengths)), ref, what="config 4 balanced")
+    assert_close(c.run(past_host=lengths), ref, what="config 4 balanced, span = capacity")
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_edge_lengths_balanced(device, d):
+    """Empty rows, one-token rows, rows at the capacity, rows past it (NaN), single-unit rows beside rows
+    of many units."""
+    lengths = [0, 1, 700, 2000, 2049, 3, 2048, 5000]
+    c = Case(device, 8, 4, d, lengths, 2048)
+    _, slots, _ = _plan(c, lengths)
+    assert slots > 1
+    got = c.run(past_host=lengths)
+    ref = c.reference()
+    assert np.isnan(got[4 * 4:5 * 4]).all() and np.isnan(got[7 * 4:]).all()
+    assert_close(got, ref, what=f"edge lengths d={d}")
+
+
+def test_rows_beyond_max_past_give_nan(device):
+    lengths = [300, 1200, 40, 1100]
+    c = Case(device, 4, 8, 128, lengths, 1500)
+    got = c.run(past_host=lengths, max_past=1000)
+    ref = c.reference()
+    bad = np.repeat(np.array(lengths) > 1000, 8)
+    assert np.isnan(got[bad]).all() and not np.isnan(got[~bad]).any()
+    assert_close(got[~bad], ref[~bad], what="rows within max_past")
+
+
+def test_short_rows_are_one_launch(device):
+    """Every row within one unit: no records, no merge launch, outputs written by the decode launch."""
+    lengths = [10, 0, 60, 64]
+    c = Case(device, 4, 16, 64, lengths, 1024)
+    assert _plan(c, lengths, max_past=900) == (64, 1, 0)
+    ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_MERGE, reset=True)
+    ppk.set_profiling(True)
+    got = c.run(past_host=lengths, max_past=900)
+    ppk.set_profiling(False)
+    assert ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_MERGE, reset=True)[0] == 0
+    assert_close(got, c.reference(), what="one-unit rows")
+
+
+def test_bf16_history_balanced(device):
+    """The reference-exact mode (history rounded through bf16, int8_kv.cu:23-27) at the reference's 2e-5."""
+    lengths = [900, 30, 2500, 1700]
+    c = Case(device, 4, 8, 64, lengths, 2600)
+    got = c.run(past_host=lengths, bf16_history=True)
+    assert_close(got, c.reference(history_bf16=True), atol=2e-5, rtol=0, what="balanced bf16 history")
+
+
+@pytest.mark.parametrize("q_dtype,out_dtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                                (torch.float16, torch.float16)])
+def test_balanced_dtypes(device, q_dtype, out_dtype):
+    lengths = [1500, 333, 2900]
+    c = Case(device, 3, 8, 128, lengths, 3000, q_dtype=q_dtype, scratch_dtype=q_dtype)
+    got = c.run(past_host=lengths, out_dtype=out_dtype)
+    narrow = {torch.float32: None, torch.bfloat16: "bf16", torch.float16: "f16"}[out_dtype]
+    assert_close(got, c.reference(), what=f"balanced {q_dtype} -> {out_dtype}", out_dtype=narrow)
+
+
+def test_decode_step_balanced_appends_and_attends(device):
+    """The fused step over the balanced plan: each row's new token quantised into slot past[b] (bit-exact
+    against the oracle), attention over the pre-append history plus the current token."""
+    lengths = [2047, 0, 610, 1300, 2048]
+    B, H, D, cap = 5, 8, 128, 2048
+    c = Case(device, B, H, D, lengths, cap, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    ref = c.reference()
+    before = [t.clone() for t in (c.kc, c.vc, c.ks, c.vs)]
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, flags=flags, past_host=lengths)
+    torch.cuda.synchronize()
+    assert_close(out.reshape(c.rows, D).cpu().numpy(), ref, what="balanced decode step")
+    assert int(flags.item()) & ppk.PPK_FLAG_OVERFLOW  # the row at the capacity could not append
+    for src, codes, scales, old in ((c.sk32, c.kc, c.ks, before[0]), (c.sv32, c.vc, c.vs, before[1])):
+        exp_c, exp_s, _ = oracle.quantize(src.reshape(c.rows, 1, D))
+        got_c, got_s = codes.cpu().numpy(), scales.cpu().numpy()
+        for b, p in enumerate(lengths):
+            rows = slice(b * H, (b + 1) * H)
+            if p < cap:
+                assert np.array_equal(got_c[rows, p], exp_c[rows, 0])
+                assert np.array_equal(got_s[rows, p].view(np.uint32), exp_s[rows, 0].view(np.uint32))
+    # Nothing else in the arenas moved.
+    for got, old in zip((c.kc, c.vc), before[:2]):
+        g, o = got.cpu().numpy(), old.cpu().numpy()
+        for b, p in enumerate(lengths):
+            if p < cap:
+                g[b * H:(b + 1) * H, p] = o[b * H:(b + 1) * H, p]
+        assert np.array_equal(g, o)
+
+
+def test_stale_host_lengths_give_nan_and_a_flag(device):
+    """A host copy that no longer matches the device's lengths never yields a wrong row: the sequences whose
+    device value differs give NaN and the step's flags carry PPK_FLAG_STALE_LENGTHS; the others stay right."""
+    lengths = [1500, 700, 2000, 20]
+    c = Case(device, 4, 8, 128, lengths, 2100)
+    stale = [1500, 650, 2000, 21]  # sequences 1 and 3 differ
+    ref = c.reference()
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, flags=flags, past_host=stale)
+    torch.cuda.synchronize()
+    got = out.reshape(c.rows, c.D).cpu().numpy()
+    bad = np.repeat(np.array(lengths) != np.array(stale), 8)
+    assert np.isnan(got[bad]).all()
+    assert_close(got[~bad], ref[~bad], what="fresh sequences beside stale ones")
+    assert int(flags.item()) & ppk.PPK_FLAG_STALE_LENGTHS
+
+
+def test_balanced_plan_through_the_noalloc_entry_point(device):
+    """ppk_decode_step_noalloc takes the same balanced plan (host lengths in the argument block)."""
+    import ctypes
+
+    from ppk import _abi
+
+    lengths = [3000, 120, 1800]
+    c = Case(device, 3, 8, 128, lengths, 3001, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    ref = c.reference()
+    a, out = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H,
+                                            past_host=lengths)
+    step = ppk.int8_kv_ops._step_args(a, c.sk, c.sv, None, c.D)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    assert _abi.lib().ppk_decode_step_noalloc(ppk.context(device), stream, ctypes.byref(step)) == 0, _abi.last_error()
+    torch.cuda.synchronize()
+    assert_close(out.reshape(c.rows, c.D).cpu().numpy(), ref, what="balanced no-alloc")
+
+
+def test_balanced_step_captured_in_a_hip_graph(device):
+    """A prepared balanced step replays in a HIP graph bit for bit (the table travels in the kernel
+    arguments; no memset)."""
+    lengths = [2500, 64, 900, 1700]
+    c = Case(device, 4, 16, 128, lengths, 2600, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    st = ppk.DecodeAttention(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, past_host=lengths)
+    eager = st().clone()
+    torch.cuda.synchronize()
+    assert_close(eager.reshape(c.rows, c.D).cpu().numpy(), c.reference(), what="balanced eager")
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        st(side)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st()
+    for _ in range(3):
+        st.out.fill_(float("nan"))
+        junk = torch.randn(1 << 20, device=device).sin_().sum()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(junk)
+        assert torch.equal(st.out, eager)
