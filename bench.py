@@ -62,7 +62,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run one plain 1 GiB elementwise copy (torch.neg, f32) first: the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
-    p.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "ppk_decode_d128_b32_h16_ctx8192_traffic.json"),
+    p.add_argument("--traffic", default=None,
                    help="JSON with measured HBM bytes per partial launch (rocprofv3 --pmc), if present")
     return p.parse_args()
 
@@ -541,6 +541,11 @@ def bench_config(args) -> int:
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:  # the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        torch.neg(src, out=torch.empty_like(src))
+        torch.cuda.synchronize()
+        del src
     B, H, D, layers = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["layers"]
     if cfg["lengths"] is None:
         lengths = [int(x) for x in np.random.default_rng(SEED).integers(256, 4097, size=B)]
@@ -1073,9 +1078,10 @@ def main() -> int:
 
     kname = "ppk_decode_d%d" % D
     traffic = None
-    if os.path.exists(args.traffic):
+    tpath = args.traffic or os.path.join(ROOT, "profiles", f"ppk_decode_d{D}_b{B}_h{H}_ctx{L}_traffic.json")
+    if os.path.exists(tpath):
         try:
-            with open(args.traffic) as f:
+            with open(tpath) as f:
                 t = json.load(f)
             if t.get("split") == split and t.get("workload") == f"B{B}H{H}D{D}L{L}" and t.get("kernel") == kname:
                 traffic = t.get("hbm_bytes_per_launch")
