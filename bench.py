@@ -57,7 +57,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--device-lengths", action="store_true",
                    help="configs 1, 3, 4: pass the lengths on the device only (no host copy), i.e. the per-row plan")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-rows", type=int, default=64, help="head rows timed for the CPU baseline sample")
+    p.add_argument("--cpu-rows", type=int, default=0,
+                   help="head rows timed for the CPU baseline (0 = every row of the step)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run one plain 1 GiB elementwise copy (torch.neg, f32) first: the known-size kernel that "
@@ -98,17 +99,18 @@ def _time_cpu(fn, seconds: float, max_reps: int = 1000) -> tuple[int, float]:
 def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args, *, threads: int | None = None,
                  rows: int | None = None, seconds: float | None = None, context: int | None = None,
                  repeat: int = 1, what: str = "") -> dict:
-    """The reference's Candle CPU decode (restated in C, oracle/) on a bounded sample of head rows.
+    """The reference's Candle CPU decode (restated in C, oracle/cpu_baseline.c) over the step's head rows.
 
-    The sample is the first `rows` head rows (whole sequences); its time is scaled by total/sampled rows
-    and by `repeat` (identical layers of one step)."""
+    By default every row of the step; a smaller `rows` (or --cpu-rows) times the first rows (whole
+    sequences) and scales by total/sampled rows. `repeat` scales by identical layers of one step."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # noqa: E402  (CPU baseline leg only)
 
     rows_total = q.shape[0]
-    n = min(args.cpu_rows if rows is None else rows, rows_total)
+    want = args.cpu_rows if rows is None else rows
+    n = min(want, rows_total) if want else rows_total
     n -= n % heads
     n = max(n, heads)
     L = args.context if context is None else context
@@ -121,14 +123,16 @@ def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args, *, threads: int |
     sv_h = vn.float().reshape(rows_total, -1)[:n].cpu().numpy()
     past_h = past[: n // heads].cpu().numpy().astype(np.uint32)
     if threads is None:
-        threads = max(1, min(os.cpu_count() or 1, 16))
+        threads = _host_cpus()  # every usable core, as Candle's Rayon pool
     reps, el = _time_cpu(lambda: oracle.cpu_baseline(q_h, k_h, v_h, ks_h, vs_h, sk_h, sv_h, past_h, heads, threads),
                          args.cpu_seconds if seconds is None else seconds)
     scale = rows_total / n * repeat
     us_per_step = el / reps * 1e6 * scale
+    scaled = f", scaled x{scale:g}" if scale != 1 else ""
     return {"value": round(us_per_step, 1), "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{n} of {rows_total} head rows{what} (Candle CPU path restated in C, "
-                      f"oracle/ppk_oracle.c cpu_baseline_decode), {reps} reps in {el:.1f} s, scaled x{scale:g}",
+                      f"oracle/cpu_baseline.c cpu_baseline_decode, {oracle.cpu_baseline_isa()}), "
+                      f"{reps} reps in {el:.1f} s{scaled}",
             "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
 
 
@@ -221,14 +225,14 @@ def bench_float(args) -> int:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle  # noqa: E402  (CPU baseline leg only)
 
-        n = max(1, min(args.cpu_rows, rows))
+        n = max(1, min(args.cpu_rows, rows)) if args.cpu_rows else rows
         if eb == 2:
             k_h = k[:n].view(torch.int16).cpu().numpy().view(np.uint16)
             v_h = v[:n].view(torch.int16).cpu().numpy().view(np.uint16)
         else:
             k_h, v_h = k[:n].cpu().numpy(), v[:n].cpu().numpy()
         q_h = q[:n].cpu().numpy()
-        threads = max(1, min(os.cpu_count() or 1, 16))
+        threads = _host_cpus()
         reps, t0 = 0, time.perf_counter()
         while True:
             oracle.cpu_baseline_float(q_h, k_h, v_h, threads)
@@ -239,7 +243,8 @@ def bench_float(args) -> int:
         result["cpu_baseline"] = {
             "value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{n} of {rows} head rows x {L} tokens (Candle's ordinary CPU attention restated in C, "
-                      f"cpu_baseline_float_decode), {reps} reps in {el:.1f} s, scaled x{rows / n:g}",
+                      f"oracle/cpu_baseline.c cpu_baseline_float_decode, {oracle.cpu_baseline_isa()}), "
+                      f"{reps} reps in {el:.1f} s" + (f", scaled x{rows / n:g}" if n != rows else ""),
             "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None
@@ -1119,7 +1124,7 @@ def main() -> int:
         print("# bench: cpu baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, H, args, what=f" x {L} tokens")
         result["cpu_baseline_1thread"] = cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, H, args, threads=1,
-                                                      rows=H, seconds=args.cpu_seconds / 2, what=f" x {L} tokens")
+                                                      seconds=args.cpu_seconds / 2, what=f" x {L} tokens")
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

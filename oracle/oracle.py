@@ -1,8 +1,9 @@
 """numpy front end of the CPU oracle (oracle/ppk_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker or the timed CPU baseline. The
-product path (pop2-bezier_amd/ppk) never imports it.
+cpu_baseline leg of bench.py, as the checker or (cpu_baseline*, from
+oracle/cpu_baseline.c) the timed CPU baseline. The product path
+(pop2-bezier_amd/ppk) never imports it.
 
 Array conventions match the C-ABI (include/ppk_int8_kv.h):
   codes  uint8 [rows, capacity, d] (two's-complement int8 bytes)
@@ -48,12 +49,35 @@ def lib() -> ctypes.CDLL:
         L.oracle_renyi_sample.argtypes = [P, Z, Z, P, P, ctypes.c_float, ctypes.c_float, Z, ctypes.c_uint32,
                                           ctypes.c_int, P, P, P, P]
         L.oracle_renyi_sample.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+BASELINE_PATH = os.path.join(HERE, "libppk_cpu_baseline.so")
+_baseline = None
+
+
+def baseline_lib() -> ctypes.CDLL:
+    """oracle/libppk_cpu_baseline.so: the Candle CPU path timed by bench.py (oracle/cpu_baseline.c)."""
+    global _baseline
+    if _baseline is None:
+        if not os.path.exists(BASELINE_PATH):
+            raise RuntimeError(f"CPU baseline not built: {BASELINE_PATH} (run python oracle/build.py)")
+        L = ctypes.CDLL(BASELINE_PATH)
+        P = ctypes.c_void_p
+        Z = ctypes.c_size_t
         L.cpu_baseline_float_decode.argtypes = [P, P, P, ctypes.c_int, Z, Z, Z, ctypes.c_float, Z, P]
         L.cpu_baseline_float_decode.restype = ctypes.c_int
         L.cpu_baseline_decode.argtypes = [P, P, P, P, P, P, P, P, Z, Z, Z, Z, ctypes.c_float, Z, P]
         L.cpu_baseline_decode.restype = ctypes.c_int
-        _lib = L
-    return _lib
+        L.cpu_baseline_uses_avx2.argtypes = []
+        L.cpu_baseline_uses_avx2.restype = ctypes.c_int
+        _baseline = L
+    return _baseline
+
+
+def cpu_baseline_isa() -> str:
+    return "AVX2+FMA" if baseline_lib().cpu_baseline_uses_avx2() else "x86-64 (SSE2)"
 
 
 def _c(a: np.ndarray, dtype) -> np.ndarray:
@@ -146,7 +170,7 @@ def attention_splitk_reference(q, k, v, ks, vs, sk, sv, past, heads: int, split:
 
 
 def cpu_baseline(q, k, v, ks, vs, sk, sv, past, heads: int, threads: int, scale: float | None = None) -> np.ndarray:
-    """Candle CPU decode restated op for op (see cpu_baseline_decode); float32 [rows, d]."""
+    """Candle CPU decode restated op for op (oracle/cpu_baseline.c cpu_baseline_decode); float32 [rows, d]."""
     k = _c(k, np.uint8)
     v = _c(v, np.uint8)
     rows, cap, d = k.shape
@@ -159,8 +183,8 @@ def cpu_baseline(q, k, v, ks, vs, sk, sv, past, heads: int, threads: int, scale:
     if scale is None:
         scale = 1.0 / np.sqrt(d)
     out = np.empty((rows, d), np.float32)
-    rc = lib().cpu_baseline_decode(_p(q), _p(k), _p(v), _p(ks), _p(vs), _p(sk), _p(sv), _p(past), rows, heads, cap,
-                                   d, float(scale), int(threads), _p(out))
+    rc = baseline_lib().cpu_baseline_decode(_p(q), _p(k), _p(v), _p(ks), _p(vs), _p(sk), _p(sv), _p(past), rows,
+                                            heads, cap, d, float(scale), int(threads), _p(out))
     if rc != 0:
         raise RuntimeError("cpu_baseline_decode: a worker thread failed to start (ran inline)")
     return out
@@ -225,7 +249,7 @@ def cpu_baseline_float(q, k, v, threads: int, scale: float | None = None) -> np.
     if scale is None:
         scale = 1.0 / np.sqrt(d)
     out = np.empty((rows, d), np.float32)
-    rc = lib().cpu_baseline_float_decode(_p(q), k.ctypes.data, v.ctypes.data, int(kv_bf16), rows, size, d,
+    rc = baseline_lib().cpu_baseline_float_decode(_p(q), k.ctypes.data, v.ctypes.data, int(kv_bf16), rows, size, d,
                                          float(scale), int(threads), _p(out))
     if rc != 0:
         raise RuntimeError("cpu_baseline_float_decode: a worker thread failed to start (ran inline)")

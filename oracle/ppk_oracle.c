@@ -312,114 +312,6 @@ void oracle_attention_splitk_reference(const float* q, const uint8_t* k, const u
   free(sc);
 }
 
-/* ------------------------------------------------------------------------
- * CPU baseline: the reference's Candle CPU decode for an int8 history,
- * op for op (app/src/model/mod.rs:716-720, batch.rs:211-222):
- *   1. dequantize history K and V to dense f32 tensors (int8_kv_ops.rs:33-35)
- *      and concatenate the current token (cache.rs query_int8_prefill :133-141)
- *   2. scores = q . K^T                 (gemm, cpu_backend/mod.rs:1380-1450)
- *   3. scores = scores * (1/sqrt(d))    (affine, cpu_backend/mod.rs:311-317)
- *   4. softmax_last_dim: max, exp(x - max), sum, divide (candle-nn)
- *   5. out = probs . V                  (gemm)
- * in f32, parallel over (b, h) rows like Candle's Rayon pool
- * (vendor/candle-core/src/utils.rs:327-346). The timed baseline of bench.py.
- * ------------------------------------------------------------------------ */
-typedef struct {
-  const float* q;
-  const uint8_t *k, *v;
-  const float *ks, *vs, *sk, *sv;
-  const uint32_t* past;
-  size_t rows, heads, capacity, d;
-  float scale;
-  float* out;
-  size_t row_begin, row_end;
-} BaselineJob;
-
-static void* baseline_worker(void* arg) {
-  const BaselineJob* j = (const BaselineJob*)arg;
-  const size_t d = j->d;
-  float* kd = NULL;
-  float* vd = NULL;
-  float* sc = NULL;
-  size_t have = 0;
-  for (size_t r = j->row_begin; r < j->row_end; ++r) {
-    const uint32_t p = j->past[r / j->heads];
-    float* o = j->out + r * d;
-    if (p > j->capacity) {
-      for (size_t i = 0; i < d; ++i) o[i] = NAN;
-      continue;
-    }
-    const size_t n = (size_t)p + 1;
-    if (have < n) {
-      have = n;
-      kd = (float*)realloc(kd, n * d * sizeof(float));
-      vd = (float*)realloc(vd, n * d * sizeof(float));
-      sc = (float*)realloc(sc, n * sizeof(float));
-    }
-    /* 1. dequantize + concatenate */
-    oracle_dequantize(j->k + r * j->capacity * d, j->ks + r * j->capacity, p, d, 0, kd);
-    oracle_dequantize(j->v + r * j->capacity * d, j->vs + r * j->capacity, p, d, 0, vd);
-    memcpy(kd + (size_t)p * d, j->sk + r * d, d * sizeof(float));
-    memcpy(vd + (size_t)p * d, j->sv + r * d, d * sizeof(float));
-    /* 2. q . K^T */
-    const float* qr = j->q + r * d;
-    for (size_t t = 0; t < n; ++t) {
-      float acc = 0.0f;
-      for (size_t i = 0; i < d; ++i) acc += qr[i] * kd[t * d + i];
-      sc[t] = acc;
-    }
-    /* 3. affine */
-    for (size_t t = 0; t < n; ++t) sc[t] = sc[t] * j->scale;
-    /* 4. softmax_last_dim */
-    float mx = -INFINITY;
-    for (size_t t = 0; t < n; ++t) mx = fmaxf(mx, sc[t]);
-    float z = 0.0f;
-    for (size_t t = 0; t < n; ++t) {
-      sc[t] = expf(sc[t] - mx);
-      z += sc[t];
-    }
-    for (size_t t = 0; t < n; ++t) sc[t] /= z;
-    /* 5. probs . V */
-    for (size_t i = 0; i < d; ++i) o[i] = 0.0f;
-    for (size_t t = 0; t < n; ++t)
-      for (size_t i = 0; i < d; ++i) o[i] += sc[t] * vd[t * d + i];
-  }
-  free(kd);
-  free(vd);
-  free(sc);
-  return NULL;
-}
-
-/* Runs the baseline over rows [0, rows) with `threads` POSIX threads. */
-int cpu_baseline_decode(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
-                        const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
-                        size_t capacity, size_t d, float scale, size_t threads, float* out) {
-  if (threads < 1) threads = 1;
-  if (threads > rows) threads = rows;
-  pthread_t* tid = (pthread_t*)malloc(threads * sizeof(pthread_t));
-  BaselineJob* jobs = (BaselineJob*)malloc(threads * sizeof(BaselineJob));
-  for (size_t t = 0; t < threads; ++t) {
-    BaselineJob jb = {q, k, v, ks, vs, sk, sv, past, rows, heads, capacity, d, scale, out,
-                      rows * t / threads, rows * (t + 1) / threads};
-    jobs[t] = jb;
-  }
-  int rc = 0;
-  char* started = (char*)calloc(threads, 1);
-  for (size_t t = 1; t < threads; ++t) {
-    if (pthread_create(&tid[t], NULL, baseline_worker, &jobs[t]) == 0) started[t] = 1;
-    else rc = -1;
-  }
-  baseline_worker(&jobs[0]);
-  for (size_t t = 1; t < threads; ++t) {
-    if (started[t]) pthread_join(tid[t], NULL);
-    else baseline_worker(&jobs[t]); /* run a job whose thread failed to start inline */
-  }
-  free(started);
-  free(tid);
-  free(jobs);
-  return rc;
-}
-
 /*
  * Float-KV decode attention, the semantics of fused_attention::decode_attention
  * (app/src/model/fused_attention.rs:8-30) as computed by pp_attention_part and
@@ -585,92 +477,4 @@ int oracle_renyi_sample(const float* raw, size_t physical_rows, size_t choices, 
   free(logits);
   free(order);
   return 0;
-}
-
-/* ------------------------------------------------------------------------
- * CPU baseline of the float-KV path: Candle's ordinary attention on the CPU
- * for a bf16 / f32 store (app/src/model/batch.rs:211-222, mod.rs:716-721),
- * op for op in f32: keys / values .to_dtype(F32), scores = q . K^T,
- * scores * (1/sqrt(d)), softmax_last_dim, probs . V; parallel over rows.
- * Every row attends all `size` tokens. The timed baseline of bench.py --kv.
- * ------------------------------------------------------------------------ */
-typedef struct {
-  const float* q;
-  const void *k, *v;
-  int kv_bf16;
-  size_t size, d;
-  float scale;
-  float* out;
-  size_t row_begin, row_end;
-} FloatBaselineJob;
-
-static float widen(const void* base, int bf16, size_t i) {
-  if (!bf16) return ((const float*)base)[i];
-  const uint32_t bits = (uint32_t)((const uint16_t*)base)[i] << 16;
-  float x;
-  memcpy(&x, &bits, 4);
-  return x;
-}
-
-static void* float_baseline_worker(void* arg) {
-  const FloatBaselineJob* j = (const FloatBaselineJob*)arg;
-  const size_t n = j->size, d = j->d;
-  float* kd = (float*)malloc(n * d * sizeof(float));
-  float* vd = (float*)malloc(n * d * sizeof(float));
-  float* sc = (float*)malloc((n ? n : 1) * sizeof(float));
-  for (size_t r = j->row_begin; r < j->row_end; ++r) {
-    for (size_t e = 0; e < n * d; ++e) {
-      kd[e] = widen(j->k, j->kv_bf16, r * n * d + e);
-      vd[e] = widen(j->v, j->kv_bf16, r * n * d + e);
-    }
-    const float* qr = j->q + r * d;
-    for (size_t t = 0; t < n; ++t) {
-      float acc = 0.0f;
-      for (size_t i = 0; i < d; ++i) acc += qr[i] * kd[t * d + i];
-      sc[t] = acc * j->scale;
-    }
-    float mx = -INFINITY;
-    for (size_t t = 0; t < n; ++t) mx = fmaxf(mx, sc[t]);
-    float z = 0.0f;
-    for (size_t t = 0; t < n; ++t) {
-      sc[t] = expf(sc[t] - mx);
-      z += sc[t];
-    }
-    for (size_t t = 0; t < n; ++t) sc[t] /= z;
-    float* o = j->out + r * d;
-    for (size_t i = 0; i < d; ++i) o[i] = 0.0f;
-    for (size_t t = 0; t < n; ++t)
-      for (size_t i = 0; i < d; ++i) o[i] += sc[t] * vd[t * d + i];
-  }
-  free(kd);
-  free(vd);
-  free(sc);
-  return NULL;
-}
-
-int cpu_baseline_float_decode(const float* q, const void* k, const void* v, int kv_bf16, size_t rows, size_t size,
-                              size_t d, float scale, size_t threads, float* out) {
-  if (threads < 1) threads = 1;
-  if (threads > rows) threads = rows;
-  pthread_t* tid = (pthread_t*)malloc(threads * sizeof(pthread_t));
-  FloatBaselineJob* jobs = (FloatBaselineJob*)malloc(threads * sizeof(FloatBaselineJob));
-  for (size_t t = 0; t < threads; ++t) {
-    FloatBaselineJob jb = {q, k, v, kv_bf16, size, d, scale, out, rows * t / threads, rows * (t + 1) / threads};
-    jobs[t] = jb;
-  }
-  int rc = 0;
-  char* started = (char*)calloc(threads, 1);
-  for (size_t t = 1; t < threads; ++t) {
-    if (pthread_create(&tid[t], NULL, float_baseline_worker, &jobs[t]) == 0) started[t] = 1;
-    else rc = -1;
-  }
-  float_baseline_worker(&jobs[0]);
-  for (size_t t = 1; t < threads; ++t) {
-    if (started[t]) pthread_join(tid[t], NULL);
-    else float_baseline_worker(&jobs[t]);
-  }
-  free(started);
-  free(tid);
-  free(jobs);
-  return rc;
 }
