@@ -346,9 +346,11 @@ PPK_API int32_t ppk_renyi_sample(ppk_context* ctx, void* stream, const PpkRenyiS
    (a first write, growth, copy-on-write, a new batch arena) refuse to run
    under HIP graph capture. Arenas and plan vectors come from a memory pool
    owned by the context (not the runtime's default pool); the storage of
-   released caches is kept by the context (up to 32 GiB) for the next arena
-   of the same size (the reusing stream first waits for an event recorded
-   on the stream that last used it), and returned at ppk_context_release. */
+   released caches is kept by the context (up to 32 GiB, or an eighth of the
+   device's memory if less; the oldest goes first) for the next arena of the
+   same size (the reusing stream first waits for an event recorded on the
+   stream that last used it), handed back when an allocation would otherwise
+   run out of device memory, and returned at ppk_context_release. */
 enum { PPK_KV_INT8 = 0, PPK_KV_BF16 = 1, PPK_KV_F16 = 2, PPK_KV_F32 = 3 };
 
 typedef struct ppk_kv_cache ppk_kv_cache;
@@ -444,10 +446,11 @@ PPK_API int32_t ppk_kv_cache_view(const ppk_kv_cache* cache, PpkKvView* out);
 PPK_API int32_t ppk_kv_query(ppk_context* ctx, void* stream, ppk_kv_cache* cache, uint32_t past,
                              const PpkKvWrite* write, PpkKvView* out);
 /* BatchWritePlan::new: the write offsets of one decode round as a device
-   vector (uploaded on stream), shared by every layer's ppk_kv_query_batch.
-   Release returns the vector to the context, which hands it to the next plan
-   created on the same stream (stream order keeps the new upload behind the
-   old plan's work); plans are released before their context. */
+   vector (uploaded on stream), shared by every layer's ppk_kv_query_batch,
+   which must run on the same stream (status 1 otherwise). Release returns
+   the vector to the context, which hands it to the next plan created on the
+   same stream (stream order keeps the new upload behind the old plan's work);
+   plans are released before their context. */
 PPK_API int32_t ppk_write_plan_create(ppk_context* ctx, void* stream, const uint32_t* past_lens, uint32_t batch,
                                       uint32_t heads, uint32_t head_dim, ppk_write_plan** out);
 PPK_API int32_t ppk_write_plan_release(ppk_write_plan* plan);

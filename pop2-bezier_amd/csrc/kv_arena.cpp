@@ -86,8 +86,19 @@ struct Arena {
     ppk::DeviceGuard guard(ctx->device);
     {
       std::lock_guard<std::mutex> lock(ctx->block_mutex);
+      // Room for this block: the oldest kept blocks go first (sizes that no
+      // later arena asked for age out), each once its last use has finished.
+      auto& cache = ctx->block_cache;
+      while (!cache.empty() && bytes <= ctx->block_cache_limit &&
+             ctx->block_cache_bytes + bytes > ctx->block_cache_limit) {
+        (void)hipEventSynchronize(cache.front().released);
+        (void)hipFree(cache.front().ptr);
+        ctx->spare_events.push_back(cache.front().released);
+        ctx->block_cache_bytes -= cache.front().bytes;
+        cache.erase(cache.begin());
+      }
       hipEvent_t ev = nullptr;
-      if (ctx->block_cache_bytes + bytes <= ppk_context::kBlockCacheBytes) {
+      if (ctx->block_cache_bytes + bytes <= ctx->block_cache_limit) {
         if (!ctx->spare_events.empty()) {
           ev = ctx->spare_events.back();
           ctx->spare_events.pop_back();
@@ -148,7 +159,7 @@ std::shared_ptr<Arena> make_arena(ppk_context* ctx, hipStream_t stream, const Pp
       }
   }
   if (!a->base) {
-    const hipError_t st = hipMallocFromPoolAsync(&a->base, a->bytes, ctx->mem_pool, stream);
+    const hipError_t st = ppk::kv::pool_alloc(ctx, &a->base, a->bytes, stream);
     if (st != hipSuccess) {
       a->base = nullptr;
       throw PreconditionError(std::string("KV arena allocation of ") + std::to_string(a->bytes) +
@@ -212,8 +223,7 @@ struct SourceSnapshot {
   SourceSnapshot(const void* k_src, const void* v_src, size_t n, const Arena& dst, hipStream_t s)
       : k(k_src), v(v_src), stream(s) {
     if (!dst.contains(k_src, n) && !dst.contains(v_src, n)) return;
-    check_exec(hipMallocFromPoolAsync(&tmp, 2 * align256(n), dst.ctx->mem_pool, s),
-               "hipMallocFromPoolAsync (aliased source)");
+    check_exec(ppk::kv::pool_alloc(dst.ctx, &tmp, 2 * align256(n), s), "hipMallocFromPoolAsync (aliased source)");
     uint8_t* t = static_cast<uint8_t*>(tmp);
     check_exec(hipMemcpyAsync(t, k_src, n, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (aliased K)");
     check_exec(hipMemcpyAsync(t + align256(n), v_src, n, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (aliased V)");
@@ -287,23 +297,69 @@ struct ppk_write_plan {
   uint32_t* dev = nullptr;
   size_t bytes = 0;
   hipStream_t stream = nullptr;
+  hipEvent_t released = nullptr;  // the vector's event, carried from buffer to buffer
   // The device vector goes back to the context's pool (up to 8 kept) for the
-  // next plan on the same stream; beyond that it is freed in stream order.
+  // next plan on the same stream, with an event recorded here that the next
+  // plan's stream waits for; beyond that it is freed in stream order.
   ~ppk_write_plan() {
     if (!dev) return;
-    {
+    ppk::DeviceGuard guard(ctx->device);
+    if (!released && hipEventCreateWithFlags(&released, hipEventDisableTiming) != hipSuccess) released = nullptr;
+    if (released && hipEventRecord(released, stream) == hipSuccess) {
       std::lock_guard<std::mutex> lock(ctx->plan_mutex);
       if (ctx->plan_pool.size() < 8) {
-        ctx->plan_pool.push_back({dev, bytes, stream});
+        ctx->plan_pool.push_back({dev, bytes, stream, released});
         return;
       }
     }
-    ppk::DeviceGuard guard(ctx->device);
+    if (released) (void)hipEventDestroy(released);
     (void)hipFreeAsync(dev, stream);
   }
 };
 
 namespace ppk::kv {
+
+uint64_t drain_blocks(ppk_context* ctx) {
+  DeviceGuard guard(ctx->device);
+  std::vector<ppk_context::CachedBlock> blocks;
+  {
+    std::lock_guard<std::mutex> lock(ctx->block_mutex);
+    blocks.swap(ctx->block_cache);
+    ctx->block_cache_bytes = 0;
+  }
+  uint64_t freed = 0;
+  for (auto& b : blocks) {
+    (void)hipEventSynchronize(b.released);  // the block's last use has finished
+    (void)hipFree(b.ptr);
+    freed += b.bytes;
+    std::lock_guard<std::mutex> lock(ctx->block_mutex);
+    ctx->spare_events.push_back(b.released);
+  }
+  if (ctx->mem_pool) (void)hipMemPoolTrimTo(ctx->mem_pool, 0);
+  return freed;
+}
+
+hipError_t pool_alloc(ppk_context* ctx, void** ptr, size_t bytes, hipStream_t stream) {
+  hipError_t st = hipMallocFromPoolAsync(ptr, bytes, ctx->mem_pool, stream);
+  if (st == hipSuccess) return st;
+  // The failure is reported through this library's status; leave no HIP
+  // error behind for the caller's next launch check to pick up.
+  (void)hipGetLastError();
+  *ptr = nullptr;
+  bool kept = false;
+  {
+    std::lock_guard<std::mutex> lock(ctx->block_mutex);
+    kept = !ctx->block_cache.empty();
+  }
+  if (st != hipErrorOutOfMemory || !kept) return st;
+  drain_blocks(ctx);
+  st = hipMallocFromPoolAsync(ptr, bytes, ctx->mem_pool, stream);
+  if (st != hipSuccess) {
+    (void)hipGetLastError();
+    *ptr = nullptr;
+  }
+  return st;
+}
 
 ppk_kv_cache* create(ppk_context* ctx, const PpkKvConfig& in) {
   require(ctx != nullptr, "KV cache needs a context");
@@ -490,16 +546,18 @@ ppk_write_plan* plan_create(ppk_context* ctx, hipStream_t stream, const uint32_t
     std::lock_guard<std::mutex> lock(ctx->plan_mutex);
     auto& pool = ctx->plan_pool;
     for (size_t i = 0; i < pool.size(); ++i)
-      if (pool[i].stream == stream && pool[i].bytes >= bytes) {
+      if (pool[i].stream == stream && pool[i].bytes >= bytes &&
+          hipStreamWaitEvent(stream, pool[i].released, 0) == hipSuccess) {
         plan->dev = pool[i].dev;
         plan->bytes = pool[i].bytes;
+        plan->released = pool[i].released;
         pool.erase(pool.begin() + std::ptrdiff_t(i));
         break;
       }
   }
   if (!plan->dev) {
     void* dev = nullptr;
-    const hipError_t st = hipMallocFromPoolAsync(&dev, bytes, ctx->mem_pool, stream);
+    const hipError_t st = pool_alloc(ctx, &dev, bytes, stream);
     if (st != hipSuccess)
       throw PreconditionError(std::string("write plan allocation failed: ") + hipGetErrorString(st));
     plan->dev = static_cast<uint32_t*>(dev);
@@ -566,6 +624,10 @@ void query_batch(ppk_context* ctx, hipStream_t stream, ppk_kv_cache* const* cach
   if (out) require(out->struct_size >= sizeof(PpkKvView), "PpkKvView.struct_size too small");
   if (plan) {
     require(plan->ctx == ctx, "write plan device differs from the current KV device");
+    // The plan's vector was uploaded on its own stream and is recycled in that
+    // stream's order: another stream could read it before the upload lands, or
+    // while a later plan overwrites it.
+    require(plan->stream == stream, "write plan was created on another stream");
     require(plan->offsets.size() == batch && std::equal(plan->offsets.begin(), plan->offsets.end(), past_lens) &&
                 plan->heads == cfg.heads && plan->head_dim == cfg.head_dim,
             "write plan key does not match the current row offsets and head shape");

@@ -789,6 +789,9 @@ int32_t ppk_context_create(int32_t device, const char* code_object_path, ppk_con
       ctx->scratch = nullptr;
       ctx->scratch_error = e.what();
     }
+    size_t total_mem = 0;
+    if (hipDeviceTotalMem(&total_mem, device) == hipSuccess && total_mem > 0)
+      ctx->block_cache_limit = std::min(ppk_context::kBlockCacheBytes, total_mem / 8);
     hipMemPoolProps props{};
     props.allocType = hipMemAllocationTypePinned;
     props.handleTypes = hipMemHandleTypeNone;
@@ -809,22 +812,7 @@ int32_t ppk_context_trim(ppk_context* ctx, uint64_t* released_bytes) {
   if (released_bytes) *released_bytes = 0;
   return call([&] {
     ppk::require(ctx != nullptr, "ppk_context_trim: null context");
-    ppk::DeviceGuard guard(ctx->device);
-    std::vector<ppk_context::CachedBlock> blocks;
-    {
-      std::lock_guard<std::mutex> lock(ctx->block_mutex);
-      blocks.swap(ctx->block_cache);
-      ctx->block_cache_bytes = 0;
-    }
-    uint64_t freed = 0;
-    for (auto& b : blocks) {
-      (void)hipEventSynchronize(b.released);  // the block's last use has finished
-      (void)hipFree(b.ptr);
-      freed += b.bytes;
-      std::lock_guard<std::mutex> lock(ctx->block_mutex);
-      ctx->spare_events.push_back(b.released);
-    }
-    if (ctx->mem_pool) (void)hipMemPoolTrimTo(ctx->mem_pool, 0);
+    const uint64_t freed = ppk::kv::drain_blocks(ctx);
     if (released_bytes) *released_bytes = freed;
   });
 }
@@ -844,7 +832,10 @@ int32_t ppk_context_release(ppk_context* ctx) {
       (void)hipEventDestroy(ev.stop);
     }
     // Recycled write-plan vectors: a synchronous free (their streams may be gone).
-    for (auto& b : ctx->plan_pool) (void)hipFree(b.dev);
+    for (auto& b : ctx->plan_pool) {
+      (void)hipFree(b.dev);
+      if (b.released) (void)hipEventDestroy(b.released);
+    }
     for (auto& b : ctx->block_cache) {  // released arenas kept for reuse
       (void)hipEventSynchronize(b.released);
       (void)hipEventDestroy(b.released);

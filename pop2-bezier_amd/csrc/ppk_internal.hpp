@@ -85,11 +85,14 @@ struct ppk_context {
 
   // Device vectors of released write plans, recycled by the next plan created
   // on the same stream (stream order puts its upload after the old plan's
-  // readers); an allocation per plan costs ~9 us of host time.
+  // readers; the event recorded at release also orders it when a new stream
+  // reuses the handle of a destroyed one); an allocation per plan costs ~9 us
+  // of host time.
   struct PlanBuffer {
     uint32_t* dev = nullptr;
     size_t bytes = 0;
     hipStream_t stream = nullptr;
+    hipEvent_t released = nullptr;  // recorded on `stream` when the plan was released
   };
   std::mutex plan_mutex;
   std::vector<PlanBuffer> plan_pool;
@@ -106,16 +109,19 @@ struct ppk_context {
   // stream synchronisation whatever its release threshold, and a 24-layer
   // join of B = 32 that took its batch arenas from the runtime spent
   // 160-210 ms allocating; with released blocks kept here it takes 2-3 ms
-  // (1.8 ms of it the copy kernel). Bounded by kBlockCacheBytes; freed at
-  // release.
+  // (1.8 ms of it the copy kernel). Bounded by block_cache_limit (32 GiB, or
+  // an eighth of the device's memory if that is less): a release that would
+  // pass it first frees the oldest idle blocks. An allocation that fails while
+  // blocks are kept frees them all and tries once more. Freed at release.
   struct CachedBlock {
     void* ptr = nullptr;
     size_t bytes = 0;
     hipEvent_t released = nullptr;  // recorded after the block's last use
   };
   static constexpr size_t kBlockCacheBytes = size_t(32) << 30;
+  size_t block_cache_limit = kBlockCacheBytes;
   std::mutex block_mutex;
-  std::vector<CachedBlock> block_cache;
+  std::vector<CachedBlock> block_cache;  // oldest first
   size_t block_cache_bytes = 0;
   std::vector<hipEvent_t> spare_events;  // events of reused blocks, recorded again by later releases
 
@@ -230,6 +236,13 @@ void query(ppk_context* ctx, hipStream_t stream, ppk_kv_cache& c, uint32_t past,
            PpkKvView* out);
 ppk_write_plan* plan_create(ppk_context* ctx, hipStream_t stream, const uint32_t* past_lens, uint32_t batch,
                             uint32_t heads, uint32_t head_dim);
+// Frees every kept arena block once the work that last used it has finished,
+// then returns the pool's unused memory to the device; the bytes freed.
+uint64_t drain_blocks(ppk_context* ctx);
+// hipMallocFromPoolAsync from the context's pool; when it runs out of memory
+// while released blocks are kept (reused only at an equal size), drains them
+// and tries once more.
+hipError_t pool_alloc(ppk_context* ctx, void** ptr, size_t bytes, hipStream_t stream);
 void query_batch(ppk_context* ctx, hipStream_t stream, ppk_kv_cache* const* caches, uint32_t batch,
                  const uint32_t* past_lens, const PpkKvWrite& w, const ppk_write_plan* plan, PpkKvView* out);
 ppk_kv_cache* clone(const ppk_kv_cache& c);

@@ -356,6 +356,53 @@ def test_wrong_shared_write_plan_is_rejected_before_history_or_scratch_is_touche
                 assert len(caches[row]) == offsets[row] and caches[row].info().storage_id == owners[row]
 
 
+def _read_u32(ptr, n):
+    out = torch.empty(n, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ppk.kv_arena._hip_runtime().hipMemcpy2DAsync(out.data_ptr(), 4 * n, ptr, 4 * n, 4 * n, 1, 3, None)
+    torch.cuda.synchronize()
+    return out.tolist()
+
+
+def test_write_plan_is_refused_on_another_stream_and_recycled_on_its_own(device):
+    """A plan's device vector is uploaded and recycled in its creation stream's order, so a batch write on
+    another stream is refused (status 1, nothing touched); released plans hand their vectors to the next
+    plans on the same stream, which wait for the release event before uploading."""
+    offsets = [2, 0, 1]
+    caches = [LayerCache(F32, 2, 3) for _ in range(3)]
+    for row, c in enumerate(caches):
+        if offsets[row]:
+            c.query(data(2, offsets[row], 3, row * 10.0), data(2, offsets[row], 3, row * 10.0 + 5), 0, True)
+    cur = batch_data(3, 2, 3, 300.0)
+    plan = WritePlan(offsets, 2, 3)
+    owners = [c.info().storage_id for c in caches]
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        expect_status(_abi.PPK_PRECONDITION, lambda: LayerCache.query_batch(caches, cur, cur, offsets, True, plan))
+    torch.cuda.current_stream(device).wait_stream(side)
+    assert [len(c) for c in caches] == offsets and [c.info().storage_id for c in caches] == owners
+    # On its own stream the plan works; then a chain of plans, each released before the next is created,
+    # recycles vectors and every upload lands.
+    view = LayerCache.query_batch(caches, cur, cur, offsets, False, plan)
+    assert _read_u32(view.past, 3) == offsets
+    del plan
+    for step in range(12):
+        lens = [offsets[row] + (step + row) % 4 for row in range(3)]
+        plan = WritePlan(lens, 2, 3)
+        for row, c in enumerate(caches):
+            if len(c) != lens[row]:
+                c.truncate_committed(min(len(c), lens[row]))
+                extra = lens[row] - len(c)
+                if extra:
+                    c.query(data(2, extra, 3, 40.0 + row), data(2, extra, 3, 70.0 + row), len(c), True)
+        view = LayerCache.query_batch(caches, cur, cur, lens, False, plan)
+        assert _read_u32(view.past, 3) == lens and _read_u32(view.lengths, 3) == [n + 1 for n in lens], step
+        for row in range(3):
+            assert torch.equal(rows_of(view, row, 2, view.length)[:, lens[row]], cur[row].reshape(2, 3))
+        del plan
+
+
 def test_committed_offsets_require_a_fresh_shared_plan(device):
     caches = [LayerCache(F32, 1, 2) for _ in range(2)]
     for row, c in enumerate(caches):
@@ -635,6 +682,36 @@ def test_context_trim_returns_kept_storage_and_caches_stay_valid(device):
     fresh = LayerCache(F32, 2, 16)
     fresh.query(data(2, 3, 16, 9.0), data(2, 3, 16, 9.0), 0, True)
     assert torch.equal(fresh.key(), data(2, 3, 16, 9.0))
+
+
+def test_allocation_that_runs_out_of_memory_drains_the_kept_storage(device):
+    """Released caches are kept for reuse at an equal size only. An arena of another size that does not fit
+    beside them (device memory otherwise full) frees them and succeeds on the second try, instead of failing
+    while that memory sits idle."""
+    gib = 1 << 30
+    ppk.kv_arena.trim(device)
+    torch.cuda.empty_cache()
+    tok = torch.arange(16 * 256, dtype=F32, device=device).reshape(16, 1, 256)
+    # Four released caches of 2 GiB each (16 rows x 65536 slots x 256 f32, K and V).
+    kept = [LayerCache(F32, 16, 256, max_context=65536, min_capacity=65536) for _ in range(4)]
+    for c in kept:
+        c.query(tok, tok, 0, True)
+    assert kept[0].info().reserved_bytes >= 2 * gib
+    del kept, c
+    torch.cuda.synchronize()
+    free, _ = torch.cuda.mem_get_info(device)
+    filler = torch.empty(free - 2 * gib, dtype=torch.uint8, device=device)  # leaves 2 GiB
+    try:
+        tok24 = torch.arange(24 * 256, dtype=F32, device=device).reshape(24, 1, 256)
+        big = LayerCache(F32, 24, 256, max_context=65536, min_capacity=65536)
+        big.query(tok24, tok24, 0, True)  # 3 GiB: fits only once the 8 GiB kept are freed
+        assert big.info().reserved_bytes >= 3 * gib
+        assert torch.equal(big.key(), tok24)
+        del big
+    finally:
+        del filler
+        torch.cuda.empty_cache()
+    assert ppk.kv_arena.trim(device) < 4 * gib, "the kept storage was not handed back"
 
 
 def test_truncate_is_metadata_only_and_append_preserves_longer_snapshots(device):
