@@ -665,11 +665,16 @@ __device__ __forceinline__ float current_score(const ppk::DecodeArgs& a, const f
 // Streams this wave's n tokens (from `begin`) of one row: phase K scores,
 // phase V accumulation. Two batches (A, B) ping-pong so the next batch's loads
 // are always in flight while the current one is consumed; addresses past the
-// end clamp to the last token and those tokens are masked out.
+// end clamp to the last token and those tokens are masked out. With `pre`
+// (nspec beyond the short window) the caller has already issued the first
+// two K batches into ra/sa and rb/sb, clamped to nspec instead of n (tokens
+// at or past n are masked by their scores, so the wider clamp only reads
+// other slots of the same arena row).
 template <int D, bool BF16H>
 __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_t row, uint32_t begin, uint32_t n,
                                                uint32_t nspec, const float (&qr)[16], float* s_lds, int lane,
-                                               WavePartial& out) {
+                                               WavePartial& out, bool pre, u4 (&ra)[4], u4 (&rb)[4], float& sa,
+                                               float& sb) {
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
   constexpr int U = 4;  // tiles per batch
@@ -735,8 +740,6 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   }
   if (n == 0) return;  // uniform per wave
   const uint32_t ntiles = (n + TPL - 1) / TPL;
-  u4 ra[U], rb[U];
-  float sa, sb;
   float mloc = -INFINITY;
   float m, z = 0.f;
   QInt qi{};
@@ -748,10 +751,10 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
     const bool two = ntiles > U;  // uniform per wave
     u4 va[U], vb2[U];
     float vsa, vsb2;
-    load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
+    if (!pre) load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
     load_batch<D, U>(vb, vsb, 0, n, j, lane, va, vsa);
     if (two) {
-      load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
+      if (!pre) load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
       load_batch<D, U>(vb, vsb, U, n, j, lane, vb2, vsb2);
     }
     if constexpr (!BF16H) {
@@ -771,8 +774,10 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
     // is quantised, so the q load and its reductions overlap the first memory
     // round trip. Batch A of the last phase-K iteration already fetches phase
     // V's first batch, so the V stream starts without a full memory latency.
-    load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
-    load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
+    if (!pre) {
+      load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
+      load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
+    }
     if constexpr (!BF16H) {
       qi = quantize_query<LPT>(qr);
       sl2 *= qi.unscale;
@@ -824,42 +829,55 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   const uint32_t p = a.past[row / a.heads];
   const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.ngroups) * W * S;
 
-  // Fused commit of the current token (kernel 1 inside this launch). Done
-  // before the stream: deferring it past the stream (its loads issued early)
-  // measured slower at B=32 x 8192 tokens, the commit then adding to the
-  // block's tail instead of overlapping the other waves' ramp-up.
-  if (a.append && group == 0) {
-    const bool kw = wave == 0, vw = wave == (W > 1 ? 1 : 0);
-    if (kw || vw) {
-      if (p >= a.capacity) {
-        if (lane == 0 && a.flags) atomicOr(a.flags, 2u);
-      } else {
-        const size_t slot = size_t(row) * a.capacity + p;
-        if (kw) quantize_row<D>(a.k_new, row, a.new_dtype, a.k + slot * D, a.ks + slot, a.flags, lane);
-        if (vw) quantize_row<D>(a.v_new, row, a.new_dtype, a.v + slot * D, a.vs + slot, a.flags, lane);
-      }
-    }
-  }
-
+  // Everything the wave reads before its stream is requested first, in one
+  // round trip: q, the current token (wave 0 of a block that covers its
+  // row), the new K/V row of the fused commit (waves 0 and 1 of group 0) and
+  // the stream's first two K batches, clamped to the arena (not to the
+  // row's length, which arrives with them). The commit and the current
+  // token's score then run while the K batches are in flight. Measured at
+  // B=32 x 8192 tokens against committing first and loading the stream after
+  // the length: D=64 94.8 -> 91.6 us, D=128 165.5 -> 165.0 us, bitwise the
+  // same output. The slot the commit writes is past every wave's length, so
+  // the speculative reads of it are masked.
   float qr[16];
   load_vec<16>(a.q, size_t(row) * D + size_t(c) * 16, a.q_dtype, qr);
-  // Wave 0 of a block that covers its whole row also folds in the current
-  // token (from the sk/sv scratch): it is scored here, with loads issued
-  // beside q's, so that no memory round trip is left after the stream.
   const bool final_out = a.ngroups == 1;
   float s_cur = -INFINITY;
-  float sv[EPL];
+  float sv[EPL], kv[16];
   if (final_out && wave == 0) {
-    float kv[16];
     load_vec<16>(a.sk, size_t(row) * D + size_t(c) * 16, a.scratch_dtype, kv);
     load_vec<EPL>(a.sv, size_t(row) * D + size_t(lane) * EPL, a.scratch_dtype, sv);
-    s_cur = current_score<D>(a, kv, qr);
   }
+  const bool kw = a.append && group == 0 && wave == 0;
+  const bool vw = a.append && group == 0 && wave == (W > 1 ? 1 : 0);
+  float kx[EPL], vx[EPL];
+  if (kw) load_vec<EPL>(a.k_new, size_t(row) * D + size_t(lane) * EPL, a.new_dtype, kx);
+  if (vw) load_vec<EPL>(a.v_new, size_t(row) * D + size_t(lane) * EPL, a.new_dtype, vx);
   const uint32_t begin = (group * W + wave) * S;
+  const uint32_t nspec = begin < a.capacity ? min(S, a.capacity - begin) : 0u;
+  constexpr int TPL = ppk::kWave / LPT;
+  const bool pre = nspec > uint32_t(8 * TPL);  // the wave takes a streamed (not short-window) path
+  u4 ra[4], rb[4];
+  float sa = 0.f, sb = 0.f;
+  if (pre) {
+    const size_t tok0 = size_t(row) * a.capacity + begin;
+    const int j = lane / LPT;
+    load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, 0, nspec, j, lane, ra, sa);
+    load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, 4, nspec, j, lane, rb, sb);
+  }
+  if (kw || vw) {
+    if (p >= a.capacity) {
+      if (lane == 0 && a.flags) atomicOr(a.flags, 2u);
+    } else {
+      const size_t slot = size_t(row) * a.capacity + p;
+      if (kw) quantize_values<D>(kx, a.k + slot * D, a.ks + slot, a.flags, lane);
+      if (vw) quantize_values<D>(vx, a.v + slot * D, a.vs + slot, a.flags, lane);
+    }
+  }
+  if (final_out && wave == 0) s_cur = current_score<D>(a, kv, qr);
   const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
   WavePartial part;
-  const uint32_t nspec = begin < a.capacity ? min(S, a.capacity - begin) : 0u;
-  wave_attention<D, BF16H>(a, row, begin, n, nspec, qr, lds + size_t(wave) * S, lane, part);
+  wave_attention<D, BF16H>(a, row, begin, n, nspec, qr, lds + size_t(wave) * S, lane, part, pre, ra, rb, sa, sb);
 
   // Combine the block's waves through LDS (the staging area is reused).
   // Record of wave w at mrg + w * R: m, z, 2 pad floats, y[D] (16-byte aligned).
