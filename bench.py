@@ -594,7 +594,7 @@ def bench_config(args) -> int:
     per_row = ppk.DecodeStep(q[0], kc[0, 0], vc[0, 0], ks[0, 0], vs[0, 0], kn[0], vn[0], past, H,
                              split_tokens=args.split, max_past=L, out=out)
     balanced = host is not None and (split, ngroups) != (per_row.split_tokens, per_row.ngroups)
-    launches = 1 if ngroups == 1 else 2
+    layer_launches = 1 if ngroups == 1 else 2  # decode (+ merge when rows span blocks)
     del per_row
     torch.cuda.synchronize()
 
@@ -675,7 +675,7 @@ def bench_config(args) -> int:
                    "layers": layers, "capacity": cap, "kv": "int8 + f32 scales", "query": cfg["query"],
                    "plan": "balanced work list (host lengths)" if balanced else "per-row blocks",
                    "tokens_per_wave": split, ("units_per_row_max" if balanced else "blocks_per_row"): ngroups,
-                   "launches_per_step": layers * launches},
+                   "launches_per_step": layers * layer_launches},
         "median_us": round(statistics.median(warm_each), 2),
         "cold": {"mean_us": round(cold_mean, 2), "median_us": round(statistics.median(cold_each), 2),
                  "history_copies": copies, "rotated_bytes": copies * hist_bytes * layers,

@@ -5,7 +5,8 @@
  * fused multiply-adds (Candle calls the `gemm` crate 0.19, which picks
  * AVX2/FMA kernels at run time: vendor/candle-core/src/cpu_backend/mod.rs:1380-1450),
  * the elementwise passes vectorised, rows shared out over every host core
- * (Candle's Rayon pool, vendor/candle-core/src/utils.rs:327-346).
+ * by a pool of threads kept between calls (Candle's Rayon pool,
+ * vendor/candle-core/src/utils.rs:327-346).
  *
  * The hot loops are written once and compiled twice, for AVX2 + FMA and for
  * the baseline x86-64 instruction set; the AVX2 form is taken when the CPU
@@ -128,6 +129,74 @@ static int have_avx2(void) {
   return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
 }
 
+/* ---- a persistent worker pool (Rayon keeps its threads between calls) ----
+   run_jobs(fn, jobs, size, n): job 0 and any job beyond the pool's workers
+   run on the calling thread, job i (1 <= i <= workers) on worker i - 1;
+   returns once every job has finished. Workers are created on first need
+   and then wait for the next call. Calls are serialised by the pool. */
+
+#define POOL_MAX 256
+static pthread_mutex_t g_call = PTHREAD_MUTEX_INITIALIZER;  /* one call at a time */
+static pthread_mutex_t g_mu = PTHREAD_MUTEX_INITIALIZER;
+static pthread_cond_t g_go = PTHREAD_COND_INITIALIZER;
+static pthread_cond_t g_done = PTHREAD_COND_INITIALIZER;
+static size_t g_workers = 0;
+static unsigned long g_gen = 0;
+static void* (*g_fn)(void*);
+static char* g_jobs;
+static size_t g_size, g_njobs, g_left;
+
+static void* pool_worker(void* arg) {
+  const size_t id = (size_t)(uintptr_t)arg; /* runs job id + 1 */
+  unsigned long seen = 0;
+  pthread_mutex_lock(&g_mu);
+  for (;;) {
+    while (g_gen == seen) pthread_cond_wait(&g_go, &g_mu);
+    seen = g_gen;
+    if (id + 1 < g_njobs) {
+      void* (*fn)(void*) = g_fn;
+      void* job = g_jobs + (id + 1) * g_size;
+      pthread_mutex_unlock(&g_mu);
+      fn(job);
+      pthread_mutex_lock(&g_mu);
+      if (--g_left == 0) pthread_cond_signal(&g_done);
+    }
+  }
+  return NULL;
+}
+
+/* Returns 0, or -1 if a worker could not be started (its jobs then ran on the calling thread). */
+static int run_jobs(void* (*fn)(void*), void* jobs, size_t size, size_t njobs) {
+  int rc = 0;
+  pthread_mutex_lock(&g_call);
+  pthread_mutex_lock(&g_mu);
+  while (g_workers + 1 < njobs && g_workers < POOL_MAX) {
+    pthread_t t;
+    if (pthread_create(&t, NULL, pool_worker, (void*)(uintptr_t)g_workers) != 0) {
+      rc = -1;
+      break;
+    }
+    pthread_detach(t);
+    ++g_workers;
+  }
+  const size_t pooled = njobs - 1 < g_workers ? njobs - 1 : g_workers; /* jobs 1 .. pooled */
+  g_fn = fn;
+  g_jobs = (char*)jobs;
+  g_size = size;
+  g_njobs = pooled + 1;
+  g_left = pooled;
+  ++g_gen;
+  pthread_cond_broadcast(&g_go);
+  pthread_mutex_unlock(&g_mu);
+  fn(jobs);
+  for (size_t i = pooled + 1; i < njobs; ++i) fn((char*)jobs + i * size);
+  pthread_mutex_lock(&g_mu);
+  while (g_left > 0) pthread_cond_wait(&g_done, &g_mu);
+  pthread_mutex_unlock(&g_mu);
+  pthread_mutex_unlock(&g_call);
+  return rc;
+}
+
 /* ---- int8 history --------------------------------------------------------- */
 
 static void* int8_worker(void* arg) {
@@ -177,35 +246,22 @@ static void* int8_worker(void* arg) {
   return NULL;
 }
 
-/* Runs the baseline over rows [0, rows) with `threads` POSIX threads.
-   Returns 0, or -1 if a worker thread could not start (its rows then ran on
-   the calling thread). */
+/* Runs the baseline over rows [0, rows) on `threads` threads (the caller's
+   and threads - 1 pool workers), a contiguous range of rows each. Returns 0,
+   or -1 if a worker could not start (its rows then ran on the calling thread). */
 int cpu_baseline_decode(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
                         const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
                         size_t capacity, size_t d, float scale, size_t threads, float* out) {
   if (threads < 1) threads = 1;
   if (threads > rows) threads = rows;
   const int avx2 = have_avx2();
-  pthread_t* tid = (pthread_t*)malloc(threads * sizeof(pthread_t));
   Int8Job* jobs = (Int8Job*)malloc(threads * sizeof(Int8Job));
-  char* started = (char*)calloc(threads, 1);
-  int rc = 0;
   for (size_t t = 0; t < threads; ++t) {
     Int8Job jb = {q, k, v, ks, vs, sk, sv, past, heads, capacity, d, scale, out,
                   rows * t / threads, rows * (t + 1) / threads, avx2};
     jobs[t] = jb;
   }
-  for (size_t t = 1; t < threads; ++t) {
-    if (pthread_create(&tid[t], NULL, int8_worker, &jobs[t]) == 0) started[t] = 1;
-    else rc = -1;
-  }
-  int8_worker(&jobs[0]);
-  for (size_t t = 1; t < threads; ++t) {
-    if (started[t]) pthread_join(tid[t], NULL);
-    else int8_worker(&jobs[t]);
-  }
-  free(started);
-  free(tid);
+  const int rc = run_jobs(int8_worker, jobs, sizeof(Int8Job), threads);
   free(jobs);
   return rc;
 }
@@ -249,25 +305,12 @@ int cpu_baseline_float_decode(const float* q, const void* k, const void* v, int 
   if (threads < 1) threads = 1;
   if (threads > rows) threads = rows;
   const int avx2 = have_avx2();
-  pthread_t* tid = (pthread_t*)malloc(threads * sizeof(pthread_t));
   FloatJob* jobs = (FloatJob*)malloc(threads * sizeof(FloatJob));
-  char* started = (char*)calloc(threads, 1);
-  int rc = 0;
   for (size_t t = 0; t < threads; ++t) {
     FloatJob jb = {q, k, v, kv_bf16, size, d, scale, out, rows * t / threads, rows * (t + 1) / threads, avx2};
     jobs[t] = jb;
   }
-  for (size_t t = 1; t < threads; ++t) {
-    if (pthread_create(&tid[t], NULL, float_worker, &jobs[t]) == 0) started[t] = 1;
-    else rc = -1;
-  }
-  float_worker(&jobs[0]);
-  for (size_t t = 1; t < threads; ++t) {
-    if (started[t]) pthread_join(tid[t], NULL);
-    else float_worker(&jobs[t]);
-  }
-  free(started);
-  free(tid);
+  const int rc = run_jobs(float_worker, jobs, sizeof(FloatJob), threads);
   free(jobs);
   return rc;
 }
