@@ -350,6 +350,20 @@ def test_cpu_baseline_matches_oracle():
         np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
 
 
+def test_cpu_baseline_thread_pool_reuse():
+    """The baseline's worker threads persist between calls: calls that ask for more threads than before, fewer,
+    more than there are rows, and one, give the same rows bit for bit (each row is computed by one thread)."""
+    rng = np.random.default_rng(SEED + 8)
+    args = _problem(rng, 8, 2, 200, 64, [0, 199])
+    first = oracle.cpu_baseline(*args, 2, 1)
+    for threads in (5, 2, 16, 3, 40, 1, 8):
+        assert np.array_equal(oracle.cpu_baseline(*args, 2, threads), first), threads
+    k = rng.standard_normal((8, 70, 64)).astype(np.float32)
+    v = rng.standard_normal((8, 70, 64)).astype(np.float32)
+    fgot = [oracle.cpu_baseline_float(args[0], k, v, threads=t) for t in (1, 6, 2, 9)]
+    assert all(np.array_equal(fgot[0], x) for x in fgot[1:])
+
+
 def test_bf16_helpers_match_torch():
     x = np.random.default_rng(SEED).standard_normal(10000).astype(np.float32) * 100
     ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
