@@ -354,8 +354,9 @@ def test_cpu_baseline_thread_pool_reuse():
     """The baseline's worker threads persist between calls: calls that ask for more threads than before, fewer,
     more than there are rows, and one, give the same rows bit for bit (each row is computed by one thread)."""
     rng = np.random.default_rng(SEED + 8)
-    args = _problem(rng, 8, 2, 200, 64, [0, 199])
+    args = _problem(rng, 8, 2, 200, 64, [0, 199, 57, 200])
     first = oracle.cpu_baseline(*args, 2, 1)
+    assert np.isfinite(first).all()
     for threads in (5, 2, 16, 3, 40, 1, 8):
         assert np.array_equal(oracle.cpu_baseline(*args, 2, threads), first), threads
     k = rng.standard_normal((8, 70, 64)).astype(np.float32)
