@@ -122,6 +122,8 @@ def cpu_baseline(q, kc, vc, ks, vs, kn, vn, past, heads, args, *, threads: int |
     sk_h = kn.float().reshape(rows_total, -1)[:n].cpu().numpy()
     sv_h = vn.float().reshape(rows_total, -1)[:n].cpu().numpy()
     past_h = past[: n // heads].cpu().numpy().astype(np.uint32)
+    # Dense host copies made once, outside the timed calls (the history views skip the arena's spare slots).
+    q_h, k_h, v_h, ks_h, vs_h, sk_h, sv_h = (np.ascontiguousarray(x) for x in (q_h, k_h, v_h, ks_h, vs_h, sk_h, sv_h))
     if threads is None:
         threads = _host_cpus()  # every usable core, as Candle's Rayon pool
     reps, el = _time_cpu(lambda: oracle.cpu_baseline(q_h, k_h, v_h, ks_h, vs_h, sk_h, sv_h, past_h, heads, threads),

@@ -161,6 +161,7 @@ def attention_splitk_reference(q, k, v, ks, vs, sk, sv, past, heads: int, split:
     ks = _c(ks, np.float32).reshape(rows, cap)
     vs = _c(vs, np.float32).reshape(rows, cap)
     past = _c(past, np.uint32)
+    assert past.size == rows // heads and rows % heads == 0
     if scale is None:
         scale = 1.0 / np.sqrt(d)
     out = np.empty((rows, d), np.float32)
@@ -180,6 +181,7 @@ def cpu_baseline(q, k, v, ks, vs, sk, sv, past, heads: int, threads: int, scale:
     ks = _c(ks, np.float32).reshape(rows, cap)
     vs = _c(vs, np.float32).reshape(rows, cap)
     past = _c(past, np.uint32)
+    assert past.size == rows // heads and rows % heads == 0
     if scale is None:
         scale = 1.0 / np.sqrt(d)
     out = np.empty((rows, d), np.float32)
