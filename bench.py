@@ -430,6 +430,57 @@ def bench_arena(args) -> int:
     arena_ids = {c.info().arena_id for caches in layers for c in caches}
     append_bytes = 2 * B * H * D * 2 + 2 * B * H * (D + 4)
 
+    # Whole decode rounds, append and attention per layer (bf16 q, the current token bf16): the two-call
+    # path (ppk_kv_query_batch writes the token, ppk_decode_attention reads the view) against the reserving
+    # write and ppk_decode_step on the view (one launch per layer). Argument blocks are built once per
+    # layer; each call refreshes the view's pointers, lengths vector and length bound.
+    q_step = torch.randn((B * H, D), generator=g, device=dev, dtype=torch.bfloat16)
+    out_step = torch.empty((B * H, 1, D), dtype=torch.float32, device=dev)
+    reserve = _abi.PpkKvWrite(struct_size=ctypes.sizeof(_abi.PpkKvWrite), src_dtype=_abi.PPK_BF16, tokens=1,
+                              commit=1, k=None, v=None)
+    steps_ = [_abi.PpkDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkDecodeStepArgs), new_dtype=_abi.PPK_BF16,
+                                     k_new=kv.data_ptr(), v_new=kv.data_ptr(), flags=None) for _ in layers]
+    for st_ in steps_:
+        a = st_.attn
+        a.struct_size, a.q_dtype, a.scratch_dtype, a.out_dtype = ctypes.sizeof(_abi.PpkAttentionArgs), 1, 1, 0
+        a.rows, a.heads, a.head_dim, a.q, a.sk, a.sv, a.out = B * H, H, D, q_step.data_ptr(), kv.data_ptr(), \
+            kv.data_ptr(), out_step.data_ptr()
+    ws_step = torch.empty(1 << 24, dtype=torch.uint8, device=dev)
+
+    def full_round(fused: bool):
+        nonlocal past
+        lens = (ctypes.c_uint32 * B)(*past)
+        plan = ctypes.c_void_p()
+        _abi.check(lib.ppk_write_plan_create(ctx, stream, lens, B, H, D, ctypes.byref(plan)), "plan")
+        for h, st_ in zip(handles, steps_):
+            _abi.check(fn(ctx, stream, h, B, lens, ctypes.byref(reserve if fused else write), plan,
+                          ctypes.byref(view)), "ppk_kv_query_batch")
+            a = st_.attn
+            a.k_codes, a.v_codes, a.k_scales, a.v_scales = view.k, view.v, view.k_scales, view.v_scales
+            a.capacity, a.past, a.max_past = view.capacity, view.past, view.length - 1
+            a.workspace, a.workspace_bytes = ws_step.data_ptr(), ws_step.numel()
+            if fused:
+                _abi.check(lib.ppk_decode_step(ctx, stream, ctypes.byref(st_)), "ppk_decode_step")
+            else:
+                _abi.check(lib.ppk_decode_attention(ctx, stream, ctypes.byref(a)), "ppk_decode_attention")
+        lib.ppk_write_plan_release(plan)
+        past = [p + 1 for p in past]
+
+    full = {"layers": Lyr, "tokens_at_start": past[0]}
+    for fused in (False, True, False, True):
+        for _ in range(10):
+            full_round(fused)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            full_round(fused)
+        e1.record()
+        torch.cuda.synchronize()
+        key = "reserve_then_decode_step" if fused else "write_then_attention"
+        full.setdefault(key, []).append({"us": round(e0.elapsed_time(e1) / args.steps * 1e3, 1),
+                                         "host_us": round((time.perf_counter() - t0) * 1e6 / args.steps, 1)})
+
     # The same prefill and join once more after every cache was released: the
     # context's pool keeps freed arenas mapped, so this join reuses memory
     # instead of mapping new pages (the first join's host time).
@@ -463,6 +514,7 @@ def bench_arena(args) -> int:
                    "arenas_after_join": len(arena_ids)},
         "host_us_per_round": round(host_ms * 1e3, 1),
         "append_kernel_us": round(append_us, 2),
+        "decode_round_with_attention": full,
         "prefill": {"caches": Lyr * B, "tokens": T0, "ms": round(p0.elapsed_time(p1), 3),
                     "append_kernel_us": round(pre_us, 2), "append_bytes": pre_bytes,
                     "append_gbps": round(pre_bytes / (pre_us * 1e-6) / 1e9, 1) if pre_us else None},

@@ -261,8 +261,17 @@ bool same_config(const PpkKvConfig& a, const PpkKvConfig& b) {
          a.min_capacity == b.min_capacity;
 }
 
-void check_write(const PpkKvConfig& cfg, const PpkKvWrite& w) {
+// A batch write with both sources NULL reserves slot past[b] of every row of
+// an int8 cache (all of the write's bookkeeping, no data): the caller's fused
+// decode step fills it on the same stream.
+bool reserves(const PpkKvWrite& w) { return w.k == nullptr && w.v == nullptr; }
+
+void check_write(const PpkKvConfig& cfg, const PpkKvWrite& w, bool reserve_allowed) {
   require(w.struct_size >= sizeof(PpkKvWrite), "PpkKvWrite.struct_size too small");
+  if (reserve_allowed && reserves(w)) {
+    require(cfg.kind == PPK_KV_INT8, "a reserving KV write (NULL sources) needs an int8 cache");
+    return;
+  }
   require(w.k && w.v, "KV query null source");
   if (cfg.kind == PPK_KV_INT8)
     require(w.src_dtype == PPK_F32 || w.src_dtype == PPK_BF16 || w.src_dtype == PPK_F16,
@@ -467,7 +476,7 @@ void advance(ppk_kv_cache& c, uint32_t previous, uint32_t next) {
 void query(ppk_context* ctx, hipStream_t stream, ppk_kv_cache& c, uint32_t past, const PpkKvWrite& w,
            PpkKvView* out) {
   require(ctx == c.ctx, "KV cache belongs to another context");
-  check_write(c.cfg, w);
+  check_write(c.cfg, w, false);
   if (past != c.committed)
     throw PreconditionError("KV past_len " + std::to_string(past) + " differs from the committed length " +
                             std::to_string(c.committed));
@@ -619,7 +628,7 @@ void query_batch(ppk_context* ctx, hipStream_t stream, ppk_kv_cache* const* cach
     require(same_config(caches[b]->cfg, cfg), "batch KV existing row is incompatible");
     for (uint32_t o = 0; o < b; ++o) require(caches[o] != caches[b], "batch KV rows must be distinct caches");
   }
-  check_write(cfg, w);
+  check_write(cfg, w, true);
   require(w.tokens == 1, "batch KV requires one query token per row");
   if (out) require(out->struct_size >= sizeof(PpkKvView), "PpkKvView.struct_size too small");
   if (plan) {
@@ -662,7 +671,8 @@ void query_batch(ppk_context* ctx, hipStream_t stream, ppk_kv_cache* const* cach
   Arena& a = *arena;
   const size_t src_bytes = size_t(batch) * cfg.heads * cfg.head_dim *
                            (cfg.kind == PPK_KV_INT8 ? (w.src_dtype == PPK_F32 ? 4 : 2) : elem_bytes(cfg.kind));
-  SourceSnapshot src(w.k, w.v, src_bytes, a, stream);
+  const bool reserve = reserves(w);
+  SourceSnapshot src(w.k, w.v, reserve ? 0 : src_bytes, a, stream);
   std::vector<std::shared_ptr<Backing>> replacements;
   replacements.reserve(changed.size());
   std::vector<CopyDesc> copies;
@@ -722,7 +732,7 @@ void query_batch(ppk_context* ctx, hipStream_t stream, ppk_kv_cache* const* cach
   aw.capacity = a.capacity;
   aw.head_dim = cfg.head_dim;
   aw.elem_bytes = cfg.kind == PPK_KV_INT8 ? 0 : uint32_t(elem_bytes(cfg.kind));
-  run_arena_write(ctx, stream, aw);
+  if (!reserve) run_arena_write(ctx, stream, aw);
   a.last_stream = stream;
   {
     std::lock_guard<std::mutex> lock(a.mu);

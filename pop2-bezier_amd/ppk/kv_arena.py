@@ -193,22 +193,68 @@ class LayerCache:
         return torch.cat([prefix[0], k], 1), torch.cat([prefix[1], v], 1)
 
     @staticmethod
-    def query_batch(caches: list["LayerCache"], k: torch.Tensor, v: torch.Tensor, past_lens, commit: bool,
-                    plan: "WritePlan | None" = None) -> _abi.PpkKvView:
+    def query_batch(caches: list["LayerCache"], k: torch.Tensor | None, v: torch.Tensor | None, past_lens,
+                    commit: bool, plan: "WritePlan | None" = None) -> _abi.PpkKvView:
         """k/v [B, H, 1, D]: one token per sequence at slot past_lens[b]; returns the arena view
-        [B*H, capacity, D] with length max(past) + 1 and device past / lengths vectors."""
+        [B*H, capacity, D] with length max(past) + 1 and device past / lengths vectors. k = v = None (int8
+        caches) reserves the slot without writing it, for `decode_step(view, ...)` on the current stream."""
         b = len(caches)
-        if k.dim() != 4 or k.shape[0] != b or k.shape[2] != 1:
-            raise ValueError("batch KV requires [B,H,1,D] scratch and matching row histories")
-        k, v = k.contiguous(), v.contiguous()
-        w = _write(k, v, 1, commit)
+        if k is None and v is None:
+            w = _abi.PpkKvWrite(struct_size=ctypes.sizeof(_abi.PpkKvWrite), src_dtype=_abi.PPK_BF16, tokens=1,
+                                commit=int(bool(commit)), k=None, v=None)
+            stream = ctypes.c_void_p(torch.cuda.current_stream(caches[0].device).cuda_stream) if b else None
+        else:
+            if k.dim() != 4 or k.shape[0] != b or k.shape[2] != 1:
+                raise ValueError("batch KV requires [B,H,1,D] scratch and matching row histories")
+            k, v = k.contiguous(), v.contiguous()
+            w = _write(k, v, 1, commit)
+            stream = _stream(k)
         handles = (ctypes.c_void_p * b)(*[c.handle.value for c in caches])
         lens = (ctypes.c_uint32 * b)(*[int(x) for x in past_lens])
         out = _abi.PpkKvView(struct_size=ctypes.sizeof(_abi.PpkKvView))
-        check(lib().ppk_kv_query_batch(caches[0].ctx, _stream(k), handles, b, lens, ctypes.byref(w),
+        check(lib().ppk_kv_query_batch(caches[0].ctx, stream, handles, b, lens, ctypes.byref(w),
                                        plan.handle if plan is not None else None, ctypes.byref(out)),
               "ppk_kv_query_batch")
         return out
+
+
+def decode_step(view: _abi.PpkKvView, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, heads: int, *,
+                out_dtype: torch.dtype = torch.float32, past_host=None, flags: torch.Tensor | None = None,
+                bf16_history: bool = False) -> torch.Tensor:
+    """The fused decode step over a reserved batch view of int8 caches (LayerCache.query_batch with k = v =
+    None): quantise k_new / v_new (the current token, [B*H, D] or [B, H, 1, D]) into slot past[b] of the
+    view's arenas and attend over [0, past[b]) plus that token unquantised, in one launch (two when rows
+    span blocks); returns out [B*H, 1, D]. The commit path of forward_batched_embedding
+    (app/src/model/batch.rs:152-161) with query_int8 and int8_kv_ops::attention joined."""
+    from .int8_kv_ops import _step_args, workspace_bytes
+
+    if view.kind != _abi.PPK_KV_INT8 or not view.batch or not view.past:
+        raise ValueError("decode_step needs the batch view of int8 caches")
+    rows, d, cap = view.rows, view.head_dim, view.capacity
+    for t in (q, k_new, v_new):
+        if t.numel() != rows * d or t.dtype not in _DTYPES or not t.is_contiguous() or not t.is_cuda:
+            raise ValueError("INT8 decode step operands must be dense float [B*H, D] on the device")
+    if heads <= 0 or rows % heads or rows // heads != view.batch:
+        raise ValueError("INT8 attention geometry differs")
+    out = torch.empty((rows, 1, d), dtype=out_dtype, device=q.device)
+    a = _abi.PpkAttentionArgs(
+        struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), q_dtype=_DTYPES[q.dtype], scratch_dtype=_DTYPES[k_new.dtype],
+        out_dtype=_DTYPES[out_dtype], flags=_abi.PPK_ATTN_BF16_HISTORY if bf16_history else 0, rows=rows,
+        heads=heads, capacity=cap, head_dim=d, split_tokens=0, max_past=view.length - 1, softmax_scale=0.0,
+        q=q.data_ptr(), k_codes=view.k, v_codes=view.v, k_scales=view.k_scales, v_scales=view.v_scales,
+        sk=k_new.data_ptr(), sv=v_new.data_ptr(), past=view.past, out=out.data_ptr(), workspace=None,
+        workspace_bytes=0, past_host=None)
+    if past_host is not None:
+        a._past_host = (ctypes.c_uint32 * view.batch)(*[int(x) for x in past_host])
+        a.past_host = ctypes.cast(a._past_host, ctypes.c_void_p).value
+    step = _step_args(a, k_new, v_new, flags, d)
+    ctx = context(q.device)
+    nbytes = workspace_bytes(a, ctx)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    step.attn.workspace = ws.data_ptr()
+    step.attn.workspace_bytes = nbytes
+    check(lib().ppk_decode_step(ctx, _stream(q), ctypes.byref(step)), "ppk_decode_step")
+    return out
 
 
 def trim(device: torch.device | int | None = None) -> int:

@@ -304,12 +304,14 @@ def test_golden_config2_append(device):
         assert np.array_equal(ds.cpu().numpy().view(np.uint32), exp_s.view(np.uint32))
 
 
-def test_config5_full_size_all_rows_and_properties(device):
-    """BASELINE config 5 at full size (B=32, H=16, D=128, 8192 int8 tokens, heavy-tailed K/V, bf16 q):
-    all 512 rows of both plans against the oracle, the whole append bit-exact, plan invariance."""
+@pytest.mark.parametrize("D", [128, 64, 256])
+def test_config5_full_size_all_rows_and_properties(device, D):
+    """BASELINE config 5 at full size (B=32, H=16, D=128, 8192 int8 tokens, heavy-tailed K/V, bf16 q), and the
+    same shape at the reference's own head width 64 and at 256: all 512 rows of both plans against the
+    oracle, the whole append bit-exact, plan invariance."""
     from ppk import synthetic
 
-    B, H, D, L = 32, 16, 128, 8192
+    B, H, L = 32, 16, 8192
     rows, cap, seed = B * H, L + 1, SEED + 55
     kc = torch.empty((rows, cap, D), dtype=torch.uint8, device=device)
     vc = torch.empty_like(kc)
@@ -339,8 +341,8 @@ def test_config5_full_size_all_rows_and_properties(device):
                            vc[:, :L].cpu().numpy(), ks[:, :L].cpu().numpy(), vs[:, :L].cpu().numpy(),
                            kn.float().reshape(rows, D).cpu().numpy(), vn.float().reshape(rows, D).cpu().numpy(),
                            np.full(B, L, np.uint32), H)
-    assert_close(got, ref, what="config 5, all 512 rows")
-    assert_close(got_split, ref, what="config 5 split-K plan, all 512 rows")
+    assert_close(got, ref, what=f"config 5 D={D}, all 512 rows")
+    assert_close(got_split, ref, what=f"config 5 D={D} split-K plan, all 512 rows")
     # The history codes of the first sampled chunk are the oracle's quantisation of its source values.
     src = synthetic.history_chunk(seed, 0, 0, 16, H, 0, L, D, device).float().cpu().numpy()
     c, s, _ = oracle.quantize(src)

@@ -306,3 +306,69 @@ def test_amd_variant_self_check_known_answer_v(device):
         rows = slice(b * H, (b + 1) * H)
         assert np.array_equal(got_c[rows, slots[b]], codes[rows, 0])
         assert np.max(np.abs(got_s[rows, slots[b]] - scales[rows, 0])) < 1e-8
+
+
+def _view_attention(view, q, sk, sv, heads):
+    """ppk_decode_attention over a batch view (history [0, past[b]) plus the current token sk/sv)."""
+    rows, d = view.rows, view.head_dim
+    out = torch.empty((rows, 1, d), dtype=torch.float32, device=q.device)
+    a = _abi.PpkAttentionArgs(
+        struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), q_dtype=_abi.PPK_BF16, scratch_dtype=_abi.PPK_BF16,
+        out_dtype=_abi.PPK_F32, flags=0, rows=rows, heads=heads, capacity=view.capacity, head_dim=d,
+        split_tokens=0, max_past=view.length - 1, softmax_scale=0.0, q=q.data_ptr(), k_codes=view.k,
+        v_codes=view.v, k_scales=view.k_scales, v_scales=view.v_scales, sk=sk.data_ptr(), sv=sv.data_ptr(),
+        past=view.past, out=out.data_ptr(), workspace=None, workspace_bytes=0, past_host=None)
+    ctx = ppk.context(q.device)
+    nbytes = ppk.int8_kv_ops.workspace_bytes(a, ctx)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+    stream = ctypes.c_void_p(torch.cuda.current_stream(q.device).cuda_stream)
+    _abi.check(_abi.lib().ppk_decode_attention(ctx, stream, ctypes.byref(a)), "ppk_decode_attention")
+    return out
+
+
+def test_reserved_batch_write_and_fused_step_equal_write_then_attention(device):
+    """ppk_kv_query_batch with NULL sources (no counterpart in the reference) reserves slot past[b]; the fused
+    decode step on the returned view then quantises the token there and attends in one launch. Over a join
+    round and two steady rounds of ragged sequences, the arenas (codes and scales of every committed slot) and
+    the outputs equal the two-call path (write, then ppk_decode_attention) bit for bit."""
+    from ppk import kv_arena
+
+    heads, d, lengths = 4, 128, [37, 0, 120]
+    g = torch.Generator(device=device).manual_seed(11)
+    sets = []
+    for _ in range(2):
+        caches = [LayerCache("int8", heads, d) for _ in lengths]
+        for c, n in zip(caches, lengths):
+            if n:
+                x = torch.randn((heads, n, d), generator=torch.Generator(device=device).manual_seed(n), device=device)
+                c.query(x, x, 0, True)
+        sets.append(caches)
+    past = list(lengths)
+    for rnd in range(3):
+        q = torch.randn((len(past) * heads, d), generator=g, device=device).to(torch.bfloat16)
+        kn = torch.randn((len(past), heads, 1, d), generator=g, device=device).to(torch.bfloat16)
+        vn = torch.randn((len(past), heads, 1, d), generator=g, device=device).to(torch.bfloat16)
+        va = LayerCache.query_batch(sets[0], kn, vn, past, True, WritePlan(past, heads, d))
+        out_a = _view_attention(va, q, kn, vn, heads)
+        vb = LayerCache.query_batch(sets[1], None, None, past, True, WritePlan(past, heads, d))
+        out_b = kv_arena.decode_step(vb, q, kn.reshape(-1, d), vn.reshape(-1, d), heads)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, out_b), f"round {rnd}"
+        assert torch.isfinite(out_a).all()
+        n = max(past) + 1
+        for which in ("k", "v", "k_scales", "v_scales"):
+            ra, rb = read(va, which, n), read(vb, which, n)
+            for row, p in enumerate(past):
+                rows = slice(row * heads, (row + 1) * heads)
+                assert torch.equal(ra[rows, :p + 1], rb[rows, :p + 1]), f"round {rnd} {which} sequence {row}"
+        assert [len(c) for c in sets[1]] == [p + 1 for p in past]
+        past = [p + 1 for p in past]
+
+
+def test_reserving_write_needs_int8_caches(device):
+    caches = [LayerCache(torch.float32, 2, 64) for _ in range(2)]
+    with pytest.raises(ppk.PpkError) as e:
+        LayerCache.query_batch(caches, None, None, [0, 0], True)
+    assert e.value.status == _abi.PPK_PRECONDITION
+    assert [len(c) for c in caches] == [0, 0]
