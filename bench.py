@@ -55,7 +55,11 @@ def parse() -> argparse.Namespace:
     p.add_argument("--choices", type=int, default=2048)
     p.add_argument("--guidance", type=int, default=2)
     p.add_argument("--device-lengths", action="store_true",
-                   help="configs 1, 3, 4: pass the lengths on the device only (no host copy), i.e. the per-row plan")
+                   help="configs 1, 3, 4 and --lengths: pass the lengths on the device only (no host copy), i.e. "
+                        "the per-row plan")
+    p.add_argument("--lengths", default=None,
+                   help="with --kv bf16/f32: comma-separated per-sequence lengths of a ragged batch (NxL repeats "
+                        "L N times); the batch is their count and the store holds the longest")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0,
                    help="head rows timed for the CPU baseline (0 = every row of the step)")
@@ -147,7 +151,16 @@ def bench_float(args) -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    B, H, D, L = args.batch, args.heads, args.head_dim, args.context
+    H, D = args.heads, args.head_dim
+    if args.lengths:
+        seq = []
+        for part in args.lengths.split(","):
+            n, _, length = part.strip().rpartition("x")
+            seq += [int(length)] * (int(n) if n else 1)
+        B, L = len(seq), max(seq)
+    else:
+        B, L = args.batch, args.context
+        seq = [L] * B
     rows = B * H
     kv_dtype = torch.bfloat16 if args.kv == "bf16" else torch.float32
     eb = 2 if args.kv == "bf16" else 4
@@ -156,8 +169,11 @@ def bench_float(args) -> int:
     k = torch.randn((rows, L, D), generator=g, device=dev, dtype=kv_dtype)
     v = torch.randn((rows, L, D), generator=g, device=dev, dtype=kv_dtype)
     q = torch.randn((rows, 1, D), generator=g, device=dev, dtype=torch.float32)
-    lengths = torch.full((B,), L, dtype=torch.int32, device=dev)
-    call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L)
+    lengths = torch.tensor(seq, dtype=torch.int32, device=dev)
+    host = seq if args.lengths and not args.device_lengths else None
+    call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host)
+    flat = host is not None and ppk.fused_attention.plan(call.args, call.ctx) != ppk.fused_attention.plan(
+        ppk.fused_attention.decode_attention_args(q, k, v, lengths, H, args.split, max_length=L)[0], call.ctx)
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -188,13 +204,16 @@ def bench_float(args) -> int:
     launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_FLOAT_ATTENTION, reset=True)
     kernel_avg_ms = kernel_ms / max(launches, 1)
 
-    # Algorithmic bytes: every row's K and V (L tokens x D x element size), the f32 query and output.
-    kv_bytes = rows * L * 2 * D * eb
+    # Algorithmic bytes: every row's K and V (its live tokens x D x element size), the f32 query and output.
+    kv_bytes = sum(seq) * H * 2 * D * eb
     step_bytes = kv_bytes + rows * D * 4 + rows * D * 4
-    kernel_bytes = step_bytes if call.ngroups == 1 else kv_bytes + rows * D * 4 + rows * call.ngroups * (D + 2) * 4
+    if flat:  # the balanced decode launch; its records (a small share here) are not counted
+        kernel_bytes = step_bytes
+    else:
+        kernel_bytes = step_bytes if call.ngroups == 1 else kv_bytes + rows * D * 4 + rows * call.ngroups * (D + 2) * 4
     achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
-    kname = f"ppk_fdecode_{args.kv}_d{D}"
+    kname = f"ppk_fdecode_{'flat_' if flat else ''}{args.kv}_d{D}"
     traffic = None
     tpath = os.path.join(ROOT, "profiles", f"ppk_fdecode_{args.kv}_d{D}_b{B}_h{H}_ctx{L}_traffic.json")
     if os.path.exists(tpath):
@@ -207,7 +226,8 @@ def bench_float(args) -> int:
         except (OSError, ValueError):
             traffic = None
     result = {
-        "metric": f"float-KV decode-attention µs/step + achieved HBM GB/s (% of peak), B={B} ctx={L} {args.kv} KV",
+        "metric": f"float-KV decode-attention µs/step + achieved HBM GB/s (% of peak), B={B} ctx={L} {args.kv} KV"
+                  + (f", ragged lengths {args.lengths}" if args.lengths else ""),
         "value": round(step_ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": args.kv,
@@ -215,7 +235,8 @@ def bench_float(args) -> int:
         "config": {"workload": "float-KV decode attention (ppk_float_decode_attention, the reference's "
                                "fused_attention::decode_attention)", "batch": B, "heads": H, "head_dim": D,
                    "context": L, "kv": args.kv, "query": "f32", "tokens_per_wave": call.split_tokens,
-                   "blocks_per_row": call.ngroups, "launches_per_step": 1 if call.ngroups == 1 else 2},
+                   "blocks_per_row": call.ngroups, "launches_per_step": 1 if call.ngroups == 1 else 2,
+                   "lengths": args.lengths, "plan": "balanced" if flat else "per-row"},
         "step_hbm_gbps": round(step_gbps, 1), "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
@@ -228,25 +249,30 @@ def bench_float(args) -> int:
         import oracle  # noqa: E402  (CPU baseline leg only)
 
         n = max(1, min(args.cpu_rows, rows)) if args.cpu_rows else rows
-        if eb == 2:
-            k_h = k[:n].view(torch.int16).cpu().numpy().view(np.uint16)
-            v_h = v[:n].view(torch.int16).cpu().numpy().view(np.uint16)
-        else:
-            k_h, v_h = k[:n].cpu().numpy(), v[:n].cpu().numpy()
-        q_h = q[:n].cpu().numpy()
+        n = max(H, n - n % H)
+
+        def host_bits(t):
+            return t.view(torch.int16).cpu().numpy().view(np.uint16) if eb == 2 else t.cpu().numpy()
+
+        # One call per sequence over its live tokens (dense host copies made once, outside the timed calls).
+        parts = [(np.ascontiguousarray(q[b * H:(b + 1) * H].cpu().numpy()),
+                  np.ascontiguousarray(host_bits(k[b * H:(b + 1) * H, :seq[b]])),
+                  np.ascontiguousarray(host_bits(v[b * H:(b + 1) * H, :seq[b]]))) for b in range(n // H) if seq[b]]
         threads = _host_cpus()
         reps, t0 = 0, time.perf_counter()
         while True:
-            oracle.cpu_baseline_float(q_h, k_h, v_h, threads)
+            for q_h, k_h, v_h in parts:
+                oracle.cpu_baseline_float(q_h, k_h, v_h, threads)
             reps += 1
             el = time.perf_counter() - t0
             if el >= args.cpu_seconds or reps >= 1000:
                 break
+        scale = sum(seq) / max(sum(seq[: n // H]), 1)
         result["cpu_baseline"] = {
-            "value": round(el / reps * 1e6 * rows / n, 1), "unit": "us/step", "cores": threads, "kind": "port",
-            "sample": f"{n} of {rows} head rows x {L} tokens (Candle's ordinary CPU attention restated in C, "
-                      f"oracle/cpu_baseline.c cpu_baseline_float_decode, {oracle.cpu_baseline_isa()}), "
-                      f"{reps} reps in {el:.1f} s" + (f", scaled x{rows / n:g}" if n != rows else ""),
+            "value": round(el / reps * 1e6 * scale, 1), "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": f"{n} of {rows} head rows over their live tokens (Candle's ordinary CPU attention restated "
+                      f"in C, oracle/cpu_baseline.c cpu_baseline_float_decode, {oracle.cpu_baseline_isa()}), "
+                      f"{reps} reps in {el:.1f} s" + (f", scaled x{scale:g} by live tokens" if n != rows else ""),
             "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None

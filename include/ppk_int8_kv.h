@@ -271,6 +271,13 @@ typedef struct PpkFloatAttentionArgs {
   void* out;               /* [rows, head_dim] */
   void* workspace;         /* ppk_float_attention_plan() bytes, 256-byte aligned (may be NULL if 0) */
   uint64_t workspace_bytes;
+  /* Optional (NULL, or absent when struct_size ends before it): a host copy
+     of lengths[] (needs lengths). With it a ragged batch is balanced as in
+     PpkAttentionArgs.past_host: the plan and the workspace size follow the
+     actual lengths, each device lengths[b] is still read and compared, and a
+     sequence whose device value differs gives NaN rows, never a wrong
+     result. Only read during the call. */
+  const uint32_t* lengths_host;
 } PpkFloatAttentionArgs;
 /* Launch plan for args (ctx may be NULL: assumes 256 CUs), as ppk_attention_plan. */
 PPK_API int32_t ppk_float_attention_plan(ppk_context* ctx, const PpkFloatAttentionArgs* args,

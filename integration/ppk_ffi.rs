@@ -199,6 +199,7 @@ pub struct PpkFloatAttentionArgs {
     pub out: *mut c_void,
     pub workspace: *mut c_void,
     pub workspace_bytes: u64,
+    pub lengths_host: *const u32,
 }
 
 /// CFG + Renyi sampler (hip_sampling::sample, app/src/inference/hip_sampling.rs:71-106).

@@ -64,6 +64,9 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_decode_flat_d64", "ppk_decode_flat_d128", "ppk_decode_flat_d256",
     "ppk_decode_flat_bf16h_d64", "ppk_decode_flat_bf16h_d128", "ppk_decode_flat_bf16h_d256",
     "ppk_attn_merge_flat_d64", "ppk_attn_merge_flat_d128", "ppk_attn_merge_flat_d256",
+    "ppk_fdecode_flat_bf16_d64", "ppk_fdecode_flat_bf16_d128", "ppk_fdecode_flat_bf16_d256",
+    "ppk_fdecode_flat_f32_d64", "ppk_fdecode_flat_f32_d128", "ppk_fdecode_flat_f32_d256",
+    "ppk_fmerge_flat_d64", "ppk_fmerge_flat_d128", "ppk_fmerge_flat_d256",
 };
 
 std::string default_code_object() {
@@ -225,56 +228,70 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   // config 3 within 2 %. Uniform lengths keep the per-row plan (B=32 x 8192:
   // one launch, 166 us, against 171 us balanced).
   const uint32_t* host = host_lengths(a);
-  const uint32_t batch = a.rows / a.heads;
-  const uint64_t flat_waves = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * kFlatWavesPerCu;
-  if (host && a.split_tokens == 0 && batch <= uint32_t(kFlatMaxBatch) && 2 * uint64_t(a.rows) <= flat_waves) {
-    uint64_t sum = 0, most = 0;
-    for (uint32_t b = 0; b < batch; ++b) {
-      const uint64_t live = (host[b] <= a.capacity && host[b] <= span) ? host[b] : 0;
-      sum += live;
-      most = std::max(most, live);
-    }
-    if (most * batch * 10 > sum * 11)  // the longest row beyond 1.1 x the mean
-      plan = plan_flat(ctx, a, uint32_t(span));
+  const uint64_t limit = std::min<uint64_t>(a.capacity, span);
+  if (host && a.split_tokens == 0 && flat_pays(ctx, a.rows, a.heads, host, limit)) {
+    plan = plan_flat(ctx, a.rows, a.heads, host, limit, a.head_dim);
+    plan.span = uint32_t(span);
   }
   return plan;
+}
+
+uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit) {
+  uint64_t most = 0;
+  for (uint32_t b = 0; b < batch; ++b)
+    if (host[b] <= limit) most = std::max<uint64_t>(most, host[b]);
+  return most;
+}
+
+bool flat_pays(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t limit) {
+  const uint32_t batch = rows / heads;
+  const uint64_t flat_waves = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * kFlatWavesPerCu;
+  if (batch > uint32_t(kFlatMaxBatch) || 2 * uint64_t(rows) > flat_waves) return false;
+  uint64_t sum = 0, most = 0;
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint64_t live = host[b] <= limit ? host[b] : 0;
+    sum += live;
+    most = std::max(most, live);
+  }
+  return most * batch * 10 > sum * 11;  // the longest row beyond 1.1 x the mean
 }
 
 // Balanced plan (ragged batches with host lengths): eight waves per CU, all
 // resident; units of at most Q tokens of one row, Q the least share (>= 64)
 // for which the units, sum over rows of max(1, ceil(len / Q)), fit the
-// waves; waves 0 .. 2 rows - 1 also append the current tokens (so waves >= 2
-// rows).
+// waves; in the int8 decode step waves 0 .. 2 rows - 1 also append the
+// current tokens (so waves >= 2 rows).
 // Record slots per row = the most units of any row (none when every row is
 // one unit: then the decode launch writes every output and no merge runs).
-AttentionPlan plan_flat(const ppk_context* ctx, const PpkAttentionArgs& a, uint32_t span) {
+AttentionPlan plan_flat(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t limit,
+                        uint32_t head_dim) {
   constexpr uint32_t kWavesPerBlock = 4, kMinUnit = 64;
   AttentionPlan plan;
-  plan.head_dim = a.head_dim;
+  plan.head_dim = head_dim;
   plan.flat = true;
   plan.waves = kWavesPerBlock;
-  plan.span = span;
   const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
   plan.blocks = uint32_t(cus * kFlatWavesPerCu / kWavesPerBlock);
   const uint64_t waves = uint64_t(plan.blocks) * kWavesPerBlock;
-  const uint32_t* host = host_lengths(a);
+  require(rows % heads == 0 && rows / heads <= uint32_t(kFlatMaxBatch) && 2 * uint64_t(rows) <= waves,
+          "balanced plan: batch or rows beyond its limits");
   FlatTable& t = plan.table;
-  t.batch = a.rows / a.heads;
+  t.batch = rows / heads;
   uint64_t total = 0;
   for (uint32_t b = 0; b < t.batch; ++b) {
     t.past[b] = host[b];
-    t.len[b] = (host[b] <= a.capacity && host[b] <= span) ? host[b] : 0u;
-    total += uint64_t(t.len[b]) * a.heads;
+    t.len[b] = host[b] <= limit ? host[b] : 0u;
+    total += uint64_t(t.len[b]) * heads;
   }
   // The least share whose units fit the waves: units(Q) = sum over rows of
   // max(1, ceil(len / Q)) falls as Q grows, and Q = ceil(T / (waves - rows))
   // always fits (units <= T / Q + rows), so a binary search between 64 and it.
   auto units_for = [&](uint64_t q) {
     uint64_t u = 0;
-    for (uint32_t b = 0; b < t.batch; ++b) u += uint64_t(a.heads) * std::max<uint64_t>(1, (t.len[b] + q - 1) / q);
+    for (uint32_t b = 0; b < t.batch; ++b) u += uint64_t(heads) * std::max<uint64_t>(1, (t.len[b] + q - 1) / q);
     return u;
   };
-  const uint64_t spare = waves - a.rows;  // the caller keeps rows <= waves / 2
+  const uint64_t spare = waves - rows;
   uint64_t lo = kMinUnit, hi = std::max<uint64_t>((total + spare - 1) / spare, kMinUnit);
   while (lo < hi) {
     const uint64_t mid = (lo + hi) / 2;
@@ -291,7 +308,7 @@ AttentionPlan plan_flat(const ppk_context* ctx, const PpkAttentionArgs& a, uint3
     }
     t.units[b] = std::max<uint32_t>(1, (t.len[b] + t.share - 1) / t.share);
     t.first[b] = uint32_t(first);
-    first += uint64_t(t.units[b]) * a.heads;
+    first += uint64_t(t.units[b]) * heads;
     most = std::max(most, t.units[b]);
   }
   require(first <= waves, "balanced plan: units exceed the launched waves");
@@ -300,8 +317,8 @@ AttentionPlan plan_flat(const ppk_context* ctx, const PpkAttentionArgs& a, uint3
   plan.ngroups = most;
   plan.lds_bytes = 0;
   if (most > 1) {
-    plan.y_bytes = (uint64_t(a.rows) * most * a.head_dim * 4 + 255) / 256 * 256;
-    plan.mz_bytes = (uint64_t(a.rows) * most * 2 * 4 + 255) / 256 * 256;
+    plan.y_bytes = (uint64_t(rows) * most * head_dim * 4 + 255) / 256 * 256;
+    plan.mz_bytes = (uint64_t(rows) * most * 2 * 4 + 255) / 256 * 256;
   }
   plan.workspace_bytes = plan.y_bytes + plan.mz_bytes;
   return plan;
@@ -545,8 +562,16 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
 // reference requires head_dim 64, size <= 1024 and F32 Q/out; here head_dim
 // 64/128/256, any size, and f32/bf16/f16 Q and output are accepted. Every
 // span is checked against the stated strides before the first enqueue.
+// The float argument block up to workspace_bytes is required; lengths_host
+// (added later) is read only when struct_size covers it.
+constexpr size_t kFloatArgsMin = offsetof(PpkFloatAttentionArgs, lengths_host);
+const uint32_t* host_lengths(const PpkFloatAttentionArgs& a) {
+  return a.struct_size >= offsetof(PpkFloatAttentionArgs, lengths_host) + sizeof(a.lengths_host) ? a.lengths_host
+                                                                                                  : nullptr;
+}
+
 AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttentionArgs& a) {
-  require(a.struct_size >= sizeof(PpkFloatAttentionArgs), "PpkFloatAttentionArgs.struct_size too small");
+  require(a.struct_size >= kFloatArgsMin, "PpkFloatAttentionArgs.struct_size too small");
   dim_index(a.head_dim);
   require(a.kv_dtype == PPK_BF16 || a.kv_dtype == PPK_F32, "float attention K/V dtype must be bf16 or f32");
   require(valid_dtype(a.q_dtype) && valid_dtype(a.out_dtype), "float attention Q/out dtype must be f32, bf16 or f16");
@@ -565,7 +590,24 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   require(uint64_t(a.rows) * std::max(ks, vs) <= (uint64_t(1) << 46), "float attention K/V span too large");
   const uint32_t tpl = 64u / (a.head_dim / uint32_t(16 / eb));
   const uint64_t span = a.max_length ? a.max_length : a.size;
-  return plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
+  AttentionPlan plan =
+      plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
+  // With the host's copy of the lengths, a ragged batch takes the balanced
+  // plan (as the int8 path does) once its longest row holds more than
+  // 512 KiB of K and V. Measured on MI355X (bf16, H = 16, per step,
+  // per-row -> balanced): 4 sequences of 8192 tokens beside 28 of 512,
+  // D = 64 57.1 -> 38.5 us, D = 128 111.8 -> 68.9 us; 2 of 16384 beside 14
+  // of 256, D = 64 74.0 -> 30.3 us, D = 128 147.7 -> 53.8 us; 4 of 1024
+  // beside 28 of 64 (256 / 512 KiB rows), D = 64 9.3 -> 11.5 us (the merge
+  // launch costs more than the balance gains), D = 128 16.1 -> 15.9 us.
+  constexpr uint64_t kFloatFlatMinRowBytes = 512u << 10;
+  const uint32_t* host = host_lengths(a);
+  require(!host || a.lengths, "float attention lengths_host needs the device lengths");
+  if (host && a.split_tokens == 0 && flat_pays(ctx, a.rows, a.heads, host, span) &&
+      longest_live(host, a.rows / a.heads, span) * 2 * eb * a.head_dim > kFloatFlatMinRowBytes)
+    plan = plan_flat(ctx, a.rows, a.heads, host, span, a.head_dim);
+  plan.span = uint32_t(span);
+  return plan;
 }
 
 void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a) {
@@ -606,22 +648,40 @@ void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAtt
   d.q_dtype = a.q_dtype;
   d.out_dtype = a.out_dtype;
   d.scale_log2 = scale * 1.4426950408889634f;
+  d.span = plan.span;
 
-  const Fn decode = Fn((a.kv_dtype == PPK_BF16 ? kFDecodeBf16_64 : kFDecodeF32_64) + di);
+  FloatMergeArgs m{};
+  m.lengths = a.lengths;
+  m.part_y = d.part_y;
+  m.part_mz = d.part_mz;
+  m.out = a.out;
+  m.rows = a.rows;
+  m.heads = a.heads;
+  m.size = a.size;
+  m.nsplits = plan.ngroups;
+  m.out_dtype = a.out_dtype;
+  m.span = plan.span;
+  const bool bf16 = a.kv_dtype == PPK_BF16;
   DeviceGuard guard(ctx->device);
+  if (plan.flat) {
+    FloatDecodeFlatArgs fd{};
+    fd.d = d;
+    fd.t = plan.table;
+    launch(ctx, PPK_KERNEL_FLOAT_ATTENTION, Fn((bf16 ? kFDecodeFlatBf16_64 : kFDecodeFlatF32_64) + di), plan.blocks,
+           64 * plan.waves, 0, stream, fd);
+    if (plan.ngroups > 1) {
+      FloatMergeFlatArgs fm{};
+      fm.m = m;
+      fm.m.split_tokens = plan.split;
+      fm.t = plan.table;
+      launch(ctx, PPK_KERNEL_FLOAT_MERGE, Fn(kFMergeFlat64 + di), a.rows, 64, 0, stream, fm);
+    }
+    return;
+  }
+  const Fn decode = Fn((bf16 ? kFDecodeBf16_64 : kFDecodeF32_64) + di);
   launch(ctx, PPK_KERNEL_FLOAT_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d);
   if (plan.ngroups > 1) {
-    FloatMergeArgs m{};
-    m.lengths = a.lengths;
-    m.part_y = d.part_y;
-    m.part_mz = d.part_mz;
-    m.out = a.out;
-    m.rows = a.rows;
-    m.heads = a.heads;
-    m.size = a.size;
     m.split_tokens = plan.split * plan.waves;  // tokens per group
-    m.nsplits = plan.ngroups;
-    m.out_dtype = a.out_dtype;
     launch(ctx, PPK_KERNEL_FLOAT_MERGE, Fn(kFMerge64 + di), a.rows, 64, 0, stream, m);
   }
 }

@@ -53,6 +53,9 @@ enum Fn : int {
   kDecodeFlat64, kDecodeFlat128, kDecodeFlat256,
   kDecodeFlatBf16h64, kDecodeFlatBf16h128, kDecodeFlatBf16h256,
   kMergeFlat64, kMergeFlat128, kMergeFlat256,
+  kFDecodeFlatBf16_64, kFDecodeFlatBf16_128, kFDecodeFlatBf16_256,
+  kFDecodeFlatF32_64, kFDecodeFlatF32_128, kFDecodeFlatF32_256,
+  kFMergeFlat64, kFMergeFlat128, kFMergeFlat256,
   kFnCount
 };
 
@@ -157,9 +160,9 @@ struct AttentionPlan {
   uint32_t ngroups = 0;  // blocks per row; 1 = final output in the same launch (flat: record slots per row)
   uint32_t lds_bytes = 0;
   uint64_t y_bytes = 0, mz_bytes = 0, workspace_bytes = 0;
-  // Balanced work list (int8 attention over a ragged batch whose host
-  // lengths are known, see FlatTable); ngroups = record slots per row, 1 when
-  // every row is a single unit (then no merge launch).
+  // Balanced work list (attention over a ragged batch whose host lengths
+  // are known, see FlatTable); ngroups = record slots per row, 1 when every
+  // row is a single unit (then no merge launch).
   bool flat = false;
   uint32_t blocks = 0;   // flat: blocks launched
   uint32_t span = 0;     // flat: rows with past beyond it give NaN
@@ -170,8 +173,16 @@ struct AttentionPlan {
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
                         uint32_t tpl, uint64_t token_bytes, uint32_t head_dim);
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
-// The balanced plan of the int8 decode from the host lengths (at most 64 sequences).
-AttentionPlan plan_flat(const ppk_context* ctx, const PpkAttentionArgs& a, uint32_t span);
+// The balanced plan of `rows` rows, `heads` per sequence, from the host
+// lengths host[0 .. rows / heads) (at most 64 sequences); a length above
+// `limit` has no live history. Needs 2 * rows <= the plan's waves.
+AttentionPlan plan_flat(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t limit,
+                        uint32_t head_dim);
+// Whether the balanced plan pays for these host lengths: the longest live
+// row beyond 1.1 x the mean, at most 64 sequences, 2 * rows within its waves.
+bool flat_pays(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t limit);
+// The most live tokens of any of `batch` sequences (a length above limit has none).
+uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit);
 AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttentionArgs& a);
 
 void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a);

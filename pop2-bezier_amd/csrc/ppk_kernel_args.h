@@ -131,8 +131,8 @@ struct MergeFlatArgs {
 // Float-KV decode attention: the same block geometry over unquantised bf16 or
 // f32 K/V. Row r attends its first n = lengths ? lengths[r / heads] : size
 // tokens (the current token is already stored); no separate current token.
-// ngroups > 1 leaves partial records for the float merge kernel, laid out as
-// for DecodeArgs.
+// n == 0 or n > span (= max_length, or size) gives NaN. ngroups > 1 leaves
+// partial records for the float merge kernel, laid out as for DecodeArgs.
 struct FloatDecodeArgs {
   const void* q;            // row r at q + r * q_stride elements
   const void* k;            // row r at k + r * k_stride elements, tokens D apart
@@ -145,6 +145,7 @@ struct FloatDecodeArgs {
   uint32_t rows, heads, size, split_tokens, ngroups;
   uint32_t q_dtype, out_dtype;
   float scale_log2;         // softmax_scale * log2(e)
+  uint32_t span;            // most tokens a row may attend (<= size)
 };
 
 struct FloatMergeArgs {
@@ -152,7 +153,19 @@ struct FloatMergeArgs {
   const float* part_y;
   const float* part_mz;
   void* out;                // [rows, D]
-  uint32_t rows, heads, size, split_tokens, nsplits, out_dtype;
+  uint32_t rows, heads, size, split_tokens, nsplits, out_dtype, span;
+};
+
+// Float-KV decode over the balanced work list: the table as for the int8
+// path, with past[b] the host's lengths[b] and len[b] its live tokens (0 for
+// a length outside (0, min(size, max_length)], whose rows give NaN).
+struct FloatDecodeFlatArgs {
+  FloatDecodeArgs d;
+  FlatTable t;
+};
+struct FloatMergeFlatArgs {
+  FloatMergeArgs m;
+  FlatTable t;
 };
 
 // Batched rectangle copies: block (x, y) serves rectangle y. Each of its

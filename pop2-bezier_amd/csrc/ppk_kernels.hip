@@ -10,6 +10,8 @@
 //   ppk_attn_merge_flat_d{..}          merge of the balanced work list's records + current token
 //   ppk_fdecode_{bf16,f32}_d{..}       decode attention over float (bf16/f32) K/V
 //   ppk_fmerge_d{..}                   cross-group merge of the float path
+//   ppk_fdecode_flat_{bf16,f32}_d{..}  float-path decode over a balanced work list (ragged batches)
+//   ppk_fmerge_flat_d{..}              merge of the float balanced work list's records
 //   ppk_renyi_sample                   CFG + Renyi effective-support sampler
 //   ppk_kv_scatter_u{16,4,2}           float-store append of token records into arena slots
 //   ppk_copy2d_batch                   batched rectangle copies + zero fill (arena joins, growth, copy-on-write)
@@ -1382,7 +1384,8 @@ __device__ __forceinline__ void attn_merge_flat_body(const ppk::MergeFlatArgs& f
 // (app/src/model/decode_attention.hip:9-66, fused_attention.rs:8-30) on the
 // block geometry of the int8 kernel. K/V are stored bf16 or f32; row r attends
 // its first n = lengths ? lengths[r / heads] : size tokens (the current token
-// is already in the store) and gives NaN if n == 0 or n > size.
+// is already in the store) and gives NaN if n == 0 or n > span (max_length,
+// or size).
 //
 // Lane layout: a lane holds one 16-byte chunk of a token, EPC = 8 (bf16) or 4
 // (f32) channels; LPT = D / EPC lanes share a token and a wave-wide dwordx4
@@ -1561,7 +1564,7 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
   const uint32_t group = blockIdx.x / a.rows;
   const uint32_t S = a.split_tokens;
   const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
-  const bool valid = len > 0 && len <= a.size && uint64_t(len) <= uint64_t(a.ngroups) * W * S;
+  const bool valid = len > 0 && len <= a.span && len <= a.size && uint64_t(len) <= uint64_t(a.ngroups) * W * S;
 
   float qr[G::kEpc];
   load_vec<G::kEpc>(a.q, size_t(row) * a.q_stride + size_t(c) * G::kEpc, a.q_dtype, qr);
@@ -1625,7 +1628,8 @@ __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
   const int lane = threadIdx.x;
   const uint32_t row = blockIdx.x;
   const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
-  const bool valid = len > 0 && len <= a.size && uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
+  const bool valid =
+      len > 0 && len <= a.span && len <= a.size && uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
   float m, zsum, y[EPL];
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
                      lane, [] { return -INFINITY; }, m, zsum, y);
@@ -1635,6 +1639,188 @@ __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
     const float o = (valid && zsum > 0.f) ? y[e] / zsum : __builtin_nanf("");
     store_elem(a.out, base + e, a.out_dtype, o);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Float-KV decode over the balanced work list (ragged batches with the host's
+// copy of the lengths): the int8 path's table and assignment (wave i takes
+// unit i, at most Q tokens of one row), each unit streamed as (K, V) batch
+// pairs through a window of two pairs with an online softmax. A row of one
+// unit is finished in the decode launch; longer rows leave one record per
+// unit for ppk_fmerge_flat_d*. A row whose host length lies outside
+// (0, min(size, max_length)], or whose device lengths[b] differs from the
+// table's, gives NaN.
+// ---------------------------------------------------------------------------
+// One (K, V) batch pair under the online softmax: token group j (the lanes
+// of one token of each tile) keeps its running max m, sum z and channel
+// accumulators; the batch's four scores, one rescale, then the V rows.
+template <int D, bool BF16KV>
+__device__ __forceinline__ void fonline_pair(const u4 (&kraw)[4], const u4 (&vraw)[4], uint32_t t0, uint32_t n, int j,
+                                             const float (&qr)[FloatGeom<D, BF16KV>::kEpc], float sl2, float& m,
+                                             float& z, float (&acc)[FloatGeom<D, BF16KV>::kEpc]) {
+  using G = FloatGeom<D, BF16KV>;
+  float s[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t tok = (t0 + u) * G::kTpl + j;
+    float x[G::kEpc];
+    unpack_chunk<BF16KV>(kraw[u], x);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < G::kEpc; ++e) d = fmaf(qr[e], x[e], d);
+    const float sc = token_sum<G::kLpt>(d) * sl2;
+    s[u] = tok < n ? sc : -INFINITY;
+  }
+  const float mb = fmaxf(fmaxf(m, fmaxf(s[0], s[1])), fmaxf(s[2], s[3]));
+  const float f = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mb);
+  z *= f;
+#pragma unroll
+  for (int e = 0; e < G::kEpc; ++e) acc[e] *= f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float pr = s[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[u] - mb);
+    z += pr;
+    float x[G::kEpc];
+    unpack_chunk<BF16KV>(vraw[u], x);
+#pragma unroll
+    for (int e = 0; e < G::kEpc; ++e) acc[e] = fmaf(pr, x[e], acc[e]);
+  }
+  m = mb;
+}
+
+// Streams tokens [begin, begin + n) of one row (n >= 1) through the window
+// of two (K, V) pairs; the partial (m, z in every lane, the channel sums in
+// lanes j == 0), as fwave_attention returns it.
+template <int D, bool BF16KV>
+__device__ __forceinline__ void fwave_attention_window(const ppk::FloatDecodeArgs& a, uint32_t row, uint32_t begin,
+                                                       uint32_t n, const float (&qr)[FloatGeom<D, BF16KV>::kEpc],
+                                                       int lane, FloatWavePartial<D, BF16KV>& out) {
+  using G = FloatGeom<D, BF16KV>;
+  constexpr int U = 4, NP = 2;
+  const int j = lane / G::kLpt;
+  const int c = lane % G::kLpt;
+  const char* kb = static_cast<const char*>(a.k) +
+                   (size_t(row) * a.k_stride + size_t(begin) * D) * G::kElemBytes + size_t(c) * ppk::kLaneBytes;
+  const char* vb = static_cast<const char*>(a.v) +
+                   (size_t(row) * a.v_stride + size_t(begin) * D) * G::kElemBytes + size_t(c) * ppk::kLaneBytes;
+  const uint32_t nb = (n + U * G::kTpl - 1) / (U * G::kTpl);  // batches per phase
+  u4 kr[NP][U], vr[NP][U];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    if (uint32_t(p) < nb) {  // uniform per wave
+      load_fbatch<D, BF16KV, U>(kb, uint32_t(p) * U, n, j, kr[p]);
+      load_fbatch<D, BF16KV, U>(vb, uint32_t(p) * U, n, j, vr[p]);
+    }
+  }
+  float m = -INFINITY, z = 0.f, acc[G::kEpc];
+#pragma unroll
+  for (int e = 0; e < G::kEpc; ++e) acc[e] = 0.f;
+  for (uint32_t b0 = 0; b0 < nb; b0 += NP) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const uint32_t bi = b0 + uint32_t(p);
+      if (bi < nb) {  // uniform per wave
+        fonline_pair<D, BF16KV>(kr[p], vr[p], bi * U, n, j, qr, a.scale_log2, m, z, acc);
+        if (bi + NP < nb) {
+          load_fbatch<D, BF16KV, U>(kb, (bi + NP) * U, n, j, kr[p]);
+          load_fbatch<D, BF16KV, U>(vb, (bi + NP) * U, n, j, vr[p]);
+        }
+      }
+    }
+  }
+  float mm = m;
+#pragma unroll
+  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+  const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
+  z *= w;
+#pragma unroll
+  for (int e = 0; e < G::kEpc; ++e) acc[e] *= w;
+#pragma unroll
+  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) {
+    z += __shfl_xor(z, o);
+#pragma unroll
+    for (int e = 0; e < G::kEpc; ++e) acc[e] += __shfl_xor(acc[e], o);
+  }
+  out.m = mm;
+  out.z = z;
+#pragma unroll
+  for (int e = 0; e < G::kEpc; ++e) out.acc[e] = acc[e];
+}
+
+template <int D, bool BF16KV>
+__device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs& fa) {
+  const ppk::FloatDecodeArgs& a = fa.d;
+  const ppk::FlatTable& t = fa.t;
+  using G = FloatGeom<D, BF16KV>;
+  const int lane = threadIdx.x & 63;
+  const uint32_t W = blockDim.x >> 6;
+  const uint32_t wid = blockIdx.x * W + (threadIdx.x >> 6);
+  if (wid >= t.units_total) return;  // uniform per wave
+  const int c = lane % G::kLpt;
+  const int j = lane / G::kLpt;
+  const uint32_t b = flat_sequence(t, wid);
+  const uint32_t units = t.units[b];
+  const uint32_t len = t.len[b];
+  const uint32_t k = wid - t.first[b];
+  const uint32_t h = k / units;
+  const uint32_t slot = k - h * units;
+  const uint32_t row = b * a.heads + h;
+  const uint32_t t0 = slot * t.share;
+  const uint32_t n = len > t0 ? min(t.share, len - t0) : 0u;
+  const uint32_t ldev = a.lengths[b];
+  float qr[G::kEpc];
+  if (n > 0) load_vec<G::kEpc>(a.q, size_t(row) * a.q_stride + size_t(c) * G::kEpc, a.q_dtype, qr);
+  FloatWavePartial<D, BF16KV> part;
+  part.m = -INFINITY;
+  part.z = 0.f;
+#pragma unroll
+  for (int e = 0; e < G::kEpc; ++e) part.acc[e] = 0.f;
+  if (n > 0) fwave_attention_window<D, BF16KV>(a, row, t0, n, qr, lane, part);
+  const bool valid = len > 0 && ldev == t.past[b];
+  if (units == 1) {
+    if (j == 0) {
+#pragma unroll
+      for (int e = 0; e < G::kEpc; ++e) {
+        const float o = (valid && part.z > 0.f) ? part.acc[e] / part.z : __builtin_nanf("");
+        store_elem(a.out, size_t(row) * D + size_t(c) * G::kEpc + e, a.out_dtype, o);
+      }
+    }
+  } else if (slot < a.ngroups) {  // always, by the host's count of slots
+    const size_t rec = size_t(row) * a.ngroups + slot;
+    if (j == 0) {
+      f4* o = reinterpret_cast<f4*>(a.part_y + rec * D + size_t(c) * G::kEpc);
+#pragma unroll
+      for (int w = 0; w < G::kEpc / 4; ++w)
+        o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
+    }
+    if (lane == 0) {
+      a.part_mz[rec * 2] = part.m;
+      a.part_mz[rec * 2 + 1] = part.z;
+    }
+  }
+}
+
+// Merge of the float balanced work list: one wave per row of two or more
+// units (the others were written by the decode launch).
+template <int D>
+__device__ __forceinline__ void fmerge_flat_body(const ppk::FloatMergeFlatArgs& fa) {
+  const ppk::FloatMergeArgs& a = fa.m;
+  const ppk::FlatTable& t = fa.t;
+  constexpr int EPL = D / ppk::kWave;
+  const int lane = threadIdx.x;
+  const uint32_t row = blockIdx.x;
+  const uint32_t b = row / a.heads;
+  const uint32_t units = t.units[b];
+  if (units < 2) return;  // uniform per wave
+  const uint32_t ldev = a.lengths[b];
+  float m, zsum, y[EPL];
+  combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D,
+                     min(units, a.nsplits), lane, [] { return -INFINITY; }, m, zsum, y);
+  const bool valid = t.len[b] > 0 && ldev == t.past[b];
+  const size_t base = size_t(row) * D + size_t(lane) * EPL;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e)
+    store_elem(a.out, base + e, a.out_dtype, (valid && zsum > 0.f) ? y[e] / zsum : __builtin_nanf(""));
 }
 
 // ---------------------------------------------------------------------------
@@ -2052,6 +2238,21 @@ PPK_ATTN_FLAT(256)
 PPK_FLOAT_ATTN(64)
 PPK_FLOAT_ATTN(128)
 PPK_FLOAT_ATTN(256)
+
+#define PPK_FLOAT_ATTN_FLAT(D)                                                                                 \
+  extern "C" __global__ __launch_bounds__(512) void ppk_fdecode_flat_bf16_d##D(ppk::FloatDecodeFlatArgs a) { \
+    fdecode_flat_body<D, true>(a);                                                                             \
+  }                                                                                                            \
+  extern "C" __global__ __launch_bounds__(512) void ppk_fdecode_flat_f32_d##D(ppk::FloatDecodeFlatArgs a) {  \
+    fdecode_flat_body<D, false>(a);                                                                            \
+  }                                                                                                            \
+  extern "C" __global__ __launch_bounds__(64) void ppk_fmerge_flat_d##D(ppk::FloatMergeFlatArgs a) {          \
+    fmerge_flat_body<D>(a);                                                                                    \
+  }
+PPK_FLOAT_ATTN_FLAT(64)
+PPK_FLOAT_ATTN_FLAT(128)
+PPK_FLOAT_ATTN_FLAT(256)
+#undef PPK_FLOAT_ATTN_FLAT
 
 extern "C" __global__ __launch_bounds__(256) void ppk_renyi_sample(ppk::RenyiArgs a) { renyi_sample_body(a); }
 

@@ -62,7 +62,7 @@ class PpkFloatAttentionArgs(ctypes.Structure):
                 ("max_length", _u32), ("softmax_scale", _f32), ("reserved", _u32),
                 ("q_row_stride", _u64), ("k_row_stride", _u64), ("v_row_stride", _u64),
                 ("q", _ptr), ("k", _ptr), ("v", _ptr), ("lengths", _ptr), ("out", _ptr), ("workspace", _ptr),
-                ("workspace_bytes", _u64)]
+                ("workspace_bytes", _u64), ("lengths_host", _ptr)]
 
 
 class PpkRenyiSampleArgs(ctypes.Structure):

@@ -27,8 +27,11 @@ _KV_DTYPES = {torch.bfloat16: _abi.PPK_BF16, torch.float32: _abi.PPK_F32}
 
 def decode_attention_args(q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
                           out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-                          softmax_scale: float = 0.0) -> tuple[_abi.PpkFloatAttentionArgs, torch.Tensor]:
-    """Validate like fused_attention::decode_attention and build the ABI block (workspace unset)."""
+                          softmax_scale: float = 0.0,
+                          lengths_host=None) -> tuple[_abi.PpkFloatAttentionArgs, torch.Tensor]:
+    """Validate like fused_attention::decode_attention and build the ABI block (workspace unset).
+    lengths_host: an optional host copy of `lengths` (a sequence of ints), with which the library balances
+    ragged batches."""
     _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "fused decode attention requires 3-d q/k/v")
     rows, query, width = q.shape
     key_rows, length, key_width = k.shape
@@ -56,7 +59,13 @@ def decode_attention_args(q, k, v, lengths, heads: int, split_tokens: int = 0, *
         q_row_stride=q.stride(0), k_row_stride=k.stride(0), v_row_stride=v.stride(0),
         q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
         lengths=lengths.data_ptr() if lengths is not None else None, out=out.data_ptr(), workspace=None,
-        workspace_bytes=0)
+        workspace_bytes=0, lengths_host=None)
+    if lengths_host is not None:
+        host = [int(x) for x in lengths_host]
+        _require(lengths is not None and len(host) == rows // heads and all(0 <= x < 2 ** 32 for x in host),
+                 "fused attention host lengths require device lengths of the same batch")
+        a._lengths_host = (ctypes.c_uint32 * len(host))(*host)  # kept alive with the argument block
+        a.lengths_host = ctypes.cast(a._lengths_host, ctypes.c_void_p).value
     return a, out
 
 
@@ -69,10 +78,12 @@ def plan(args: _abi.PpkFloatAttentionArgs, ctx: ctypes.c_void_p | None = None) -
 
 
 def decode_attention(q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
-                     out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0) -> torch.Tensor:
-    """fused_attention::decode_attention -> out [rows, 1, D] (float32 by default)."""
+                     out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0,
+                     lengths_host=None) -> torch.Tensor:
+    """fused_attention::decode_attention -> out [rows, 1, D] (float32 by default). lengths_host: optional
+    host copy of lengths."""
     a, out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length,
-                                   out_dtype=out_dtype, softmax_scale=softmax_scale)
+                                   out_dtype=out_dtype, softmax_scale=softmax_scale, lengths_host=lengths_host)
     ctx = context(q.device)
     nbytes = plan(a, ctx)[2]
     # Stream-ordered caching allocator: the block outlives the queued kernels.
@@ -88,9 +99,9 @@ class FloatDecodeAttention:
     __call__ only enqueues the kernels (bench and serving loops, graph capture)."""
 
     def __init__(self, q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
-                 out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32):
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32, lengths_host=None):
         self.args, self.out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length,
-                                                    out=out, out_dtype=out_dtype)
+                                                    out=out, out_dtype=out_dtype, lengths_host=lengths_host)
         self.ctx = context(q.device)
         self.split_tokens, self.ngroups, nbytes = plan(self.args, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)

@@ -205,8 +205,12 @@ def _float_args(**kw) -> _abi.PpkFloatAttentionArgs:
     a = _abi.PpkFloatAttentionArgs(struct_size=ctypes.sizeof(_abi.PpkFloatAttentionArgs), kv_dtype=_abi.PPK_BF16,
                                    q_dtype=0, out_dtype=0, rows=512, heads=16, size=8192, head_dim=128,
                                    split_tokens=0, max_length=0, softmax_scale=0.0)
+    host = kw.pop("lengths_host", None)
     for k, v in kw.items():
         setattr(a, k, v)
+    if host is not None:
+        a._lengths_host = (ctypes.c_uint32 * len(host))(*[int(x) for x in host])
+        a.lengths_host = ctypes.cast(a._lengths_host, ctypes.c_void_p).value
     return a
 
 
@@ -223,6 +227,44 @@ def test_float_plan_without_a_device():
     assert split == 34 and groups == -(-(-(-8192 // 34)) // 16)
     # max_length bounds the planned span.
     assert ppk.fused_attention.plan(_float_args(max_length=1024, lengths=8))[:2] == (256, 1)
+
+
+def test_float_balanced_plan_without_a_device():
+    """Host lengths of a ragged batch take the balanced plan of the int8 path (the same table from the same
+    rule); uniform lengths, an explicit split or a batch beyond 64 sequences keep the per-row plan."""
+    skew = [8192] * 4 + [512] * 28
+    per_row = ppk.fused_attention.plan(_float_args(lengths=8))
+    split, groups, nbytes = ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=skew))
+    units, share = _flat_units(skew, 16, 512, 8192, 8192, 2048)
+    assert (split, groups) == (share, max(units)) and groups > 1
+    assert nbytes == 512 * groups * 128 * 4 + -(-(512 * groups * 8) // 256) * 256
+    # The same table as the int8 plan of the same lengths.
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=512, capacity=8192, max_past=8192, past_host=skew))[:2] == \
+        (split, groups)
+    assert ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=[8192] * 32)) == per_row
+    assert ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=skew, split_tokens=128)) == \
+        ppk.fused_attention.plan(_float_args(split_tokens=128))
+    many = [5000] + [10] * 79
+    assert ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8, lengths_host=many)) == \
+        ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8))
+    # Lengths beyond max_length count as empty rows (NaN): one live long row among them.
+    split, groups, _ = ppk.fused_attention.plan(_float_args(rows=64, heads=16, max_length=4000, lengths=8,
+                                                            lengths_host=[4000, 9000, 10, 0]))
+    units, share = _flat_units([4000, 9000, 10, 0], 16, 64, 8192, 4000, 2048)
+    assert (split, groups) == (share, max(units))
+    # A ragged batch whose longest row holds at most 512 KiB of K and V keeps the per-row plan (one launch
+    # there beats the balanced plan's two): bf16, D = 64, 1024 tokens is 256 KiB; f32 is 512 KiB.
+    short = [1024] * 4 + [64] * 28
+    for kv, d, flat in ((_abi.PPK_BF16, 64, False), (_abi.PPK_F32, 64, False), (_abi.PPK_F32, 128, True)):
+        base = dict(kv_dtype=kv, head_dim=d, size=1024, lengths=8)
+        got = ppk.fused_attention.plan(_float_args(lengths_host=short, **base))
+        assert (got != ppk.fused_attention.plan(_float_args(**base))) == flat, (kv, d)
+    # Host lengths need the device lengths; an argument block that ends before lengths_host is still taken.
+    with pytest.raises(ppk.PpkPreconditionError):
+        ppk.fused_attention.plan(_float_args(lengths_host=skew))
+    old = _float_args(lengths=8, lengths_host=skew)
+    old.struct_size = _abi.PpkFloatAttentionArgs.lengths_host.offset
+    assert ppk.fused_attention.plan(old) == per_row
 
 
 @pytest.mark.parametrize("bad", [dict(kv_dtype=_abi.PPK_F16), dict(head_dim=96), dict(size=0), dict(rows=30),
