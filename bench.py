@@ -215,12 +215,18 @@ def bench_float(args) -> int:
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
     kname = f"ppk_fdecode_{'flat_' if flat else ''}{args.kv}_d{D}"
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"ppk_fdecode_{args.kv}_d{D}_b{B}_h{H}_ctx{L}_traffic.json")
+    if args.lengths:
+        skew = args.lengths.replace(",", "_")
+        tpath = os.path.join(ROOT, "profiles", f"{kname}_h{H}_skew{skew}_traffic.json")
+        workload = f"H{H}D{D}skew{skew}{args.kv}"
+    else:
+        tpath = os.path.join(ROOT, "profiles", f"ppk_fdecode_{args.kv}_d{D}_b{B}_h{H}_ctx{L}_traffic.json")
+        workload = f"B{B}H{H}D{D}L{L}{args.kv}"
     if os.path.exists(tpath):
         try:
             with open(tpath) as f:
                 t = json.load(f)
-            if (t.get("split") == call.split_tokens and t.get("workload") == f"B{B}H{H}D{D}L{L}{args.kv}"
+            if (t.get("split") == call.split_tokens and t.get("workload") == workload
                     and t.get("kernel") == kname):
                 traffic = t.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
