@@ -221,19 +221,72 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   // Per history token: K and V codes plus two fp32 scales.
   AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
   // With the host's lengths of a ragged batch, the balanced plan gives every
-  // wave the same share of the live history. Measured on MI355X (B x H=16 x
-  // D=128, per step, per-row -> balanced): 4 sequences of 8192 tokens beside
-  // 28 of 512, 75 -> 43 us; B=16 of 256..16384 tokens, 103 -> 89 us; B=32 of
-  // 256..8192, 111 -> 103 us; B=64 of 64..4096, 113 -> 106 us; config 4 and
-  // config 3 within 2 %. Uniform lengths keep the per-row plan (B=32 x 8192:
-  // one launch, 166 us, against 171 us balanced).
+  // wave the same share of the live history. It is taken when the per-row
+  // plan's busiest CU would stream at least 1.2 x the history the balanced
+  // plan's busiest CU streams (the int8 kernel's rate is set per CU: the
+  // blocks of a long row all sit on one CU). Measured on MI355X (H = 16,
+  // bf16 q, D = 64 / 128, per step, per-row -> balanced), taken: 4 sequences
+  // of 8192 tokens beside 28 of 512, 41.3 -> 26.6 / 76.6 -> 42.8 us; 8 of
+  // 4096 beside 24 of 1024, 30.2 -> 27.3 / 53.2 -> 45.3 us; B = 16 of
+  // 256..16384, 62.4 -> 53.1 / 109.4 -> 96.4 us; B = 32 of 256..8192, 58.0
+  // -> 54.5 / 108.9 -> 97.9 us; B = 64 of 64..4096, 57.1 -> 55.6 / 106.5 ->
+  // 99.5 us; B = 8 of 1024..2048, 16.7 -> 15.0 / 18.5 -> 18.2 us; config 4
+  // 15.4 -> 17.0 / 20.8 -> 20.7 us. Kept per-row (the model's ratio below
+  // 1.2; balanced would have been slower): 16 of 2048 beside 16 of 1536,
+  // 22.8 / 39.1 us (balanced 27.5 / 44.5); 4 of 2048 beside 28 of 1024; 16
+  // of 8192 beside 16 of 6000; 2 of 4096 beside 30 of 3000; B = 32 of
+  // 4096..8192. Uniform lengths keep the per-row plan (B = 32 x 8192: one
+  // launch, 166 us, against 171 us balanced).
   const uint32_t* host = host_lengths(a);
   const uint64_t limit = std::min<uint64_t>(a.capacity, span);
   if (host && a.split_tokens == 0 && flat_pays(ctx, a.rows, a.heads, host, limit)) {
-    plan = plan_flat(ctx, a.rows, a.heads, host, limit, a.head_dim);
-    plan.span = uint32_t(span);
+    AttentionPlan flat = plan_flat(ctx, a.rows, a.heads, host, limit, a.head_dim);
+    const uint32_t cus = uint32_t(std::max(ctx ? ctx->cu_count : 256, 1));
+    if (5 * per_row_cu_peak(plan, a.rows, a.heads, host, limit, cus) >= 6 * flat_cu_peak(flat, a.heads, cus)) {
+      plan = flat;
+      plan.span = uint32_t(span);
+    }
   }
   return plan;
+}
+
+// Placement model of an all-resident launch: block i runs on CU i mod cus
+// (the dispatcher deals blocks round-robin over the XCDs and, within one,
+// over its CUs). Returns the most live history tokens one CU streams.
+uint64_t per_row_cu_peak(const AttentionPlan& p, uint32_t rows, uint32_t heads, const uint32_t* host,
+                         uint64_t limit, uint32_t cus) {
+  std::vector<uint64_t> load(cus, 0);
+  const uint64_t per_block = uint64_t(p.waves) * p.split;  // tokens of a row one block covers
+  for (uint32_t r = 0; r < rows; ++r) {
+    const uint64_t len = host[r / heads] <= limit ? host[r / heads] : 0;
+    for (uint64_t g = 0; g < p.ngroups && g * per_block < len; ++g)  // blocks numbered group-major
+      load[(g * rows + r) % cus] += std::min(per_block, len - g * per_block);
+  }
+  return *std::max_element(load.begin(), load.end());
+}
+
+uint64_t flat_cu_peak(const AttentionPlan& p, uint32_t heads, uint32_t cus) {
+  std::vector<uint64_t> load(cus, 0);
+  const FlatTable& t = p.table;
+  uint64_t unit = 0;  // unit u on block u / waves (the int8 kernel's assignment)
+  for (uint32_t b = 0; b < t.batch; ++b)
+    for (uint32_t h = 0; h < heads; ++h)
+      for (uint32_t s = 0; s < t.units[b]; ++s, ++unit) {
+        const uint64_t t0 = uint64_t(s) * t.share;
+        if (t.len[b] > t0) load[(unit / p.waves) % cus] += std::min<uint64_t>(t.share, t.len[b] - t0);
+      }
+  return *std::max_element(load.begin(), load.end());
+}
+
+bool per_row_waves_uneven(uint32_t batch, const uint32_t* host, uint64_t limit, uint32_t split) {
+  uint64_t tokens = 0, waves = 0, most = 0;
+  for (uint32_t b = 0; b < batch; ++b) {
+    const uint64_t len = host[b] <= limit ? host[b] : 0;
+    tokens += len;
+    waves += (len + split - 1) / split;
+    most = std::max(most, std::min<uint64_t>(len, split));
+  }
+  return waves > 0 && most * waves * 10 > tokens * 11;
 }
 
 uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit) {
@@ -593,18 +646,28 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   AttentionPlan plan =
       plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
   // With the host's copy of the lengths, a ragged batch takes the balanced
-  // plan (as the int8 path does) once its longest row holds more than
-  // 512 KiB of K and V. Measured on MI355X (bf16, H = 16, per step,
-  // per-row -> balanced): 4 sequences of 8192 tokens beside 28 of 512,
-  // D = 64 57.1 -> 38.5 us, D = 128 111.8 -> 68.9 us; 2 of 16384 beside 14
-  // of 256, D = 64 74.0 -> 30.3 us, D = 128 147.7 -> 53.8 us; 4 of 1024
-  // beside 28 of 64 (256 / 512 KiB rows), D = 64 9.3 -> 11.5 us (the merge
-  // launch costs more than the balance gains), D = 128 16.1 -> 15.9 us.
+  // plan (the int8 path's table) when its longest row holds more than
+  // 512 KiB of K and V and the per-row plan's waves are uneven (the most
+  // tokens a wave streams beyond 1.1 x the mean over the waves that stream
+  // any): the float kernel streams at the rate of its slowest waves, not
+  // CU by CU. Measured on MI355X (bf16, H = 16, D = 64 / 128, per step,
+  // per-row -> balanced), taken: 4 sequences of 8192 tokens beside 28 of
+  // 512, 57.3 -> 37.4 / 112.0 -> 67.1 us; 2 of 16384 beside 14 of 256, 74.0
+  // -> 30.3 / 147.7 -> 53.8 us; 1 of 8192 beside 31 of 256, 53.7 -> 17.8 /
+  // 106.4 -> 28.8 us; B = 16 of 256..16384, 94.1 -> 90.7 / 187.3 -> 172.4
+  // us; B = 32 of 256..8192 and B = 64 of 64..4096 within 2 %. Kept
+  // per-row (balanced was slower): 8 of 4096 beside 24 of 1024, 39.3 /
+  // 71.4 us (balanced 41.7 / 78.2); config 4, 15.7 / 24.9 us (17.6 /
+  // 28.9); rows of at most 512 KiB, e.g. 4 of 1024 beside 28 of 64 at
+  // D = 64, 9.3 us (11.5: the merge launch costs more than the balance
+  // gains).
   constexpr uint64_t kFloatFlatMinRowBytes = 512u << 10;
   const uint32_t* host = host_lengths(a);
   require(!host || a.lengths, "float attention lengths_host needs the device lengths");
+  const uint32_t batch = a.rows / a.heads;
   if (host && a.split_tokens == 0 && flat_pays(ctx, a.rows, a.heads, host, span) &&
-      longest_live(host, a.rows / a.heads, span) * 2 * eb * a.head_dim > kFloatFlatMinRowBytes)
+      longest_live(host, batch, span) * 2 * eb * a.head_dim > kFloatFlatMinRowBytes &&
+      per_row_waves_uneven(batch, host, span, plan.split))
     plan = plan_flat(ctx, a.rows, a.heads, host, span, a.head_dim);
   plan.span = uint32_t(span);
   return plan;

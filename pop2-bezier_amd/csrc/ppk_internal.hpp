@@ -183,6 +183,15 @@ AttentionPlan plan_flat(const ppk_context* ctx, uint32_t rows, uint32_t heads, c
 bool flat_pays(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t limit);
 // The most live tokens of any of `batch` sequences (a length above limit has none).
 uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit);
+// The most live history tokens one CU streams under a per-row plan p or a
+// balanced plan (block i on CU i mod cus, as an all-resident launch is
+// placed).
+uint64_t per_row_cu_peak(const AttentionPlan& p, uint32_t rows, uint32_t heads, const uint32_t* host,
+                         uint64_t limit, uint32_t cus);
+uint64_t flat_cu_peak(const AttentionPlan& p, uint32_t heads, uint32_t cus);
+// Whether the per-row plan's waves of `split` tokens are uneven: the most
+// tokens one streams beyond 1.1 x the mean over those that stream any.
+bool per_row_waves_uneven(uint32_t batch, const uint32_t* host, uint64_t limit, uint32_t split);
 AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttentionArgs& a);
 
 void run_quantize(ppk_context* ctx, hipStream_t stream, const PpkQuantizeArgs& a);

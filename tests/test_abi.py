@@ -114,16 +114,58 @@ def test_plan_sizes_workspace_without_a_device():
     # Uniform host lengths keep the per-row plan.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048, past_host=[2048])) == \
         (split, groups, nbytes)
-    # Ragged host lengths (longest row beyond 1.1 x the mean): the balanced plan over 2048 waves (8 per CU);
-    # the least unit (>= 64 tokens) whose units fit is 64, so rows of 2048 tokens are 32 units (record slots).
-    split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(rows=16, heads=8, capacity=2049, max_past=2048,
-                                                            past_host=[2048, 1000]))
-    assert split == 64 and groups == 32 and nbytes == 16 * 32 * 128 * 4 + 16 * 32 * 2 * 4
-    # Short ragged rows with host lengths: every row one unit, so no records and no merge launch.
+    # Ragged host lengths whose per-row plan loads one CU with 1.2 x what the balanced plan's busiest CU
+    # streams: the balanced plan over 2048 waves (8 per CU). 4 sequences of 8192 tokens beside 28 of 512: the
+    # least unit (>= 64 tokens) whose units fit is 456, so rows of 8192 tokens are 18 units (record slots).
+    skew = [8192] * 4 + [512] * 28
+    split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(past_host=skew))
+    assert split == 456 and groups == 18 and nbytes == 512 * 18 * 128 * 4 + 512 * 18 * 2 * 4
+    # Few ragged rows: the per-row plan already spreads them over every CU (16 two-wave blocks per row), while
+    # the balanced plan's 384 units would fill only 96 CUs: per-row kept.
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=16, heads=8, capacity=2049, max_past=2048,
+                                           past_host=[2048, 1000])) == (64, 16, 16 * 16 * 128 * 4 + 16 * 16 * 8)
+    # Short ragged rows with host lengths: the one-block-per-row plan puts each row on its own CU, the balanced
+    # plan four rows on one: per-row kept.
+    per_row = ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900))
     assert ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900,
-                                           past_host=[10, 0, 60, 64])) == (64, 1, 0)
+                                           past_host=[10, 0, 60, 64])) == per_row
     # Few short rows (config 1 shape): one block per row, one launch.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=513, max_past=512, head_dim=64)) == (64, 1, 0)
+
+
+def _per_row_waves(rows, span, split, token_bytes, cus=256):
+    """Waves per block of the per-row plan with automatic split `split`: a row's ceil(span / split) waves in
+    one block of at most min(16, 16384 / split); rows fewer than the CUs holding more than 128 KiB are cut
+    into blocks of about 256 KiB, then smaller until the blocks cover every CU."""
+    per_row = -(-span // split)
+    most = max(1, min(16, 16384 // split))
+    if rows < cus and span * token_bytes > 128 << 10:
+        w = max(1, min(most, (256 << 10) // (split * token_bytes)))
+        while w > 1 and rows * -(-per_row // w) < cus:
+            w -= 1
+        most = w
+    return min(per_row, most)
+
+
+def _cu_peaks(lens, heads, per_row, share, cus=256, waves_per_block=4):
+    """Most live tokens one CU streams under the per-row plan (split S, W waves per block, G groups; block
+    g * rows + r on CU (g * rows + r) mod cus) and under the balanced plan (unit u on block u / 4, same
+    placement); lens are the live lengths per sequence."""
+    S, W, G = per_row
+    rows = len(lens) * heads
+    row_cu = np.zeros(cus, np.int64)
+    for r in range(rows):
+        n = lens[r // heads]
+        for g in range(G):
+            row_cu[(g * rows + r) % cus] += max(0, min(W * S, n - g * W * S))
+    flat_cu = np.zeros(cus, np.int64)
+    u = 0
+    for n in lens:
+        for _ in range(heads):
+            for s in range(max(1, -(-n // share))):
+                flat_cu[(u // waves_per_block) % cus] += max(0, min(share, n - s * share))
+                u += 1
+    return int(row_cu.max()), int(flat_cu.max())
 
 
 def _flat_units(past, heads, rows, capacity, span, waves, min_unit=64):
@@ -141,8 +183,9 @@ def _flat_units(past, heads, rows, capacity, span, waves, min_unit=64):
 def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
     """Ragged batches of up to 64 sequences (zero, tiny, capacity-long and past-capacity rows) with host
     lengths: the balanced plan is taken when the longest live row exceeds 1.1 x the mean (and rows fit half
-    the waves); its units cover every live token, never outnumber the launched waves (2048 on the 256 CUs
-    assumed without a context), and the record slots per row are the most units of any row."""
+    the waves) and the per-row plan's busiest CU streams at least 1.2 x what the balanced plan's does; its
+    units cover every live token, never outnumber the launched waves (2048 on the 256 CUs assumed without a
+    context), and the record slots per row are the most units of any row."""
     rng = np.random.default_rng(SEED + heads + d)
     checked = 0
     for trial in range(500):
@@ -170,6 +213,11 @@ def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
             assert (split, groups, nbytes) == per_row
             continue
         units, share = _flat_units([int(p) for p in past], heads, rows, cap, span, 2048)
+        S, G = per_row[:2]
+        row_peak, flat_peak = _cu_peaks(live, heads, (S, _per_row_waves(rows, span, S, 2 * d + 8), G), share)
+        if 5 * row_peak < 6 * flat_peak:
+            assert (split, groups, nbytes) == per_row, "per-row plan kept"
+            continue
         assert split == share and groups == max(units)
         assert sum(units) <= 2048, "every unit has a wave"
         for p, u in zip(np.repeat(past, heads), units):
@@ -248,10 +296,19 @@ def test_float_balanced_plan_without_a_device():
     assert ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8, lengths_host=many)) == \
         ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8))
     # Lengths beyond max_length count as empty rows (NaN): one live long row among them.
-    split, groups, _ = ppk.fused_attention.plan(_float_args(rows=64, heads=16, max_length=4000, lengths=8,
-                                                            lengths_host=[4000, 9000, 10, 0]))
-    units, share = _flat_units([4000, 9000, 10, 0], 16, 64, 8192, 4000, 2048)
+    host = [8000, 9000, 10, 0] + [600] * 28
+    split, groups, _ = ppk.fused_attention.plan(_float_args(max_length=8100, lengths=8, lengths_host=host))
+    units, share = _flat_units(host, 16, 512, 8192, 8100, 2048)
     assert (split, groups) == (share, max(units))
+    # Few rows: the per-row plan's waves (128 tokens, 33 per row of 4000) are already even; kept.
+    few = _float_args(rows=64, heads=16, max_length=4000, lengths=8)
+    assert ppk.fused_attention.plan(_float_args(rows=64, heads=16, max_length=4000, lengths=8,
+                                                lengths_host=[4000, 9000, 10, 0])) == ppk.fused_attention.plan(few)
+    # Even per-row waves in a large batch: 8 sequences of 4096 tokens beside 24 of 1024 take 1024-token waves
+    # everywhere (the balanced plan measured slower there); kept.
+    even = [4096] * 8 + [1024] * 24
+    assert ppk.fused_attention.plan(_float_args(size=4096, lengths=8, lengths_host=even)) == \
+        ppk.fused_attention.plan(_float_args(size=4096, lengths=8))
     # A ragged batch whose longest row holds at most 512 KiB of K and V keeps the per-row plan (one launch
     # there beats the balanced plan's two): bf16, D = 64, 1024 tokens is 256 KiB; f32 is 512 KiB.
     short = [1024] * 4 + [64] * 28

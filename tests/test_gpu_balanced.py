@@ -1,7 +1,9 @@
 """GPU parity of the balanced plan for ragged batches (ppk_decode_flat + ppk_attn_merge_flat).
 
 The plan is taken when the caller passes its host copy of the lengths
-(PpkAttentionArgs.past_host) and rows would otherwise span several blocks.
+(PpkAttentionArgs.past_host) for a ragged batch whose per-row plan would
+load one CU with at least 1.2 x the history the balanced plan's busiest CU
+streams; every test below asserts that its shape takes it.
 Bars as for the per-row plan (tests/test_gpu_attention.py): against the f64
 oracle, max abs error <= 2e-3 and max relative error <= 1e-2 (|oracle| >=
 1e-3); the bf16-history mode within 2e-5 absolute; appended codes and scales
@@ -28,12 +30,18 @@ def _plan(c: Case, past_host, max_past=0, **kw):
     return ppk.int8_kv_ops.plan(a, ppk.context(c.q.device))
 
 
+def _balanced(c: Case, past_host, max_past=0) -> int:
+    """Asserts the host lengths change the plan (the balanced one) and returns its record slots per row."""
+    plan = _plan(c, past_host, max_past)
+    assert plan != _plan(c, None, max_past), "the balanced plan is taken"
+    return plan[1]
+
+
 def test_config4_ragged_balanced(device):
     """BASELINE config 4 (B=8, H=16, D=128, lengths U[256, 4096], bf16 q) through the balanced plan."""
     lengths = [int(x) for x in np.random.default_rng(SEED).integers(256, 4097, size=8)]
     c = Case(device, 8, 16, 128, lengths, max(lengths) + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
-    split, slots, _ = _plan(c, lengths, max_past=max(lengths))
-    assert slots > 1, "config 4 rows span several units"
+    assert _balanced(c, lengths, max_past=max(lengths)) > 1, "config 4 rows span several units"
     ref = c.reference()
     assert_close(c.run(past_host=lengths, max_past=max(lengths)), ref, what="config 4 balanced")
     assert_close(c.run(past_host=lengths), ref, what="config 4 balanced, span = capacity")
@@ -43,19 +51,20 @@ def test_config4_ragged_balanced(device):
 def test_edge_lengths_balanced(device, d):
     """Empty rows, one-token rows, rows at the capacity, rows past it (NaN), single-unit rows beside rows
     of many units."""
-    lengths = [0, 1, 700, 2000, 2049, 3, 2048, 5000]
-    c = Case(device, 8, 4, d, lengths, 2048)
-    _, slots, _ = _plan(c, lengths)
-    assert slots > 1
+    lengths = [0, 1, 700, 2000, 2049, 3, 2048, 5000] + [2000] * 4 + [10] * 20
+    c = Case(device, 32, 8, d, lengths, 2048)
+    assert _balanced(c, lengths) > 1
     got = c.run(past_host=lengths)
     ref = c.reference()
-    assert np.isnan(got[4 * 4:5 * 4]).all() and np.isnan(got[7 * 4:]).all()
+    bad = np.repeat(np.array(lengths) > 2048, 8)
+    assert np.isnan(got[bad]).all() and not np.isnan(got[~bad]).any()
     assert_close(got, ref, what=f"edge lengths d={d}")
 
 
 def test_rows_beyond_max_past_give_nan(device):
-    lengths = [300, 1200, 40, 1100]
-    c = Case(device, 4, 8, 128, lengths, 1500)
+    lengths = [900, 1200, 40, 1100, 30, 950, 20, 10] * 4
+    c = Case(device, 32, 8, 128, lengths, 1500)
+    _balanced(c, lengths, max_past=1000)
     got = c.run(past_host=lengths, max_past=1000)
     ref = c.reference()
     bad = np.repeat(np.array(lengths) > 1000, 8)
@@ -63,11 +72,12 @@ def test_rows_beyond_max_past_give_nan(device):
     assert_close(got[~bad], ref[~bad], what="rows within max_past")
 
 
-def test_short_rows_are_one_launch(device):
-    """Every row within one unit: no records, no merge launch, outputs written by the decode launch."""
+def test_short_rows_keep_the_per_row_plan(device):
+    """Short ragged rows: one block per row puts every row on a CU of its own, so the host lengths change
+    nothing (one launch, no merge) and the result is the per-row plan's."""
     lengths = [10, 0, 60, 64]
     c = Case(device, 4, 16, 64, lengths, 1024)
-    assert _plan(c, lengths, max_past=900) == (64, 1, 0)
+    assert _plan(c, lengths, max_past=900) == _plan(c, None, max_past=900) == (64, 1, 0)
     ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_MERGE, reset=True)
     ppk.set_profiling(True)
     got = c.run(past_host=lengths, max_past=900)
@@ -80,6 +90,7 @@ def test_bf16_history_balanced(device):
     """The reference-exact mode (history rounded through bf16, int8_kv.cu:23-27) at the reference's 2e-5."""
     lengths = [900, 30, 2500, 1700]
     c = Case(device, 4, 8, 64, lengths, 2600)
+    _balanced(c, lengths)
     got = c.run(past_host=lengths, bf16_history=True)
     assert_close(got, c.reference(history_bf16=True), atol=2e-5, rtol=0, what="balanced bf16 history")
 
@@ -89,6 +100,7 @@ def test_bf16_history_balanced(device):
 def test_balanced_dtypes(device, q_dtype, out_dtype):
     lengths = [1500, 333, 2900]
     c = Case(device, 3, 8, 128, lengths, 3000, q_dtype=q_dtype, scratch_dtype=q_dtype)
+    _balanced(c, lengths)
     got = c.run(past_host=lengths, out_dtype=out_dtype)
     narrow = {torch.float32: None, torch.bfloat16: "bf16", torch.float16: "f16"}[out_dtype]
     assert_close(got, c.reference(), what=f"balanced {q_dtype} -> {out_dtype}", out_dtype=narrow)
@@ -100,6 +112,7 @@ def test_decode_step_balanced_appends_and_attends(device):
     lengths = [2047, 0, 610, 1300, 2048]
     B, H, D, cap = 5, 8, 128, 2048
     c = Case(device, B, H, D, lengths, cap, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    _balanced(c, lengths)
     ref = c.reference()
     before = [t.clone() for t in (c.kc, c.vc, c.ks, c.vs)]
     flags = torch.zeros(1, dtype=torch.int32, device=device)
@@ -127,9 +140,10 @@ def test_decode_step_balanced_appends_and_attends(device):
 def test_stale_host_lengths_give_nan_and_a_flag(device):
     """A host copy that no longer matches the device's lengths never yields a wrong row: the sequences whose
     device value differs give NaN and the step's flags carry PPK_FLAG_STALE_LENGTHS; the others stay right."""
-    lengths = [1500, 700, 2000, 20]
-    c = Case(device, 4, 8, 128, lengths, 2100)
-    stale = [1500, 650, 2000, 21]  # sequences 1 and 3 differ
+    lengths = [1500, 700, 2000, 20] + [1900] * 2 + [30] * 26
+    c = Case(device, 32, 8, 128, lengths, 2100)
+    stale = [1500, 650, 2000, 21] + lengths[4:]  # sequences 1 and 3 differ
+    _balanced(c, stale)
     ref = c.reference()
     flags = torch.zeros(1, dtype=torch.int32, device=device)
     out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, flags=flags, past_host=stale)
@@ -147,8 +161,9 @@ def test_balanced_plan_through_the_noalloc_entry_point(device):
 
     from ppk import _abi
 
-    lengths = [3000, 120, 1800]
-    c = Case(device, 3, 8, 128, lengths, 3001, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    lengths = [3000, 120, 1800] + [50] * 29
+    c = Case(device, 32, 8, 128, lengths, 3001, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    _balanced(c, lengths)
     ref = c.reference()
     a, out = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H,
                                             past_host=lengths)
@@ -164,6 +179,7 @@ def test_balanced_step_captured_in_a_hip_graph(device):
     arguments; no memset)."""
     lengths = [2500, 64, 900, 1700]
     c = Case(device, 4, 16, 128, lengths, 2600, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    _balanced(c, lengths)
     st = ppk.DecodeAttention(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, past_host=lengths)
     eager = st().clone()
     torch.cuda.synchronize()
