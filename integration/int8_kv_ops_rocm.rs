@@ -32,118 +32,17 @@
 
 use super::*;
 use crate::model::ppk_ffi as ffi;
+use crate::model::ppk_ffi::{context, device_context, dtype_code, span, workspace, Bound, STREAM};
 use candle_core::{
     backend::BackendStorage, CpuStorage, CustomOp1, CustomOp2, CustomOp3, InplaceOp1, Layout, RocmStorage, Shape,
-    Storage,
 };
-use std::{
-    collections::HashMap,
-    ffi::c_void,
-    sync::{Mutex, OnceLock, RwLockReadGuard},
-};
+use std::ffi::c_void;
 
 /// History dequantisation of the attention ops. PPK_ATTN_BF16_HISTORY gives
 /// the reference's results (pp_i8_load rounds each history value to bf16,
 /// app/src/model/int8_kv.cu:23-27); 0 dequantises in f32 (closer to the
 /// unquantised attention, and what the library is measured with).
 pub const HISTORY: u32 = ffi::PPK_ATTN_BF16_HISTORY;
-
-const STREAM: *mut c_void = std::ptr::null_mut();
-
-struct Context(*mut ffi::ppk_context);
-// SAFETY: a ppk_context may be used from any thread; the library serialises
-// its own state.
-unsafe impl Send for Context {}
-
-/// The library context of a HIP device, created once per process (the module
-/// cache of app/src/model/hip_kernel.rs:45,107) and kept until exit. Creation
-/// loads the gfx950 code object beside libppk.so and resolves every kernel.
-fn context(ordinal: usize) -> candle_core::Result<*mut ffi::ppk_context> {
-    static CONTEXTS: OnceLock<Mutex<HashMap<usize, Context>>> = OnceLock::new();
-    let mut map = CONTEXTS
-        .get_or_init(|| Mutex::new(HashMap::new()))
-        .lock()
-        .map_err(|_| candle_core::Error::Msg("HIP_PREPARATION: ppk context cache poisoned".into()))?;
-    if let Some(ctx) = map.get(&ordinal) {
-        return Ok(ctx.0);
-    }
-    if unsafe { ffi::ppk_abi_version() } != ffi::PPK_ABI_VERSION {
-        candle_core::bail!("HIP_PREPARATION: libppk ABI version differs from ppk_ffi.rs");
-    }
-    let mut ctx = std::ptr::null_mut();
-    ffi::check(unsafe { ffi::ppk_context_create(ordinal as i32, std::ptr::null(), &mut ctx) })?;
-    map.insert(ordinal, Context(ctx));
-    Ok(ctx)
-}
-
-fn device_context(device: &Device) -> candle_core::Result<*mut ffi::ppk_context> {
-    match device {
-        Device::Rocm(d) => context(d.ordinal()),
-        _ => candle_core::bail!("HIP_PREPARATION: INT8 KV ROCm op on a non-ROCm device"),
-    }
-}
-
-fn dtype_code(dtype: DType) -> candle_core::Result<u32> {
-    match dtype {
-        DType::F32 => Ok(ffi::PPK_F32),
-        DType::BF16 => Ok(ffi::PPK_BF16),
-        DType::F16 => Ok(ffi::PPK_F16),
-        other => candle_core::bail!("HIP_PREPARATION: INT8 KV does not take {other:?} tensors"),
-    }
-}
-
-/// Device address of a dense view of `elems` elements, after checking that
-/// the view lies inside its storage (as checked_span does, hip_attention.rs:63-69).
-fn span(
-    storage: &RocmStorage,
-    layout: &Layout,
-    elems: usize,
-    elem_bytes: usize,
-    what: &str,
-) -> candle_core::Result<*mut c_void> {
-    let (start, end) = layout
-        .contiguous_offsets()
-        .ok_or_else(|| candle_core::Error::Msg(format!("HIP_PREPARATION: {what} is not contiguous")))?;
-    if end - start != elems || end.checked_mul(elem_bytes).is_none_or(|n| n > storage.byte_len()) {
-        candle_core::bail!("HIP_PREPARATION: {what} view exceeds its storage");
-    }
-    Ok(unsafe { storage.device_ptr().add(start * elem_bytes) } as *mut c_void)
-}
-
-/// The read guards of the side tensors an op reads or writes, held until the
-/// library call has been enqueued (as the reference holds its `lengths`
-/// storage, hip_attention.rs:93-101).
-struct Bound<'a> {
-    guards: Vec<RwLockReadGuard<'a, Storage>>,
-}
-
-impl<'a> Bound<'a> {
-    fn new() -> Self {
-        Bound { guards: Vec::new() }
-    }
-
-    fn ptr(&mut self, t: &'a Tensor, dtype: DType, what: &str) -> candle_core::Result<*mut c_void> {
-        if t.dtype() != dtype {
-            candle_core::bail!("HIP_PREPARATION: {what} must be {dtype:?}");
-        }
-        let (guard, layout) = t.storage_and_layout();
-        let ptr = match &*guard {
-            Storage::Rocm(s) => span(s, layout, t.elem_count(), dtype.size_in_bytes(), what)?,
-            _ => candle_core::bail!("HIP_PREPARATION: {what} is not on the ROCm device"),
-        };
-        self.guards.push(guard);
-        Ok(ptr)
-    }
-}
-
-fn workspace(device: &candle_core::rocm_backend::RocmDevice, bytes: u64) -> candle_core::Result<Option<RocmStorage>> {
-    use candle_core::backend::BackendDevice;
-    if bytes == 0 {
-        return Ok(None);
-    }
-    // hipMalloc memory: 256-byte aligned, as the library requires.
-    Ok(Some(unsafe { device.alloc_uninit(&Shape::from(bytes as usize), DType::U8)? }))
-}
 
 // ---- quantize / dequantize -------------------------------------------------
 

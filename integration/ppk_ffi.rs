@@ -19,7 +19,12 @@
 
 #![allow(non_camel_case_types, dead_code)]
 
-use std::ffi::{c_char, c_void, CStr};
+use candle_core::{backend::BackendStorage, DType, Device, Layout, RocmStorage, Shape, Storage, Tensor};
+use std::{
+    collections::HashMap,
+    ffi::{c_char, c_void, CStr},
+    sync::{Mutex, OnceLock, RwLockReadGuard},
+};
 
 pub const PPK_ABI_VERSION: u32 = 1;
 
@@ -408,4 +413,109 @@ pub fn check(status: i32) -> candle_core::Result<()> {
         PPK_OK => Ok(()),
         _ => Err(candle_core::Error::Msg(last_error())),
     }
+}
+
+// ---- Candle helpers shared by the ROCm ops ------------------------------------
+// (int8_kv_ops_rocm.rs, hip_attention_rocm.rs, hip_sampling_rocm.rs)
+
+/// The stream of every library call: the null HIP stream, the one the
+/// reference's own HIP kernels are launched on (hip_kernel::launch ->
+/// HipModule::launch), so the calls stay ordered with them.
+pub const STREAM: *mut c_void = std::ptr::null_mut();
+
+struct Context(*mut ppk_context);
+// SAFETY: a ppk_context may be used from any thread; the library serialises
+// its own state.
+unsafe impl Send for Context {}
+
+/// The library context of a HIP device, created once per process (the module
+/// cache of app/src/model/hip_kernel.rs:45,107) and kept until exit. Creation
+/// loads the gfx950 code object beside libppk.so and resolves every kernel.
+pub fn context(ordinal: usize) -> candle_core::Result<*mut ppk_context> {
+    static CONTEXTS: OnceLock<Mutex<HashMap<usize, Context>>> = OnceLock::new();
+    let mut map = CONTEXTS
+        .get_or_init(|| Mutex::new(HashMap::new()))
+        .lock()
+        .map_err(|_| candle_core::Error::Msg("HIP_PREPARATION: ppk context cache poisoned".into()))?;
+    if let Some(ctx) = map.get(&ordinal) {
+        return Ok(ctx.0);
+    }
+    if unsafe { ppk_abi_version() } != PPK_ABI_VERSION {
+        candle_core::bail!("HIP_PREPARATION: libppk ABI version differs from ppk_ffi.rs");
+    }
+    let mut ctx = std::ptr::null_mut();
+    check(unsafe { ppk_context_create(ordinal as i32, std::ptr::null(), &mut ctx) })?;
+    map.insert(ordinal, Context(ctx));
+    Ok(ctx)
+}
+
+pub fn device_context(device: &Device) -> candle_core::Result<*mut ppk_context> {
+    match device {
+        Device::Rocm(d) => context(d.ordinal()),
+        _ => candle_core::bail!("HIP_PREPARATION: libppk op on a non-ROCm device"),
+    }
+}
+
+pub fn dtype_code(dtype: DType) -> candle_core::Result<u32> {
+    match dtype {
+        DType::F32 => Ok(PPK_F32),
+        DType::BF16 => Ok(PPK_BF16),
+        DType::F16 => Ok(PPK_F16),
+        other => candle_core::bail!("HIP_PREPARATION: libppk does not take {other:?} tensors"),
+    }
+}
+
+/// Device address of a dense view of `elems` elements, after checking that
+/// the view lies inside its storage (as checked_span does, hip_attention.rs:63-69).
+pub fn span(
+    storage: &RocmStorage,
+    layout: &Layout,
+    elems: usize,
+    elem_bytes: usize,
+    what: &str,
+) -> candle_core::Result<*mut c_void> {
+    let (start, end) = layout
+        .contiguous_offsets()
+        .ok_or_else(|| candle_core::Error::Msg(format!("HIP_PREPARATION: {what} is not contiguous")))?;
+    if end - start != elems || end.checked_mul(elem_bytes).is_none_or(|n| n > storage.byte_len()) {
+        candle_core::bail!("HIP_PREPARATION: {what} view exceeds its storage");
+    }
+    Ok(unsafe { storage.device_ptr().add(start * elem_bytes) } as *mut c_void)
+}
+
+/// The read guards of the side tensors an op reads or writes, held until the
+/// library call has been enqueued (as the reference holds its `lengths`
+/// storage, hip_attention.rs:93-101).
+pub struct Bound<'a> {
+    guards: Vec<RwLockReadGuard<'a, Storage>>,
+}
+
+impl<'a> Bound<'a> {
+    pub fn new() -> Self {
+        Bound { guards: Vec::new() }
+    }
+
+    pub fn ptr(&mut self, t: &'a Tensor, dtype: DType, what: &str) -> candle_core::Result<*mut c_void> {
+        if t.dtype() != dtype {
+            candle_core::bail!("HIP_PREPARATION: {what} must be {dtype:?}");
+        }
+        let (guard, layout) = t.storage_and_layout();
+        let ptr = match &*guard {
+            Storage::Rocm(s) => span(s, layout, t.elem_count(), dtype.size_in_bytes(), what)?,
+            _ => candle_core::bail!("HIP_PREPARATION: {what} is not on the ROCm device"),
+        };
+        self.guards.push(guard);
+        Ok(ptr)
+    }
+}
+
+/// Device scratch of `bytes` (None for 0), released when the op returns, as
+/// the reference releases its `partial` buffer (hip_attention.rs:87-110).
+pub fn workspace(device: &candle_core::rocm_backend::RocmDevice, bytes: u64) -> candle_core::Result<Option<RocmStorage>> {
+    use candle_core::backend::BackendDevice;
+    if bytes == 0 {
+        return Ok(None);
+    }
+    // hipMalloc memory: 256-byte aligned, as the library requires.
+    Ok(Some(unsafe { device.alloc_uninit(&Shape::from(bytes as usize), DType::U8)? }))
 }

@@ -1,4 +1,5 @@
-"""The Rust drop-in (integration/ppk_ffi.rs, integration/int8_kv_ops_rocm.rs)
+"""The Rust drop-in (integration/ppk_ffi.rs and the ROCm ops files
+integration/int8_kv_ops_rocm.rs, hip_attention_rocm.rs, hip_sampling_rocm.rs)
 against the C header, without a Rust toolchain (there is none in this image).
 
 * every argument struct of include/ppk_int8_kv.h has a #[repr(C)] twin with
@@ -8,7 +9,7 @@ against the C header, without a Rust toolchain (there is none in this image).
 * every PPK_API function has an extern "C" declaration with the same
   parameters (pointer constness included) and return type;
 * the constants carry the header's values;
-* the ROCm ops file uses only names ppk_ffi.rs defines and only fields of the
+* the ROCm ops files use only names ppk_ffi.rs defines and only fields of the
   argument block each variable holds.
 """
 from __future__ import annotations
@@ -23,6 +24,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "ppk_int8_kv.h")
 FFI = os.path.join(ROOT, "integration", "ppk_ffi.rs")
 OPS = os.path.join(ROOT, "integration", "int8_kv_ops_rocm.rs")
+FLOAT_OPS = os.path.join(ROOT, "integration", "hip_attention_rocm.rs")
+SAMPLER_OPS = os.path.join(ROOT, "integration", "hip_sampling_rocm.rs")
+ALL_OPS = (OPS, FLOAT_OPS, SAMPLER_OPS)
 
 C_SCALARS = {"uint32_t": "u32", "int32_t": "i32", "uint64_t": "u64", "float": "f32", "double": "f64",
              "uint8_t": "u8", "char": "c_char", "void": "c_void"}
@@ -221,28 +225,59 @@ def test_constants_match_the_header():
         assert rust[k] == v, k
 
 
-def test_rocm_ops_use_only_declared_names_and_fields():
+def _declared() -> set[str]:
     ffi_text = _rust_text(FFI)
     declared = set(rust_functions()) | set(rust_constants()) | set(rust_structs())
-    declared |= set(re.findall(r"^pub fn (\w+)", ffi_text, flags=re.M))
-    ops = _rust_text(OPS)
+    for kind in ("fn", "struct", "const"):
+        declared |= set(re.findall(rf"^pub {kind} (\w+)", ffi_text, flags=re.M))
+    return declared
+
+
+@pytest.mark.parametrize("path", ALL_OPS, ids=os.path.basename)
+def test_rocm_ops_use_only_declared_names(path):
+    ops = _rust_text(path)
     used = set(re.findall(r"(?<!std::)\bffi::(\w+)", ops)) - {"c_void"}  # std::ffi's, imported by name
-    assert used and used <= declared, sorted(used - declared)
+    for names in re.findall(r"use crate::model::ppk_ffi::\{([^}]*)\};", ops):
+        used |= {n.strip() for n in names.split(",") if n.strip()}
+    assert used and used <= _declared(), sorted(used - _declared())
+    # Helpers imported by name are used (and so checked for their declaration above).
+    for names in re.findall(r"use crate::model::ppk_ffi::\{([^}]*)\};", ops):
+        for name in (n.strip() for n in names.split(",") if n.strip()):
+            assert len(re.findall(rf"\b{name}\b", ops)) > 1, f"{name} imported but unused"
+
+
+def test_rocm_ops_set_only_fields_of_their_argument_blocks():
     # Each argument block is built by ffi::args() and only its own fields are set (checked per function body,
     # where the variable names are bound).
     structs = rust_structs()
     seen = set()
-    for body in re.split(r"\n\s*(?:pub\(super\) )?fn ", ops)[1:]:
-        for var, ty in re.findall(r"let mut (\w+): ffi::(\w+) = ffi::args\(\);", body):
-            seen.add(ty)
-            fields = {f for f, _ in structs[ty]}
-            for field in re.findall(rf"\b{var}\.(\w+)\s*=", body):
-                assert field in fields, f"{ty}.{field}"
+    for path in ALL_OPS:
+        for body in re.split(r"\n\s*(?:pub(?:\((?:super|crate)\))? )?fn ", _rust_text(path))[1:]:
+            for var, ty in re.findall(r"let mut (\w+): ffi::(\w+) = ffi::args\(\);", body):
+                seen.add(ty)
+                fields = {f for f, _ in structs[ty]}
+                for field in re.findall(rf"\b{var}\.(\w+)\s*=", body):
+                    assert field in fields, f"{os.path.basename(path)}: {ty}.{field}"
     assert seen == {"PpkQuantizeArgs", "PpkDequantizeArgs", "PpkAttentionArgs", "PpkDecodeStepArgs",
-                    "PpkAppendArgs"}
+                    "PpkAppendArgs", "PpkFloatAttentionArgs", "PpkRenyiSampleArgs"}
+
+
+def test_rocm_ops_cover_the_reference_functions():
+    ops = _rust_text(OPS)
     # Every ROCm branch the header's int8 entry points replace is present.
     for fn in ("quantize", "dequantize", "attention", "decode_step", "commit_append", "prepare"):
         assert re.search(rf"pub\(super\) fn {fn}\(", ops), fn
     for call in ("ppk_quantize", "ppk_dequantize", "ppk_decode_attention", "ppk_decode_step",
                  "ppk_quantize_append", "ppk_prepare", "ppk_attention_workspace_bytes"):
         assert f"ffi::{call}(" in ops, call
+    # hip_attention.rs's three functions (hip_attention.rs:7,18,47) with the reference's visibility.
+    fl = _rust_text(FLOAT_OPS)
+    for vis, fn in (("crate", "prepare"), ("crate", "validate_split_k"), ("super", "decode_attention"),
+                    ("super", "decode_attention_with_host_lengths")):
+        assert re.search(rf"pub\({vis}\) fn {fn}\(", fl), fn
+    for call in ("ppk_float_decode_attention", "ppk_float_attention_plan", "ppk_float_attention_prepare"):
+        assert f"ffi::{call}(" in fl, call
+    # HipSampler::rocm_fwd's body (hip_sampling.rs:120-214).
+    sm = _rust_text(SAMPLER_OPS)
+    assert re.search(r"pub\(super\) fn rocm_fwd\(\s*op: &super::HipSampler,", sm)
+    assert "ffi::ppk_renyi_sample(" in sm
