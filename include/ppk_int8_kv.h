@@ -66,7 +66,17 @@ enum {
   /* Dequantise history as bf16(code * scale) before the dot products, exactly as
      pp_i8_load does (app/src/model/int8_kv.cu:23-27). Default (0) dequantises in
      fp32 with the per-token scale folded into the score and the probability. */
-  PPK_ATTN_BF16_HISTORY = 1u
+  PPK_ATTN_BF16_HISTORY = 1u,
+  /* Launch plan (no counterpart in the reference; the result does not depend
+     on it beyond fp32 summation order). With host lengths (past_host /
+     lengths_host) the library chooses between its per-row plan and the
+     balanced plan for ragged batches; these bits fix the choice. PER_ROW
+     ignores the host lengths for planning (they are still compared with the
+     device's). BALANCED needs the host lengths, split_tokens == 0, at most 64
+     sequences and rows at most 4 per CU; otherwise the call fails with status
+     1 and nothing enqueued. Setting both is an error. */
+  PPK_ATTN_PLAN_PER_ROW = 2u,
+  PPK_ATTN_PLAN_BALANCED = 4u
 };
 
 typedef struct ppk_context ppk_context;
@@ -260,7 +270,7 @@ typedef struct PpkFloatAttentionArgs {
   uint32_t split_tokens;   /* tokens per wave; 0 = automatic. Result does not depend on it. */
   uint32_t max_length;     /* host upper bound of max(lengths); 0 = size. Needs lengths. */
   float softmax_scale;     /* 0 = 1/sqrt(head_dim) (the reference's 0.125 at head_dim 64) */
-  uint32_t reserved;
+  uint32_t flags;          /* PPK_ATTN_PLAN_* (PPK_ATTN_BF16_HISTORY does not apply) */
   uint64_t q_row_stride;   /* elements between rows of q; 0 = head_dim */
   uint64_t k_row_stride;   /* elements between rows of k; 0 = size * head_dim; 16-byte multiple */
   uint64_t v_row_stride;   /* elements between rows of v; 0 = size * head_dim; 16-byte multiple */

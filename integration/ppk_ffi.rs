@@ -46,6 +46,10 @@ pub const PPK_FLAG_STALE_LENGTHS: u32 = 4;
 /// Attention flags: dequantise history as bf16(code * scale) before the dot
 /// products, exactly as pp_i8_load does (app/src/model/int8_kv.cu:23-27).
 pub const PPK_ATTN_BF16_HISTORY: u32 = 1;
+/// Launch plan with host lengths: force the per-row plan, or the balanced
+/// plan for ragged batches (default: the library chooses).
+pub const PPK_ATTN_PLAN_PER_ROW: u32 = 2;
+pub const PPK_ATTN_PLAN_BALANCED: u32 = 4;
 
 /// Bytes of the per-GPU array behind `ppk_decode_step_noalloc`.
 pub const PPK_NOALLOC_SCRATCH_BYTES: u32 = 8 << 20;
@@ -193,7 +197,7 @@ pub struct PpkFloatAttentionArgs {
     pub split_tokens: u32,
     pub max_length: u32,
     pub softmax_scale: f32,
-    pub reserved: u32,
+    pub flags: u32,
     pub q_row_stride: u64,
     pub k_row_stride: u64,
     pub v_row_stride: u64,

@@ -209,7 +209,8 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   dim_index(a.head_dim);
   require(valid_dtype(a.q_dtype) && valid_dtype(a.scratch_dtype) && valid_dtype(a.out_dtype),
           "INT8 attention dtype must be f32, bf16 or f16");
-  require((a.flags & ~uint32_t(PPK_ATTN_BF16_HISTORY)) == 0, "unknown INT8 attention flags");
+  require((a.flags & ~uint32_t(PPK_ATTN_BF16_HISTORY | kPlanFlags)) == 0, "unknown INT8 attention flags");
+  require((a.flags & kPlanFlags) != kPlanFlags, "INT8 attention plan flags PER_ROW and BALANCED both set");
   require(a.heads > 0 && a.rows > 0 && a.rows % a.heads == 0, "INT8 attention geometry differs: rows % heads");
   require(a.capacity > 0, "INT8 attention capacity must be positive");
   require(uint64_t(a.capacity) * a.head_dim <= (uint64_t(1) << 40), "INT8 attention capacity too large");
@@ -239,7 +240,12 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   // launch, 166 us, against 171 us balanced).
   const uint32_t* host = host_lengths(a);
   const uint64_t limit = std::min<uint64_t>(a.capacity, span);
-  if (host && a.split_tokens == 0 && flat_pays(ctx, a.rows, a.heads, host, limit)) {
+  if (a.flags & PPK_ATTN_PLAN_BALANCED) {
+    require_balanced(ctx, a.rows, a.heads, host, a.split_tokens);
+    plan = plan_flat(ctx, a.rows, a.heads, host, limit, a.head_dim);
+    plan.span = uint32_t(span);
+  } else if (!(a.flags & PPK_ATTN_PLAN_PER_ROW) && host && a.split_tokens == 0 &&
+             flat_pays(ctx, a.rows, a.heads, host, limit)) {
     AttentionPlan flat = plan_flat(ctx, a.rows, a.heads, host, limit, a.head_dim);
     const uint32_t cus = uint32_t(std::max(ctx ? ctx->cu_count : 256, 1));
     if (5 * per_row_cu_peak(plan, a.rows, a.heads, host, limit, cus) >= 6 * flat_cu_peak(flat, a.heads, cus)) {
@@ -296,10 +302,23 @@ uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit) {
   return most;
 }
 
+bool flat_fits(const ppk_context* ctx, uint32_t rows, uint32_t heads) {
+  const uint64_t flat_waves = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * kFlatWavesPerCu;
+  return rows / heads <= uint32_t(kFlatMaxBatch) && 2 * uint64_t(rows) <= flat_waves;
+}
+
+void require_balanced(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host,
+                      uint32_t split_tokens) {
+  require(host != nullptr, "PPK_ATTN_PLAN_BALANCED needs the host lengths");
+  require(split_tokens == 0, "PPK_ATTN_PLAN_BALANCED needs split_tokens == 0");
+  if (!flat_fits(ctx, rows, heads))
+    throw PreconditionError("PPK_ATTN_PLAN_BALANCED: at most 64 sequences and 4 rows per CU, got " +
+                            std::to_string(rows / heads) + " sequences of " + std::to_string(heads) + " rows");
+}
+
 bool flat_pays(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t limit) {
   const uint32_t batch = rows / heads;
-  const uint64_t flat_waves = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * kFlatWavesPerCu;
-  if (batch > uint32_t(kFlatMaxBatch) || 2 * uint64_t(rows) > flat_waves) return false;
+  if (!flat_fits(ctx, rows, heads)) return false;
   uint64_t sum = 0, most = 0;
   for (uint32_t b = 0; b < batch; ++b) {
     const uint64_t live = host[b] <= limit ? host[b] : 0;
@@ -633,6 +652,8 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   require(a.max_length <= a.size, "max_length exceeds size");
   require(a.max_length == 0 || a.lengths != nullptr, "max_length requires per-sequence lengths");
   require(std::isfinite(a.softmax_scale) && a.softmax_scale >= 0.f, "softmax_scale must be finite and >= 0");
+  require((a.flags & ~kPlanFlags) == 0, "unknown float attention flags");
+  require((a.flags & kPlanFlags) != kPlanFlags, "float attention plan flags PER_ROW and BALANCED both set");
   const uint64_t eb = a.kv_dtype == PPK_BF16 ? 2 : 4;
   const uint64_t row_elems = uint64_t(a.size) * a.head_dim;
   require(row_elems <= (uint64_t(1) << 40), "float attention size too large");
@@ -665,10 +686,15 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   const uint32_t* host = host_lengths(a);
   require(!host || a.lengths, "float attention lengths_host needs the device lengths");
   const uint32_t batch = a.rows / a.heads;
-  if (host && a.split_tokens == 0 && flat_pays(ctx, a.rows, a.heads, host, span) &&
-      longest_live(host, batch, span) * 2 * eb * a.head_dim > kFloatFlatMinRowBytes &&
-      per_row_waves_uneven(batch, host, span, plan.split))
+  if (a.flags & PPK_ATTN_PLAN_BALANCED) {
+    require_balanced(ctx, a.rows, a.heads, host, a.split_tokens);
     plan = plan_flat(ctx, a.rows, a.heads, host, span, a.head_dim);
+  } else if (!(a.flags & PPK_ATTN_PLAN_PER_ROW) && host && a.split_tokens == 0 &&
+             flat_pays(ctx, a.rows, a.heads, host, span) &&
+             longest_live(host, batch, span) * 2 * eb * a.head_dim > kFloatFlatMinRowBytes &&
+             per_row_waves_uneven(batch, host, span, plan.split)) {
+    plan = plan_flat(ctx, a.rows, a.heads, host, span, a.head_dim);
+  }
   plan.span = uint32_t(span);
   return plan;
 }

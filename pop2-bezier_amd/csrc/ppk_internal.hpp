@@ -181,6 +181,14 @@ AttentionPlan plan_flat(const ppk_context* ctx, uint32_t rows, uint32_t heads, c
 // Whether the balanced plan pays for these host lengths: the longest live
 // row beyond 1.1 x the mean, at most 64 sequences, 2 * rows within its waves.
 bool flat_pays(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t limit);
+// Whether a batch fits the balanced plan (at most 64 sequences, 2 * rows
+// within its waves); require_balanced throws PreconditionError, naming what
+// is missing, for a caller that asked for the balanced plan.
+bool flat_fits(const ppk_context* ctx, uint32_t rows, uint32_t heads);
+void require_balanced(const ppk_context* ctx, uint32_t rows, uint32_t heads, const uint32_t* host,
+                      uint32_t split_tokens);
+// The PPK_ATTN_PLAN_* bits.
+constexpr uint32_t kPlanFlags = PPK_ATTN_PLAN_PER_ROW | PPK_ATTN_PLAN_BALANCED;
 // The most live tokens of any of `batch` sequences (a length above limit has none).
 uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit);
 // The most live history tokens one CU streams under a per-row plan p or a

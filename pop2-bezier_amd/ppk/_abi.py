@@ -17,6 +17,7 @@ PPK_OK, PPK_PRECONDITION, PPK_INVALID_OUTPUT, PPK_EXECUTION_UNCERTAIN = 0, 1, 2,
 PPK_F32, PPK_BF16, PPK_F16 = 0, 1, 2
 PPK_FLAG_NONFINITE, PPK_FLAG_OVERFLOW, PPK_FLAG_STALE_LENGTHS = 1, 2, 4
 PPK_ATTN_BF16_HISTORY = 1
+PPK_ATTN_PLAN_PER_ROW, PPK_ATTN_PLAN_BALANCED = 2, 4
 PPK_NOALLOC_SCRATCH_BYTES = 8 << 20
 (PPK_KERNEL_QUANTIZE, PPK_KERNEL_APPEND, PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_ATTENTION, PPK_KERNEL_ATTN_MERGE,
  PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_RENYI_SAMPLE, PPK_KERNEL_COPY,
@@ -59,7 +60,7 @@ class PpkDecodeStepArgs(ctypes.Structure):
 class PpkFloatAttentionArgs(ctypes.Structure):
     _fields_ = [("struct_size", _u32), ("kv_dtype", _u32), ("q_dtype", _u32), ("out_dtype", _u32),
                 ("rows", _u32), ("heads", _u32), ("size", _u32), ("head_dim", _u32), ("split_tokens", _u32),
-                ("max_length", _u32), ("softmax_scale", _f32), ("reserved", _u32),
+                ("max_length", _u32), ("softmax_scale", _f32), ("flags", _u32),
                 ("q_row_stride", _u64), ("k_row_stride", _u64), ("v_row_stride", _u64),
                 ("q", _ptr), ("k", _ptr), ("v", _ptr), ("lengths", _ptr), ("out", _ptr), ("workspace", _ptr),
                 ("workspace_bytes", _u64), ("lengths_host", _ptr)]
@@ -197,3 +198,12 @@ def check(status: int, what: str) -> None:
     if status != PPK_OK:
         msg = (lib().ppk_last_error() or b"").decode("utf-8", "replace")
         raise _ERRORS.get(status, PpkError)(f"{what} failed with status {status}: {msg}")
+
+
+def plan_flags(plan: str) -> int:
+    """PPK_ATTN_PLAN_* bits of a plan choice: "auto" (the library decides from the host lengths), "per-row" or
+    "balanced"."""
+    flags = {"auto": 0, "per-row": PPK_ATTN_PLAN_PER_ROW, "balanced": PPK_ATTN_PLAN_BALANCED}.get(plan)
+    if flags is None:
+        raise ValueError(f"plan must be 'auto', 'per-row' or 'balanced', got {plan!r}")
+    return flags

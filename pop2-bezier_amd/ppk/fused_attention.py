@@ -27,11 +27,11 @@ _KV_DTYPES = {torch.bfloat16: _abi.PPK_BF16, torch.float32: _abi.PPK_F32}
 
 def decode_attention_args(q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
                           out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-                          softmax_scale: float = 0.0,
-                          lengths_host=None) -> tuple[_abi.PpkFloatAttentionArgs, torch.Tensor]:
+                          softmax_scale: float = 0.0, lengths_host=None,
+                          plan: str = "auto") -> tuple[_abi.PpkFloatAttentionArgs, torch.Tensor]:
     """Validate like fused_attention::decode_attention and build the ABI block (workspace unset).
     lengths_host: an optional host copy of `lengths` (a sequence of ints), with which the library balances
-    ragged batches."""
+    ragged batches; plan: "auto", "per-row" or "balanced" (PPK_ATTN_PLAN_*)."""
     _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "fused decode attention requires 3-d q/k/v")
     rows, query, width = q.shape
     key_rows, length, key_width = k.shape
@@ -56,6 +56,7 @@ def decode_attention_args(q, k, v, lengths, heads: int, split_tokens: int = 0, *
         struct_size=ctypes.sizeof(_abi.PpkFloatAttentionArgs), kv_dtype=_KV_DTYPES[k.dtype],
         q_dtype=_DTYPES[q.dtype], out_dtype=_DTYPES[out.dtype], rows=rows, heads=heads, size=length,
         head_dim=width, split_tokens=split_tokens, max_length=max_length, softmax_scale=softmax_scale,
+        flags=_abi.plan_flags(plan),
         q_row_stride=q.stride(0), k_row_stride=k.stride(0), v_row_stride=v.stride(0),
         q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
         lengths=lengths.data_ptr() if lengths is not None else None, out=out.data_ptr(), workspace=None,
@@ -77,15 +78,20 @@ def plan(args: _abi.PpkFloatAttentionArgs, ctx: ctypes.c_void_p | None = None) -
     return split.value, nsplits.value, nbytes.value
 
 
+# The parameter `plan` of the calls below shadows the function inside them.
+launch_plan = plan
+
+
 def decode_attention(q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
                      out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0,
-                     lengths_host=None) -> torch.Tensor:
+                     lengths_host=None, plan: str = "auto") -> torch.Tensor:
     """fused_attention::decode_attention -> out [rows, 1, D] (float32 by default). lengths_host: optional
     host copy of lengths."""
     a, out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length,
-                                   out_dtype=out_dtype, softmax_scale=softmax_scale, lengths_host=lengths_host)
+                                   out_dtype=out_dtype, softmax_scale=softmax_scale, lengths_host=lengths_host,
+                                   plan=plan)
     ctx = context(q.device)
-    nbytes = plan(a, ctx)[2]
+    nbytes = launch_plan(a, ctx)[2]
     # Stream-ordered caching allocator: the block outlives the queued kernels.
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     a.workspace = ws.data_ptr()
@@ -99,11 +105,13 @@ class FloatDecodeAttention:
     __call__ only enqueues the kernels (bench and serving loops, graph capture)."""
 
     def __init__(self, q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
-                 out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32, lengths_host=None):
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32, lengths_host=None,
+                 plan: str = "auto"):
         self.args, self.out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length,
-                                                    out=out, out_dtype=out_dtype, lengths_host=lengths_host)
+                                                    out=out, out_dtype=out_dtype, lengths_host=lengths_host,
+                                                    plan=plan)
         self.ctx = context(q.device)
-        self.split_tokens, self.ngroups, nbytes = plan(self.args, self.ctx)
+        self.split_tokens, self.ngroups, nbytes = launch_plan(self.args, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.workspace = self.workspace.data_ptr()
         self.args.workspace_bytes = nbytes

@@ -126,9 +126,11 @@ def append(k_new: torch.Tensor, v_new: torch.Tensor, past: torch.Tensor, k_codes
 
 def attention_args(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *, bf16_history: bool = False,
                    max_past: int = 0, out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-                   softmax_scale: float = 0.0, past_host=None) -> tuple[_abi.PpkAttentionArgs, torch.Tensor]:
+                   softmax_scale: float = 0.0, past_host=None,
+                   plan: str = "auto") -> tuple[_abi.PpkAttentionArgs, torch.Tensor]:
     """Validate like int8_kv_ops::attention and build the ABI argument block (workspace unset). past_host: an
-    optional host copy of `past` (a sequence of ints), with which the library balances ragged batches."""
+    optional host copy of `past` (a sequence of ints), with which the library balances ragged batches; plan:
+    "auto" (the library chooses from past_host), "per-row" or "balanced" (PPK_ATTN_PLAN_*)."""
     rows, capacity = _geometry(k)
     d = k.shape[2]
     _require(heads > 0 and rows % heads == 0 and v.shape == k.shape and v.is_contiguous()
@@ -149,7 +151,8 @@ def attention_args(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int 
              "INT8 attention output must be a dense float tensor of rows*D elements")
     a = _abi.PpkAttentionArgs(
         struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), q_dtype=_DTYPES[q.dtype], scratch_dtype=_DTYPES[sk.dtype],
-        out_dtype=_DTYPES[out.dtype], flags=_abi.PPK_ATTN_BF16_HISTORY if bf16_history else 0, rows=rows,
+        out_dtype=_DTYPES[out.dtype],
+        flags=(_abi.PPK_ATTN_BF16_HISTORY if bf16_history else 0) | _abi.plan_flags(plan), rows=rows,
         heads=heads, capacity=capacity, head_dim=d, split_tokens=split_tokens, max_past=max_past,
         softmax_scale=softmax_scale, q=q.data_ptr(), k_codes=k.data_ptr(), v_codes=v.data_ptr(),
         k_scales=ks.data_ptr(), v_scales=vs.data_ptr(), sk=sk.data_ptr(), sv=sv.data_ptr(), past=past.data_ptr(),
@@ -178,13 +181,18 @@ def plan(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = None) -> tup
     return split.value, nsplits.value, nbytes.value
 
 
+# The parameter `plan` of the calls below shadows the function inside them.
+launch_plan = plan
+
+
 def attention(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *, bf16_history: bool = False,
               max_past: int = 0, out_dtype: torch.dtype = torch.float32, softmax_scale: float = 0.0,
-              past_host=None) -> torch.Tensor:
+              past_host=None, plan: str = "auto") -> torch.Tensor:
     """int8_kv_ops::attention: q/sk/sv [rows,1,D], k/v uint8 [rows,cap,D], ks/vs f32 [rows,cap],
     past U32 [rows/heads] -> out [rows,1,D] (float32 by default). past_host: optional host copy of past."""
     a, out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
-                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale, past_host=past_host)
+                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale, past_host=past_host,
+                            plan=plan)
     ctx = context(q.device)
     nbytes = workspace_bytes(a, ctx)
     # The caching allocator is stream-ordered: the block is not reused before
@@ -199,12 +207,13 @@ def attention(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, 
 def decode_step(q, k, v, ks, vs, sk, sv, past, heads: int, k_new: torch.Tensor | None = None,
                 v_new: torch.Tensor | None = None, split_tokens: int = 0, *, flags: torch.Tensor | None = None,
                 bf16_history: bool = False, max_past: int = 0, out_dtype: torch.dtype = torch.float32,
-                softmax_scale: float = 0.0, past_host=None) -> torch.Tensor:
+                softmax_scale: float = 0.0, past_host=None, plan: str = "auto") -> torch.Tensor:
     """Commit + attend in one call: quantise k_new/v_new [rows, D] (default: sk/sv) into slot past[b] of the
     arenas, then attention over [0, past[b]) plus the current token, as forward_embedding's commit path does
     (query_int8 then int8_kv_ops::attention, app/src/model/mod.rs:699-705)."""
     a, out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
-                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale, past_host=past_host)
+                            max_past=max_past, out_dtype=out_dtype, softmax_scale=softmax_scale, past_host=past_host,
+                            plan=plan)
     step = _step_args(a, sk if k_new is None else k_new, sv if v_new is None else v_new, flags, k.shape[2])
     ctx = context(q.device)
     nbytes = workspace_bytes(a, ctx)
@@ -235,12 +244,12 @@ class DecodeAttention:
 
     def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *,
                  bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
-                 out_dtype: torch.dtype = torch.float32, past_host=None):
+                 out_dtype: torch.dtype = torch.float32, past_host=None, plan: str = "auto"):
         self.args, self.out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens,
                                              bf16_history=bf16_history, max_past=max_past, out=out,
-                                             out_dtype=out_dtype, past_host=past_host)
+                                             out_dtype=out_dtype, past_host=past_host, plan=plan)
         self.ctx = context(q.device)
-        self.split_tokens, self.ngroups, nbytes = plan(self.args, self.ctx)
+        self.split_tokens, self.ngroups, nbytes = launch_plan(self.args, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.workspace = self.workspace.data_ptr()
         self.args.workspace_bytes = nbytes
@@ -261,14 +270,15 @@ class DecodeStep:
 
     def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, k_new=None, v_new=None, split_tokens: int = 0, *,
                  flags=None, bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
-                 out_dtype: torch.dtype = torch.float32, past_host=None):
+                 out_dtype: torch.dtype = torch.float32, past_host=None, plan: str = "auto"):
         a, self.out = attention_args(q, k, v, ks, vs, sk, sv, past, heads, split_tokens, bf16_history=bf16_history,
-                                     max_past=max_past, out=out, out_dtype=out_dtype, past_host=past_host)
+                                     max_past=max_past, out=out, out_dtype=out_dtype, past_host=past_host,
+                                     plan=plan)
         k_new = sk if k_new is None else k_new
         v_new = sv if v_new is None else v_new
         self.args = _step_args(a, k_new, v_new, flags, k.shape[2])
         self.ctx = context(q.device)
-        self.split_tokens, self.ngroups, nbytes = plan(self.args.attn, self.ctx)
+        self.split_tokens, self.ngroups, nbytes = launch_plan(self.args.attn, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.attn.workspace = self.workspace.data_ptr()
         self.args.attn.workspace_bytes = nbytes

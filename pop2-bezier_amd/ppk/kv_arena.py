@@ -220,7 +220,7 @@ class LayerCache:
 
 def decode_step(view: _abi.PpkKvView, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, heads: int, *,
                 out_dtype: torch.dtype = torch.float32, past_host=None, flags: torch.Tensor | None = None,
-                bf16_history: bool = False) -> torch.Tensor:
+                bf16_history: bool = False, plan: str = "auto") -> torch.Tensor:
     """The fused decode step over a reserved batch view of int8 caches (LayerCache.query_batch with k = v =
     None): quantise k_new / v_new (the current token, [B*H, D] or [B, H, 1, D]) into slot past[b] of the
     view's arenas and attend over [0, past[b]) plus that token unquantised, in one launch (two when rows
@@ -239,7 +239,8 @@ def decode_step(view: _abi.PpkKvView, q: torch.Tensor, k_new: torch.Tensor, v_ne
     out = torch.empty((rows, 1, d), dtype=out_dtype, device=q.device)
     a = _abi.PpkAttentionArgs(
         struct_size=ctypes.sizeof(_abi.PpkAttentionArgs), q_dtype=_DTYPES[q.dtype], scratch_dtype=_DTYPES[k_new.dtype],
-        out_dtype=_DTYPES[out_dtype], flags=_abi.PPK_ATTN_BF16_HISTORY if bf16_history else 0, rows=rows,
+        out_dtype=_DTYPES[out_dtype],
+        flags=(_abi.PPK_ATTN_BF16_HISTORY if bf16_history else 0) | _abi.plan_flags(plan), rows=rows,
         heads=heads, capacity=cap, head_dim=d, split_tokens=0, max_past=view.length - 1, softmax_scale=0.0,
         q=q.data_ptr(), k_codes=view.k, v_codes=view.v, k_scales=view.k_scales, v_scales=view.v_scales,
         sk=k_new.data_ptr(), sv=v_new.data_ptr(), past=view.past, out=out.data_ptr(), workspace=None,

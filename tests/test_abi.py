@@ -324,6 +324,39 @@ def test_float_balanced_plan_without_a_device():
     assert ppk.fused_attention.plan(old) == per_row
 
 
+def test_plan_flags_fix_the_choice():
+    """PPK_ATTN_PLAN_PER_ROW / _BALANCED override the library's choice between its two plans (int8 and float);
+    BALANCED needs host lengths, split_tokens == 0 and a batch within the balanced plan's limits."""
+    P, B = _abi.PPK_ATTN_PLAN_PER_ROW, _abi.PPK_ATTN_PLAN_BALANCED
+    skew, uniform = [8192] * 4 + [512] * 28, [8192] * 32
+    per_row = ppk.int8_kv_ops.plan(_attn_args())
+    balanced = ppk.int8_kv_ops.plan(_attn_args(past_host=skew))
+    assert balanced != per_row
+    assert ppk.int8_kv_ops.plan(_attn_args(past_host=skew, flags=P)) == per_row
+    units, share = _flat_units(uniform, 16, 512, 8193, 8192, 2048)
+    assert ppk.int8_kv_ops.plan(_attn_args(past_host=uniform, flags=B))[:2] == (share, max(units))
+    assert ppk.int8_kv_ops.plan(_attn_args(past_host=uniform, flags=B | _abi.PPK_ATTN_BF16_HISTORY))[:2] == \
+        (share, max(units))
+    # Short rows that the library keeps per-row: forced balanced, every row one unit (no records, no merge).
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900, flags=B,
+                                           past_host=[10, 0, 60, 64])) == (64, 1, 0)
+    fl_per_row = ppk.fused_attention.plan(_float_args(lengths=8))
+    assert ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=skew, flags=P)) == fl_per_row
+    assert ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=uniform, flags=B))[:2] == (share, max(units))
+    for bad in (dict(flags=P | B, past_host=skew), dict(flags=B), dict(flags=B, past_host=skew, split_tokens=128),
+                dict(flags=B, rows=65 * 16, heads=16, past_host=[100] * 65),
+                dict(flags=B, rows=1040, heads=1040, past_host=[100])):
+        with pytest.raises(ppk.PpkPreconditionError):
+            ppk.int8_kv_ops.plan(_attn_args(**bad))
+    for bad in (dict(flags=P | B, lengths_host=skew), dict(flags=B), dict(flags=B, lengths_host=skew, split_tokens=64),
+                dict(flags=8, lengths_host=skew), dict(flags=_abi.PPK_ATTN_BF16_HISTORY)):
+        with pytest.raises(ppk.PpkPreconditionError):
+            ppk.fused_attention.plan(_float_args(lengths=8, **bad))
+    assert "PPK_ATTN_PLAN" in _abi.lib().ppk_last_error().decode() or "flags" in _abi.lib().ppk_last_error().decode()
+    with pytest.raises(ValueError):
+        _abi.plan_flags("fastest")
+
+
 @pytest.mark.parametrize("bad", [dict(kv_dtype=_abi.PPK_F16), dict(head_dim=96), dict(size=0), dict(rows=30),
                                  dict(q_dtype=5), dict(out_dtype=9), dict(k_row_stride=8191 * 128),
                                  dict(v_row_stride=8192 * 128 + 4), dict(max_length=8193),
