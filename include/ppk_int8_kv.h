@@ -293,6 +293,33 @@ typedef struct PpkFloatAttentionArgs {
 PPK_API int32_t ppk_float_attention_plan(ppk_context* ctx, const PpkFloatAttentionArgs* args,
                                          uint32_t* split_tokens, uint32_t* nsplits, uint64_t* workspace_bytes);
 PPK_API int32_t ppk_float_decode_attention(ppk_context* ctx, void* stream, const PpkFloatAttentionArgs* args);
+
+/* The float path's fused decode step: the caller's commit and attention in
+   one launch per layer (two when rows span blocks). Replaces the graph-decode
+   session's per-layer pair scatter_set(write_indices, k / v) +
+   decode_attention(valid_lengths = lengths + 1)
+   (app/src/model/graph_decode.rs:290-305) and the float cache's commit +
+   fused_attention::decode_attention of forward_embedding
+   (app/src/model/mod.rs:699-720). With attn.lengths[b] = p, the tokens
+   already stored for sequence b (required), row r's current key and value
+   (k_new / v_new [rows, head_dim] of new_dtype, rounded to kv_dtype) are
+   written at slot p of attn.k / attn.v, which the call writes, when p < size
+   (otherwise PPK_FLAG_OVERFLOW in *flags, if given, and nothing is written),
+   and out_r is attention over the p stored tokens plus that token, exactly
+   what ppk_float_decode_attention gives after the write with lengths p + 1.
+   A row gives NaN unless p < size and p + 1 <= max_length (when set).
+   attn.lengths_host, if given, holds p, and the plan and workspace are those
+   of ppk_float_attention_plan(attn). No counterpart fuses these in the
+   reference. */
+typedef struct PpkFloatDecodeStepArgs {
+  uint32_t struct_size;
+  uint32_t new_dtype;      /* PPK_F32, PPK_BF16 or PPK_F16 */
+  const void* k_new;       /* [rows, head_dim] current keys */
+  const void* v_new;       /* [rows, head_dim] current values */
+  uint32_t* flags;         /* optional device word, PPK_FLAG_* bits OR-ed in */
+  PpkFloatAttentionArgs attn;
+} PpkFloatDecodeStepArgs;
+PPK_API int32_t ppk_float_decode_step(ppk_context* ctx, void* stream, const PpkFloatDecodeStepArgs* args);
 /* The float path's private known-answer check: hip_attention::validate_split_k
    (app/src/model/hip_attention.rs:18-45; bf16 and f32 stores of 257 tokens,
    split 0 and 128 within 1e-4 of an f32 softmax reference and of each other)

@@ -211,6 +211,19 @@ pub struct PpkFloatAttentionArgs {
     pub lengths_host: *const u32,
 }
 
+/// The float path's fused decode step (the graph-decode session's scatter_set
+/// pair + decode_attention, app/src/model/graph_decode.rs:290-305).
+#[repr(C)]
+#[derive(Clone, Copy)]
+pub struct PpkFloatDecodeStepArgs {
+    pub struct_size: u32,
+    pub new_dtype: u32,
+    pub k_new: *const c_void,
+    pub v_new: *const c_void,
+    pub flags: *mut u32,
+    pub attn: PpkFloatAttentionArgs,
+}
+
 /// CFG + Renyi sampler (hip_sampling::sample, app/src/inference/hip_sampling.rs:71-106).
 #[repr(C)]
 #[derive(Clone, Copy)]
@@ -335,6 +348,7 @@ extern "C" {
         workspace_bytes: *mut u64,
     ) -> i32;
     pub fn ppk_float_decode_attention(ctx: *mut ppk_context, stream: *mut c_void, args: *const PpkFloatAttentionArgs) -> i32;
+    pub fn ppk_float_decode_step(ctx: *mut ppk_context, stream: *mut c_void, args: *const PpkFloatDecodeStepArgs) -> i32;
     pub fn ppk_float_attention_prepare(ctx: *mut ppk_context) -> i32;
     pub fn ppk_renyi_sample(ctx: *mut ppk_context, stream: *mut c_void, args: *const PpkRenyiSampleArgs) -> i32;
     pub fn ppk_kv_cache_create(ctx: *mut ppk_context, config: *const PpkKvConfig, out: *mut *mut ppk_kv_cache) -> i32;

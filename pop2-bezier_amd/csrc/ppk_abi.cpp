@@ -67,6 +67,10 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_fdecode_flat_bf16_d64", "ppk_fdecode_flat_bf16_d128", "ppk_fdecode_flat_bf16_d256",
     "ppk_fdecode_flat_f32_d64", "ppk_fdecode_flat_f32_d128", "ppk_fdecode_flat_f32_d256",
     "ppk_fmerge_flat_d64", "ppk_fmerge_flat_d128", "ppk_fmerge_flat_d256",
+    "ppk_fstep_bf16_d64", "ppk_fstep_bf16_d128", "ppk_fstep_bf16_d256",
+    "ppk_fstep_f32_d64", "ppk_fstep_f32_d128", "ppk_fstep_f32_d256",
+    "ppk_fstep_flat_bf16_d64", "ppk_fstep_flat_bf16_d128", "ppk_fstep_flat_bf16_d256",
+    "ppk_fstep_flat_f32_d64", "ppk_fstep_flat_f32_d128", "ppk_fstep_flat_f32_d256",
 };
 
 std::string default_code_object() {
@@ -699,8 +703,18 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   return plan;
 }
 
-void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a) {
+void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a,
+                         const PpkFloatDecodeStepArgs* step) {
   const AttentionPlan plan = plan_float_attention(ctx, a);
+  if (step) {
+    require(step->struct_size >= sizeof(PpkFloatDecodeStepArgs), "PpkFloatDecodeStepArgs.struct_size too small");
+    require(a.lengths != nullptr, "the float decode step needs the device lengths");
+    require(valid_dtype(step->new_dtype), "float decode step new-token dtype must be f32, bf16 or f16");
+    require(step->k_new && step->v_new, "float decode step null new token");
+    require(aligned(step->k_new, dtype_bytes(step->new_dtype)) && aligned(step->v_new, dtype_bytes(step->new_dtype)) &&
+                (!step->flags || aligned(step->flags, 4)),
+            "float decode step operand misaligned");
+  }
   require(a.q && a.k && a.v && a.out, "float attention null pointer");
   require(aligned(a.k, 16) && aligned(a.v, 16), "float attention K/V must be 16-byte aligned");
   require(aligned(a.q, dtype_bytes(a.q_dtype)) && aligned(a.out, dtype_bytes(a.out_dtype)) &&
@@ -738,6 +752,12 @@ void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAtt
   d.out_dtype = a.out_dtype;
   d.scale_log2 = scale * 1.4426950408889634f;
   d.span = plan.span;
+  if (step) {
+    d.k_new = step->k_new;
+    d.v_new = step->v_new;
+    d.flags = step->flags;
+    d.new_dtype = step->new_dtype;
+  }
 
   FloatMergeArgs m{};
   m.lengths = a.lengths;
@@ -751,13 +771,25 @@ void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAtt
   m.out_dtype = a.out_dtype;
   m.span = plan.span;
   const bool bf16 = a.kv_dtype == PPK_BF16;
+  if (step) {
+    m.step = 1;
+    m.q = a.q;
+    m.q_stride = qs;
+    m.q_dtype = a.q_dtype;
+    m.k_new = step->k_new;
+    m.v_new = step->v_new;
+    m.new_dtype = step->new_dtype;
+    m.kv_bf16 = bf16 ? 1u : 0u;
+    m.scale_log2 = d.scale_log2;
+  }
   DeviceGuard guard(ctx->device);
   if (plan.flat) {
     FloatDecodeFlatArgs fd{};
     fd.d = d;
     fd.t = plan.table;
-    launch(ctx, PPK_KERNEL_FLOAT_ATTENTION, Fn((bf16 ? kFDecodeFlatBf16_64 : kFDecodeFlatF32_64) + di), plan.blocks,
-           64 * plan.waves, 0, stream, fd);
+    const Fn flat = step ? Fn((bf16 ? kFStepFlatBf16_64 : kFStepFlatF32_64) + di)
+                         : Fn((bf16 ? kFDecodeFlatBf16_64 : kFDecodeFlatF32_64) + di);
+    launch(ctx, PPK_KERNEL_FLOAT_ATTENTION, flat, plan.blocks, 64 * plan.waves, 0, stream, fd);
     if (plan.ngroups > 1) {
       FloatMergeFlatArgs fm{};
       fm.m = m;
@@ -767,7 +799,8 @@ void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAtt
     }
     return;
   }
-  const Fn decode = Fn((bf16 ? kFDecodeBf16_64 : kFDecodeF32_64) + di);
+  const Fn decode = step ? Fn((bf16 ? kFStepBf16_64 : kFStepF32_64) + di)
+                        : Fn((bf16 ? kFDecodeBf16_64 : kFDecodeF32_64) + di);
   launch(ctx, PPK_KERNEL_FLOAT_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d);
   if (plan.ngroups > 1) {
     m.split_tokens = plan.split * plan.waves;  // tokens per group
@@ -1074,6 +1107,14 @@ int32_t ppk_float_decode_attention(ppk_context* ctx, void* stream, const PpkFloa
   return call([&] {
     ppk::require(ctx && args, "ppk_float_decode_attention: null context or arguments");
     ppk::run_float_attention(ctx, static_cast<hipStream_t>(stream), *args);
+  });
+}
+
+int32_t ppk_float_decode_step(ppk_context* ctx, void* stream, const PpkFloatDecodeStepArgs* args) {
+  return call([&] {
+    ppk::require(ctx && args, "ppk_float_decode_step: null context or arguments");
+    ppk::require(args->struct_size >= sizeof(PpkFloatDecodeStepArgs), "PpkFloatDecodeStepArgs.struct_size too small");
+    ppk::run_float_attention(ctx, static_cast<hipStream_t>(stream), args->attn, args);
   });
 }
 

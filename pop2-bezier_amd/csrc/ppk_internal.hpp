@@ -56,6 +56,10 @@ enum Fn : int {
   kFDecodeFlatBf16_64, kFDecodeFlatBf16_128, kFDecodeFlatBf16_256,
   kFDecodeFlatF32_64, kFDecodeFlatF32_128, kFDecodeFlatF32_256,
   kFMergeFlat64, kFMergeFlat128, kFMergeFlat256,
+  kFStepBf16_64, kFStepBf16_128, kFStepBf16_256,
+  kFStepF32_64, kFStepF32_128, kFStepF32_256,
+  kFStepFlatBf16_64, kFStepFlatBf16_128, kFStepFlatBf16_256,
+  kFStepFlatF32_64, kFStepFlatF32_128, kFStepFlatF32_256,
   kFnCount
 };
 
@@ -217,7 +221,9 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
 // then served from a per-device table. Throws PreconditionError if the
 // lookup failed.
 void* scratch_lookup(int device);
-void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a);
+// step == nullptr: attention only; otherwise the fused float decode step.
+void run_float_attention(ppk_context* ctx, hipStream_t stream, const PpkFloatAttentionArgs& a,
+                         const PpkFloatDecodeStepArgs* step = nullptr);
 void run_renyi_sample(ppk_context* ctx, hipStream_t stream, const PpkRenyiSampleArgs& a);
 
 // Arena writes for the KV cache manager (kv_arena.cpp). Rows of `heads`

@@ -141,11 +141,20 @@ struct FloatDecodeArgs {
   float* part_y;
   float* part_mz;
   void* out;                // [rows, D]
+  // The fused step (ppk_fstep_* kernels): lengths[b] = p tokens are stored;
+  // row r's current token k_new/v_new[r] (new_dtype, rounded to the store's
+  // dtype) is written at slot p when p < size (else PPK_FLAG_OVERFLOW in
+  // *flags) and the row attends the p stored tokens plus that token: NaN
+  // unless p < size and p + 1 <= span.
+  const void* k_new;
+  const void* v_new;
+  uint32_t* flags;
   uint64_t q_stride, k_stride, v_stride;
   uint32_t rows, heads, size, split_tokens, ngroups;
   uint32_t q_dtype, out_dtype;
   float scale_log2;         // softmax_scale * log2(e)
   uint32_t span;            // most tokens a row may attend (<= size)
+  uint32_t new_dtype;
 };
 
 struct FloatMergeArgs {
@@ -153,7 +162,15 @@ struct FloatMergeArgs {
   const float* part_y;
   const float* part_mz;
   void* out;                // [rows, D]
+  // The fused step (step != 0): the current token joins the records as in
+  // the int8 merge; q, k_new and v_new as in FloatDecodeArgs.
+  const void* q;
+  const void* k_new;
+  const void* v_new;
+  uint64_t q_stride;
   uint32_t rows, heads, size, split_tokens, nsplits, out_dtype, span;
+  uint32_t step, q_dtype, new_dtype, kv_bf16;
+  float scale_log2;
 };
 
 // Float-KV decode over the balanced work list: the table as for the int8

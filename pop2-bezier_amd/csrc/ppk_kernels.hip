@@ -11,6 +11,7 @@
 //   ppk_fdecode_{bf16,f32}_d{..}       decode attention over float (bf16/f32) K/V
 //   ppk_fmerge_d{..}                   cross-group merge of the float path
 //   ppk_fdecode_flat_{bf16,f32}_d{..}  float-path decode over a balanced work list (ragged batches)
+//   ppk_fstep[_flat]_{bf16,f32}_d{..}  the float path's fused step: write the current token, then attend
 //   ppk_fmerge_flat_d{..}              merge of the float balanced work list's records
 //   ppk_renyi_sample                   CFG + Renyi effective-support sampler
 //   ppk_kv_scatter_u{16,4,2}           float-store append of token records into arena slots
@@ -1548,7 +1549,33 @@ __device__ __forceinline__ uint32_t float_row_length(const uint32_t* lengths, ui
   return lengths ? lengths[row / heads] : size;
 }
 
-template <int D, bool BF16KV>
+// The fused step's current token of row `row`, channels lane * EPL .. + EPL,
+// rounded to the store's dtype (the value a stored token would hold).
+template <int EPL, bool BF16KV>
+__device__ __forceinline__ void load_current(const void* src, uint32_t row, uint32_t dtype, int lane,
+                                             float (&x)[EPL]) {
+  load_vec<EPL>(src, size_t(row) * (EPL * ppk::kWave) + size_t(lane) * EPL, dtype, x);
+  if constexpr (BF16KV) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = bf16_to_f32(f32_to_bf16_bits(x[e]));
+  }
+}
+
+// The fused step's write of one current-token tensor of `row` at slot p of
+// the store (or the overflow flag when the slot is past the store).
+template <int EPL, bool BF16KV>
+__device__ __forceinline__ void write_current(void* store, uint64_t stride, uint32_t row, uint32_t p, uint32_t size,
+                                              const float (&x)[EPL], uint32_t* flags, int lane) {
+  if (p >= size) {
+    if (lane == 0 && flags) atomicOr(flags, 2u);
+    return;
+  }
+  const size_t base = size_t(row) * stride + size_t(p) * (EPL * ppk::kWave) + size_t(lane) * EPL;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) store_elem(store, base + e, BF16KV ? kBF16 : kF32, x[e]);
+}
+
+template <int D, bool BF16KV, bool STEP>
 __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
   using G = FloatGeom<D, BF16KV>;
   constexpr int EPL = D / ppk::kWave;
@@ -1563,11 +1590,30 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
   const uint32_t row = blockIdx.x % a.rows;
   const uint32_t group = blockIdx.x / a.rows;
   const uint32_t S = a.split_tokens;
+  // The stored tokens a row streams: lengths[b] (the step's current token
+  // comes from k_new / v_new instead).
   const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
-  const bool valid = len > 0 && len <= a.span && len <= a.size && uint64_t(len) <= uint64_t(a.ngroups) * W * S;
+  bool valid;
+  if constexpr (STEP)
+    valid = len < a.size && len + 1 <= a.span && uint64_t(len) <= uint64_t(a.ngroups) * W * S;
+  else
+    valid = len > 0 && len <= a.span && len <= a.size && uint64_t(len) <= uint64_t(a.ngroups) * W * S;
 
   float qr[G::kEpc];
   load_vec<G::kEpc>(a.q, size_t(row) * a.q_stride + size_t(c) * G::kEpc, a.q_dtype, qr);
+  // The step: group 0's waves 0 and 1 write the current key and value at slot
+  // len (never read here: every stream stops before it); wave 0 of a block
+  // that finishes its row also folds the current token into the result.
+  const bool final_out = a.ngroups == 1;
+  const bool kw = STEP && group == 0 && wave == 0;
+  const bool vw = STEP && group == 0 && wave == (W > 1 ? 1 : 0);
+  const bool cur = STEP && final_out && wave == 0;
+  float kcur[EPL], vcur[EPL], qcur[EPL];
+  if (kw || cur) load_current<EPL, BF16KV>(a.k_new, row, a.new_dtype, lane, kcur);
+  if (vw || cur) load_current<EPL, BF16KV>(a.v_new, row, a.new_dtype, lane, vcur);
+  if (cur) load_vec<EPL>(a.q, size_t(row) * a.q_stride + size_t(lane) * EPL, a.q_dtype, qcur);
+  if (kw) write_current<EPL, BF16KV>(const_cast<void*>(a.k), a.k_stride, row, len, a.size, kcur, a.flags, lane);
+  if (vw) write_current<EPL, BF16KV>(const_cast<void*>(a.v), a.v_stride, row, len, a.size, vcur, a.flags, lane);
   const uint32_t begin = (group * W + wave) * S;
   const uint32_t n = (valid && begin < len) ? min(S, len - begin) : 0u;
   FloatWavePartial<D, BF16KV> part;
@@ -1593,6 +1639,14 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
 
   float m = -INFINITY;
   for (int w = 0; w < W; ++w) m = fmaxf(m, mrg[w * R]);
+  float s_cur = -INFINITY;
+  if (cur) {
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) d = fmaf(qcur[e], kcur[e], d);
+    s_cur = wave_sum(d) * a.scale_log2;
+    m = fmaxf(m, s_cur);
+  }
   float y[EPL], zsum = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) y[e] = 0.f;
@@ -1601,6 +1655,12 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
     zsum = fmaf(wt, mrg[w * R + 1], zsum);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) y[e] = fmaf(wt, mrg[w * R + 4 + lane * EPL + e], y[e]);
+  }
+  if (cur) {
+    const float wc = __builtin_amdgcn_exp2f(s_cur - m);
+    zsum += wc;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) y[e] = fmaf(wc, vcur[e], y[e]);
   }
   if (a.ngroups == 1) {
 #pragma unroll
@@ -1622,17 +1682,52 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
 // Cross-group merge of the float path (pp_attention_merge,
 // decode_attention.hip:55-66): one wave per row, log-sum-exp weights, NaN for
 // invalid rows or a non-positive total weight.
+// The fused step's current token in a merge: q . k_new (rounded to the
+// store's dtype) as a log2-domain score, with v_new kept for the fold.
+template <int D>
+__device__ __forceinline__ float merge_current(const ppk::FloatMergeArgs& a, uint32_t row, int lane,
+                                               float (&vcur)[D / ppk::kWave]) {
+  constexpr int EPL = D / ppk::kWave;
+  float qv[EPL], kv[EPL];
+  load_vec<EPL>(a.q, size_t(row) * a.q_stride + size_t(lane) * EPL, a.q_dtype, qv);
+  load_vec<EPL>(a.k_new, size_t(row) * D + size_t(lane) * EPL, a.new_dtype, kv);
+  load_vec<EPL>(a.v_new, size_t(row) * D + size_t(lane) * EPL, a.new_dtype, vcur);
+  if (a.kv_bf16) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      kv[e] = bf16_to_f32(f32_to_bf16_bits(kv[e]));
+      vcur[e] = bf16_to_f32(f32_to_bf16_bits(vcur[e]));
+    }
+  }
+  float d = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) d = fmaf(qv[e], kv[e], d);
+  return wave_sum(d) * a.scale_log2;
+}
+
 template <int D>
 __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
   constexpr int EPL = D / ppk::kWave;
   const int lane = threadIdx.x;
   const uint32_t row = blockIdx.x;
   const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
-  const bool valid =
-      len > 0 && len <= a.span && len <= a.size && uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
-  float m, zsum, y[EPL];
+  const bool cover = uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
+  const bool valid = a.step ? (len < a.size && len + 1 <= a.span && cover)
+                            : (len > 0 && len <= a.span && len <= a.size && cover);
+  float m, zsum, y[EPL], vcur[EPL];
+  float s_cur = -INFINITY;
+  auto current = [&]() {
+    if (a.step) s_cur = merge_current<D>(a, row, lane, vcur);
+    return s_cur;
+  };
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
-                     lane, [] { return -INFINITY; }, m, zsum, y);
+                     lane, current, m, zsum, y);
+  if (a.step) {
+    const float wc = __builtin_amdgcn_exp2f(s_cur - m);
+    zsum += wc;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) y[e] = fmaf(wc, vcur[e], y[e]);
+  }
   const size_t base = size_t(row) * D + size_t(lane) * EPL;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
@@ -1747,7 +1842,7 @@ __device__ __forceinline__ void fwave_attention_window(const ppk::FloatDecodeArg
   for (int e = 0; e < G::kEpc; ++e) out.acc[e] = acc[e];
 }
 
-template <int D, bool BF16KV>
+template <int D, bool BF16KV, bool STEP>
 __device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs& fa) {
   const ppk::FloatDecodeArgs& a = fa.d;
   const ppk::FlatTable& t = fa.t;
@@ -1762,6 +1857,19 @@ __device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs
   // within 2 % elsewhere. (The int8 kernel keeps consecutive units per
   // block: this mapping did not help it.)
   const uint32_t wid = (threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+  if constexpr (STEP) {
+    // The step's writes: wave q < 2 rows writes tensor q & 1 of row q >> 1 at
+    // slot lengths[b] (the device value; every stream stops before it).
+    if (wid < 2 * a.rows) {  // uniform per wave (the host keeps waves >= 2 rows)
+      constexpr int EPL = D / ppk::kWave;
+      const uint32_t arow = wid >> 1;
+      const bool value = (wid & 1u) != 0;
+      float x[EPL];
+      load_current<EPL, BF16KV>(value ? a.v_new : a.k_new, arow, a.new_dtype, lane, x);
+      write_current<EPL, BF16KV>(const_cast<void*>(value ? a.v : a.k), value ? a.v_stride : a.k_stride, arow,
+                                 a.lengths[arow / a.heads], a.size, x, a.flags, lane);
+    }
+  }
   if (wid >= t.units_total) return;  // uniform per wave
   const int c = lane % G::kLpt;
   const int j = lane / G::kLpt;
@@ -1775,15 +1883,45 @@ __device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs
   const uint32_t t0 = slot * t.share;
   const uint32_t n = len > t0 ? min(t.share, len - t0) : 0u;
   const uint32_t ldev = a.lengths[b];
-  float qr[G::kEpc];
-  if (n > 0) load_vec<G::kEpc>(a.q, size_t(row) * a.q_stride + size_t(c) * G::kEpc, a.q_dtype, qr);
+  // The step's current token, folded by the wave of a one-unit row (longer
+  // rows: by the merge), in this kernel's lane layout and token arithmetic.
+  const bool cur = STEP && units == 1;
+  float qr[G::kEpc], kx[G::kEpc], vx[G::kEpc];
+  if (n > 0 || cur) load_vec<G::kEpc>(a.q, size_t(row) * a.q_stride + size_t(c) * G::kEpc, a.q_dtype, qr);
+  if (cur) {
+    load_vec<G::kEpc>(a.k_new, size_t(row) * D + size_t(c) * G::kEpc, a.new_dtype, kx);
+    load_vec<G::kEpc>(a.v_new, size_t(row) * D + size_t(c) * G::kEpc, a.new_dtype, vx);
+    if constexpr (BF16KV) {
+#pragma unroll
+      for (int e = 0; e < G::kEpc; ++e) {
+        kx[e] = bf16_to_f32(f32_to_bf16_bits(kx[e]));
+        vx[e] = bf16_to_f32(f32_to_bf16_bits(vx[e]));
+      }
+    }
+  }
   FloatWavePartial<D, BF16KV> part;
   part.m = -INFINITY;
   part.z = 0.f;
 #pragma unroll
   for (int e = 0; e < G::kEpc; ++e) part.acc[e] = 0.f;
   if (n > 0) fwave_attention_window<D, BF16KV>(a, row, t0, n, qr, lane, part);
-  const bool valid = len > 0 && ldev == t.past[b];
+  bool valid;
+  if constexpr (STEP)
+    valid = ldev == t.past[b] && t.past[b] < a.size && t.past[b] + 1 <= a.span;
+  else
+    valid = len > 0 && ldev == t.past[b];
+  if (cur) {
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < G::kEpc; ++e) d = fmaf(qr[e], kx[e], d);
+    const float s_cur = token_sum<G::kLpt>(d) * a.scale_log2;
+    const float m2 = fmaxf(part.m, s_cur);
+    const float w1 = part.m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(part.m - m2);
+    const float wc = __builtin_amdgcn_exp2f(s_cur - m2);
+    part.z = fmaf(part.z, w1, wc);
+#pragma unroll
+    for (int e = 0; e < G::kEpc; ++e) part.acc[e] = fmaf(part.acc[e], w1, wc * vx[e]);
+  }
   if (units == 1) {
     if (j == 0) {
 #pragma unroll
@@ -1820,10 +1958,22 @@ __device__ __forceinline__ void fmerge_flat_body(const ppk::FloatMergeFlatArgs& 
   const uint32_t units = t.units[b];
   if (units < 2) return;  // uniform per wave
   const uint32_t ldev = a.lengths[b];
-  float m, zsum, y[EPL];
+  float m, zsum, y[EPL], vcur[EPL];
+  float s_cur = -INFINITY;
+  auto current = [&]() {
+    if (a.step) s_cur = merge_current<D>(a, row, lane, vcur);
+    return s_cur;
+  };
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D,
-                     min(units, a.nsplits), lane, [] { return -INFINITY; }, m, zsum, y);
-  const bool valid = t.len[b] > 0 && ldev == t.past[b];
+                     min(units, a.nsplits), lane, current, m, zsum, y);
+  if (a.step) {
+    const float wc = __builtin_amdgcn_exp2f(s_cur - m);
+    zsum += wc;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) y[e] = fmaf(wc, vcur[e], y[e]);
+  }
+  const bool valid = a.step ? (ldev == t.past[b] && t.past[b] < a.size && t.past[b] + 1 <= a.span)
+                            : (t.len[b] > 0 && ldev == t.past[b]);
   const size_t base = size_t(row) * D + size_t(lane) * EPL;
 #pragma unroll
   for (int e = 0; e < EPL; ++e)
@@ -2234,10 +2384,16 @@ PPK_ATTN_FLAT(256)
 
 #define PPK_FLOAT_ATTN(D)                                                                        \
   extern "C" __global__ __launch_bounds__(1024) void ppk_fdecode_bf16_d##D(ppk::FloatDecodeArgs a) { \
-    fdecode_body<D, true>(a);                                                                    \
+    fdecode_body<D, true, false>(a);                                                             \
   }                                                                                              \
   extern "C" __global__ __launch_bounds__(1024) void ppk_fdecode_f32_d##D(ppk::FloatDecodeArgs a) {  \
-    fdecode_body<D, false>(a);                                                                   \
+    fdecode_body<D, false, false>(a);                                                            \
+  }                                                                                              \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_fstep_bf16_d##D(ppk::FloatDecodeArgs a) {   \
+    fdecode_body<D, true, true>(a);                                                              \
+  }                                                                                              \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_fstep_f32_d##D(ppk::FloatDecodeArgs a) {    \
+    fdecode_body<D, false, true>(a);                                                             \
   }                                                                                              \
   extern "C" __global__ __launch_bounds__(64) void ppk_fmerge_d##D(ppk::FloatMergeArgs a) {      \
     fmerge_body<D>(a);                                                                           \
@@ -2248,10 +2404,16 @@ PPK_FLOAT_ATTN(256)
 
 #define PPK_FLOAT_ATTN_FLAT(D)                                                                                 \
   extern "C" __global__ __launch_bounds__(512) void ppk_fdecode_flat_bf16_d##D(ppk::FloatDecodeFlatArgs a) { \
-    fdecode_flat_body<D, true>(a);                                                                             \
+    fdecode_flat_body<D, true, false>(a);                                                                      \
   }                                                                                                            \
   extern "C" __global__ __launch_bounds__(512) void ppk_fdecode_flat_f32_d##D(ppk::FloatDecodeFlatArgs a) {  \
-    fdecode_flat_body<D, false>(a);                                                                            \
+    fdecode_flat_body<D, false, false>(a);                                                                     \
+  }                                                                                                            \
+  extern "C" __global__ __launch_bounds__(512) void ppk_fstep_flat_bf16_d##D(ppk::FloatDecodeFlatArgs a) {   \
+    fdecode_flat_body<D, true, true>(a);                                                                       \
+  }                                                                                                            \
+  extern "C" __global__ __launch_bounds__(512) void ppk_fstep_flat_f32_d##D(ppk::FloatDecodeFlatArgs a) {    \
+    fdecode_flat_body<D, false, true>(a);                                                                      \
   }                                                                                                            \
   extern "C" __global__ __launch_bounds__(64) void ppk_fmerge_flat_d##D(ppk::FloatMergeFlatArgs a) {          \
     fmerge_flat_body<D>(a);                                                                                    \

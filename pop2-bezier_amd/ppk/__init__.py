@@ -11,7 +11,7 @@ from ._abi import (PPK_ABI_VERSION, PPK_ATTN_BF16_HISTORY, PPK_ATTN_PLAN_BALANCE
                    PPK_KERNEL_DEQUANTIZE, PPK_KERNEL_FLOAT_ATTENTION, PPK_KERNEL_FLOAT_MERGE, PPK_KERNEL_QUANTIZE,
                    PPK_KERNEL_RENYI_SAMPLE, PpkError,
                    PpkExecutionUncertainError, PpkInvalidOutputError, PpkPreconditionError)
-from .fused_attention import FloatDecodeAttention
+from .fused_attention import FloatDecodeAttention, FloatDecodeStep
 from .kv_arena import LayerCache, WritePlan
 from .sampling import RenyiSampler
 from .int8_kv_ops import (AppendKV, DecodeAttention, DecodeStep, append, attention, context, decode_step,
@@ -23,7 +23,8 @@ __all__ = [
     "PPK_KERNEL_APPEND", "PPK_KERNEL_ATTN_MERGE", "PPK_KERNEL_ATTENTION", "PPK_KERNEL_COPY", "PPK_KERNEL_DEQUANTIZE",
     "PPK_KERNEL_FLOAT_ATTENTION", "PPK_KERNEL_FLOAT_MERGE", "PPK_KERNEL_QUANTIZE", "PPK_KERNEL_RENYI_SAMPLE",
     "PpkError", "PpkExecutionUncertainError", "PpkInvalidOutputError", "PpkPreconditionError",
-    "AppendKV", "DecodeAttention", "DecodeStep", "FloatDecodeAttention", "LayerCache", "RenyiSampler", "WritePlan",
+    "AppendKV", "DecodeAttention", "DecodeStep", "FloatDecodeAttention", "FloatDecodeStep", "LayerCache",
+    "RenyiSampler", "WritePlan",
     "fused_attention", "kv_arena", "sampling",
     "append", "attention", "context", "decode_step", "dequantize", "kernel_stats", "prepare", "prepare_int8_kv",
     "quantize",

@@ -66,6 +66,11 @@ class PpkFloatAttentionArgs(ctypes.Structure):
                 ("workspace_bytes", _u64), ("lengths_host", _ptr)]
 
 
+class PpkFloatDecodeStepArgs(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("new_dtype", _u32), ("k_new", _ptr), ("v_new", _ptr), ("flags", _ptr),
+                ("attn", PpkFloatAttentionArgs)]
+
+
 class PpkRenyiSampleArgs(ctypes.Structure):
     _fields_ = [("struct_size", _u32), ("batch", _u32), ("choices", _u32), ("guidance", _u32), ("alpha", _f32),
                 ("cfg", _f32), ("token_offset", _u32), ("reserved", _u32), ("raw", _ptr), ("uniforms", _ptr),
@@ -123,6 +128,7 @@ FUNCTIONS = {
     "ppk_float_attention_plan": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkFloatAttentionArgs), ctypes.POINTER(_u32),
                                                   ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
     "ppk_float_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatAttentionArgs)]),
+    "ppk_float_decode_step": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatDecodeStepArgs)]),
     "ppk_float_attention_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_renyi_sample": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkRenyiSampleArgs)]),
     "ppk_kv_cache_create": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkKvConfig), ctypes.POINTER(_ptr)]),

@@ -100,6 +100,43 @@ def decode_attention(q, k, v, lengths, heads: int, split_tokens: int = 0, *, max
     return out
 
 
+def _step_args(a: _abi.PpkFloatAttentionArgs, k_new: torch.Tensor, v_new: torch.Tensor, flags,
+               lengths) -> _abi.PpkFloatDecodeStepArgs:
+    _require(lengths is not None, "the float decode step needs the device lengths")
+    _require(k_new.dtype == v_new.dtype and k_new.dtype in _DTYPES and k_new.numel() == a.rows * a.head_dim
+             and v_new.numel() == a.rows * a.head_dim and k_new.is_contiguous() and v_new.is_contiguous()
+             and k_new.is_cuda and v_new.is_cuda, "float decode step new token must be float[rows,D] on the device")
+    if flags is not None:
+        _require(flags.dtype in (torch.int32, torch.uint32) and flags.numel() >= 1, "flags must be one 32-bit word")
+    step = _abi.PpkFloatDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkFloatDecodeStepArgs),
+                                       new_dtype=_DTYPES[k_new.dtype], k_new=k_new.data_ptr(),
+                                       v_new=v_new.data_ptr(), flags=flags.data_ptr() if flags is not None else None,
+                                       attn=a)
+    step._lengths_host = getattr(a, "_lengths_host", None)  # the copied block points at it
+    return step
+
+
+def decode_step(q, k, v, lengths, heads: int, k_new: torch.Tensor, v_new: torch.Tensor, split_tokens: int = 0, *,
+                flags: torch.Tensor | None = None, max_length: int = 0, out_dtype: torch.dtype = torch.float32,
+                softmax_scale: float = 0.0, lengths_host=None, plan: str = "auto") -> torch.Tensor:
+    """The float path's fused decode step (ppk_float_decode_step): write k_new / v_new [rows, D] (rounded to the
+    store's dtype) at slot lengths[b] of the stores k / v [rows, size, D], then attend over the lengths[b] stored
+    tokens plus that one; the graph-decode session's scatter_set pair + decode_attention(lengths + 1)
+    (app/src/model/graph_decode.rs:290-305) in one launch. A row whose slot is past the store is not written
+    (PPK_FLAG_OVERFLOW in `flags`) and gives NaN."""
+    a, out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length,
+                                   out_dtype=out_dtype, softmax_scale=softmax_scale, lengths_host=lengths_host,
+                                   plan=plan)
+    step = _step_args(a, k_new, v_new, flags, lengths)
+    ctx = context(q.device)
+    nbytes = launch_plan(a, ctx)[2]
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    step.attn.workspace = ws.data_ptr()
+    step.attn.workspace_bytes = nbytes
+    check(lib().ppk_float_decode_step(ctx, _stream(q), ctypes.byref(step)), "ppk_float_decode_step")
+    return out
+
+
 class FloatDecodeAttention:
     """A prepared float-KV attention call for fixed buffers: argument block and workspace are built once;
     __call__ only enqueues the kernels (bench and serving loops, graph capture)."""
@@ -129,3 +166,30 @@ class FloatDecodeAttention:
 def prepare(device: torch.device | int | None = None) -> None:
     """hip_attention::validate_split_k on the device (raises PpkInvalidOutputError on a mismatch)."""
     check(lib().ppk_float_attention_prepare(context(device)), "ppk_float_attention_prepare")
+
+
+class FloatDecodeStep:
+    """A prepared fused float decode step for fixed buffers (the graph-decode session's per-layer call):
+    argument block and workspace are built once; __call__ only enqueues the kernels."""
+
+    def __init__(self, q, k, v, lengths, heads: int, k_new: torch.Tensor, v_new: torch.Tensor,
+                 split_tokens: int = 0, *, flags: torch.Tensor | None = None, max_length: int = 0,
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32, lengths_host=None,
+                 plan: str = "auto"):
+        a, self.out = decode_attention_args(q, k, v, lengths, heads, split_tokens, max_length=max_length, out=out,
+                                            out_dtype=out_dtype, lengths_host=lengths_host, plan=plan)
+        self.args = _step_args(a, k_new, v_new, flags, lengths)
+        self.ctx = context(q.device)
+        self.split_tokens, self.ngroups, nbytes = launch_plan(self.args.attn, self.ctx)
+        self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+        self.args.attn.workspace = self.workspace.data_ptr()
+        self.args.attn.workspace_bytes = nbytes
+        self._keep = (q, k, v, lengths, k_new, v_new, flags)
+        self._ref = ctypes.byref(self.args)
+        self._fn = lib().ppk_float_decode_step
+        self.device = q.device
+
+    def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_float_decode_step")
+        return self.out

@@ -59,8 +59,9 @@ def c_layout(tmp_path_factory):
     exe = src.with_suffix("")
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cls in (_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs, _abi.PpkAttentionArgs,
-                _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs, _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig,
-                _abi.PpkKvView, _abi.PpkKvInfo, _abi.PpkKvWrite, _abi.PpkInt8KvStatus):
+                _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs, _abi.PpkFloatDecodeStepArgs,
+                _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig, _abi.PpkKvView, _abi.PpkKvInfo, _abi.PpkKvWrite,
+                _abi.PpkInt8KvStatus):
         name = cls.__name__
         lines.append(f'printf("{name} __sizeof__ %zu\\n", sizeof({name}));')
         for field, _ in cls._fields_:
@@ -74,8 +75,8 @@ def c_layout(tmp_path_factory):
 
 @pytest.mark.parametrize("cls", [_abi.PpkQuantizeArgs, _abi.PpkAppendArgs, _abi.PpkDequantizeArgs,
                                  _abi.PpkAttentionArgs, _abi.PpkDecodeStepArgs, _abi.PpkFloatAttentionArgs,
-                                 _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig, _abi.PpkKvView, _abi.PpkKvInfo,
-                                 _abi.PpkKvWrite, _abi.PpkInt8KvStatus])
+                                 _abi.PpkFloatDecodeStepArgs, _abi.PpkRenyiSampleArgs, _abi.PpkKvConfig,
+                                 _abi.PpkKvView, _abi.PpkKvInfo, _abi.PpkKvWrite, _abi.PpkInt8KvStatus])
 def test_struct_layout_matches_c(c_layout, cls):
     name = cls.__name__
     assert c_layout[(name, "__sizeof__")] == ctypes.sizeof(cls)

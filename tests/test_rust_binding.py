@@ -179,8 +179,8 @@ def c_offsets(tmp_path_factory):
 def test_header_parser_sees_every_struct():
     names = set(header_structs())
     assert names == {"PpkQuantizeArgs", "PpkAppendArgs", "PpkDequantizeArgs", "PpkAttentionArgs",
-                     "PpkDecodeStepArgs", "PpkFloatAttentionArgs", "PpkRenyiSampleArgs", "PpkKvConfig",
-                     "PpkKvView", "PpkKvInfo", "PpkKvWrite", "PpkInt8KvStatus"}
+                     "PpkDecodeStepArgs", "PpkFloatAttentionArgs", "PpkFloatDecodeStepArgs", "PpkRenyiSampleArgs",
+                     "PpkKvConfig", "PpkKvView", "PpkKvInfo", "PpkKvWrite", "PpkInt8KvStatus"}
     # The multi-declarator line of PpkAppendArgs and the trailing optional field of PpkAttentionArgs.
     append = dict(header_structs()["PpkAppendArgs"])
     assert [append[k] for k in ("batch", "heads", "tokens", "head_dim", "capacity")] == ["u32"] * 5
