@@ -57,6 +57,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--device-lengths", action="store_true",
                    help="configs 1, 3, 4 and --lengths: pass the lengths on the device only (no host copy), i.e. "
                         "the per-row plan")
+    p.add_argument("--step", action="store_true",
+                   help="with --kv bf16/f32: time the fused float decode step (ppk_float_decode_step: write the "
+                        "current token at slot lengths[b] - 1, attend lengths[b] tokens) beside the reference's "
+                        "order (the token written by torch indexing, then the attention call)")
     p.add_argument("--lengths", default=None,
                    help="with --kv bf16/f32: comma-separated per-sequence lengths of a ragged batch (NxL repeats "
                         "L N times); the batch is their count and the store holds the longest")
@@ -171,8 +175,28 @@ def bench_float(args) -> int:
     q = torch.randn((rows, 1, D), generator=g, device=dev, dtype=torch.float32)
     lengths = torch.tensor(seq, dtype=torch.int32, device=dev)
     host = seq if args.lengths and not args.device_lengths else None
-    call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host)
-    flat = host is not None and ppk.fused_attention.plan(call.args, call.ctx) != ppk.fused_attention.plan(
+    two_call = None
+    if args.step:
+        # Each row holds lengths - 1 tokens; the step writes the current one and attends all of them.
+        stored = torch.tensor([n - 1 for n in seq], dtype=torch.int32, device=dev)
+        k_new = torch.randn((rows, D), generator=g, device=dev, dtype=torch.float32)
+        v_new = torch.randn((rows, D), generator=g, device=dev, dtype=torch.float32)
+        call = ppk.FloatDecodeStep(q, k, v, stored, H, k_new, v_new, args.split, max_length=L,
+                                   lengths_host=[n - 1 for n in seq] if host else None)
+        plan_args = call.args.attn
+        attend = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host)
+        row_idx = torch.arange(rows, device=dev)
+        slot = stored.repeat_interleave(H).long()
+        k_cast, v_cast = k_new.to(kv_dtype), v_new.to(kv_dtype)
+
+        def two_call():
+            k[row_idx, slot] = k_cast
+            v[row_idx, slot] = v_cast
+            attend()
+    else:
+        call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host)
+        plan_args = call.args
+    flat = host is not None and ppk.fused_attention.plan(plan_args, call.ctx) != ppk.fused_attention.plan(
         ppk.fused_attention.decode_attention_args(q, k, v, lengths, H, args.split, max_length=L)[0], call.ctx)
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
@@ -193,6 +217,17 @@ def bench_float(args) -> int:
     t_end.record(stream)
     torch.cuda.synchronize()
     step_ms = t_start.elapsed_time(t_end) / args.steps
+    two_call_ms = None
+    if two_call is not None:
+        for _ in range(args.warmup):
+            two_call()
+        torch.cuda.synchronize()
+        t_start.record(stream)
+        for _ in range(args.steps):
+            two_call()
+        t_end.record(stream)
+        torch.cuda.synchronize()
+        two_call_ms = t_start.elapsed_time(t_end) / args.steps
 
     ppk.kernel_stats(ppk.PPK_KERNEL_FLOAT_ATTENTION, reset=True)
     ppk.set_profiling(True)
@@ -213,7 +248,7 @@ def bench_float(args) -> int:
         kernel_bytes = step_bytes if call.ngroups == 1 else kv_bytes + rows * D * 4 + rows * call.ngroups * (D + 2) * 4
     achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
-    kname = f"ppk_fdecode_{'flat_' if flat else ''}{args.kv}_d{D}"
+    kname = f"ppk_{'fstep' if args.step else 'fdecode'}_{'flat_' if flat else ''}{args.kv}_d{D}"
     traffic = None
     if args.lengths:
         skew = args.lengths.replace(",", "_")
@@ -232,8 +267,8 @@ def bench_float(args) -> int:
         except (OSError, ValueError):
             traffic = None
     result = {
-        "metric": f"float-KV decode-attention µs/step + achieved HBM GB/s (% of peak), B={B} ctx={L} {args.kv} KV"
-                  + (f", ragged lengths {args.lengths}" if args.lengths else ""),
+        "metric": f"float-KV decode-{'step' if args.step else 'attention'} µs/step + achieved HBM GB/s (% of peak), "
+                  f"B={B} ctx={L} {args.kv} KV" + (f", ragged lengths {args.lengths}" if args.lengths else ""),
         "value": round(step_ms * 1e3, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_ms, 5), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": args.kv,
@@ -242,13 +277,21 @@ def bench_float(args) -> int:
                                "fused_attention::decode_attention)", "batch": B, "heads": H, "head_dim": D,
                    "context": L, "kv": args.kv, "query": "f32", "tokens_per_wave": call.split_tokens,
                    "blocks_per_row": call.ngroups, "launches_per_step": 1 if call.ngroups == 1 else 2,
-                   "lengths": args.lengths, "plan": "balanced" if flat else "per-row"},
+                   "lengths": args.lengths, "plan": "balanced" if flat else "per-row",
+                   "fused_step": bool(args.step)},
         "step_hbm_gbps": round(step_gbps, 1), "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": kernel_bytes, "avg_launch_us": round(kernel_avg_ms * 1e3, 2),
                      "launches": launches},
     }
+    if args.step:
+        result["config"]["workload"] = ("float-KV fused decode step (ppk_float_decode_step: the graph-decode "
+                                        "session's scatter_set pair + fused_attention::decode_attention)")
+        result["write_then_attend_us"] = round(two_call_ms * 1e3, 2)
+        result["write_then_attend_note"] = ("the reference's order on the same buffers: the current token "
+                                            "written by torch indexing (two kernels), then "
+                                            "ppk_float_decode_attention over lengths tokens")
     if not args.no_cpu_baseline:
         print("# bench: cpu baseline", file=sys.stderr, flush=True)
         sys.path.insert(0, os.path.join(ROOT, "oracle"))

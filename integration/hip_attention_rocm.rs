@@ -79,6 +79,21 @@ pub(super) fn decode_attention_with_host_lengths(
     heads: usize,
     split_tokens: usize,
 ) -> Result<Tensor> {
+    let op = decode_attention_op(q, k, v, lengths, lengths_host, heads, split_tokens)?;
+    Ok(q.apply_op3_no_bwd(k, v, &op)?)
+}
+
+/// The op of one attention call after the checks of hip_attention.rs:48-60
+/// (widened to D = 64 / 128 / 256, any length and F32 / BF16 / F16 queries).
+fn decode_attention_op(
+    q: &Tensor,
+    k: &Tensor,
+    v: &Tensor,
+    lengths: Option<&Tensor>,
+    lengths_host: Option<&[u32]>,
+    heads: usize,
+    split_tokens: usize,
+) -> Result<Decode> {
     let (rows, query, width) = q.dims3()?;
     let (key_rows, length, key_width) = k.dims3()?;
     ensure!(
@@ -119,7 +134,7 @@ pub(super) fn decode_attention_with_host_lengths(
     if let Some(host) = lengths_host {
         ensure!(lengths.is_some() && host.len() == rows / heads, "HIP attention host lengths differ from the batch");
     }
-    let op = Decode {
+    Ok(Decode {
         heads,
         rows,
         length,
@@ -127,7 +142,46 @@ pub(super) fn decode_attention_with_host_lengths(
         split: split_tokens,
         lengths: lengths.cloned(),
         lengths_host: lengths_host.map(<[u32]>::to_vec),
-    };
+        step: None,
+    })
+}
+
+/// The graph-decode session's per-layer commit + attend
+/// (app/src/model/graph_decode.rs:290-305: scatter_set of the current K/V at
+/// write_indices, then decode_attention over lengths + 1) in one call
+/// (no counterpart fuses them in the reference): k_new / v_new [rows, 1, D]
+/// (F32, BF16 or F16) are rounded to the store's dtype and written at slot
+/// lengths[b] of k / v [rows, length, D], which the op writes in place (they
+/// must be the caller's alone, as the session's own buffers are), and each
+/// row attends its lengths[b] stored tokens plus that one. `lengths` holds
+/// the stored counts before this step (the session's `lengths`, not
+/// `valid_lengths`); `lengths_host` its host copy (`expected_lengths`). A row
+/// whose slot is past the store is not written, sets PPK_FLAG_OVERFLOW in
+/// `flags` (optional U32[1]) and gives NaN.
+#[allow(clippy::too_many_arguments)]
+pub(super) fn decode_step(
+    q: &Tensor,
+    k: &Tensor,
+    v: &Tensor,
+    lengths: &Tensor,
+    lengths_host: Option<&[u32]>,
+    heads: usize,
+    k_new: &Tensor,
+    v_new: &Tensor,
+    flags: Option<&Tensor>,
+) -> Result<Tensor> {
+    let (rows, _, width) = q.dims3()?;
+    ensure!(
+        k_new.dims() == [rows, 1, width] && v_new.dims() == k_new.dims() && k_new.dtype() == v_new.dtype(),
+        "HIP decode step current token must be [batch*heads,1,D]"
+    );
+    if let Some(flags) = flags {
+        ensure!(flags.dims1()? >= 1 && flags.dtype() == DType::U32, "HIP decode step flags must be U32[1]");
+    }
+    // The shape, dtype and stride checks of the attention (the op below is the same one with the step's
+    // operands attached).
+    let checked = decode_attention_op(q, k, v, Some(lengths), lengths_host, heads, 0)?;
+    let op = Decode { step: Some((k_new.clone(), v_new.clone(), flags.cloned())), ..checked };
     Ok(q.apply_op3_no_bwd(k, v, &op)?)
 }
 
@@ -139,6 +193,7 @@ struct Decode {
     split: usize,
     lengths: Option<Tensor>,
     lengths_host: Option<Vec<u32>>,
+    step: Option<(Tensor, Tensor, Option<Tensor>)>,
 }
 
 /// Start address and row stride (elements) of a [rows, n, D] view whose
@@ -168,7 +223,11 @@ fn rows_view(
 
 impl CustomOp3 for Decode {
     fn name(&self) -> &'static str {
-        "ppk-float-decode-attention"
+        if self.step.is_some() {
+            "ppk-float-decode-step"
+        } else {
+            "ppk-float-decode-attention"
+        }
     }
 
     fn cpu_fwd(
@@ -234,7 +293,20 @@ impl CustomOp3 for Decode {
             a.workspace = ws.device_ptr_mut() as *mut c_void;
             a.workspace_bytes = bytes;
         }
-        ffi::check(unsafe { ffi::ppk_float_decode_attention(ctx, STREAM, &a) })?;
+        match &self.step {
+            None => ffi::check(unsafe { ffi::ppk_float_decode_attention(ctx, STREAM, &a) })?,
+            Some((k_new, v_new, flags)) => {
+                let mut s: ffi::PpkFloatDecodeStepArgs = ffi::args();
+                s.new_dtype = dtype_code(k_new.dtype())?;
+                s.k_new = bound.ptr(k_new, k_new.dtype(), "HIP decode step key")?;
+                s.v_new = bound.ptr(v_new, k_new.dtype(), "HIP decode step value")?;
+                if let Some(flags) = flags {
+                    s.flags = bound.ptr(flags, DType::U32, "HIP decode step flags")? as *mut u32;
+                }
+                s.attn = a;
+                ffi::check(unsafe { ffi::ppk_float_decode_step(ctx, STREAM, &s) })?;
+            }
+        }
         Ok((out, shape))
     }
 }

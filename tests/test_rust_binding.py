@@ -259,7 +259,7 @@ def test_rocm_ops_set_only_fields_of_their_argument_blocks():
                 for field in re.findall(rf"\b{var}\.(\w+)\s*=", body):
                     assert field in fields, f"{os.path.basename(path)}: {ty}.{field}"
     assert seen == {"PpkQuantizeArgs", "PpkDequantizeArgs", "PpkAttentionArgs", "PpkDecodeStepArgs",
-                    "PpkAppendArgs", "PpkFloatAttentionArgs", "PpkRenyiSampleArgs"}
+                    "PpkAppendArgs", "PpkFloatAttentionArgs", "PpkFloatDecodeStepArgs", "PpkRenyiSampleArgs"}
 
 
 def test_rocm_ops_cover_the_reference_functions():
@@ -273,9 +273,10 @@ def test_rocm_ops_cover_the_reference_functions():
     # hip_attention.rs's three functions (hip_attention.rs:7,18,47) with the reference's visibility.
     fl = _rust_text(FLOAT_OPS)
     for vis, fn in (("crate", "prepare"), ("crate", "validate_split_k"), ("super", "decode_attention"),
-                    ("super", "decode_attention_with_host_lengths")):
+                    ("super", "decode_attention_with_host_lengths"), ("super", "decode_step")):
         assert re.search(rf"pub\({vis}\) fn {fn}\(", fl), fn
-    for call in ("ppk_float_decode_attention", "ppk_float_attention_plan", "ppk_float_attention_prepare"):
+    for call in ("ppk_float_decode_attention", "ppk_float_attention_plan", "ppk_float_attention_prepare",
+                 "ppk_float_decode_step"):
         assert f"ffi::{call}(" in fl, call
     # HipSampler::rocm_fwd's body (hip_sampling.rs:120-214).
     sm = _rust_text(SAMPLER_OPS)
