@@ -502,15 +502,17 @@ PPK_API int32_t ppk_write_plan_release(ppk_write_plan* plan);
    per sequence at slot past_lens[b] (= each cache's committed length). A plan
    (optional) must match past_lens, heads and head_dim (checked on the host,
    no device read).
-   No counterpart in the reference: for int8 caches, write->k and write->v
-   both NULL reserve the slot instead — every step of the write happens
-   (growth, copy-on-write, joins, the device past / lengths of the view, the
-   commit) except storing the token, which the caller's ppk_decode_step on the
-   returned view (attn.k_codes = view.k, attn.past = view.past, k_new / v_new
-   = the new token) then quantises into slot past[b] in the same launch as the
-   attention: one launch per layer instead of two, the same codes, scales and
-   output. The decode step must follow on the same stream before anything
-   reads the slot. */
+   No counterpart in the reference: for int8, bf16 and f32 caches, write->k
+   and write->v both NULL reserve the slot instead — every step of the write
+   happens (growth, copy-on-write, joins, the device past / lengths of the
+   view, the commit) except storing the token, which the caller's fused step
+   on the returned view then writes into slot past[b] in the same launch as
+   the attention: ppk_decode_step for int8 caches (attn.k_codes = view.k,
+   attn.past = view.past, k_new / v_new = the new token; the same codes,
+   scales and output as the two calls), ppk_float_decode_step for bf16 / f32
+   caches (attn.k = view.k, attn.size = view.capacity, attn.lengths =
+   view.past, attn.max_length = view.length). The step must follow on the
+   same stream before anything reads the slot. */
 PPK_API int32_t ppk_kv_query_batch(ppk_context* ctx, void* stream, ppk_kv_cache* const* caches, uint32_t batch,
                                    const uint32_t* past_lens, const PpkKvWrite* write, const ppk_write_plan* plan,
                                    PpkKvView* out);

@@ -262,14 +262,17 @@ bool same_config(const PpkKvConfig& a, const PpkKvConfig& b) {
 }
 
 // A batch write with both sources NULL reserves slot past[b] of every row of
-// an int8 cache (all of the write's bookkeeping, no data): the caller's fused
-// decode step fills it on the same stream.
+// an int8, bf16 or f32 cache (all of the write's bookkeeping, no data): the
+// caller's fused decode step (int8, or the float path's) fills it on the same
+// stream. F16 caches have no float decode step (the float attention reads
+// bf16 and f32 stores).
 bool reserves(const PpkKvWrite& w) { return w.k == nullptr && w.v == nullptr; }
 
 void check_write(const PpkKvConfig& cfg, const PpkKvWrite& w, bool reserve_allowed) {
   require(w.struct_size >= sizeof(PpkKvWrite), "PpkKvWrite.struct_size too small");
   if (reserve_allowed && reserves(w)) {
-    require(cfg.kind == PPK_KV_INT8, "a reserving KV write (NULL sources) needs an int8 cache");
+    require(cfg.kind == PPK_KV_INT8 || cfg.kind == PPK_KV_BF16 || cfg.kind == PPK_KV_F32,
+            "a reserving KV write (NULL sources) needs an int8, bf16 or f32 cache");
     return;
   }
   require(w.k && w.v, "KV query null source");

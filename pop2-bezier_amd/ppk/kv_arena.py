@@ -221,15 +221,23 @@ class LayerCache:
 def decode_step(view: _abi.PpkKvView, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, heads: int, *,
                 out_dtype: torch.dtype = torch.float32, past_host=None, flags: torch.Tensor | None = None,
                 bf16_history: bool = False, plan: str = "auto") -> torch.Tensor:
-    """The fused decode step over a reserved batch view of int8 caches (LayerCache.query_batch with k = v =
-    None): quantise k_new / v_new (the current token, [B*H, D] or [B, H, 1, D]) into slot past[b] of the
-    view's arenas and attend over [0, past[b]) plus that token unquantised, in one launch (two when rows
-    span blocks); returns out [B*H, 1, D]. The commit path of forward_batched_embedding
-    (app/src/model/batch.rs:152-161) with query_int8 and int8_kv_ops::attention joined."""
+    """The fused decode step over a reserved batch view (LayerCache.query_batch with k = v = None): write
+    k_new / v_new (the current token, [B*H, D] or [B, H, 1, D]) into slot past[b] of the view's arenas and
+    attend over [0, past[b]) plus that token, in one launch (two when rows span blocks); returns out
+    [B*H, 1, D]. Int8 caches (ppk_decode_step): the token is quantised there and attended unquantised, the
+    commit path of forward_batched_embedding (app/src/model/batch.rs:152-161) with query_int8 and
+    int8_kv_ops::attention joined. Bf16 / f32 caches (ppk_float_decode_step): the token is rounded to the
+    cache's dtype, written and attended, the float cache's commit + fused_attention::decode_attention
+    (app/src/model/mod.rs:699-720) joined; bf16_history does not apply."""
     from .int8_kv_ops import _step_args, workspace_bytes
 
-    if view.kind != _abi.PPK_KV_INT8 or not view.batch or not view.past:
-        raise ValueError("decode_step needs the batch view of int8 caches")
+    if not view.batch or not view.past:
+        raise ValueError("decode_step needs a batch view")
+    if view.kind in (_abi.PPK_KV_BF16, _abi.PPK_KV_F32):
+        return _float_decode_step(view, q, k_new, v_new, heads, out_dtype=out_dtype, past_host=past_host,
+                                  flags=flags, plan=plan)
+    if view.kind != _abi.PPK_KV_INT8:
+        raise ValueError("decode_step needs the batch view of int8, bf16 or f32 caches")
     rows, d, cap = view.rows, view.head_dim, view.capacity
     for t in (q, k_new, v_new):
         if t.numel() != rows * d or t.dtype not in _DTYPES or not t.is_contiguous() or not t.is_cuda:
@@ -255,6 +263,41 @@ def decode_step(view: _abi.PpkKvView, q: torch.Tensor, k_new: torch.Tensor, v_ne
     step.attn.workspace = ws.data_ptr()
     step.attn.workspace_bytes = nbytes
     check(lib().ppk_decode_step(ctx, _stream(q), ctypes.byref(step)), "ppk_decode_step")
+    return out
+
+
+def _float_decode_step(view: _abi.PpkKvView, q, k_new, v_new, heads: int, *, out_dtype, past_host, flags,
+                       plan: str) -> torch.Tensor:
+    rows, d, cap = view.rows, view.head_dim, view.capacity
+    for t in (q, k_new, v_new):
+        if t.numel() != rows * d or t.dtype not in _DTYPES or not t.is_contiguous() or not t.is_cuda:
+            raise ValueError("float decode step operands must be dense float [B*H, D] on the device")
+    if heads <= 0 or rows % heads or rows // heads != view.batch or k_new.dtype != v_new.dtype:
+        raise ValueError("float decode step geometry differs")
+    if flags is not None and (flags.dtype not in (torch.int32, torch.uint32) or flags.numel() < 1):
+        raise ValueError("flags must be one 32-bit word")
+    out = torch.empty((rows, 1, d), dtype=out_dtype, device=q.device)
+    a = _abi.PpkFloatAttentionArgs(
+        struct_size=ctypes.sizeof(_abi.PpkFloatAttentionArgs),
+        kv_dtype=_abi.PPK_BF16 if view.kind == _abi.PPK_KV_BF16 else _abi.PPK_F32, q_dtype=_DTYPES[q.dtype],
+        out_dtype=_DTYPES[out_dtype], rows=rows, heads=heads, size=cap, head_dim=d, split_tokens=0,
+        max_length=view.length, softmax_scale=0.0, flags=_abi.plan_flags(plan), q_row_stride=0, k_row_stride=0,
+        v_row_stride=0, q=q.data_ptr(), k=view.k, v=view.v, lengths=view.past, out=out.data_ptr(), workspace=None,
+        workspace_bytes=0, lengths_host=None)
+    if past_host is not None:
+        a._lengths_host = (ctypes.c_uint32 * view.batch)(*[int(x) for x in past_host])
+        a.lengths_host = ctypes.cast(a._lengths_host, ctypes.c_void_p).value
+    step = _abi.PpkFloatDecodeStepArgs(struct_size=ctypes.sizeof(_abi.PpkFloatDecodeStepArgs),
+                                       new_dtype=_DTYPES[k_new.dtype], k_new=k_new.data_ptr(), v_new=v_new.data_ptr(),
+                                       flags=flags.data_ptr() if flags is not None else None, attn=a)
+    ctx = context(q.device)
+    split, nsplits, nbytes = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+    check(lib().ppk_float_attention_plan(ctx, ctypes.byref(step.attn), ctypes.byref(split), ctypes.byref(nsplits),
+                                         ctypes.byref(nbytes)), "ppk_float_attention_plan")
+    ws = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, device=q.device)
+    step.attn.workspace = ws.data_ptr()
+    step.attn.workspace_bytes = nbytes.value
+    check(lib().ppk_float_decode_step(ctx, _stream(q), ctypes.byref(step)), "ppk_float_decode_step")
     return out
 
 

@@ -366,9 +366,57 @@ def test_reserved_batch_write_and_fused_step_equal_write_then_attention(device):
         past = [p + 1 for p in past]
 
 
-def test_reserving_write_needs_int8_caches(device):
-    caches = [LayerCache(torch.float32, 2, 64) for _ in range(2)]
+def test_reserving_write_needs_int8_bf16_or_f32_caches(device):
+    """F16 caches have no fused step (the float attention reads bf16 and f32 stores): a reserving write is
+    refused before anything changes."""
+    caches = [LayerCache(torch.float16, 2, 64) for _ in range(2)]
     with pytest.raises(ppk.PpkError) as e:
         LayerCache.query_batch(caches, None, None, [0, 0], True)
     assert e.value.status == _abi.PPK_PRECONDITION
     assert [len(c) for c in caches] == [0, 0]
+
+
+@pytest.mark.parametrize("kind", [torch.bfloat16, torch.float32])
+def test_reserved_float_batch_write_and_fused_step_equal_write_then_attention(device, kind):
+    """The float caches' reserve + ppk_float_decode_step against the two-call path (the token written by
+    ppk_kv_query_batch, then ppk_float_decode_attention over past + 1): the arenas bit for bit over a join
+    round and two steady rounds of ragged sequences; outputs within the float path's bars (the fused step
+    folds the current token from registers, a different fp32 order)."""
+    from helpers import assert_close
+    from ppk import kv_arena
+
+    heads, d, lengths = 4, 128, [37, 0, 120]
+    g = torch.Generator(device=device).manual_seed(12)
+    sets = []
+    for _ in range(2):
+        caches = [LayerCache(kind, heads, d) for _ in lengths]
+        for c, n in zip(caches, lengths):
+            if n:
+                x = torch.randn((heads, n, d), generator=torch.Generator(device=device).manual_seed(n),
+                                device=device).to(kind)
+                c.query(x, x, 0, True)
+        sets.append(caches)
+    past = list(lengths)
+    for rnd in range(3):
+        q = torch.randn((len(past) * heads, d), generator=g, device=device)
+        kn = torch.randn((len(past), heads, 1, d), generator=g, device=device).to(kind)
+        vn = torch.randn((len(past), heads, 1, d), generator=g, device=device).to(kind)
+        va = LayerCache.query_batch(sets[0], kn, vn, past, True, WritePlan(past, heads, d))
+        view_len = va.length
+        k_view, v_view = read(va, "k"), read(va, "v")
+        lengths_after = torch.tensor([p + 1 for p in past], dtype=torch.int32, device=device)
+        out_a = ppk.fused_attention.decode_attention(q.reshape(-1, 1, d), k_view, v_view, lengths_after, heads)
+        vb = LayerCache.query_batch(sets[1], None, None, past, True, WritePlan(past, heads, d))
+        out_b = kv_arena.decode_step(vb, q, kn.reshape(-1, d), vn.reshape(-1, d), heads, past_host=past)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out_b).all()
+        assert_close(out_b.reshape(-1, d).cpu().numpy(), out_a.reshape(-1, d).cpu().numpy(), atol=1e-4, rtol=1e-2,
+                     what=f"{kind} round {rnd}")
+        assert vb.length == view_len
+        for which in ("k", "v"):
+            ra, rb = read(va, which), read(vb, which)
+            for row, p in enumerate(past):
+                rows = slice(row * heads, (row + 1) * heads)
+                assert torch.equal(ra[rows, :p + 1], rb[rows, :p + 1]), f"round {rnd} {which} sequence {row}"
+        assert [len(c) for c in sets[1]] == [p + 1 for p in past]
+        past = [p + 1 for p in past]
