@@ -147,7 +147,7 @@ DeviceGuard::~DeviceGuard() {
 }
 
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
-                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim) {
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, bool even_split) {
   AttentionPlan plan;
   plan.head_dim = head_dim;
   uint32_t split;
@@ -163,6 +163,20 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 8;
     split = 64;
     while (split < 2048 && uint64_t(rows) * ((span + split - 1) / split) > budget) split <<= 1;
+    if (even_split) {
+      // The same number of waves per row, each with an equal share (rounded
+      // up to whole tiles) instead of full splits and a short last one: the
+      // int8 kernel's rate is set per CU, so the longest wave sets the time.
+      // Measured on MI355X (B = 32, H = 16, D = 64 / 128, per step): 1100
+      // tokens, 18.4 -> 16.0 / 30.1 -> 26.1 us; 5000 tokens, 59.8 -> 56.9 /
+      // 112.0 -> 106.5 us; 3000 tokens within 1.5 %; 8192 unchanged (the
+      // splits were already equal). The float kernel, whose waves run at the
+      // memory system's pace, gained nothing (5000 tokens at D = 128: 189.6
+      // -> 193.9 us) and keeps full splits.
+      const uint64_t waves = std::max<uint64_t>(1, (span + split - 1) / split);
+      const uint64_t share = ((span + waves - 1) / waves + tpl - 1) / tpl * tpl;
+      split = uint32_t(std::min<uint64_t>(split, std::max<uint64_t>(share, tpl)));
+    }
   }
   const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
   // Up to 16 waves per block; one float of LDS per history token of the block.
@@ -224,7 +238,7 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   const uint32_t tpl = 64u / (a.head_dim / 16u);
   const uint64_t span = a.max_past ? a.max_past : a.capacity;
   // Per history token: K and V codes plus two fp32 scales.
-  AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
+  AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim, true);
   // With the host's lengths of a ragged batch, the balanced plan gives every
   // wave the same share of the live history. It is taken when the per-row
   // plan's busiest CU would stream at least 1.2 x the history the balanced
@@ -669,7 +683,7 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   const uint32_t tpl = 64u / (a.head_dim / uint32_t(16 / eb));
   const uint64_t span = a.max_length ? a.max_length : a.size;
   AttentionPlan plan =
-      plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
+      plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim, false);
   // With the host's copy of the lengths, a ragged batch takes the balanced
   // plan (the int8 path's table) when its longest row holds more than
   // 512 KiB of K and V and the per-row plan's waves are uneven (the most
