@@ -164,16 +164,22 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     split = 64;
     while (split < 2048 && uint64_t(rows) * ((span + split - 1) / split) > budget) split <<= 1;
     if (even_split) {
-      // The same number of waves per row, each with an equal share (rounded
-      // up to whole tiles) instead of full splits and a short last one: the
-      // int8 kernel's rate is set per CU, so the longest wave sets the time.
-      // Measured on MI355X (B = 32, H = 16, D = 64 / 128, per step): 1100
-      // tokens, 18.4 -> 16.0 / 30.1 -> 26.1 us; 5000 tokens, 59.8 -> 56.9 /
-      // 112.0 -> 106.5 us; 3000 tokens within 1.5 %; 8192 unchanged (the
-      // splits were already equal). The float kernel, whose waves run at the
-      // memory system's pace, gained nothing (5000 tokens at D = 128: 189.6
-      // -> 193.9 us) and keeps full splits.
-      const uint64_t waves = std::max<uint64_t>(1, (span + split - 1) / split);
+      // As many waves per row as the budget holds (up to 16, none under 64
+      // tokens), each with an equal share rounded up to whole tiles, instead
+      // of full splits and a short last one: the int8 kernel's rate is set
+      // per CU, so the longest wave sets the time. Measured on MI355X (H =
+      // 16, D = 64 / 128, per step, power-of-two splits -> equal shares ->
+      // equal shares filling the budget): B = 32 x 1100 tokens, 18.4 / 30.1
+      // -> 16.0 / 26.1 -> 16.2 / 25.6 us; x 3000, 36.0 / 64.6 -> 36.4 / 64.9
+      // -> 34.8 / 64.2 us; x 5000, 59.8 / 112.0 -> 56.9 / 106.5 -> 55.4 /
+      // 102.3 us; B = 16 x 1500, 12.5 / 20.3 -> 12.1 / 20.1 -> 12.0 / 18.2
+      // us; B = 32 x 8192 (config 5) unchanged, its splits already equal and
+      // the budget full. The float kernel, whose waves run at the memory
+      // system's pace, gained nothing from equal shares (5000 tokens at
+      // D = 128: 189.6 -> 193.9 us) and keeps full splits.
+      uint64_t waves = std::max<uint64_t>(1, (span + split - 1) / split);
+      const uint64_t fill = std::min<uint64_t>(16, budget / std::max<uint64_t>(rows, 1));
+      waves = std::max<uint64_t>(waves, std::min<uint64_t>(fill, (span + 63) / 64));
       const uint64_t share = ((span + waves - 1) / waves + tpl - 1) / tpl * tpl;
       split = uint32_t(std::min<uint64_t>(split, std::max<uint64_t>(share, tpl)));
     }
