@@ -147,7 +147,7 @@ DeviceGuard::~DeviceGuard() {
 }
 
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
-                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, bool even_split) {
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim) {
   AttentionPlan plan;
   plan.head_dim = head_dim;
   uint32_t split;
@@ -163,26 +163,23 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     const uint64_t budget = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1)) * 8;
     split = 64;
     while (split < 2048 && uint64_t(rows) * ((span + split - 1) / split) > budget) split <<= 1;
-    if (even_split) {
-      // As many waves per row as the budget holds (up to 16, none under 64
-      // tokens), each with an equal share rounded up to whole tiles, instead
-      // of full splits and a short last one: the int8 kernel's rate is set
-      // per CU, so the longest wave sets the time. Measured on MI355X (H =
-      // 16, D = 64 / 128, per step, power-of-two splits -> equal shares ->
-      // equal shares filling the budget): B = 32 x 1100 tokens, 18.4 / 30.1
-      // -> 16.0 / 26.1 -> 16.2 / 25.6 us; x 3000, 36.0 / 64.6 -> 36.4 / 64.9
-      // -> 34.8 / 64.2 us; x 5000, 59.8 / 112.0 -> 56.9 / 106.5 -> 55.4 /
-      // 102.3 us; B = 16 x 1500, 12.5 / 20.3 -> 12.1 / 20.1 -> 12.0 / 18.2
-      // us; B = 32 x 8192 (config 5) unchanged, its splits already equal and
-      // the budget full. The float kernel, whose waves run at the memory
-      // system's pace, gained nothing from equal shares (5000 tokens at
-      // D = 128: 189.6 -> 193.9 us) and keeps full splits.
-      uint64_t waves = std::max<uint64_t>(1, (span + split - 1) / split);
-      const uint64_t fill = std::min<uint64_t>(16, budget / std::max<uint64_t>(rows, 1));
-      waves = std::max<uint64_t>(waves, std::min<uint64_t>(fill, (span + 63) / 64));
-      const uint64_t share = ((span + waves - 1) / waves + tpl - 1) / tpl * tpl;
-      split = uint32_t(std::min<uint64_t>(split, std::max<uint64_t>(share, tpl)));
-    }
+    // Then as many waves per row as the budget holds (up to 16, none under
+    // 64 tokens), each with an equal share rounded up to whole tiles, instead
+    // of full splits and a short last one: the longest wave sets the time.
+    // Measured on MI355X (H = 16, D = 64 / 128, per step, power-of-two splits
+    // -> equal shares filling the budget), int8: B = 32 x 1100 tokens, 18.4 /
+    // 30.1 -> 16.2 / 25.6 us; x 3000, 36.0 / 64.6 -> 34.8 / 64.2 us; x 5000,
+    // 59.8 / 112.0 -> 55.4 / 102.3 us; B = 16 x 1500, 12.5 / 20.3 -> 12.0 /
+    // 18.2 us. Float, bf16: B = 16 x 1500, 16.0 / 30.4 -> 14.4 / 29.0 us;
+    // x 4000, 40.4 / 79.4 -> 39.3 / 77.2 us; B = 32 x 3000, 58.1 / 117.4 ->
+    // 57.8 / 114.7 us; B = 32 x 1100 and B = 64 x 600 within 1.5 % (f32 the
+    // same within 2 %). B = 32 x 8192 (config 5) is unchanged: its splits
+    // are already equal and the budget full.
+    uint64_t waves = std::max<uint64_t>(1, (span + split - 1) / split);
+    const uint64_t fill = std::min<uint64_t>(16, budget / std::max<uint64_t>(rows, 1));
+    waves = std::max<uint64_t>(waves, std::min<uint64_t>(fill, (span + 63) / 64));
+    const uint64_t share = ((span + waves - 1) / waves + tpl - 1) / tpl * tpl;
+    split = uint32_t(std::min<uint64_t>(split, std::max<uint64_t>(share, tpl)));
   }
   const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
   // Up to 16 waves per block; one float of LDS per history token of the block.
@@ -244,7 +241,7 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   const uint32_t tpl = 64u / (a.head_dim / 16u);
   const uint64_t span = a.max_past ? a.max_past : a.capacity;
   // Per history token: K and V codes plus two fp32 scales.
-  AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim, true);
+  AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
   // With the host's lengths of a ragged batch, the balanced plan gives every
   // wave the same share of the live history. It is taken when the per-row
   // plan's busiest CU would stream at least 1.2 x the history the balanced
@@ -689,7 +686,7 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   const uint32_t tpl = 64u / (a.head_dim / uint32_t(16 / eb));
   const uint64_t span = a.max_length ? a.max_length : a.size;
   AttentionPlan plan =
-      plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim, false);
+      plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
   // With the host's copy of the lengths, a ragged batch takes the balanced
   // plan (the int8 path's table) when its longest row holds more than
   // 512 KiB of K and V and the per-row plan's waves are uneven (the most

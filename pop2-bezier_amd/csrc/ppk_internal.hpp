@@ -173,11 +173,9 @@ struct AttentionPlan {
   FlatTable table{};
 };
 // Split policy shared by both attention paths: span history tokens per row,
-// tpl tokens per wave-wide load, token_bytes of K+V (+scales) per token;
-// even_split: a row's waves take equal shares rather than full splits and a
-// short last one.
+// tpl tokens per wave-wide load, token_bytes of K+V (+scales) per token.
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
-                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, bool even_split);
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim);
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
 // The balanced plan of `rows` rows, `heads` per sequence, from the host
 // lengths host[0 .. rows / heads) (at most 64 sequences); a length above

@@ -132,12 +132,12 @@ def test_plan_sizes_workspace_without_a_device():
                                            past_host=[10, 0, 60, 64])) == per_row
     # Few short rows (config 1 shape): one block per row, one launch.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=513, max_past=512, head_dim=64)) == (64, 1, 0)
-    # Spans that are no multiple of the power-of-two split: the int8 plan gives each row as many waves as
-    # the budget holds (2048 / 512 rows = 4) with equal shares rounded up to whole 8-token tiles (1100 / 4 =
-    # 275 -> 280), one block per row; the float plan keeps full 512-token splits.
+    # Spans that are no multiple of the power-of-two split: each row gets as many waves as the budget holds
+    # (2048 / 512 rows = 4) with equal shares rounded up to whole tiles (1100 / 4 = 275 -> 280 for the int8
+    # path's 8-token tiles, 276 for bf16's 4-token tiles at D = 128), one block per row.
     assert ppk.int8_kv_ops.plan(_attn_args(capacity=1101, max_past=1100)) == (280, 1, 0)
     assert ppk.int8_kv_ops.plan(_attn_args(rows=256, capacity=1501, max_past=1500)) == (192, 1, 0)
-    assert ppk.fused_attention.plan(_float_args(size=1100)) == (512, 1, 0)
+    assert ppk.fused_attention.plan(_float_args(size=1100)) == (276, 1, 0)
 
 
 def _per_row_waves(rows, span, split, token_bytes, cus=256):

@@ -87,10 +87,16 @@ def test_rows_beyond_max_length_give_nan(device):
 
 
 def test_per_row_plan_nans_rows_beyond_max_length_inside_its_cover(device):
-    """max_length = 50 plans one 64-token wave per row; a 60-token row fits the wave but exceeds
-    max_length, and gives NaN as documented rather than its value."""
+    """max_length = 50 plans one wave per row; with an explicit 64-token split a 60-token row fits the wave
+    but exceeds max_length, and gives NaN as documented rather than its value (so does the automatic plan,
+    whose wave covers 52 tokens)."""
     c = FloatCase(device, 2, 4, 64, 100, torch.float32, lengths=[60, 40], seed=SEED + 14)
-    assert _plan(c, None, max_length=50)[:2] == (64, 1)
+    assert _plan(c, None, max_length=50)[1] == 1
+    a, _ = ppk.fused_attention.decode_attention_args(c.q, c.k, c.v, c.lengths_t, c.H, 64, max_length=50)
+    assert ppk.fused_attention.plan(a, ppk.context(device))[:2] == (64, 1)
+    got = c.run(64, max_length=50)
+    assert np.isnan(got[:4]).all()
+    assert_close(got[4:], c.reference()[4:], atol=ATOL, rtol=RTOL, what="row within max_length, split 64")
     got = c.run(max_length=50)
     assert np.isnan(got[:4]).all()
     assert_close(got[4:], c.reference()[4:], atol=ATOL, rtol=RTOL, what="row within max_length")
