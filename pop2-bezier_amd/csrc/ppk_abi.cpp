@@ -203,8 +203,11 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     plan.waves = uint32_t(waves_per_row);
     plan.ngroups = 1;
   } else {
-    plan.waves = uint32_t(max_waves);
+    // The fewest blocks of at most max_waves waves, then the waves spread
+    // evenly over them (16 waves in blocks of 5 are four blocks of 4, not
+    // 5 + 5 + 5 + 1, whose last block would leave its CU idle early).
     plan.ngroups = uint32_t((waves_per_row + max_waves - 1) / max_waves);
+    plan.waves = uint32_t((waves_per_row + plan.ngroups - 1) / plan.ngroups);
   }
   require(uint64_t(plan.ngroups) * rows <= 0x7fffffffu, "attention grid too large");
   // Per wave: one log2-domain score per token; after the waves are done the
@@ -243,22 +246,8 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   // Per history token: K and V codes plus two fp32 scales.
   AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
   // With the host's lengths of a ragged batch, the balanced plan gives every
-  // wave the same share of the live history. It is taken when the per-row
-  // plan's busiest CU would stream at least 1.2 x the history the balanced
-  // plan's busiest CU streams (the int8 kernel's rate is set per CU: the
-  // blocks of a long row all sit on one CU). Measured on MI355X (H = 16,
-  // bf16 q, D = 64 / 128, per step, per-row -> balanced), taken: 4 sequences
-  // of 8192 tokens beside 28 of 512, 41.3 -> 26.6 / 76.6 -> 42.8 us; 8 of
-  // 4096 beside 24 of 1024, 30.2 -> 27.3 / 53.2 -> 45.3 us; B = 16 of
-  // 256..16384, 62.4 -> 53.1 / 109.4 -> 96.4 us; B = 32 of 256..8192, 58.0
-  // -> 54.5 / 108.9 -> 97.9 us; B = 64 of 64..4096, 57.1 -> 55.6 / 106.5 ->
-  // 99.5 us; B = 8 of 1024..2048, 16.7 -> 15.0 / 18.5 -> 18.2 us; config 4
-  // 15.4 -> 17.0 / 20.8 -> 20.7 us. Kept per-row (the model's ratio below
-  // 1.2; balanced would have been slower): 16 of 2048 beside 16 of 1536,
-  // 22.8 / 39.1 us (balanced 27.5 / 44.5); 4 of 2048 beside 28 of 1024; 16
-  // of 8192 beside 16 of 6000; 2 of 4096 beside 30 of 3000; B = 32 of
-  // 4096..8192. Uniform lengths keep the per-row plan (B = 32 x 8192: one
-  // launch, 166 us, against 171 us balanced).
+  // wave the same share of the live history; balanced_pays picks between the
+  // two plans from a timing model of both.
   const uint32_t* host = host_lengths(a);
   const uint64_t limit = std::min<uint64_t>(a.capacity, span);
   if (a.flags & PPK_ATTN_PLAN_BALANCED) {
@@ -268,8 +257,7 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   } else if (!(a.flags & PPK_ATTN_PLAN_PER_ROW) && host && a.split_tokens == 0 &&
              flat_pays(ctx, a.rows, a.heads, host, limit)) {
     AttentionPlan flat = plan_flat(ctx, a.rows, a.heads, host, limit, a.head_dim);
-    const uint32_t cus = uint32_t(std::max(ctx ? ctx->cu_count : 256, 1));
-    if (5 * per_row_cu_peak(plan, a.rows, a.heads, host, limit, cus) >= 6 * flat_cu_peak(flat, a.heads, cus)) {
+    if (balanced_pays(ctx, plan, flat, a.rows, a.heads, host, limit, 2ull * a.head_dim + 8)) {
       plan = flat;
       plan.span = uint32_t(span);
     }
@@ -303,6 +291,35 @@ uint64_t flat_cu_peak(const AttentionPlan& p, uint32_t heads, uint32_t cus) {
         if (t.len[b] > t0) load[(unit / p.waves) % cus] += std::min<uint64_t>(t.share, t.len[b] - t0);
       }
   return *std::max_element(load.begin(), load.end());
+}
+
+// Modelled duration in microseconds of an int8 attention launch plan on
+// MI355X: a fixed cost (7.5 us for one launch, 9.25 us with the merge launch)
+// plus the longer of the chip streaming the whole live history at 6.4 TB/s
+// and the busiest CU streaming its share at 37 GB/s. Fitted to 42 measured
+// ragged batches (B = 4 .. 64, H = 16, D = 64 / 128, per-row and balanced
+// plans): within 2.6 us rms of the measured step.
+static double modelled_us(uint64_t total_bytes, uint64_t cu_peak_bytes, bool merge) {
+  return (merge ? 9.25 : 7.5) + std::max(double(total_bytes) / 6.4e6, double(cu_peak_bytes) / 37e3);
+}
+
+bool balanced_pays(const ppk_context* ctx, const AttentionPlan& per_row, const AttentionPlan& flat, uint32_t rows,
+                   uint32_t heads, const uint32_t* host, uint64_t limit, uint64_t token_bytes) {
+  const uint32_t cus = uint32_t(std::max(ctx ? ctx->cu_count : 256, 1));
+  const uint64_t row_peak = per_row_cu_peak(per_row, rows, heads, host, limit, cus);
+  const uint64_t flat_peak = flat_cu_peak(flat, heads, cus);
+  uint64_t total = 0;
+  for (uint32_t b = 0; b < rows / heads; ++b) total += host[b] <= limit ? host[b] : 0;
+  total *= uint64_t(heads) * token_bytes;
+  const double t_row = modelled_us(total, row_peak * token_bytes, per_row.ngroups > 1);
+  const double t_flat = modelled_us(total, flat_peak * token_bytes, flat.ngroups > 1);
+  // Balanced when the model has it at least 0.75 us faster; and when per-row
+  // waves would each stream 256 KiB or more and the per-row plan's busiest CU
+  // streams at least 1.2 x the balanced plan's (long waves run below the
+  // modelled CU rate: 8 x 4096 beside 24 x 1024 tokens at D = 128 measured
+  // 53.2 us per-row, 45.2 us balanced).
+  return t_flat + 0.75 < t_row ||
+         (uint64_t(per_row.split) * token_bytes >= (256u << 10) && 5 * row_peak >= 6 * flat_peak);
 }
 
 bool per_row_waves_uneven(uint32_t batch, const uint32_t* host, uint64_t limit, uint32_t split) {

@@ -201,6 +201,10 @@ uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit);
 uint64_t per_row_cu_peak(const AttentionPlan& p, uint32_t rows, uint32_t heads, const uint32_t* host,
                          uint64_t limit, uint32_t cus);
 uint64_t flat_cu_peak(const AttentionPlan& p, uint32_t heads, uint32_t cus);
+// Whether the balanced plan `flat` beats the per-row plan of an int8 attention
+// call over the host lengths (token_bytes of history per token and row).
+bool balanced_pays(const ppk_context* ctx, const AttentionPlan& per_row, const AttentionPlan& flat, uint32_t rows,
+                   uint32_t heads, const uint32_t* host, uint64_t limit, uint64_t token_bytes);
 // Whether the per-row plan's waves of `split` tokens are uneven: the most
 // tokens one streams beyond 1.1 x the mean over those that stream any.
 bool per_row_waves_uneven(uint32_t batch, const uint32_t* host, uint64_t limit, uint32_t split);

@@ -143,7 +143,8 @@ def test_plan_sizes_workspace_without_a_device():
 def _per_row_waves(rows, span, split, token_bytes, cus=256):
     """Waves per block of the per-row plan with automatic split `split`: a row's ceil(span / split) waves in
     one block of at most min(16, 16384 / split); rows fewer than the CUs holding more than 128 KiB are cut
-    into blocks of about 256 KiB, then smaller until the blocks cover every CU."""
+    into blocks of about 256 KiB, then smaller until the blocks cover every CU; a row's waves spread evenly
+    over its blocks."""
     per_row = -(-span // split)
     most = max(1, min(16, 16384 // split))
     if rows < cus and span * token_bytes > 128 << 10:
@@ -151,7 +152,10 @@ def _per_row_waves(rows, span, split, token_bytes, cus=256):
         while w > 1 and rows * -(-per_row // w) < cus:
             w -= 1
         most = w
-    return min(per_row, most)
+    if per_row <= most:
+        return per_row
+    groups = -(-per_row // most)
+    return -(-per_row // groups)
 
 
 def _cu_peaks(lens, heads, per_row, share, cus=256, waves_per_block=4):
@@ -175,6 +179,22 @@ def _cu_peaks(lens, heads, per_row, share, cus=256, waves_per_block=4):
     return int(row_cu.max()), int(flat_cu.max())
 
 
+def _balanced_pays(lens, heads, per_row, share, flat_groups, token_bytes):
+    """The library's pick between the plans: a modelled step of 7.5 us per launch plan (9.25 us when it has a
+    merge launch) plus the longer of the chip streaming the live history at 6.4 TB/s and the busiest CU streaming
+    its share at 37 GB/s; balanced when modelled at least 0.75 us faster, or when per-row waves stream 256 KiB or
+    more each and the per-row plan's busiest CU streams at least 1.2 x the balanced plan's."""
+    S, W, G = per_row
+    row_peak, flat_peak = _cu_peaks(lens, heads, per_row, share)
+    total = sum(lens) * heads * token_bytes
+
+    def modelled(peak, merge):
+        return (9.25 if merge else 7.5) + max(total / 6.4e6, peak * token_bytes / 37e3)
+
+    return (modelled(flat_peak, flat_groups > 1) + 0.75 < modelled(row_peak, G > 1)
+            or (S * token_bytes >= 256 << 10 and 5 * row_peak >= 6 * flat_peak))
+
+
 def _flat_units(past, heads, rows, capacity, span, waves, min_unit=64):
     """Units per row of the balanced plan from the host lengths: live length past[b] (0 beyond
     min(capacity, span)), a row of len tokens is max(1, ceil(len / Q)) units of at most Q tokens, Q the least
@@ -190,8 +210,7 @@ def _flat_units(past, heads, rows, capacity, span, waves, min_unit=64):
 def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
     """Ragged batches of up to 64 sequences (zero, tiny, capacity-long and past-capacity rows) with host
     lengths: the balanced plan is taken when the longest live row exceeds 1.1 x the mean (and rows fit half
-    the waves) and the per-row plan's busiest CU streams at least 1.2 x what the balanced plan's does; its
-    units cover every live token, never outnumber the launched waves (2048 on the 256 CUs assumed without a
+    the waves) and the timing model of both plans favours it (_balanced_pays); its units cover every live token, never outnumber the launched waves (2048 on the 256 CUs assumed without a
     context), and the record slots per row are the most units of any row."""
     rng = np.random.default_rng(SEED + heads + d)
     checked = 0
@@ -221,8 +240,8 @@ def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
             continue
         units, share = _flat_units([int(p) for p in past], heads, rows, cap, span, 2048)
         S, G = per_row[:2]
-        row_peak, flat_peak = _cu_peaks(live, heads, (S, _per_row_waves(rows, span, S, 2 * d + 8), G), share)
-        if 5 * row_peak < 6 * flat_peak:
+        if not _balanced_pays(live, heads, (S, _per_row_waves(rows, span, S, 2 * d + 8), G), share, max(units),
+                              2 * d + 8):
             assert (split, groups, nbytes) == per_row, "per-row plan kept"
             continue
         assert split == share and groups == max(units)

@@ -1,9 +1,10 @@
 """GPU parity of the balanced plan for ragged batches (ppk_decode_flat + ppk_attn_merge_flat).
 
-The plan is taken when the caller passes its host copy of the lengths
-(PpkAttentionArgs.past_host) for a ragged batch whose per-row plan would
-load one CU with at least 1.2 x the history the balanced plan's busiest CU
-streams; every test below asserts that its shape takes it.
+The library takes the plan by itself when the caller passes its host copy of the lengths
+(PpkAttentionArgs.past_host) for a ragged batch where its timing model of both plans favours it
+(test_library_balances_a_skewed_batch; the rule itself is checked on the CPU in test_abi.py); the other
+tests force it with PPK_ATTN_PLAN_BALANCED (plan="balanced") so that their small shapes exercise its
+kernels whatever the model picks, and assert that the forced plan differs from the per-row one.
 Bars as for the per-row plan (tests/test_gpu_attention.py): against the f64
 oracle, max abs error <= 2e-3 and max relative error <= 1e-2 (|oracle| >=
 1e-3); the bf16-history mode within 2e-5 absolute; appended codes and scales
@@ -30,21 +31,38 @@ def _plan(c: Case, past_host, max_past=0, **kw):
     return ppk.int8_kv_ops.plan(a, ppk.context(c.q.device))
 
 
+BAL = "balanced"
+
+
 def _balanced(c: Case, past_host, max_past=0) -> int:
-    """Asserts the host lengths change the plan (the balanced one) and returns its record slots per row."""
-    plan = _plan(c, past_host, max_past)
-    assert plan != _plan(c, None, max_past), "the balanced plan is taken"
+    """Asserts the forced balanced plan differs from the per-row one and returns its record slots per row."""
+    plan = _plan(c, past_host, max_past, plan=BAL)
+    assert plan != _plan(c, None, max_past), "the balanced plan is a plan of its own"
     return plan[1]
 
 
 def test_config4_ragged_balanced(device):
-    """BASELINE config 4 (B=8, H=16, D=128, lengths U[256, 4096], bf16 q) through the balanced plan."""
+    """BASELINE config 4 (B=8, H=16, D=128, lengths U[256, 4096], bf16 q) through the balanced plan (the
+    library itself keeps the per-row plan here: a 19 us step where the merge launch costs more than the
+    balance saves)."""
     lengths = [int(x) for x in np.random.default_rng(SEED).integers(256, 4097, size=8)]
     c = Case(device, 8, 16, 128, lengths, max(lengths) + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
     assert _balanced(c, lengths, max_past=max(lengths)) > 1, "config 4 rows span several units"
     ref = c.reference()
-    assert_close(c.run(past_host=lengths, max_past=max(lengths)), ref, what="config 4 balanced")
-    assert_close(c.run(past_host=lengths), ref, what="config 4 balanced, span = capacity")
+    assert_close(c.run(past_host=lengths, max_past=max(lengths), plan=BAL), ref, what="config 4 balanced")
+    assert_close(c.run(past_host=lengths, plan=BAL), ref, what="config 4 balanced, span = capacity")
+    assert _plan(c, lengths, max_past=max(lengths)) == _plan(c, None, max_past=max(lengths))
+
+
+def test_library_balances_a_skewed_batch(device):
+    """Two sequences of 8192 tokens beside 30 of 256 (H = 8, D = 64): with the host lengths the library
+    itself takes the balanced plan (at H = 16 measured 19.3 against 40.2 us per-row), its results within the
+    bars."""
+    lengths = [8192] * 2 + [256] * 30
+    c = Case(device, 32, 8, 64, lengths, 8193, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
+    auto = _plan(c, lengths)
+    assert auto == _plan(c, lengths, plan=BAL) != _plan(c, None)
+    assert_close(c.run(past_host=lengths), c.reference(), what="library-chosen balanced plan")
 
 
 @pytest.mark.parametrize("d", [64, 128, 256])
@@ -54,7 +72,7 @@ def test_edge_lengths_balanced(device, d):
     lengths = [0, 1, 700, 2000, 2049, 3, 2048, 5000] + [2000] * 4 + [10] * 20
     c = Case(device, 32, 8, d, lengths, 2048)
     assert _balanced(c, lengths) > 1
-    got = c.run(past_host=lengths)
+    got = c.run(past_host=lengths, plan=BAL)
     ref = c.reference()
     bad = np.repeat(np.array(lengths) > 2048, 8)
     assert np.isnan(got[bad]).all() and not np.isnan(got[~bad]).any()
@@ -65,7 +83,7 @@ def test_rows_beyond_max_past_give_nan(device):
     lengths = [900, 1200, 40, 1100, 30, 950, 20, 10] * 4
     c = Case(device, 32, 8, 128, lengths, 1500)
     _balanced(c, lengths, max_past=1000)
-    got = c.run(past_host=lengths, max_past=1000)
+    got = c.run(past_host=lengths, max_past=1000, plan=BAL)
     ref = c.reference()
     bad = np.repeat(np.array(lengths) > 1000, 8)
     assert np.isnan(got[bad]).all() and not np.isnan(got[~bad]).any()
@@ -91,7 +109,7 @@ def test_bf16_history_balanced(device):
     lengths = [900, 30, 2500, 1700]
     c = Case(device, 4, 8, 64, lengths, 2600)
     _balanced(c, lengths)
-    got = c.run(past_host=lengths, bf16_history=True)
+    got = c.run(past_host=lengths, bf16_history=True, plan=BAL)
     assert_close(got, c.reference(history_bf16=True), atol=2e-5, rtol=0, what="balanced bf16 history")
 
 
@@ -101,7 +119,7 @@ def test_balanced_dtypes(device, q_dtype, out_dtype):
     lengths = [1500, 333, 2900]
     c = Case(device, 3, 8, 128, lengths, 3000, q_dtype=q_dtype, scratch_dtype=q_dtype)
     _balanced(c, lengths)
-    got = c.run(past_host=lengths, out_dtype=out_dtype)
+    got = c.run(past_host=lengths, out_dtype=out_dtype, plan=BAL)
     narrow = {torch.float32: None, torch.bfloat16: "bf16", torch.float16: "f16"}[out_dtype]
     assert_close(got, c.reference(), what=f"balanced {q_dtype} -> {out_dtype}", out_dtype=narrow)
 
@@ -116,7 +134,8 @@ def test_decode_step_balanced_appends_and_attends(device):
     ref = c.reference()
     before = [t.clone() for t in (c.kc, c.vc, c.ks, c.vs)]
     flags = torch.zeros(1, dtype=torch.int32, device=device)
-    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, flags=flags, past_host=lengths)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, flags=flags, past_host=lengths,
+                          plan=BAL)
     torch.cuda.synchronize()
     assert_close(out.reshape(c.rows, D).cpu().numpy(), ref, what="balanced decode step")
     assert int(flags.item()) & ppk.PPK_FLAG_OVERFLOW  # the row at the capacity could not append
@@ -146,7 +165,8 @@ def test_stale_host_lengths_give_nan_and_a_flag(device):
     _balanced(c, stale)
     ref = c.reference()
     flags = torch.zeros(1, dtype=torch.int32, device=device)
-    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, flags=flags, past_host=stale)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, flags=flags, past_host=stale,
+                          plan=BAL)
     torch.cuda.synchronize()
     got = out.reshape(c.rows, c.D).cpu().numpy()
     bad = np.repeat(np.array(lengths) != np.array(stale), 8)
@@ -166,7 +186,7 @@ def test_balanced_plan_through_the_noalloc_entry_point(device):
     _balanced(c, lengths)
     ref = c.reference()
     a, out = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H,
-                                            past_host=lengths)
+                                            past_host=lengths, plan=BAL)
     step = ppk.int8_kv_ops._step_args(a, c.sk, c.sv, None, c.D)
     stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
     assert _abi.lib().ppk_decode_step_noalloc(ppk.context(device), stream, ctypes.byref(step)) == 0, _abi.last_error()
@@ -180,7 +200,7 @@ def test_balanced_step_captured_in_a_hip_graph(device):
     lengths = [2500, 64, 900, 1700]
     c = Case(device, 4, 16, 128, lengths, 2600, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16)
     _balanced(c, lengths)
-    st = ppk.DecodeAttention(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, past_host=lengths)
+    st = ppk.DecodeAttention(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, past_host=lengths, plan=BAL)
     eager = st().clone()
     torch.cuda.synchronize()
     assert_close(eager.reshape(c.rows, c.D).cpu().numpy(), c.reference(), what="balanced eager")
