@@ -57,6 +57,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--device-lengths", action="store_true",
                    help="configs 1, 3, 4 and --lengths: pass the lengths on the device only (no host copy), i.e. "
                         "the per-row plan")
+    p.add_argument("--plan", choices=("auto", "per-row", "balanced"), default="auto",
+                   help="configs 1, 3, 4 and --lengths with host lengths: the launch plan (auto = the library's "
+                        "choice; per-row or balanced fix it, PPK_ATTN_PLAN_PER_ROW / PPK_ATTN_PLAN_BALANCED)")
     p.add_argument("--step", action="store_true",
                    help="with --kv bf16/f32: time the fused float decode step (ppk_float_decode_step: write the "
                         "current token at slot lengths[b] - 1, attend lengths[b] tokens) beside the reference's "
@@ -182,9 +185,10 @@ def bench_float(args) -> int:
         k_new = torch.randn((rows, D), generator=g, device=dev, dtype=torch.float32)
         v_new = torch.randn((rows, D), generator=g, device=dev, dtype=torch.float32)
         call = ppk.FloatDecodeStep(q, k, v, stored, H, k_new, v_new, args.split, max_length=L,
-                                   lengths_host=[n - 1 for n in seq] if host else None)
+                                   lengths_host=[n - 1 for n in seq] if host else None, plan=args.plan)
         plan_args = call.args.attn
-        attend = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host)
+        attend = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host,
+                                          plan=args.plan)
         row_idx = torch.arange(rows, device=dev)
         slot = stored.repeat_interleave(H).long()
         k_cast, v_cast = k_new.to(kv_dtype), v_new.to(kv_dtype)
@@ -194,7 +198,8 @@ def bench_float(args) -> int:
             v[row_idx, slot] = v_cast
             attend()
     else:
-        call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host)
+        call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host,
+                                        plan=args.plan)
         plan_args = call.args
     flat = host is not None and ppk.fused_attention.plan(plan_args, call.ctx) != ppk.fused_attention.plan(
         ppk.fused_attention.decode_attention_args(q, k, v, lengths, H, args.split, max_length=L)[0], call.ctx)
@@ -716,7 +721,8 @@ def bench_config(args) -> int:
     # lets the library balance a ragged batch; --device-lengths times the plan without it.
     host = None if args.device_lengths else lengths
     steps = [[ppk.DecodeStep(q[li], kc[c, li], vc[c, li], ks[c, li], vs[c, li], kn[li], vn[li], past, H,
-                             split_tokens=args.split, max_past=L, out=out, past_host=host) for li in range(layers)]
+                             split_tokens=args.split, max_past=L, out=out, past_host=host, plan=args.plan)
+              for li in range(layers)]
              for c in range(copies)]
     split, ngroups = steps[0][0].split_tokens, steps[0][0].ngroups
     # The balanced plan is taken when the host lengths are given and rows would span blocks otherwise.
@@ -784,7 +790,9 @@ def bench_config(args) -> int:
     achieved = kernel_bytes / (kernel_avg_us * 1e-6) / 1e9
     tag = f"c{args.config}_b{B}_h{H}_d{D}"
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"ppk_decode_{tag}_traffic.json")
+    kbase = "ppk_decode_flat" if balanced else "ppk_decode"
+    kname = f"{kbase}_d{D}"
+    tpath = os.path.join(ROOT, "profiles", f"{kbase}_{tag}_traffic.json")
     if os.path.exists(tpath):
         try:
             with open(tpath) as f:
@@ -813,7 +821,7 @@ def bench_config(args) -> int:
         "graph_replay_us": None if graph_us is None else round(graph_us, 2),
         "algorithmic_bytes_per_step": step_bytes,
         "step_hbm_gbps": round(step_bytes / (warm_mean * 1e-6) / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": ("ppk_decode_flat_d%d" if balanced else "ppk_decode_d%d") % D,
+        "roofline": {"bound": "hbm", "kernel": kname,
                      "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "algorithmic_bytes_per_launch": kernel_bytes,
@@ -1116,6 +1124,9 @@ def main() -> int:
         print(json.dumps({"error": "this build runs on one GPU only; the int8 KV decode path shards by "
                                    "sequence or head with no collective on the hot path; run it once per GPU",
                           "n_gpus": args.gpus}))
+        return 2
+    if args.plan == "balanced" and args.device_lengths:
+        print("bench.py: --plan balanced needs the host lengths; drop --device-lengths", file=sys.stderr)
         return 2
     if args.sampler:
         return bench_sampler(args)

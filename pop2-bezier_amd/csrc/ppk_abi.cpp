@@ -262,7 +262,20 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
       plan.span = uint32_t(span);
     }
   }
+  if (!plan.flat) plan.speculate = per_row_speculates(plan, a.rows, a.heads, host, span, limit);
   return plan;
+}
+
+bool per_row_speculates(const AttentionPlan& p, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t span,
+                        uint64_t limit) {
+  const uint64_t per_row = uint64_t(p.ngroups) * p.waves;
+  uint64_t live = 0;
+  for (uint32_t b = 0; b < rows / heads; ++b) {
+    const uint64_t len = host ? (host[b] <= limit ? host[b] : 0) : span;
+    live += heads * std::min<uint64_t>(per_row, (len + p.split - 1) / p.split);
+  }
+  const uint64_t total = per_row * rows;
+  return (total - live) * 16 < total;
 }
 
 // Placement model of an all-resident launch: block i runs on CU i mod cus
@@ -608,6 +621,7 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   d.scratch_dtype = a.scratch_dtype;
   d.out_dtype = a.out_dtype;
   d.scale_log2 = scale_log2;
+  d.speculate = plan.speculate ? 1u : 0u;
 
   const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
   const bool traceable = scratch == nullptr;

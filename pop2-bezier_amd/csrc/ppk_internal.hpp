@@ -168,6 +168,10 @@ struct AttentionPlan {
   // are known, see FlatTable); ngroups = record slots per row, 1 when every
   // row is a single unit (then no merge launch).
   bool flat = false;
+  // Per-row plan: whether each wave requests its first K batches before the
+  // row's length arrives (off when 1/16 or more of the waves are known to
+  // have no history).
+  bool speculate = true;
   uint32_t blocks = 0;   // flat: blocks launched
   uint32_t span = 0;     // flat: rows with past beyond it give NaN
   FlatTable table{};
@@ -203,6 +207,11 @@ uint64_t per_row_cu_peak(const AttentionPlan& p, uint32_t rows, uint32_t heads, 
 uint64_t flat_cu_peak(const AttentionPlan& p, uint32_t heads, uint32_t cus);
 // Whether the balanced plan `flat` beats the per-row plan of an int8 attention
 // call over the host lengths (token_bytes of history per token and row).
+// Whether the per-row plan p should speculate (AttentionPlan::speculate):
+// fewer than 1/16 of its waves lie wholly past their row's live history (the
+// host lengths, or every row at `span` without them).
+bool per_row_speculates(const AttentionPlan& p, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t span,
+                        uint64_t limit);
 bool balanced_pays(const ppk_context* ctx, const AttentionPlan& per_row, const AttentionPlan& flat, uint32_t rows,
                    uint32_t heads, const uint32_t* host, uint64_t limit, uint64_t token_bytes);
 // Whether the per-row plan's waves of `split` tokens are uneven: the most

@@ -80,6 +80,7 @@ struct DecodeArgs {
   uint32_t q_dtype, scratch_dtype, out_dtype, new_dtype, append;
   float scale_log2;         // softmax_scale * log2(e)
   uint32_t span;            // rows with past[b] > span give NaN (balanced plan)
+  uint32_t speculate;       // per-row plan: request each wave's first K batches before past[] arrives
 };
 
 struct MergeArgs {

@@ -117,9 +117,22 @@ def test_float_balanced_all_rows_one_unit_is_one_launch(device):
     assert_close(got, c.reference(), atol=F_ATOL, rtol=F_RTOL, what="float one-unit rows")
 
 
-def test_forced_per_row_ignores_host_lengths_for_planning(device):
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_forced_per_row_ignores_host_lengths_for_planning(device, d):
     """PPK_ATTN_PLAN_PER_ROW with the host lengths of a batch the library would balance: the per-row plan's
-    outputs, bit for bit."""
+    outputs, bit for bit. With the host lengths most of the per-row waves are known to hold no history, so the
+    kernel does not request their first K batches before past[] arrives; without them it does: both paths
+    give the same bits, for attention and for the fused step (same appended codes and scales)."""
     lengths = [1500, 333, 2900]
-    c = Case(device, 3, 8, 128, lengths, 3000)
+    c = Case(device, 3, 8, d, lengths, 3000)
     np.testing.assert_array_equal(c.run(past_host=lengths, plan="per-row"), c.run())
+    outs, arenas = [], []
+    for host in (lengths, None):
+        kc, vc, ks, vs = (t.clone() for t in (c.kc, c.vc, c.ks, c.vs))
+        out = ppk.decode_step(c.q, kc, vc, ks, vs, c.sk, c.sv, c.past_t, c.H, past_host=host, plan="per-row")
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+        arenas.append([t.cpu().numpy() for t in (kc, vc, ks, vs)])
+    np.testing.assert_array_equal(outs[0], outs[1])
+    for x, y in zip(*arenas):
+        np.testing.assert_array_equal(x.view(np.uint8), y.view(np.uint8))
