@@ -58,7 +58,7 @@ enum { PPK_F32 = 0, PPK_BF16 = 1, PPK_F16 = 2 };
 enum {
   PPK_FLAG_NONFINITE = 1u, /* an input row held NaN or +-Inf (reference CPU path rejects these, int8_kv_ops.rs:16) */
   PPK_FLAG_OVERFLOW = 2u,  /* past[b] + tokens > capacity: that row was not written */
-  PPK_FLAG_STALE_LENGTHS = 4u /* attention: a device past[b] differed from PpkAttentionArgs.past_host[b]; its rows gave NaN */
+  PPK_FLAG_STALE_LENGTHS = 4u /* decode step: a device length differed from the host copy (past_host / lengths_host) and its rows gave NaN */
 };
 
 /* Attention flags. */
@@ -70,9 +70,11 @@ enum {
   /* Launch plan (no counterpart in the reference; the result does not depend
      on it beyond fp32 summation order). With host lengths (past_host /
      lengths_host) the library chooses between its per-row plan and the
-     balanced plan for ragged batches; these bits fix the choice. PER_ROW
-     ignores the host lengths for planning (they are still compared with the
-     device's). BALANCED needs the host lengths, split_tokens == 0, at most 64
+     balanced plan for ragged batches, and sizes its per-row plan for the
+     longest live host length; these bits fix the choice. PER_ROW ignores
+     the host lengths for planning: it is the plan of the same call without
+     them, so its result is bit for bit that call's. BALANCED needs the host
+     lengths, split_tokens == 0, at most 64
      sequences and rows at most 4 per CU; otherwise the call fails with status
      1 and nothing enqueued. Setting both is an error. */
   PPK_ATTN_PLAN_PER_ROW = 2u,
@@ -194,10 +196,12 @@ typedef struct PpkAttentionArgs {
      of past[], the lengths the caller built before copying them to the
      device (app/src/model/batch.rs:152-161). With it the library balances a
      ragged batch: the plan, the workspace size and the work each wave takes
-     follow the actual lengths. Each device past[b] is still read and
-     compared; a sequence whose device value differs gives NaN rows (and
-     PPK_FLAG_STALE_LENGTHS in a decode step's flags), never a wrong result.
-     Only read during the call (a captured graph keeps the plan it saw). */
+     follow the actual lengths (the per-row plan covers the longest live
+     one). Each device past[b] is still read; a sequence whose device value
+     differs gives its exact rows when the plan still covers them, and NaN
+     rows otherwise (with PPK_FLAG_STALE_LENGTHS in a decode step's flags),
+     never a wrong result. Only read during the call (a captured graph keeps
+     the plan it saw). */
   const uint32_t* past_host;
 } PpkAttentionArgs;
 PPK_API int32_t ppk_attention_workspace_bytes(ppk_context* ctx, const PpkAttentionArgs* args, uint64_t* bytes);
@@ -284,9 +288,10 @@ typedef struct PpkFloatAttentionArgs {
   /* Optional (NULL, or absent when struct_size ends before it): a host copy
      of lengths[] (needs lengths). With it a ragged batch is balanced as in
      PpkAttentionArgs.past_host: the plan and the workspace size follow the
-     actual lengths, each device lengths[b] is still read and compared, and a
-     sequence whose device value differs gives NaN rows, never a wrong
-     result. Only read during the call. */
+     actual lengths, each device lengths[b] is still read, and a sequence
+     whose device value differs gives its exact rows when the plan still
+     covers them and NaN rows otherwise (with PPK_FLAG_STALE_LENGTHS in a
+     decode step's flags), never a wrong result. Only read during the call. */
   const uint32_t* lengths_host;
 } PpkFloatAttentionArgs;
 /* Launch plan for args (ctx may be NULL: assumes 256 CUs), as ppk_attention_plan. */

@@ -243,13 +243,18 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
 
   const uint32_t tpl = 64u / (a.head_dim / 16u);
   const uint64_t span = a.max_past ? a.max_past : a.capacity;
-  // Per history token: K and V codes plus two fp32 scales.
-  AttentionPlan plan = plan_rows(ctx, a.rows, span, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
+  const uint32_t* host = host_lengths(a);
+  const uint64_t limit = std::min<uint64_t>(a.capacity, span);
+  // Per history token: K and V codes plus two fp32 scales. With the host's
+  // lengths (and no plan bit) the per-row plan covers the longest live row
+  // instead of the whole span, so no waves are sized for history no row
+  // holds; a device length beyond that coverage (a stale host copy) gives
+  // NaN rows and PPK_FLAG_STALE_LENGTHS in a decode step.
+  const uint64_t cover = host && !(a.flags & kPlanFlags) ? row_cover(host, a.rows / a.heads, limit) : span;
+  AttentionPlan plan = plan_rows(ctx, a.rows, cover, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
   // With the host's lengths of a ragged batch, the balanced plan gives every
   // wave the same share of the live history; balanced_pays picks between the
   // two plans from a timing model of both.
-  const uint32_t* host = host_lengths(a);
-  const uint64_t limit = std::min<uint64_t>(a.capacity, span);
   if (a.flags & PPK_ATTN_PLAN_BALANCED) {
     require_balanced(ctx, a.rows, a.heads, host, a.split_tokens);
     plan = plan_flat(ctx, a.rows, a.heads, host, limit, a.head_dim);
@@ -262,8 +267,15 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
       plan.span = uint32_t(span);
     }
   }
-  if (!plan.flat) plan.speculate = per_row_speculates(plan, a.rows, a.heads, host, span, limit);
+  if (!plan.flat) {
+    plan.speculate = per_row_speculates(plan, a.rows, a.heads, host, cover, limit);
+    plan.span = uint32_t(span);
+  }
   return plan;
+}
+
+uint64_t row_cover(const uint32_t* host, uint32_t batch, uint64_t limit) {
+  return std::max<uint64_t>(longest_live(host, batch, limit), 1);
 }
 
 bool per_row_speculates(const AttentionPlan& p, uint32_t rows, uint32_t heads, const uint32_t* host, uint64_t span,
@@ -622,11 +634,11 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   d.out_dtype = a.out_dtype;
   d.scale_log2 = scale_log2;
   d.speculate = plan.speculate ? 1u : 0u;
+  d.span = plan.span;
 
   const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
   const bool traceable = scratch == nullptr;
   if (plan.flat) {
-    d.span = plan.span;
     DecodeFlatArgs f{};
     f.d = d;
     f.t = plan.table;
@@ -716,8 +728,15 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   require(uint64_t(a.rows) * std::max(ks, vs) <= (uint64_t(1) << 46), "float attention K/V span too large");
   const uint32_t tpl = 64u / (a.head_dim / uint32_t(16 / eb));
   const uint64_t span = a.max_length ? a.max_length : a.size;
+  const uint32_t* host = host_lengths(a);
+  require(!host || a.lengths, "float attention lengths_host needs the device lengths");
+  const uint32_t batch = a.rows / a.heads;
+  // As on the int8 path: with the host's lengths (and no plan bit) the
+  // per-row plan covers the longest live row; a device length beyond it
+  // gives NaN rows (and PPK_FLAG_STALE_LENGTHS in a decode step).
+  const uint64_t cover = host && !(a.flags & kPlanFlags) ? row_cover(host, batch, span) : span;
   AttentionPlan plan =
-      plan_rows(ctx, a.rows, span, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
+      plan_rows(ctx, a.rows, cover, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
   // With the host's copy of the lengths, a ragged batch takes the balanced
   // plan (the int8 path's table) when its longest row holds more than
   // 512 KiB of K and V and the per-row plan's waves are uneven (the most
@@ -735,9 +754,6 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   // D = 64, 9.3 us (11.5: the merge launch costs more than the balance
   // gains).
   constexpr uint64_t kFloatFlatMinRowBytes = 512u << 10;
-  const uint32_t* host = host_lengths(a);
-  require(!host || a.lengths, "float attention lengths_host needs the device lengths");
-  const uint32_t batch = a.rows / a.heads;
   if (a.flags & PPK_ATTN_PLAN_BALANCED) {
     require_balanced(ctx, a.rows, a.heads, host, a.split_tokens);
     plan = plan_flat(ctx, a.rows, a.heads, host, span, a.head_dim);

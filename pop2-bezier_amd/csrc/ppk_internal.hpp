@@ -199,6 +199,9 @@ void require_balanced(const ppk_context* ctx, uint32_t rows, uint32_t heads, con
 constexpr uint32_t kPlanFlags = PPK_ATTN_PLAN_PER_ROW | PPK_ATTN_PLAN_BALANCED;
 // The most live tokens of any of `batch` sequences (a length above limit has none).
 uint64_t longest_live(const uint32_t* host, uint32_t batch, uint64_t limit);
+// The history the per-row plan covers with host lengths: the longest live
+// row, at least one token.
+uint64_t row_cover(const uint32_t* host, uint32_t batch, uint64_t limit);
 // The most live history tokens one CU streams under a per-row plan p or a
 // balanced plan (block i on CU i mod cus, as an all-resident launch is
 // placed).

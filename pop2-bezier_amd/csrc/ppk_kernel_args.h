@@ -79,7 +79,8 @@ struct DecodeArgs {
   uint32_t rows, heads, capacity, split_tokens, ngroups;
   uint32_t q_dtype, scratch_dtype, out_dtype, new_dtype, append;
   float scale_log2;         // softmax_scale * log2(e)
-  uint32_t span;            // rows with past[b] > span give NaN (balanced plan)
+  uint32_t span;            // max_past or capacity: balanced plan, rows with past[b] > span give NaN; per-row
+                            // plan, a past[b] <= span past the plan's coverage flags stale host lengths
   uint32_t speculate;       // per-row plan: request each wave's first K batches before past[] arrives
 };
 

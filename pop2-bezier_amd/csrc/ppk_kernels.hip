@@ -855,7 +855,8 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   const uint32_t group = blockIdx.x / a.rows;
   const uint32_t S = a.split_tokens;
   const uint32_t p = a.past[row / a.heads];
-  const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.ngroups) * W * S;
+  const uint64_t cover = uint64_t(a.ngroups) * W * S;
+  const bool valid = p <= a.capacity && uint64_t(p) <= cover;
 
   // Everything the wave reads before its stream is requested first, in one
   // round trip: q, the current token (wave 0 of a block that covers its
@@ -896,6 +897,9 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
     load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, 0, nspec, j, lane, ra, sa);
     load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, 4, nspec, j, lane, rb, sb);
   }
+  // A length within the caller's span that the plan does not cover: the plan
+  // was sized from a stale host copy of the lengths (the row gives NaN).
+  if (kw && lane == 0 && a.flags && p <= a.capacity && p <= a.span && uint64_t(p) > cover) atomicOr(a.flags, 4u);
   if (kw || vw) {
     if (p >= a.capacity) {
       if (lane == 0 && a.flags) atomicOr(a.flags, 2u);
@@ -1615,6 +1619,10 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
   if (kw || cur) load_current<EPL, BF16KV>(a.k_new, row, a.new_dtype, lane, kcur);
   if (vw || cur) load_current<EPL, BF16KV>(a.v_new, row, a.new_dtype, lane, vcur);
   if (cur) load_vec<EPL>(a.q, size_t(row) * a.q_stride + size_t(lane) * EPL, a.q_dtype, qcur);
+  // A stored length within the span that the plan does not cover: the plan
+  // was sized from a stale host copy of the lengths (the row gives NaN).
+  if (kw && lane == 0 && a.flags && len < a.size && len + 1 <= a.span && uint64_t(len) > uint64_t(a.ngroups) * W * S)
+    atomicOr(a.flags, 4u);
   if (kw) write_current<EPL, BF16KV>(const_cast<void*>(a.k), a.k_stride, row, len, a.size, kcur, a.flags, lane);
   if (vw) write_current<EPL, BF16KV>(const_cast<void*>(a.v), a.v_stride, row, len, a.size, vcur, a.flags, lane);
   const uint32_t begin = (group * W + wave) * S;

@@ -125,11 +125,19 @@ def test_plan_sizes_workspace_without_a_device():
     # the balanced plan's 384 units would fill only 96 CUs: per-row kept.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, heads=8, capacity=2049, max_past=2048,
                                            past_host=[2048, 1000])) == (64, 16, 16 * 16 * 128 * 4 + 16 * 16 * 8)
-    # Short ragged rows with host lengths: the one-block-per-row plan puts each row on its own CU, the balanced
-    # plan four rows on one: per-row kept.
-    per_row = ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900))
+    # Short ragged rows with host lengths: the per-row plan covers the longest live row (64 tokens) instead of
+    # the span (900: rows cut into four blocks, merged from the workspace), so one block per row, one launch;
+    # the same plan as a call whose max_past is that longest row. PPK_ATTN_PLAN_PER_ROW plans as without them.
+    span_plan = ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900))
+    assert span_plan[1] == 4
+    host = [10, 0, 60, 64]
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900, past_host=host)) == \
+        ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=64)) == (64, 1, 0)
+    assert ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900, past_host=host,
+                                           flags=_abi.PPK_ATTN_PLAN_PER_ROW)) == span_plan
+    # Every host length beyond the span (or zero): the plan covers one token (one 8-token tile per row).
     assert ppk.int8_kv_ops.plan(_attn_args(rows=64, heads=16, capacity=1024, max_past=900,
-                                           past_host=[10, 0, 60, 64])) == per_row
+                                           past_host=[0, 901, 1024, 0])) == (8, 1, 0)
     # Few short rows (config 1 shape): one block per row, one launch.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=513, max_past=512, head_dim=64)) == (64, 1, 0)
     # Spans that are no multiple of the power-of-two split: each row gets as many waves as the budget holds
@@ -232,15 +240,17 @@ def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
             past[rng.integers(0, batch, 3)] = span
         rows = batch * heads
         a = _attn_args(rows=rows, heads=heads, capacity=cap, max_past=span, head_dim=d, past_host=past)
-        per_row = ppk.int8_kv_ops.plan(_attn_args(rows=rows, heads=heads, capacity=cap, max_past=span, head_dim=d))
-        split, groups, nbytes = ppk.int8_kv_ops.plan(a)
         live = [int(p) if p <= min(cap, span) else 0 for p in past]
+        # The per-row plan with host lengths covers the longest live row (at least one token).
+        cover = max(1, max(live))
+        per_row = ppk.int8_kv_ops.plan(_attn_args(rows=rows, heads=heads, capacity=cap, max_past=cover, head_dim=d))
+        split, groups, nbytes = ppk.int8_kv_ops.plan(a)
         if 2 * rows > 2048 or max(live) * batch * 10 <= sum(live) * 11:  # too many rows, or not ragged
             assert (split, groups, nbytes) == per_row
             continue
         units, share = _flat_units([int(p) for p in past], heads, rows, cap, span, 2048)
         S, G = per_row[:2]
-        if not _balanced_pays(live, heads, (S, _per_row_waves(rows, span, S, 2 * d + 8), G), share, max(units),
+        if not _balanced_pays(live, heads, (S, _per_row_waves(rows, cover, S, 2 * d + 8), G), share, max(units),
                               2 * d + 8):
             assert (split, groups, nbytes) == per_row, "per-row plan kept"
             continue
@@ -305,7 +315,8 @@ def test_float_plan_without_a_device():
 
 def test_float_balanced_plan_without_a_device():
     """Host lengths of a ragged batch take the balanced plan of the int8 path (the same table from the same
-    rule); uniform lengths, an explicit split or a batch beyond 64 sequences keep the per-row plan."""
+    rule); uniform lengths, an explicit split or a batch beyond 64 sequences keep the per-row plan (sized for the
+    longest host length)."""
     skew = [8192] * 4 + [512] * 28
     per_row = ppk.fused_attention.plan(_float_args(lengths=8))
     split, groups, nbytes = ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=skew))
@@ -318,8 +329,14 @@ def test_float_balanced_plan_without_a_device():
     assert ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=[8192] * 32)) == per_row
     assert ppk.fused_attention.plan(_float_args(lengths=8, lengths_host=skew, split_tokens=128)) == \
         ppk.fused_attention.plan(_float_args(split_tokens=128))
+    # Beyond 64 sequences: the per-row plan, covering the longest host length (5000 of the 8192 slots) as a call
+    # with that max_length would; PPK_ATTN_PLAN_PER_ROW plans as without the host lengths.
     many = [5000] + [10] * 79
     assert ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8, lengths_host=many)) == \
+        ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8, max_length=5000)) != \
+        ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8))
+    assert ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8, lengths_host=many,
+                                                flags=_abi.PPK_ATTN_PLAN_PER_ROW)) == \
         ppk.fused_attention.plan(_float_args(rows=80, heads=1, lengths=8))
     # Lengths beyond max_length count as empty rows (NaN): one live long row among them.
     host = [8000, 9000, 10, 0] + [600] * 28

@@ -1,0 +1,98 @@
+"""GPU parity of the per-row plan sized from the host lengths: with past_host / lengths_host (and no plan bit)
+the per-row plan covers the longest live host length instead of the whole span (max_past / max_length, or the
+capacity), so a caller that passes only the arena's capacity gets the plan of its actual lengths.
+
+A device length the plan still covers gives its exact rows whatever the host copy said; one beyond the
+coverage (a stale host copy) gives NaN rows and PPK_FLAG_STALE_LENGTHS in a decode step's flags. Bars as the
+per-row tests: int8 max abs <= 2e-3 and max rel <= 1e-2 against the f64 oracle, float max abs <= 1e-4 and
+max rel <= 1e-2.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import ppk
+from helpers import SEED, assert_close
+from test_gpu_attention import Case
+from test_gpu_float_attention import ATOL as F_ATOL, RTOL as F_RTOL, FloatCase
+from test_gpu_float_step import StepCase
+
+pytestmark = pytest.mark.gpu
+
+# Near-uniform lengths (no balanced plan) far below the arena's 4096 slots.
+HOST = [1000, 950, 980]
+
+
+def _int8_plan(c: Case, host, **kw):
+    a, _ = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, past_host=host,
+                                          **kw)
+    return ppk.int8_kv_ops.plan(a, ppk.context(c.q.device))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_int8_per_row_plan_covers_the_longest_host_length(device, d):
+    c = Case(device, 3, 8, d, HOST, 4096, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16, seed=SEED + d)
+    sized = _int8_plan(c, HOST)
+    assert sized == _int8_plan(c, None, max_past=max(HOST)) != _int8_plan(c, None)
+    assert _int8_plan(c, HOST, plan="per-row") == _int8_plan(c, None)
+    ref = c.reference()
+    assert_close(c.run(past_host=HOST), ref, what=f"host-sized per-row d={d}")
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, flags=flags, past_host=HOST)
+    torch.cuda.synchronize()
+    assert int(flags.item()) == 0
+    assert_close(out.reshape(c.rows, d).cpu().numpy(), ref, what=f"host-sized per-row step d={d}")
+
+
+def test_int8_stale_host_lengths_beyond_the_coverage(device):
+    """Device lengths 1000 / 1500 / 500 against host 1000 / 950 / 980: sequence 1 lies past the plan's
+    coverage (NaN, flagged), sequence 2 is shorter than its host copy and still exact."""
+    device_lengths = [1000, 1500, 500]
+    c = Case(device, 3, 8, 128, device_lengths, 4096, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16,
+             seed=SEED + 3)
+    ref = c.reference()
+    bad = np.repeat(np.array([False, True, False]), c.H)
+    got = c.run(past_host=HOST)
+    assert np.isnan(got[bad]).all()
+    assert_close(got[~bad], ref[~bad], what="rows the plan covers")
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, flags=flags, past_host=HOST)
+    torch.cuda.synchronize()
+    step = out.reshape(c.rows, c.D).cpu().numpy()
+    assert int(flags.item()) == ppk.PPK_FLAG_STALE_LENGTHS
+    assert np.isnan(step[bad]).all()
+    assert_close(step[~bad], ref[~bad], what="step rows the plan covers")
+
+
+def _float_plan(c: FloatCase, host, **kw):
+    a, _ = ppk.fused_attention.decode_attention_args(c.q, c.k, c.v, c.lengths_t, c.H, lengths_host=host, **kw)
+    return ppk.fused_attention.plan(a, ppk.context(c.q.device))
+
+
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
+def test_float_per_row_plan_covers_the_longest_host_length(device, kv):
+    c = FloatCase(device, 3, 8, 128, 4096, kv, lengths=HOST, seed=SEED + 4)
+    # The plan of the same call with max_length = the longest host length (the (split, blocks, workspace)
+    # triple need not differ from the capacity's plan: the waves per block may be what changes).
+    assert _float_plan(c, HOST) == _float_plan(c, None, max_length=max(HOST))
+    assert_close(c.run(lengths_host=HOST), c.reference(), atol=F_ATOL, rtol=F_RTOL, what=f"host-sized {kv}")
+
+
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
+def test_float_step_stale_host_lengths_beyond_the_coverage(device, kv):
+    """The fused float step with stored lengths 999 / 1500 / 400 against host 999 / 949 / 979."""
+    host = [n - 1 for n in HOST]
+    c = StepCase(device, 3, 8, 128, 4096, kv, [999, 1500, 400], seed=SEED + 5)
+    got, flags = c.step(lengths_host=host)
+    bad = np.repeat(np.array([False, True, False]), c.H)
+    ref = c.expected()
+    assert flags == ppk.PPK_FLAG_STALE_LENGTHS
+    assert np.isnan(got[bad]).all()
+    assert_close(got[~bad], ref[~bad], atol=F_ATOL, rtol=F_RTOL, what=f"float step rows the plan covers {kv}")
+    c.check_store()  # every row's token is written, stale or not
+    c2 = StepCase(device, 3, 8, 128, 4096, kv, host, seed=SEED + 6)
+    got2, flags2 = c2.step(lengths_host=host)
+    assert flags2 == 0
+    assert_close(got2, c2.expected(), atol=F_ATOL, rtol=F_RTOL, what=f"float step host-sized {kv}")
