@@ -140,7 +140,8 @@ pub struct PpkDequantizeArgs {
 
 /// int8_kv_ops::attention (int8_kv_ops.rs:41-55). `past_host` is optional
 /// (null): the host copy of `past` that lets the library balance a ragged
-/// batch; the device `past` is still read and any difference gives NaN rows.
+/// batch (or size its per-row plan for the longest length); the device
+/// `past` is still read, and a length the plan does not cover gives NaN rows.
 #[repr(C)]
 #[derive(Clone, Copy)]
 pub struct PpkAttentionArgs {

@@ -31,7 +31,8 @@ def decode_attention_args(q, k, v, lengths, heads: int, split_tokens: int = 0, *
                           plan: str = "auto") -> tuple[_abi.PpkFloatAttentionArgs, torch.Tensor]:
     """Validate like fused_attention::decode_attention and build the ABI block (workspace unset).
     lengths_host: an optional host copy of `lengths` (a sequence of ints), with which the library balances
-    ragged batches; plan: "auto", "per-row" or "balanced" (PPK_ATTN_PLAN_*)."""
+    ragged batches or sizes its per-row plan for the longest one; plan: "auto", "per-row" (plans as without
+    lengths_host) or "balanced" (PPK_ATTN_PLAN_*)."""
     _require(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "fused decode attention requires 3-d q/k/v")
     rows, query, width = q.shape
     key_rows, length, key_width = k.shape

@@ -129,8 +129,9 @@ def attention_args(q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int 
                    softmax_scale: float = 0.0, past_host=None,
                    plan: str = "auto") -> tuple[_abi.PpkAttentionArgs, torch.Tensor]:
     """Validate like int8_kv_ops::attention and build the ABI argument block (workspace unset). past_host: an
-    optional host copy of `past` (a sequence of ints), with which the library balances ragged batches; plan:
-    "auto" (the library chooses from past_host), "per-row" or "balanced" (PPK_ATTN_PLAN_*)."""
+    optional host copy of `past` (a sequence of ints), with which the library balances ragged batches or sizes
+    its per-row plan for the longest one; plan: "auto" (the library chooses from past_host), "per-row" (plans as
+    without past_host) or "balanced" (PPK_ATTN_PLAN_*)."""
     rows, capacity = _geometry(k)
     d = k.shape[2]
     _require(heads > 0 and rows % heads == 0 and v.shape == k.shape and v.is_contiguous()
