@@ -320,12 +320,13 @@ uint64_t flat_cu_peak(const AttentionPlan& p, uint32_t heads, uint32_t cus) {
 
 // Modelled duration in microseconds of an int8 attention launch plan on
 // MI355X: a fixed cost (7.5 us for one launch, 9.25 us with the merge launch)
-// plus the longer of the chip streaming the whole live history at 6.4 TB/s
+// plus the longer of the device streaming the whole live history at 25 GB/s
+// per CU (6.4 TB/s over 256 CUs; a partition of the device has its share)
 // and the busiest CU streaming its share at 37 GB/s. Fitted to 42 measured
 // ragged batches (B = 4 .. 64, H = 16, D = 64 / 128, per-row and balanced
 // plans): within 2.6 us rms of the measured step.
-static double modelled_us(uint64_t total_bytes, uint64_t cu_peak_bytes, bool merge) {
-  return (merge ? 9.25 : 7.5) + std::max(double(total_bytes) / 6.4e6, double(cu_peak_bytes) / 37e3);
+static double modelled_us(uint64_t total_bytes, uint64_t cu_peak_bytes, bool merge, uint32_t cus) {
+  return (merge ? 9.25 : 7.5) + std::max(double(total_bytes) / (25e3 * cus), double(cu_peak_bytes) / 37e3);
 }
 
 bool balanced_pays(const ppk_context* ctx, const AttentionPlan& per_row, const AttentionPlan& flat, uint32_t rows,
@@ -336,8 +337,8 @@ bool balanced_pays(const ppk_context* ctx, const AttentionPlan& per_row, const A
   uint64_t total = 0;
   for (uint32_t b = 0; b < rows / heads; ++b) total += host[b] <= limit ? host[b] : 0;
   total *= uint64_t(heads) * token_bytes;
-  const double t_row = modelled_us(total, row_peak * token_bytes, per_row.ngroups > 1);
-  const double t_flat = modelled_us(total, flat_peak * token_bytes, flat.ngroups > 1);
+  const double t_row = modelled_us(total, row_peak * token_bytes, per_row.ngroups > 1, cus);
+  const double t_flat = modelled_us(total, flat_peak * token_bytes, flat.ngroups > 1, cus);
   // Balanced when the model has it at least 0.75 us faster; and when per-row
   // waves would each stream 256 KiB or more and the per-row plan's busiest CU
   // streams at least 1.2 x the balanced plan's (long waves run below the

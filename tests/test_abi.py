@@ -189,15 +189,15 @@ def _cu_peaks(lens, heads, per_row, share, cus=256, waves_per_block=4):
 
 def _balanced_pays(lens, heads, per_row, share, flat_groups, token_bytes):
     """The library's pick between the plans: a modelled step of 7.5 us per launch plan (9.25 us when it has a
-    merge launch) plus the longer of the chip streaming the live history at 6.4 TB/s and the busiest CU streaming
-    its share at 37 GB/s; balanced when modelled at least 0.75 us faster, or when per-row waves stream 256 KiB or
+    merge launch) plus the longer of the 256 CUs streaming the live history at 25 GB/s each (6.4 TB/s) and the
+    busiest CU streaming its share at 37 GB/s; balanced when modelled at least 0.75 us faster, or when per-row waves stream 256 KiB or
     more each and the per-row plan's busiest CU streams at least 1.2 x the balanced plan's."""
     S, W, G = per_row
     row_peak, flat_peak = _cu_peaks(lens, heads, per_row, share)
     total = sum(lens) * heads * token_bytes
 
     def modelled(peak, merge):
-        return (9.25 if merge else 7.5) + max(total / 6.4e6, peak * token_bytes / 37e3)
+        return (9.25 if merge else 7.5) + max(total / (25e3 * 256), peak * token_bytes / 37e3)
 
     return (modelled(flat_peak, flat_groups > 1) + 0.75 < modelled(row_peak, G > 1)
             or (S * token_bytes >= 256 << 10 and 5 * row_peak >= 6 * flat_peak))
