@@ -2050,6 +2050,19 @@ __device__ __forceinline__ void renyi_sample_body(const ppk::RenyiArgs& a) {
   const uint32_t row = blockIdx.x;
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
+  // The whole head is requested first, beside the row's metadata: each
+  // thread's columns (at most PER of each head, inside the row's raw logits
+  // whatever the metadata say) before any is used, so the pass costs one
+  // memory round trip instead of one or two per column.
+  const float* c_row = a.raw + size_t(row) * a.guidance * a.choices;
+  const bool guided = a.guidance == 2;
+  float cv[PER], uv[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t col = uint32_t(t) + uint32_t(k) * T;
+    cv[k] = col < a.choices ? c_row[col] : 0.f;
+    uv[k] = guided && col < a.choices ? c_row[a.choices + col] : 0.f;
+  }
   const uint32_t start = a.bounds[2 * row];
   const uint32_t count = a.bounds[2 * row + 1];
   const float uniform = a.uniforms[row];
@@ -2060,16 +2073,19 @@ __device__ __forceinline__ void renyi_sample_body(const ppk::RenyiArgs& a) {
     return;
   }
 
-  // Whole head: CFG combine and finiteness; legal values to LDS; arg-max.
-  const float* c_row = a.raw + size_t(row) * a.guidance * a.choices;
+  // Whole head, in column order: CFG combine and finiteness; legal values to
+  // LDS; arg-max.
   float lmax = -INFINITY;
   uint32_t lid = 0xffffffffu, lbad = 0;
-  for (uint32_t col = t; col < a.choices; col += T) {
-    const float c = c_row[col];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t col = uint32_t(t) + uint32_t(k) * T;
+    if (col >= a.choices) continue;
+    const float c = cv[k];
     float value = c;
     bool finite = finite_bits(c);
-    if (a.guidance == 2) {
-      const float u = c_row[a.choices + col];
+    if (guided) {
+      const float u = uv[k];
       finite = finite && finite_bits(u);
       value = u + a.cfg * (c - u);
     }
