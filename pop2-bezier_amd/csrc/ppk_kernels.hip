@@ -1041,8 +1041,6 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   constexpr int EPL = D / ppk::kWave;
   const int lane = threadIdx.x;
   const uint32_t row = blockIdx.x;
-  const uint32_t p = a.past[row / a.heads];
-  const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.nsplits) * a.split_tokens;
 
   float sv[EPL];
   float s_cur = -INFINITY;
@@ -1062,6 +1060,11 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   float m, zsum, y[EPL];
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
                      lane, current, m, zsum, y);
+  // The row's length is first needed here: read after the records went out
+  // (deciding validity up front would hold every record load back by the
+  // length's round trip).
+  const uint32_t p = a.past[row / a.heads];
+  const bool valid = p <= a.capacity && uint64_t(p) <= uint64_t(a.nsplits) * a.split_tokens;
   const float wc = __builtin_amdgcn_exp2f(s_cur - m);
   zsum += wc;
 #pragma unroll
@@ -1721,10 +1724,6 @@ __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
   constexpr int EPL = D / ppk::kWave;
   const int lane = threadIdx.x;
   const uint32_t row = blockIdx.x;
-  const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
-  const bool cover = uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
-  const bool valid = a.step ? (len < a.size && len + 1 <= a.span && cover)
-                            : (len > 0 && len <= a.span && len <= a.size && cover);
   float m, zsum, y[EPL], vcur[EPL];
   float s_cur = -INFINITY;
   auto current = [&]() {
@@ -1733,6 +1732,13 @@ __device__ __forceinline__ void fmerge_body(const ppk::FloatMergeArgs& a) {
   };
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
                      lane, current, m, zsum, y);
+  // The row's length is first needed here: read after the records went out
+  // (deciding validity up front would hold every record load back by the
+  // length's round trip).
+  const uint32_t len = float_row_length(a.lengths, row, a.heads, a.size);
+  const bool cover = uint64_t(len) <= uint64_t(a.nsplits) * a.split_tokens;
+  const bool valid = a.step ? (len < a.size && len + 1 <= a.span && cover)
+                            : (len > 0 && len <= a.span && len <= a.size && cover);
   if (a.step) {
     const float wc = __builtin_amdgcn_exp2f(s_cur - m);
     zsum += wc;
