@@ -11,7 +11,8 @@
  *
  * Shapes: B = 2 sequences, H = 4 heads, D = 128, capacity 300, past = {257, 100}
  * (ragged), under the library's plan, 8-token splits (several blocks per row
- * joined by the merge kernel) and host lengths.
+ * joined by the merge kernel) and host lengths; dequantize; and the fused
+ * decode step (commit of the current token + attention).
  */
 #include <math.h>
 #include <stdint.h>
@@ -28,6 +29,7 @@ size_t oracle_quantize(const float* x, size_t rows, size_t d, uint8_t* codes, fl
 void oracle_attention(const float* q, const uint8_t* k, const uint8_t* v, const float* ks, const float* vs,
                       const float* sk, const float* sv, const uint32_t* past, size_t rows, size_t heads,
                       size_t capacity, size_t d, float scale, int history_bf16, double* out);
+void oracle_dequantize(const uint8_t* codes, const float* scales, size_t rows, size_t d, int round, float* out);
 
 enum { B = 2, H = 4, D = 128, CAP = 300, ROWS = B * H };
 
@@ -201,6 +203,71 @@ int main(void) {
   bad.head_dim = 100;
   const int32_t st = ppk_decode_attention(ctx, NULL, &bad);
   check(st == 1 && strlen(ppk_last_error()) > 0, "head_dim 100 refused with status 1 and an error text");
+
+  /* Dequantize the K codes back to f32 (int8_kv_ops.rs:30-40), bit-exact against the oracle. */
+  PpkDequantizeArgs da;
+  memset(&da, 0, sizeof da);
+  da.struct_size = sizeof da;
+  da.out_dtype = PPK_F32;
+  da.codes = d_kc;
+  da.scales = d_ks;
+  da.out = d_src;
+  da.rows = hist_rows;
+  da.head_dim = D;
+  if (ppk_ok(ppk_dequantize(ctx, NULL, &da), "ppk_dequantize") && hip_ok(hipDeviceSynchronize(), "sync") &&
+      hip_ok(hipMemcpy(hist_v, d_src, sizeof(float) * hist_rows * D, hipMemcpyDeviceToHost), "copy dq")) {
+    oracle_dequantize(kc, ks, hist_rows, D, 0, hist_k);
+    check(memcmp(hist_v, hist_k, sizeof(float) * hist_rows * D) == 0,
+          "ppk_dequantize to f32 bit-exact against the oracle");
+  }
+
+  /* The fused decode step (commit of the current token at slot past[b], then attention; the callers'
+     commit + attend, app/src/model/mod.rs:699-705): the output is the attention above (the committed
+     slot lies past every history), the committed codes and scales are the oracle's of the token. */
+  uint32_t* d_flags = dev_alloc(sizeof(uint32_t));
+  if (d_flags && hip_ok(hipMemset(d_flags, 0, sizeof(uint32_t)), "clear flags")) {
+    PpkDecodeStepArgs sa;
+    memset(&sa, 0, sizeof sa);
+    sa.struct_size = sizeof sa;
+    sa.new_dtype = PPK_F32;
+    sa.k_new = d_sk;
+    sa.v_new = d_sv;
+    sa.flags = d_flags;
+    sa.attn = aa;
+    sa.attn.past_host = NULL;
+    uint32_t split = 0, nsplits = 0;
+    uint64_t ws = 0;
+    void* workspace = NULL;
+    if (ppk_ok(ppk_attention_plan(ctx, &sa.attn, &split, &nsplits, &ws), "plan") &&
+        (!ws || (workspace = dev_alloc(ws)) != NULL)) {
+      sa.attn.workspace = workspace;
+      sa.attn.workspace_bytes = ws;
+      uint32_t flags = ~0u;
+      if (ppk_ok(ppk_decode_step(ctx, NULL, &sa), "ppk_decode_step") && hip_ok(hipDeviceSynchronize(), "sync") &&
+          hip_ok(hipMemcpy(out, d_out, sizeof(float) * ROWS * D, hipMemcpyDeviceToHost), "copy out") &&
+          hip_ok(hipMemcpy(kc, d_kc, hist_rows * D, hipMemcpyDeviceToHost), "copy codes") &&
+          hip_ok(hipMemcpy(ks, d_ks, sizeof(float) * hist_rows, hipMemcpyDeviceToHost), "copy scales") &&
+          hip_ok(hipMemcpy(&flags, d_flags, sizeof flags, hipMemcpyDeviceToHost), "copy flags")) {
+        double max_abs = 0.0;
+        for (size_t i = 0; i < (size_t)ROWS * D; ++i) {
+          const double err = fabs((double)out[i] - ref[i]);
+          if (!(err <= max_abs)) max_abs = err; /* NaN propagates */
+        }
+        int committed = 1;
+        for (size_t r = 0; r < ROWS; ++r) {
+          const size_t slot = r * CAP + past[r / H];
+          oracle_quantize(sk + r * D, 1, D, okc, oks);
+          committed = committed && memcmp(kc + slot * D, okc, D) == 0 && ks[slot] == oks[0];
+        }
+        char line[160];
+        snprintf(line, sizeof line, "ppk_decode_step: output max abs %.3e, committed K bit-exact %s, flags %u",
+                 max_abs, committed ? "yes" : "no", flags);
+        check(max_abs <= 2e-3 && committed && flags == 0, line);
+      }
+    }
+    if (workspace) hipFree(workspace);
+  }
+  if (d_flags) hipFree(d_flags);
 
   hipFree(d_src);
   hipFree(d_kc);

@@ -2,7 +2,8 @@
 quantize and attention calls through include/ppk_int8_kv.h, no Python or torch in the process. The
 program checks codes and scales bit for bit and attention within the north-star bar (max abs <= 2e-3,
 max relative <= 1e-2) against the CPU oracle, on a ragged batch (past = 257 and 100 of capacity 300,
-H = 4, D = 128) under the library's plan, 8-token splits (merge kernel) and host lengths, and a refused call."""
+H = 4, D = 128) under the library's plan, 8-token splits (merge kernel) and host lengths, a refused call,
+dequantize (bit-exact) and the fused decode step (output, committed codes and scales, flags)."""
 import os
 import subprocess
 
