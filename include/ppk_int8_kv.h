@@ -213,6 +213,24 @@ PPK_API int32_t ppk_attention_workspace_bytes(ppk_context* ctx, const PpkAttenti
 PPK_API int32_t ppk_attention_plan(ppk_context* ctx, const PpkAttentionArgs* args, uint32_t* split_tokens,
                                    uint32_t* nsplits, uint64_t* workspace_bytes);
 PPK_API int32_t ppk_decode_attention(ppk_context* ctx, void* stream, const PpkAttentionArgs* args);
+/* The whole launch plan (no counterpart in the reference; for benchmarks and
+   callers that size their own buffers): which of the two plans the library
+   takes for args (PPK_ATTN_PLAN_PER_ROW, or PPK_ATTN_PLAN_BALANCED for a
+   ragged batch's work list), the fields of ppk_attention_plan, the decode
+   launch's grid and the number of launches a call makes (2 when a merge
+   launch follows). info->struct_size must be set. */
+typedef struct PpkAttentionPlanInfo {
+  uint32_t struct_size;
+  uint32_t kind;             /* PPK_ATTN_PLAN_PER_ROW or PPK_ATTN_PLAN_BALANCED */
+  uint32_t split_tokens;     /* as ppk_attention_plan */
+  uint32_t nsplits;          /* as ppk_attention_plan */
+  uint32_t waves_per_block;
+  uint32_t blocks;           /* blocks of the decode launch */
+  uint32_t launches;         /* 1, or 2 with the merge launch */
+  uint32_t reserved;
+  uint64_t workspace_bytes;  /* as ppk_attention_plan */
+} PpkAttentionPlanInfo;
+PPK_API int32_t ppk_attention_plan_info(ppk_context* ctx, const PpkAttentionArgs* args, PpkAttentionPlanInfo* info);
 
 /* One decode step in as few launches as the plan allows (one when a block of
    waves covers a whole row): quantise the current token k_new/v_new[row] and
@@ -298,6 +316,9 @@ typedef struct PpkFloatAttentionArgs {
 PPK_API int32_t ppk_float_attention_plan(ppk_context* ctx, const PpkFloatAttentionArgs* args,
                                          uint32_t* split_tokens, uint32_t* nsplits, uint64_t* workspace_bytes);
 PPK_API int32_t ppk_float_decode_attention(ppk_context* ctx, void* stream, const PpkFloatAttentionArgs* args);
+/* The float path's launch plan, as ppk_attention_plan_info. */
+PPK_API int32_t ppk_float_attention_plan_info(ppk_context* ctx, const PpkFloatAttentionArgs* args,
+                                              PpkAttentionPlanInfo* info);
 
 /* The float path's fused decode step: the caller's commit and attention in
    one launch per layer (two when rows span blocks). Replaces the graph-decode
@@ -517,7 +538,13 @@ PPK_API int32_t ppk_write_plan_release(ppk_write_plan* plan);
    scales and output as the two calls), ppk_float_decode_step for bf16 / f32
    caches (attn.k = view.k, attn.size = view.capacity, attn.lengths =
    view.past, attn.max_length = view.length). The step must follow on the
-   same stream before anything reads the slot. */
+   same stream before anything reads the slot. The reservation is a commit:
+   if the step is then refused (status 1, nothing enqueued), each cache's
+   slot past[b] stays committed and unwritten. Check the step's arguments
+   first (ppk_attention_plan / ppk_float_attention_plan run every check the
+   step runs on them), or undo the reservation with
+   ppk_kv_cache_truncate(cache, past_lens[b]) on every cache of the batch
+   before anything reads the slot. */
 PPK_API int32_t ppk_kv_query_batch(ppk_context* ctx, void* stream, ppk_kv_cache* const* caches, uint32_t batch,
                                    const uint32_t* past_lens, const PpkKvWrite* write, const ppk_write_plan* plan,
                                    PpkKvView* out);

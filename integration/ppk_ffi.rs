@@ -320,6 +320,21 @@ pub struct PpkInt8KvStatus {
     pub reason: [c_char; 256],
 }
 
+/// The whole launch plan (no counterpart in the reference).
+#[repr(C)]
+#[derive(Clone, Copy)]
+pub struct PpkAttentionPlanInfo {
+    pub struct_size: u32,
+    pub kind: u32,
+    pub split_tokens: u32,
+    pub nsplits: u32,
+    pub waves_per_block: u32,
+    pub blocks: u32,
+    pub launches: u32,
+    pub reserved: u32,
+    pub workspace_bytes: u64,
+}
+
 #[link(name = "ppk")]
 extern "C" {
     pub fn ppk_abi_version() -> u32;
@@ -341,6 +356,16 @@ extern "C" {
     pub fn ppk_decode_attention(ctx: *mut ppk_context, stream: *mut c_void, args: *const PpkAttentionArgs) -> i32;
     pub fn ppk_decode_step(ctx: *mut ppk_context, stream: *mut c_void, args: *const PpkDecodeStepArgs) -> i32;
     pub fn ppk_decode_step_noalloc(ctx: *mut ppk_context, stream: *mut c_void, args: *const PpkDecodeStepArgs) -> i32;
+    pub fn ppk_attention_plan_info(
+        ctx: *mut ppk_context,
+        args: *const PpkAttentionArgs,
+        info: *mut PpkAttentionPlanInfo,
+    ) -> i32;
+    pub fn ppk_float_attention_plan_info(
+        ctx: *mut ppk_context,
+        args: *const PpkFloatAttentionArgs,
+        info: *mut PpkAttentionPlanInfo,
+    ) -> i32;
     pub fn ppk_float_attention_plan(
         ctx: *mut ppk_context,
         args: *const PpkFloatAttentionArgs,

@@ -84,16 +84,16 @@ struct Arena {
   ~Arena() {
     if (!base) return;
     ppk::DeviceGuard guard(ctx->device);
+    std::vector<ppk_context::CachedBlock> evicted;
+    bool kept = false;
     {
       std::lock_guard<std::mutex> lock(ctx->block_mutex);
       // Room for this block: the oldest kept blocks go first (sizes that no
-      // later arena asked for age out), each once its last use has finished.
+      // later arena asked for age out). They are freed below, after the lock.
       auto& cache = ctx->block_cache;
       while (!cache.empty() && bytes <= ctx->block_cache_limit &&
              ctx->block_cache_bytes + bytes > ctx->block_cache_limit) {
-        (void)hipEventSynchronize(cache.front().released);
-        (void)hipFree(cache.front().ptr);
-        ctx->spare_events.push_back(cache.front().released);
+        evicted.push_back(cache.front());
         ctx->block_cache_bytes -= cache.front().bytes;
         cache.erase(cache.begin());
       }
@@ -110,12 +110,25 @@ struct Arena {
         if (hipEventRecord(ev, last_stream) == hipSuccess) {
           ctx->block_cache.push_back({base, bytes, ev});
           ctx->block_cache_bytes += bytes;
-          return;
+          kept = true;
+        } else {
+          (void)hipEventDestroy(ev);
         }
-        (void)hipEventDestroy(ev);
       }
     }
-    (void)hipFreeAsync(base, last_stream);
+    // Evicted blocks are freed in stream order behind their last use (this
+    // stream waits for the event recorded at their release), so neither the
+    // host nor other arena calls wait here; the host waits only if the
+    // runtime refuses the stream wait.
+    for (const auto& b : evicted) {
+      if (hipStreamWaitEvent(last_stream, b.released, 0) != hipSuccess) (void)hipEventSynchronize(b.released);
+      (void)hipFreeAsync(b.ptr, last_stream);
+    }
+    if (!evicted.empty()) {
+      std::lock_guard<std::mutex> lock(ctx->block_mutex);
+      for (const auto& b : evicted) ctx->spare_events.push_back(b.released);
+    }
+    if (!kept) (void)hipFreeAsync(base, last_stream);
   }
 };
 

@@ -71,6 +71,8 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_fstep_f32_d64", "ppk_fstep_f32_d128", "ppk_fstep_f32_d256",
     "ppk_fstep_flat_bf16_d64", "ppk_fstep_flat_bf16_d128", "ppk_fstep_flat_bf16_d256",
     "ppk_fstep_flat_f32_d64", "ppk_fstep_flat_f32_d128", "ppk_fstep_flat_f32_d256",
+    "ppk_decode_w16_d64", "ppk_decode_w16_d128", "ppk_decode_w16_d256",
+    "ppk_decode_w16_bf16h_d64", "ppk_decode_w16_bf16h_d128", "ppk_decode_w16_bf16h_d256",
 };
 
 std::string default_code_object() {
@@ -669,7 +671,12 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
     launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMergeFlat64 + di), a.rows, 64, 0, stream, m, 1, traceable);
     return;
   }
-  const Fn decode = Fn((bf16h ? kDecodeBf16h64 : kDecode64) + di);
+  // Blocks of at most 8 waves run the kernels bounded to 512 threads (two
+  // waves per SIMD, up to 256 VGPRs: a deeper ring of batches in flight);
+  // larger blocks the 1024-thread ones (at most 128 VGPRs).
+  const bool w16 = plan.waves > 8;
+  const Fn decode =
+      Fn((w16 ? (bf16h ? kDecodeW16Bf16h64 : kDecodeW16_64) : (bf16h ? kDecodeBf16h64 : kDecode64)) + di);
   DeviceGuard guard(ctx->device);
   launch(ctx, PPK_KERNEL_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d, 1,
          traceable);
@@ -1134,6 +1141,28 @@ int32_t ppk_attention_plan(ppk_context* ctx, const PpkAttentionArgs* args, uint3
   });
 }
 
+namespace {
+void fill_plan_info(const ppk::AttentionPlan& plan, uint32_t rows, PpkAttentionPlanInfo* info) {
+  ppk::require(info != nullptr && info->struct_size >= sizeof(PpkAttentionPlanInfo),
+               "PpkAttentionPlanInfo missing or struct_size too small");
+  info->kind = plan.flat ? PPK_ATTN_PLAN_BALANCED : PPK_ATTN_PLAN_PER_ROW;
+  info->split_tokens = plan.split;
+  info->nsplits = plan.ngroups;
+  info->waves_per_block = plan.waves;
+  info->blocks = plan.flat ? plan.blocks : plan.ngroups * rows;
+  info->launches = plan.flat ? (plan.ngroups >= 2 ? 2u : 1u) : (plan.ngroups > 1 ? 2u : 1u);
+  info->reserved = 0;
+  info->workspace_bytes = plan.workspace_bytes;
+}
+}  // namespace
+
+int32_t ppk_attention_plan_info(ppk_context* ctx, const PpkAttentionArgs* args, PpkAttentionPlanInfo* info) {
+  return call([&] {
+    ppk::require(args != nullptr, "ppk_attention_plan_info: null arguments");
+    fill_plan_info(ppk::plan_attention(ctx, *args), args->rows, info);
+  });
+}
+
 int32_t ppk_decode_attention(ppk_context* ctx, void* stream, const PpkAttentionArgs* args) {
   return call([&] {
     ppk::require(ctx && args, "ppk_decode_attention: null context or arguments");
@@ -1165,6 +1194,14 @@ int32_t ppk_float_attention_plan(ppk_context* ctx, const PpkFloatAttentionArgs* 
     if (split_tokens) *split_tokens = plan.split;
     if (nsplits) *nsplits = plan.ngroups;
     if (workspace_bytes) *workspace_bytes = plan.workspace_bytes;
+  });
+}
+
+int32_t ppk_float_attention_plan_info(ppk_context* ctx, const PpkFloatAttentionArgs* args,
+                                      PpkAttentionPlanInfo* info) {
+  return call([&] {
+    ppk::require(args != nullptr, "ppk_float_attention_plan_info: null arguments");
+    fill_plan_info(ppk::plan_float_attention(ctx, *args), args->rows, info);
   });
 }
 

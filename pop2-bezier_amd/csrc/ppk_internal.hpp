@@ -60,6 +60,8 @@ enum Fn : int {
   kFStepF32_64, kFStepF32_128, kFStepF32_256,
   kFStepFlatBf16_64, kFStepFlatBf16_128, kFStepFlatBf16_256,
   kFStepFlatF32_64, kFStepFlatF32_128, kFStepFlatF32_256,
+  kDecodeW16_64, kDecodeW16_128, kDecodeW16_256,
+  kDecodeW16Bf16h64, kDecodeW16Bf16h128, kDecodeW16Bf16h256,
   kFnCount
 };
 

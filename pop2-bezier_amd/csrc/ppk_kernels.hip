@@ -4,7 +4,8 @@
 //
 //   ppk_quantize_d{64,128,256}         quantize rows densely or append into arenas
 //   ppk_dequantize                     codes * scales -> f32/bf16/f16
-//   ppk_decode[_bf16h]_d{..}           decode attention (+ fused append, + in-block merge)
+//   ppk_decode[_w16][_bf16h]_d{..}     decode attention (+ fused append, + in-block merge); _w16: 9-16 waves
+//                                      per block
 //   ppk_attn_merge_d{..}               cross-group merge + current token
 //   ppk_decode_flat[_bf16h]_d{..}      decode attention over a balanced work list (ragged batches, + fused append)
 //   ppk_attn_merge_flat_d{..}          merge of the balanced work list's records + current token
@@ -691,18 +692,21 @@ __device__ __forceinline__ float current_score(const ppk::DecodeArgs& a, const f
 }
 
 // Streams this wave's n tokens (from `begin`) of one row: phase K scores,
-// phase V accumulation. Two batches (A, B) ping-pong so the next batch's loads
-// are always in flight while the current one is consumed; addresses past the
-// end clamp to the last token and those tokens are masked out. With `pre`
-// (nspec beyond the short window) the caller has already issued the first
-// two K batches into ra/sa and rb/sb, clamped to nspec instead of n (tokens
-// at or past n are masked by their scores, so the wider clamp only reads
-// other slots of the same arena row).
-template <int D, bool BF16H>
+// phase V accumulation. A ring of NB batches (rr[b], rs[b]) keeps NB - 1
+// batches' loads in flight while one is consumed: batch i of the sequence
+// K_0 .. K_{nb-1}, (padding to a whole ring), V_0 .. V_{nb-1} lives in slot
+// i % NB, and each slot is refilled with batch i + NB as soon as batch i is
+// used, so phase V's first batches are requested during phase K's last ones.
+// Addresses past the end clamp to the last token and those tokens are masked
+// out. With `pre` (nspec beyond the short window) the caller has already
+// issued the first K batches into the ring, clamped to nspec instead of n
+// (tokens at or past n are masked by their scores, so the wider clamp only
+// reads other slots of the same arena row).
+template <int D, bool BF16H, int NB>
 __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_t row, uint32_t begin, uint32_t n,
                                                uint32_t nspec, const float (&qr)[16], float* s_lds, int lane,
-                                               WavePartial& out, bool pre, u4 (&ra)[4], u4 (&rb)[4], float& sa,
-                                               float& sb) {
+                                               WavePartial& out, bool pre, u4 (&rr)[NB][4], float (&rs)[NB]) {
+  static_assert(NB >= 2, "the short-stream path keeps its K batches in ring slots 0 and 1");
   constexpr int LPT = D / 16;
   constexpr int TPL = ppk::kWave / LPT;
   constexpr int U = 4;  // tiles per batch
@@ -779,18 +783,18 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
     const bool two = ntiles > U;  // uniform per wave
     u4 va[U], vb2[U];
     float vsa, vsb2;
-    if (!pre) load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
+    if (!pre) load_batch<D, U>(kb, ksb, 0, n, j, lane, rr[0], rs[0]);
     load_batch<D, U>(vb, vsb, 0, n, j, lane, va, vsa);
     if (two) {
-      if (!pre) load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
+      if (!pre) load_batch<D, U>(kb, ksb, U, n, j, lane, rr[1], rs[1]);
       load_batch<D, U>(vb, vsb, U, n, j, lane, vb2, vsb2);
     }
     if constexpr (!BF16H) {
       qi = quantize_query<LPT>(qr);
       sl2 *= qi.unscale;
     }
-    mloc = score_batch<D, BF16H, U>(ra, sa, 0, n, j, c, qr, qi, sl2, s_lds, mloc);
-    if (two) mloc = score_batch<D, BF16H, U>(rb, sb, U, n, j, c, qr, qi, sl2, s_lds, mloc);
+    mloc = score_batch<D, BF16H, U>(rr[0], rs[0], 0, n, j, c, qr, qi, sl2, s_lds, mloc);
+    if (two) mloc = score_batch<D, BF16H, U>(rr[1], rs[1], U, n, j, c, qr, qi, sl2, s_lds, mloc);
     m = mloc;
 #pragma unroll
     for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -798,34 +802,46 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
     accumulate_batch<D, BF16H, U>(va, vsa, 0, n, j, lane, m, s_lds, z, out.acc);
     if (two) accumulate_batch<D, BF16H, U>(vb2, vsb2, U, n, j, lane, m, s_lds, z, out.acc);
   } else {
-    // The first two K batches do not depend on q: issue them before the query
-    // is quantised, so the q load and its reductions overlap the first memory
-    // round trip. Batch A of the last phase-K iteration already fetches phase
-    // V's first batch, so the V stream starts without a full memory latency.
+    // The first K batches do not depend on q: issue them before the query is
+    // quantised, so the q load and its reductions overlap the first memory
+    // round trip. Every ring load is issued unconditionally (batches past the
+    // end clamp to the row's last token, a cached line) so that each wait is
+    // for exactly the oldest batch: a conditional load leaves the compiler's
+    // count of loads in flight unknown on one path, and it then waits for
+    // all of them (vmcnt(0)), which drains the ring every batch. Only the
+    // arithmetic of batches past the end is skipped (uniform branches).
+    const uint32_t nb = (ntiles + U - 1) / U;       // K batches (and V batches)
+    const uint32_t nbp = (nb + NB - 1) / NB * NB;   // rounded up to whole rings
     if (!pre) {
-      load_batch<D, U>(kb, ksb, 0, n, j, lane, ra, sa);
-      load_batch<D, U>(kb, ksb, U, n, j, lane, rb, sb);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) load_batch<D, U>(kb, ksb, uint32_t(b) * U, n, j, lane, rr[b], rs[b]);
     }
     if constexpr (!BF16H) {
       qi = quantize_query<LPT>(qr);
       sl2 *= qi.unscale;
     }
-    for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
-      if (t0 != 0) load_batch<D, U>(kb, ksb, t0 + U, n, j, lane, rb, sb);
-      mloc = score_batch<D, BF16H, U>(ra, sa, t0, n, j, c, qr, qi, sl2, s_lds, mloc);
-      const bool last = t0 + 2 * U >= ntiles;
-      load_batch<D, U>(last ? vb : kb, last ? vsb : ksb, last ? 0u : t0 + 2 * U, n, j, lane, ra, sa);
-      mloc = score_batch<D, BF16H, U>(rb, sb, t0 + U, n, j, c, qr, qi, sl2, s_lds, mloc);
+    for (uint32_t k0 = 0; k0 < nbp; k0 += NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t i = k0 + uint32_t(b);
+        if (i < nb) mloc = score_batch<D, BF16H, U>(rr[b], rs[b], i * U, n, j, c, qr, qi, sl2, s_lds, mloc);
+        // Refill slot b with item i + NB: K batch i + NB, or V batch i + NB - nbp.
+        const bool isv = i + NB >= nbp;
+        load_batch<D, U>(isv ? vb : kb, isv ? vsb : ksb, (isv ? i + NB - nbp : i + NB) * U, n, j, lane, rr[b],
+                         rs[b]);
+      }
     }
     m = mloc;
 #pragma unroll
     for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
     __builtin_amdgcn_wave_barrier();
-    for (uint32_t t0 = 0; t0 < ntiles; t0 += 2 * U) {
-      load_batch<D, U>(vb, vsb, t0 + U, n, j, lane, rb, sb);
-      accumulate_batch<D, BF16H, U>(ra, sa, t0, n, j, lane, m, s_lds, z, out.acc);
-      load_batch<D, U>(vb, vsb, t0 + 2 * U, n, j, lane, ra, sa);
-      accumulate_batch<D, BF16H, U>(rb, sb, t0 + U, n, j, lane, m, s_lds, z, out.acc);
+    for (uint32_t v0 = 0; v0 < nbp; v0 += NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t i = v0 + uint32_t(b);
+        if (i < nb) accumulate_batch<D, BF16H, U>(rr[b], rs[b], i * U, n, j, lane, m, s_lds, z, out.acc);
+        load_batch<D, U>(vb, vsb, (i + NB) * U, n, j, lane, rr[b], rs[b]);  // past the end on the last ring
+      }
     }
   }
   // Each token's p was added once, by its owning lane: sum over the wave.
@@ -839,13 +855,16 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   out.z = z;
 }
 
-template <int D, bool BF16H>
+template <int D, bool BF16H, int NB>
 __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   constexpr int LPT = D / 16;
   constexpr int EPL = D / ppk::kWave;
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // The wave index is uniform: in a scalar register, every quantity derived
+  // from it (the wave's range, its length, its batch counts) is too, and the
+  // stream's loop and batch conditions become scalar branches.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int c = lane % LPT;
   // Blocks are numbered group-major: consecutive blocks belong to different
@@ -889,13 +908,14 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   const uint32_t nspec = (a.speculate && begin < a.capacity) ? min(S, a.capacity - begin) : 0u;
   constexpr int TPL = ppk::kWave / LPT;
   const bool pre = nspec > uint32_t(8 * TPL);  // the wave takes a streamed (not short-window) path
-  u4 ra[4], rb[4];
-  float sa = 0.f, sb = 0.f;
+  u4 rr[NB][4];
+  float rs[NB];
   if (pre) {
     const size_t tok0 = size_t(row) * a.capacity + begin;
     const int j = lane / LPT;
-    load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, 0, nspec, j, lane, ra, sa);
-    load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, 4, nspec, j, lane, rb, sb);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, uint32_t(b) * 4, nspec, j, lane, rr[b], rs[b]);
   }
   // A length within the caller's span that the plan does not cover: the plan
   // was sized from a stale host copy of the lengths (the row gives NaN).
@@ -912,7 +932,7 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   if (final_out && wave == 0) s_cur = current_score<D>(a, kv, qr);
   const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
   WavePartial part;
-  wave_attention<D, BF16H>(a, row, begin, n, nspec, qr, lds + size_t(wave) * S, lane, part, pre, ra, rb, sa, sb);
+  wave_attention<D, BF16H, NB>(a, row, begin, n, nspec, qr, lds + size_t(wave) * S, lane, part, pre, rr, rs);
 
   // Combine the block's waves through LDS (the staging area is reused).
   // Record of wave w at mrg + w * R: m, z, 2 pad floats, y[D] (16-byte aligned).
@@ -1923,10 +1943,14 @@ __device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs
   for (int e = 0; e < G::kEpc; ++e) part.acc[e] = 0.f;
   if (n > 0) fwave_attention_window<D, BF16KV>(a, row, t0, n, qr, lane, part);
   bool valid;
-  if constexpr (STEP)
+  if constexpr (STEP) {
     valid = ldev == t.past[b] && t.past[b] < a.size && t.past[b] + 1 <= a.span;
-  else
+    // A device length that differs from the host copy the table was built
+    // from: the row gives NaN, and a decode step says why in its flags.
+    if (ldev != t.past[b] && lane == 0 && a.flags) atomicOr(a.flags, 4u);
+  } else {
     valid = len > 0 && ldev == t.past[b];
+  }
   if (cur) {
     float d = 0.f;
 #pragma unroll
@@ -2385,12 +2409,24 @@ PPK_QSTREAM(128)
 PPK_QSTREAM(256)
 #undef PPK_QSTREAM
 
+// Blocks of up to 8 waves (2 per SIMD, up to 256 VGPRs) stream through a
+// ring of kRing batches; blocks of 9 to 16 waves (4 per SIMD, at most 128
+// VGPRs) through a ring of two.
+constexpr int kRing = 3;
 #define PPK_ATTN(D)                                                                          \
-  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_d##D(ppk::DecodeArgs a) {     \
-    decode_body<D, false>(a);                                                                \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))    \
+  void ppk_decode_d##D(ppk::DecodeArgs a) {                                                  \
+    decode_body<D, false, kRing>(a);                                                         \
   }                                                                                          \
-  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_bf16h_d##D(ppk::DecodeArgs a) { \
-    decode_body<D, true>(a);                                                                 \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))    \
+  void ppk_decode_bf16h_d##D(ppk::DecodeArgs a) {                                            \
+    decode_body<D, true, kRing>(a);                                                          \
+  }                                                                                          \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_w16_d##D(ppk::DecodeArgs a) { \
+    decode_body<D, false, 2>(a);                                                             \
+  }                                                                                          \
+  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_w16_bf16h_d##D(ppk::DecodeArgs a) { \
+    decode_body<D, true, 2>(a);                                                              \
   }                                                                                          \
   extern "C" __global__ __launch_bounds__(64) void ppk_attn_merge_d##D(ppk::MergeArgs a) {   \
     attn_merge_body<D>(a);                                                                   \

@@ -108,6 +108,12 @@ class PpkInt8KvStatus(ctypes.Structure):
                 ("format", ctypes.c_char * 64), ("reason", ctypes.c_char * 256)]
 
 
+class PpkAttentionPlanInfo(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("kind", _u32), ("split_tokens", _u32), ("nsplits", _u32),
+                ("waves_per_block", _u32), ("blocks", _u32), ("launches", _u32), ("reserved", _u32),
+                ("workspace_bytes", _u64)]
+
+
 # Every function the header declares: name -> (restype, argtypes).
 FUNCTIONS = {
     "ppk_abi_version": (_u32, []),
@@ -122,11 +128,15 @@ FUNCTIONS = {
                                                        ctypes.POINTER(_u64)]),
     "ppk_attention_plan": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkAttentionArgs), ctypes.POINTER(_u32),
                                             ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
+    "ppk_attention_plan_info": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkAttentionArgs),
+                                                 ctypes.POINTER(PpkAttentionPlanInfo)]),
     "ppk_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkAttentionArgs)]),
     "ppk_decode_step": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDecodeStepArgs)]),
     "ppk_decode_step_noalloc": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkDecodeStepArgs)]),
     "ppk_float_attention_plan": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkFloatAttentionArgs), ctypes.POINTER(_u32),
                                                   ctypes.POINTER(_u32), ctypes.POINTER(_u64)]),
+    "ppk_float_attention_plan_info": (ctypes.c_int32, [_ptr, ctypes.POINTER(PpkFloatAttentionArgs),
+                                                       ctypes.POINTER(PpkAttentionPlanInfo)]),
     "ppk_float_decode_attention": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatAttentionArgs)]),
     "ppk_float_decode_step": (ctypes.c_int32, [_ptr, _ptr, ctypes.POINTER(PpkFloatDecodeStepArgs)]),
     "ppk_float_attention_prepare": (ctypes.c_int32, [_ptr]),

@@ -79,6 +79,17 @@ def plan(args: _abi.PpkFloatAttentionArgs, ctx: ctypes.c_void_p | None = None) -
     return split.value, nsplits.value, nbytes.value
 
 
+def plan_info(args: _abi.PpkFloatAttentionArgs, ctx: ctypes.c_void_p | None = None) -> dict:
+    """The whole launch plan the library takes for args (ppk_float_attention_plan_info): kind ("per-row" or
+    "balanced"), split_tokens, nsplits, waves_per_block, blocks, launches and workspace_bytes."""
+    info = _abi.PpkAttentionPlanInfo(struct_size=ctypes.sizeof(_abi.PpkAttentionPlanInfo))
+    check(lib().ppk_float_attention_plan_info(ctx, ctypes.byref(args), ctypes.byref(info)),
+          "ppk_float_attention_plan_info")
+    return {"kind": "balanced" if info.kind == _abi.PPK_ATTN_PLAN_BALANCED else "per-row",
+            "split_tokens": info.split_tokens, "nsplits": info.nsplits, "waves_per_block": info.waves_per_block,
+            "blocks": info.blocks, "launches": info.launches, "workspace_bytes": info.workspace_bytes}
+
+
 # The parameter `plan` of the calls below shadows the function inside them.
 launch_plan = plan
 
@@ -138,9 +149,35 @@ def decode_step(q, k, v, lengths, heads: int, k_new: torch.Tensor, v_new: torch.
     return out
 
 
+def _replan(obj, attn: _abi.PpkFloatAttentionArgs, lengths_host) -> None:
+    """Point attn at a new host copy of lengths[] (or none), re-plan, and grow obj's workspace if the new plan
+    needs more (the old workspace is released to torch's stream-ordered allocator)."""
+    if lengths_host is None:
+        obj._lengths_host = None
+        attn.lengths_host = None
+    else:
+        host = [int(x) for x in lengths_host]
+        _require(attn.lengths is not None and len(host) == attn.rows // attn.heads
+                 and all(0 <= x < 2 ** 32 for x in host),
+                 "fused attention host lengths require device lengths of the same batch")
+        obj._lengths_host = (ctypes.c_uint32 * len(host))(*host)
+        attn.lengths_host = ctypes.cast(obj._lengths_host, ctypes.c_void_p).value
+    obj.split_tokens, obj.ngroups, nbytes = launch_plan(attn, obj.ctx)
+    obj.plan_info = plan_info(attn, obj.ctx)
+    if nbytes > obj.workspace.numel():
+        obj.workspace = torch.empty(nbytes, dtype=torch.uint8, device=obj.device)
+    attn.workspace = obj.workspace.data_ptr()
+    attn.workspace_bytes = nbytes
+
+
 class FloatDecodeAttention:
     """A prepared float-KV attention call for fixed buffers: argument block and workspace are built once;
-    __call__ only enqueues the kernels (bench and serving loops, graph capture)."""
+    __call__ only enqueues the kernels (bench and serving loops, graph capture).
+
+    lengths_host, if given, is the host copy of lengths[] for the calls that follow: the plan is sized from
+    it and every call checks it against the device lengths (a differing sequence gives NaN rows, never wrong
+    ones). A caller whose lengths move between calls passes each call's copy to set_lengths_host() first, or
+    builds the call without one (device lengths only)."""
 
     def __init__(self, q, k, v, lengths, heads: int, split_tokens: int = 0, *, max_length: int = 0,
                  out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32, lengths_host=None,
@@ -150,6 +187,7 @@ class FloatDecodeAttention:
                                                     plan=plan)
         self.ctx = context(q.device)
         self.split_tokens, self.ngroups, nbytes = launch_plan(self.args, self.ctx)
+        self.plan_info = plan_info(self.args, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.workspace = self.workspace.data_ptr()
         self.args.workspace_bytes = nbytes
@@ -157,6 +195,10 @@ class FloatDecodeAttention:
         self._ref = ctypes.byref(self.args)
         self._fn = lib().ppk_float_decode_attention
         self.device = q.device
+
+    def set_lengths_host(self, lengths_host) -> None:
+        """Replace the host copy of lengths[] (None: none) and re-plan for it."""
+        _replan(self, self.args, lengths_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
@@ -171,7 +213,11 @@ def prepare(device: torch.device | int | None = None) -> None:
 
 class FloatDecodeStep:
     """A prepared fused float decode step for fixed buffers (the graph-decode session's per-layer call):
-    argument block and workspace are built once; __call__ only enqueues the kernels."""
+    argument block and workspace are built once; __call__ only enqueues the kernels.
+
+    lengths_host is the host copy of lengths[] for the calls that follow (see FloatDecodeAttention): in a
+    graph-decode session, whose lengths grow by one every step, pass each step's copy to set_lengths_host()
+    before the call, or build the step without one (device lengths only)."""
 
     def __init__(self, q, k, v, lengths, heads: int, k_new: torch.Tensor, v_new: torch.Tensor,
                  split_tokens: int = 0, *, flags: torch.Tensor | None = None, max_length: int = 0,
@@ -182,6 +228,7 @@ class FloatDecodeStep:
         self.args = _step_args(a, k_new, v_new, flags, lengths)
         self.ctx = context(q.device)
         self.split_tokens, self.ngroups, nbytes = launch_plan(self.args.attn, self.ctx)
+        self.plan_info = plan_info(self.args.attn, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.attn.workspace = self.workspace.data_ptr()
         self.args.attn.workspace_bytes = nbytes
@@ -189,6 +236,10 @@ class FloatDecodeStep:
         self._ref = ctypes.byref(self.args)
         self._fn = lib().ppk_float_decode_step
         self.device = q.device
+
+    def set_lengths_host(self, lengths_host) -> None:
+        """Replace the host copy of lengths[] (None: none) and re-plan for it."""
+        _replan(self, self.args.attn, lengths_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)

@@ -182,6 +182,17 @@ def plan(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = None) -> tup
     return split.value, nsplits.value, nbytes.value
 
 
+def plan_info(args: _abi.PpkAttentionArgs, ctx: ctypes.c_void_p | None = None) -> dict:
+    """The whole launch plan the library takes for args (ppk_attention_plan_info): kind ("per-row" or
+    "balanced"), split_tokens, nsplits, waves_per_block, blocks, launches and workspace_bytes."""
+    info = _abi.PpkAttentionPlanInfo(struct_size=ctypes.sizeof(_abi.PpkAttentionPlanInfo))
+    check(lib().ppk_attention_plan_info(ctx, ctypes.byref(args), ctypes.byref(info)),
+          "ppk_attention_plan_info")
+    return {"kind": "balanced" if info.kind == _abi.PPK_ATTN_PLAN_BALANCED else "per-row",
+            "split_tokens": info.split_tokens, "nsplits": info.nsplits, "waves_per_block": info.waves_per_block,
+            "blocks": info.blocks, "launches": info.launches, "workspace_bytes": info.workspace_bytes}
+
+
 # The parameter `plan` of the calls below shadows the function inside them.
 launch_plan = plan
 
@@ -239,9 +250,34 @@ def _step_args(a: _abi.PpkAttentionArgs, k_new: torch.Tensor, v_new: torch.Tenso
     return step
 
 
+def _replan(obj, attn: _abi.PpkAttentionArgs, past_host) -> None:
+    """Point attn at a new host copy of past[] (or none), re-plan, and grow obj's workspace if the new plan
+    needs more (the old workspace is released to torch's stream-ordered allocator)."""
+    if past_host is None:
+        obj._past_host = None
+        attn.past_host = None
+    else:
+        host = [int(x) for x in past_host]
+        _require(len(host) == attn.rows // attn.heads and all(0 <= x < 2 ** 32 for x in host),
+                 "INT8 attention lengths differ")
+        obj._past_host = (ctypes.c_uint32 * len(host))(*host)
+        attn.past_host = ctypes.cast(obj._past_host, ctypes.c_void_p).value
+    obj.split_tokens, obj.ngroups, nbytes = launch_plan(attn, obj.ctx)
+    obj.plan_info = plan_info(attn, obj.ctx)
+    if nbytes > obj.workspace.numel():
+        obj.workspace = torch.empty(nbytes, dtype=torch.uint8, device=obj.device)
+    attn.workspace = obj.workspace.data_ptr()
+    attn.workspace_bytes = nbytes
+
+
 class DecodeAttention:
     """A prepared attention call for a fixed set of buffers (bench / serving loops): the argument
-    block and workspace are built once; __call__ only enqueues the two kernels."""
+    block and workspace are built once; __call__ only enqueues the two kernels.
+
+    past_host, if given, is the host copy of past[] for the calls that follow: the plan is sized from it and
+    every call checks it against the device past[] (a differing sequence gives NaN rows, never wrong ones).
+    A caller whose lengths move between calls passes each call's copy to set_past_host() first, or builds
+    the call without one (device lengths only)."""
 
     def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, split_tokens: int = 0, *,
                  bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
@@ -251,6 +287,7 @@ class DecodeAttention:
                                              out_dtype=out_dtype, past_host=past_host, plan=plan)
         self.ctx = context(q.device)
         self.split_tokens, self.ngroups, nbytes = launch_plan(self.args, self.ctx)
+        self.plan_info = plan_info(self.args, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.workspace = self.workspace.data_ptr()
         self.args.workspace_bytes = nbytes
@@ -258,6 +295,10 @@ class DecodeAttention:
         self._ref = ctypes.byref(self.args)
         self._fn = lib().ppk_decode_attention
         self.device = q.device
+
+    def set_past_host(self, past_host) -> None:
+        """Replace the host copy of past[] (None: none) and re-plan for it."""
+        _replan(self, self.args, past_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
@@ -267,7 +308,11 @@ class DecodeAttention:
 
 class DecodeStep:
     """A prepared decode step (append of the current token + attention) for fixed buffers: the argument
-    block and workspace are built once; __call__ enqueues one launch (two when the plan splits rows)."""
+    block and workspace are built once; __call__ enqueues one launch (two when the plan splits rows).
+
+    past_host is the host copy of past[] for the calls that follow (see DecodeAttention): a decode loop
+    whose lengths grow every step passes each step's copy to set_past_host() before the call, or builds the
+    step without one."""
 
     def __init__(self, q, k, v, ks, vs, sk, sv, past, heads: int, k_new=None, v_new=None, split_tokens: int = 0, *,
                  flags=None, bf16_history: bool = False, max_past: int = 0, out: torch.Tensor | None = None,
@@ -280,6 +325,7 @@ class DecodeStep:
         self.args = _step_args(a, k_new, v_new, flags, k.shape[2])
         self.ctx = context(q.device)
         self.split_tokens, self.ngroups, nbytes = launch_plan(self.args.attn, self.ctx)
+        self.plan_info = plan_info(self.args.attn, self.ctx)
         self.workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         self.args.attn.workspace = self.workspace.data_ptr()
         self.args.attn.workspace_bytes = nbytes
@@ -287,6 +333,10 @@ class DecodeStep:
         self._ref = ctypes.byref(self.args)
         self._fn = lib().ppk_decode_step
         self.device = q.device
+
+    def set_past_host(self, past_host) -> None:
+        """Replace the host copy of past[] (None: none) and re-plan for it."""
+        _replan(self, self.args.attn, past_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)

@@ -510,3 +510,29 @@ def test_error_text_is_thread_local():
         t.join()
     for field, texts in seen.items():
         assert len(texts) == 1 and bad[field] in next(iter(texts)), (field, texts)
+
+
+def test_plan_info_reports_the_plan_taken():
+    """ppk_attention_plan_info / ppk_float_attention_plan_info (no device: 256 CUs): the plan kind the
+    library takes, its grid and launches, consistent with ppk_attention_plan."""
+    skew = [8192] * 4 + [512] * 28
+    info = ppk.int8_kv_ops.plan_info(_attn_args())  # config 5: one 4-wave block per row, one launch
+    assert info == {"kind": "per-row", "split_tokens": 2048, "nsplits": 1, "waves_per_block": 4, "blocks": 512,
+                    "launches": 1, "workspace_bytes": 0}
+    info = ppk.int8_kv_ops.plan_info(_attn_args(split_tokens=100))  # 16-wave blocks, merge launch
+    split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
+    assert (info["split_tokens"], info["nsplits"], info["workspace_bytes"]) == (split, groups, nbytes)
+    assert info["kind"] == "per-row" and info["waves_per_block"] == 16 and info["blocks"] == 512 * groups
+    assert info["launches"] == 2
+    info = ppk.int8_kv_ops.plan_info(_attn_args(past_host=skew))
+    assert info["kind"] == "balanced" and info["launches"] == 2
+    assert (info["split_tokens"], info["nsplits"], info["workspace_bytes"]) == ppk.int8_kv_ops.plan(
+        _attn_args(past_host=skew))
+    info = ppk.int8_kv_ops.plan_info(_attn_args(past_host=skew, flags=_abi.PPK_ATTN_PLAN_PER_ROW))
+    assert info["kind"] == "per-row"
+    finfo = ppk.fused_attention.plan_info(_float_args(lengths=8, lengths_host=skew))
+    assert finfo["kind"] == "balanced"
+    assert ppk.fused_attention.plan_info(_float_args(lengths=8))["kind"] == "per-row"
+    small = _abi.PpkAttentionPlanInfo(struct_size=8)
+    assert _abi.lib().ppk_attention_plan_info(None, ctypes.byref(_attn_args()), ctypes.byref(small)) == \
+        _abi.PPK_PRECONDITION

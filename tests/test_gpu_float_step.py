@@ -121,6 +121,27 @@ def test_step_balanced_plan(device, kv, d):
     c.check_store()
 
 
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
+def test_step_balanced_plan_stale_host_lengths(device, kv):
+    """The balanced step with host lengths that differ from the stored ones for two sequences (one longer,
+    one shorter than the host copy): those rows give NaN and the step's flags carry PPK_FLAG_STALE_LENGTHS;
+    every other row is exact, and every row's token is still written at its device length."""
+    lengths = [0, 1500, 3, 64, 1000, 1400, 65, 900]
+    host = [0, 1500, 3, 64, 1100, 1400, 65, 700]
+    c = StepCase(device, 8, 4, 128, 1536, kv, lengths, seed=SEED + 14)
+    got, flags = c.step(lengths_host=host, plan="balanced")
+    bad = np.repeat(np.array(host) != np.array(lengths), c.H)
+    assert flags & ppk.PPK_FLAG_STALE_LENGTHS
+    assert np.isnan(got[bad]).all()
+    assert_close(got[~bad], c.expected()[~bad], atol=ATOL, rtol=RTOL, what=f"balanced step fresh rows {kv}")
+    c.check_store()
+    # The same store with the right host copy: no flag.
+    c2 = StepCase(device, 8, 4, 128, 1536, kv, lengths, seed=SEED + 15)
+    got2, flags2 = c2.step(lengths_host=lengths, plan="balanced")
+    assert not flags2 & ppk.PPK_FLAG_STALE_LENGTHS
+    assert_close(got2, c2.expected(), atol=ATOL, rtol=RTOL, what=f"balanced step {kv}")
+
+
 def test_step_balanced_plan_taken_by_the_library(device):
     """A ragged batch the library balances by itself (host lengths, auto plan)."""
     lengths = [4000, 200, 200, 3900] + [100] * 28

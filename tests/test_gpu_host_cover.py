@@ -96,3 +96,38 @@ def test_float_step_stale_host_lengths_beyond_the_coverage(device, kv):
     got2, flags2 = c2.step(lengths_host=host)
     assert flags2 == 0
     assert_close(got2, c2.expected(), atol=F_ATOL, rtol=F_RTOL, what=f"float step host-sized {kv}")
+
+
+def test_prepared_int8_call_follows_new_host_lengths(device):
+    """A prepared balanced call built with one host copy of past[] and run after the device lengths moved:
+    the stale sequences give NaN; set_past_host() with the new copy re-plans and every row is exact."""
+    old = [1000, 300, 300, 900, 120, 700, 40, 1000]
+    new = [1000, 301, 305, 950, 121, 700, 41, 999]
+    c = Case(device, 8, 4, 128, new, 1001, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16, seed=SEED + 7)
+    call = ppk.DecodeAttention(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, past_host=old,
+                               plan="balanced")
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    bad = np.repeat(np.array(old) != np.array(new), c.H)
+    ref = c.reference()
+    assert np.isnan(got[bad]).all()
+    assert_close(got[~bad], ref[~bad], what="prepared call, unchanged sequences")
+    call.set_past_host(new)
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    assert_close(got, ref, what="prepared call after set_past_host")
+
+
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
+def test_prepared_float_call_follows_new_host_lengths(device, kv):
+    old = [1000, 300, 300, 900, 120, 700, 40, 1000]
+    new = [1000, 301, 305, 950, 121, 700, 41, 999]
+    c = FloatCase(device, 8, 4, 128, 1024, kv, lengths=new, seed=SEED + 8)
+    call = ppk.fused_attention.FloatDecodeAttention(c.q, c.k, c.v, c.lengths_t, c.H, lengths_host=old,
+                                                    plan="balanced")
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    bad = np.repeat(np.array(old) != np.array(new), c.H)
+    ref = c.reference()
+    assert np.isnan(got[bad]).all()
+    assert_close(got[~bad], ref[~bad], atol=F_ATOL, rtol=F_RTOL, what=f"prepared float call, unchanged {kv}")
+    call.set_lengths_host(new)
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    assert_close(got, ref, atol=F_ATOL, rtol=F_RTOL, what=f"prepared float call after set_lengths_host {kv}")

@@ -366,6 +366,49 @@ def test_reserved_batch_write_and_fused_step_equal_write_then_attention(device):
         past = [p + 1 for p in past]
 
 
+def test_refused_step_after_a_reserving_write_is_undone_by_truncation(device):
+    """A reserving write commits slot past[b] unwritten; a fused step refused after it (status 1, nothing
+    enqueued: here the balanced plan without host lengths) leaves that commit in place. Truncating each
+    cache back to past[b] undoes it, and the round then runs as if the reservation had never happened: codes,
+    scales and output equal those of a second set of caches that only ever saw the plain write."""
+    from ppk import kv_arena
+
+    heads, d, lengths = 4, 128, [37, 0, 120]
+    sets = []
+    for _ in range(2):
+        caches = [LayerCache("int8", heads, d) for _ in lengths]
+        for c, n in zip(caches, lengths):
+            if n:
+                x = torch.randn((heads, n, d), generator=torch.Generator(device=device).manual_seed(n), device=device)
+                c.query(x, x, 0, True)
+        sets.append(caches)
+    g = torch.Generator(device=device).manual_seed(12)
+    q = torch.randn((len(lengths) * heads, d), generator=g, device=device).to(torch.bfloat16)
+    kn = torch.randn((len(lengths), heads, 1, d), generator=g, device=device).to(torch.bfloat16)
+    vn = torch.randn((len(lengths), heads, 1, d), generator=g, device=device).to(torch.bfloat16)
+    view = LayerCache.query_batch(sets[1], None, None, lengths, True)
+    assert [len(c) for c in sets[1]] == [p + 1 for p in lengths]  # committed, not yet written
+    with pytest.raises(ppk.PpkError) as e:
+        kv_arena.decode_step(view, q, kn.reshape(-1, d), vn.reshape(-1, d), heads, plan="balanced")
+    assert e.value.status == _abi.PPK_PRECONDITION
+    assert [len(c) for c in sets[1]] == [p + 1 for p in lengths]  # the refusal left the commit in place
+    for c, p in zip(sets[1], lengths):
+        c.truncate_committed(p)
+    assert [len(c) for c in sets[1]] == lengths
+    va = LayerCache.query_batch(sets[0], kn, vn, lengths, True)
+    out_a = _view_attention(va, q, kn, vn, heads)
+    vb = LayerCache.query_batch(sets[1], kn, vn, lengths, True)
+    out_b = _view_attention(vb, q, kn, vn, heads)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b) and torch.isfinite(out_a).all()
+    n = max(lengths) + 1
+    for which in ("k", "v", "k_scales", "v_scales"):
+        ra, rb = read(va, which, n), read(vb, which, n)
+        for row, p in enumerate(lengths):
+            rows = slice(row * heads, (row + 1) * heads)
+            assert torch.equal(ra[rows, :p + 1], rb[rows, :p + 1]), f"{which} sequence {row}"
+
+
 def test_reserving_write_needs_int8_bf16_or_f32_caches(device):
     """F16 caches have no fused step (the float attention reads bf16 and f32 stores): a reserving write is
     refused before anything changes."""

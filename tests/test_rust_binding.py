@@ -180,7 +180,7 @@ def test_header_parser_sees_every_struct():
     names = set(header_structs())
     assert names == {"PpkQuantizeArgs", "PpkAppendArgs", "PpkDequantizeArgs", "PpkAttentionArgs",
                      "PpkDecodeStepArgs", "PpkFloatAttentionArgs", "PpkFloatDecodeStepArgs", "PpkRenyiSampleArgs",
-                     "PpkKvConfig", "PpkKvView", "PpkKvInfo", "PpkKvWrite", "PpkInt8KvStatus"}
+                     "PpkKvConfig", "PpkKvView", "PpkKvInfo", "PpkKvWrite", "PpkInt8KvStatus", "PpkAttentionPlanInfo"}
     # The multi-declarator line of PpkAppendArgs and the trailing optional field of PpkAttentionArgs.
     append = dict(header_structs()["PpkAppendArgs"])
     assert [append[k] for k in ("batch", "heads", "tokens", "head_dim", "capacity")] == ["u32"] * 5
