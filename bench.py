@@ -67,6 +67,13 @@ def parse() -> argparse.Namespace:
     p.add_argument("--lengths", default=None,
                    help="with --kv bf16/f32: comma-separated per-sequence lengths of a ragged batch (NxL repeats "
                         "L N times); the batch is their count and the store holds the longest")
+    p.add_argument("--bf16-history", action="store_true",
+                   help="int8 decode: round every dequantised history element to bf16 before the fp32 dot "
+                        "(PPK_ATTN_BF16_HISTORY, the reference kernel's pp_i8_load arithmetic; kernels "
+                        "ppk_decode_bf16h_d*) instead of the default fp32 dequantisation")
+    p.add_argument("--no-append", action="store_true",
+                   help="int8 config 5: time ppk_decode_attention alone (the uncommitted partial query: the current "
+                        "token attended from its copy, nothing written to the arenas) instead of the fused step")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0,
                    help="head rows timed for the CPU baseline (0 = every row of the step)")
@@ -77,6 +84,24 @@ def parse() -> argparse.Namespace:
     p.add_argument("--traffic", default=None,
                    help="JSON with measured HBM bytes per partial launch (rocprofv3 --pmc), if present")
     return p.parse_args()
+
+
+def committed_traffic(tpath: str, **match) -> tuple[int | None, str | None]:
+    """HBM bytes per launch from a committed rocprofv3 traffic summary (profiles/*_traffic.json), if it was
+    measured on this exact workload (every `match` key equal). The figure comes from a separate profiled run
+    (FETCH_SIZE and WRITE_SIZE, scaled by a copy kernel of known size), not from this process: the returned
+    source string says so, and the bench line carries it beside the number."""
+    if not os.path.exists(tpath):
+        return None, None
+    try:
+        with open(tpath) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    if any(t.get(k) != v for k, v in match.items()):
+        return None, None
+    return t.get("hbm_bytes_per_launch"), (os.path.relpath(tpath, ROOT) + ": rocprofv3 FETCH_SIZE + WRITE_SIZE of "
+                                          "a separate profiled run of this workload, scaled by a copy kernel")
 
 
 def _host_cpus() -> int:
@@ -201,8 +226,8 @@ def bench_float(args) -> int:
         call = ppk.FloatDecodeAttention(q, k, v, lengths, H, args.split, max_length=L, lengths_host=host,
                                         plan=args.plan)
         plan_args = call.args
-    flat = host is not None and ppk.fused_attention.plan(plan_args, call.ctx) != ppk.fused_attention.plan(
-        ppk.fused_attention.decode_attention_args(q, k, v, lengths, H, args.split, max_length=L)[0], call.ctx)
+    # The library reports the plan it takes (ppk_float_attention_plan_info).
+    flat = ppk.fused_attention.plan_info(plan_args, call.ctx)["kind"] == "balanced"
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -254,7 +279,6 @@ def bench_float(args) -> int:
     achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
     kname = f"ppk_{'fstep' if args.step else 'fdecode'}_{'flat_' if flat else ''}{args.kv}_d{D}"
-    traffic = None
     if args.lengths:
         skew = args.lengths.replace(",", "_")
         tpath = os.path.join(ROOT, "profiles", f"{kname}_h{H}_skew{skew}_traffic.json")
@@ -262,15 +286,7 @@ def bench_float(args) -> int:
     else:
         tpath = os.path.join(ROOT, "profiles", f"ppk_fdecode_{args.kv}_d{D}_b{B}_h{H}_ctx{L}_traffic.json")
         workload = f"B{B}H{H}D{D}L{L}{args.kv}"
-    if os.path.exists(tpath):
-        try:
-            with open(tpath) as f:
-                t = json.load(f)
-            if (t.get("split") == call.split_tokens and t.get("workload") == workload
-                    and t.get("kernel") == kname):
-                traffic = t.get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic, traffic_source = committed_traffic(tpath, split=call.split_tokens, workload=workload, kernel=kname)
     result = {
         "metric": f"float-KV decode-{'step' if args.step else 'attention'} µs/step + achieved HBM GB/s (% of peak), "
                   f"B={B} ctx={L} {args.kv} KV" + (f", ragged lengths {args.lengths}" if args.lengths else ""),
@@ -287,6 +303,7 @@ def bench_float(args) -> int:
         "step_hbm_gbps": round(step_gbps, 1), "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_source,
                      "algorithmic_bytes_per_launch": kernel_bytes, "avg_launch_us": round(kernel_avg_ms * 1e3, 2),
                      "launches": launches},
     }
@@ -725,12 +742,11 @@ def bench_config(args) -> int:
               for li in range(layers)]
              for c in range(copies)]
     split, ngroups = steps[0][0].split_tokens, steps[0][0].ngroups
-    # The balanced plan is taken when the host lengths are given and rows would span blocks otherwise.
-    per_row = ppk.DecodeStep(q[0], kc[0, 0], vc[0, 0], ks[0, 0], vs[0, 0], kn[0], vn[0], past, H,
-                             split_tokens=args.split, max_past=L, out=out)
-    balanced = host is not None and (split, ngroups) != (per_row.split_tokens, per_row.ngroups)
-    layer_launches = 1 if ngroups == 1 else 2  # decode (+ merge when rows span blocks)
-    del per_row
+    # The library reports the plan it takes (ppk_attention_plan_info): per-row or balanced, its waves per
+    # block (blocks of more than 8 waves run the _w16 kernels) and its launches (decode, + merge).
+    info = steps[0][0].plan_info
+    balanced = info["kind"] == "balanced"
+    layer_launches = info["launches"]
     torch.cuda.synchronize()
 
     def warm(_i):
@@ -789,18 +805,10 @@ def bench_config(args) -> int:
     step_bytes = layer_bytes * layers
     achieved = kernel_bytes / (kernel_avg_us * 1e-6) / 1e9
     tag = f"c{args.config}_b{B}_h{H}_d{D}"
-    traffic = None
-    kbase = "ppk_decode_flat" if balanced else "ppk_decode"
+    kbase = "ppk_decode_flat" if balanced else "ppk_decode_w16" if info["waves_per_block"] > 8 else "ppk_decode"
     kname = f"{kbase}_d{D}"
     tpath = os.path.join(ROOT, "profiles", f"{kbase}_{tag}_traffic.json")
-    if os.path.exists(tpath):
-        try:
-            with open(tpath) as f:
-                t = json.load(f)
-            if t.get("split") == split and t.get("workload") == tag:
-                traffic = t.get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic, traffic_source = committed_traffic(tpath, split=split, workload=tag)
 
     result = {
         "metric": METRIC, "value": round(warm_mean, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
@@ -824,7 +832,8 @@ def bench_config(args) -> int:
         "roofline": {"bound": "hbm", "kernel": kname,
                      "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": kernel_bytes,
+                     "traffic": traffic, "traffic_source": traffic_source,
+                     "algorithmic_bytes_per_launch": kernel_bytes,
                      "avg_launch_us": round(kernel_avg_us, 2), "launches": launches,
                      "merge_avg_launch_us": round(merge_ms / m_launches * 1e3, 2) if m_launches else None},
     }
@@ -976,16 +985,8 @@ def bench_quantize(args) -> int:
     kernel_us = kernel_ms / max(launches, 1) * 1e3
     nbytes = rows * L * D * x.element_size() + rows * L * D + rows * L * 4
     achieved = nbytes / (kernel_us * 1e-6) / 1e9
-    traffic = None
     tpath = os.path.join(ROOT, "profiles", f"ppk_quantize_{args.quantize}_b{B}_h{H}_d{D}_ctx{L}_traffic.json")
-    if os.path.exists(tpath):
-        try:
-            with open(tpath) as f:
-                t = json.load(f)
-            if t.get("workload") == f"B{B}H{H}D{D}L{L}{args.quantize}":
-                traffic = t.get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic, traffic_source = committed_traffic(tpath, workload=f"B{B}H{H}D{D}L{L}{args.quantize}")
     result = {
         "metric": "%s -> int8 quantize, us per history tensor + achieved HBM GB/s" % args.quantize,
         "value": round(mean_us, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -997,7 +998,8 @@ def bench_quantize(args) -> int:
         "step_hbm_gbps": round(nbytes / (mean_us * 1e-6) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "ppk_quantize_d%d" % D, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(kernel_us, 2),
+                     "traffic": traffic, "traffic_source": traffic_source,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(kernel_us, 2),
                      "launches": launches},
     }
     if not args.no_cpu_baseline:
@@ -1075,16 +1077,8 @@ def bench_dequantize(args) -> int:
     kernel_us = kernel_ms / max(launches, 1) * 1e3
     nbytes = rows * L * D + rows * L * 4 + rows * L * D * out.element_size()
     achieved = nbytes / (kernel_us * 1e-6) / 1e9
-    traffic = None
     tpath = os.path.join(ROOT, "profiles", f"ppk_dequantize_{args.dequantize}_b{B}_h{H}_d{D}_ctx{L}_traffic.json")
-    if os.path.exists(tpath):
-        try:
-            with open(tpath) as f:
-                t = json.load(f)
-            if t.get("workload") == f"B{B}H{H}D{D}L{L}{args.dequantize}":
-                traffic = t.get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic, traffic_source = committed_traffic(tpath, workload=f"B{B}H{H}D{D}L{L}{args.dequantize}")
     result = {
         "metric": "int8 -> %s dequantize, us per history tensor + achieved HBM GB/s" % args.dequantize,
         "value": round(mean_us, 2), "unit": "us/call", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -1096,7 +1090,8 @@ def bench_dequantize(args) -> int:
         "step_hbm_gbps": round(nbytes / (mean_us * 1e-6) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "ppk_dequantize", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(kernel_us, 2),
+                     "traffic": traffic, "traffic_source": traffic_source,
+                     "algorithmic_bytes_per_launch": nbytes, "avg_launch_us": round(kernel_us, 2),
                      "launches": launches},
     }
     if not args.no_cpu_baseline:
@@ -1165,9 +1160,15 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # The current token is both attended from its bf16 copy (sk, sv) and
-    # committed into slot L of the arenas, in one launch.
-    step = ppk.DecodeStep(q, kc, vc, ks, vs, kn.reshape(rows, 1, D), vn.reshape(rows, 1, D), past, H,
-                          split_tokens=args.split, max_past=L, out=out)
+    # committed into slot L of the arenas, in one launch; with --no-append it
+    # is only attended (the reference's uncommitted partial queries).
+    append = not args.no_append
+    if append:
+        step = ppk.DecodeStep(q, kc, vc, ks, vs, kn.reshape(rows, 1, D), vn.reshape(rows, 1, D), past, H,
+                              split_tokens=args.split, max_past=L, out=out, bf16_history=args.bf16_history)
+    else:
+        step = ppk.DecodeAttention(q, kc, vc, ks, vs, kn.reshape(rows, 1, D), vn.reshape(rows, 1, D), past, H,
+                                   split_tokens=args.split, max_past=L, out=out, bf16_history=args.bf16_history)
     split = step.split_tokens
 
     if args.calibrate_copy:
@@ -1215,23 +1216,24 @@ def main() -> int:
     # row, the bf16 query, the bf16 current K/V token (read once: quantised
     # into the arena and scored as the current token), the f32 output and the
     # appended codes + scales: sum_b L_b*H*(2D+8) + q + current k,v + out + append.
+    # Without the append: the same less the appended codes + scales.
     hist_bytes = rows * L * (2 * D + 8)
-    step_bytes = hist_bytes + rows * D * 2 + 2 * rows * D * 2 + rows * D * 4 + 2 * rows * (D + 4)
-    kernel_bytes = step_bytes if step.ngroups == 1 else hist_bytes + rows * D * 2 + 2 * rows * (D + 4) + 2 * rows * D * 2
+    app_bytes = 2 * rows * (D + 4) if append else 0
+    step_bytes = hist_bytes + rows * D * 2 + 2 * rows * D * 2 + rows * D * 4 + app_bytes
+    kernel_bytes = step_bytes if step.ngroups == 1 else hist_bytes + rows * D * 2 + app_bytes + 2 * rows * D * 2
     achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
 
-    kname = "ppk_decode_d%d" % D
-    traffic = None
-    tpath = args.traffic or os.path.join(ROOT, "profiles", f"ppk_decode_d{D}_b{B}_h{H}_ctx{L}_traffic.json")
-    if os.path.exists(tpath):
-        try:
-            with open(tpath) as f:
-                t = json.load(f)
-            if t.get("split") == split and t.get("workload") == f"B{B}H{H}D{D}L{L}" and t.get("kernel") == kname:
-                traffic = t.get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    kname = ("ppk_decode" + ("_w16" if step.plan_info["waves_per_block"] > 8 else "")
+             + ("_bf16h" if args.bf16_history else "") + f"_d{D}")
+    tag = ("_bf16h" if args.bf16_history else "") + ("" if append else "_noappend")
+    tpath = args.traffic or os.path.join(ROOT, "profiles", f"ppk_decode_d{D}_b{B}_h{H}_ctx{L}{tag}_traffic.json")
+    traffic, traffic_source = committed_traffic(tpath, split=split, workload=f"B{B}H{H}D{D}L{L}", kernel=kname,
+                                                algorithmic_bytes_per_launch=kernel_bytes)
+    workload = ("BASELINE config 5: decode step = append of the current token + attention over the int8 history "
+                "(ppk_decode_step)" if append else
+                "BASELINE config 5 shape, uncommitted query: attention over the int8 history + the current token "
+                "from its copy, nothing appended (ppk_decode_attention)")
 
     result = {
         "metric": METRIC,
@@ -1246,9 +1248,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels, quantised on device; bf16 q and new K/V)",
-        "config": {"workload": "BASELINE config 5: decode step = append of the current token + attention over "
-                               "the int8 history (ppk_decode_step)",
+        "config": {"workload": workload,
                    "batch": B, "heads": H, "head_dim": D, "context": L, "capacity": cap, "kv": "int8 + f32 scales",
+                   "history": "bf16-rounded (PPK_ATTN_BF16_HISTORY)" if args.bf16_history else "fp32 dequantised",
                    "query": "bf16", "tokens_per_wave": split, "blocks_per_row": step.ngroups,
                    "launches_per_step": 1 if step.ngroups == 1 else 2},
         "median_us": round(median_us, 2),
@@ -1257,7 +1259,8 @@ def main() -> int:
         "step_hbm_frac": round(step_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": kernel_bytes,
+                     "traffic": traffic, "traffic_source": traffic_source,
+                     "algorithmic_bytes_per_launch": kernel_bytes,
                      "avg_launch_us": round(kernel_avg_ms * 1e3, 2), "launches": launches},
     }
     if not args.no_cpu_baseline:

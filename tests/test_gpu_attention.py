@@ -112,6 +112,29 @@ def test_config4_ragged_parallel_branches(device):
     assert_close(c.run(split=256), ref, what="config 4 split 256")
 
 
+@pytest.mark.parametrize("plan", ["auto", "per-row", "balanced", "device-lengths"])
+def test_config4_bench_lengths_decode_step(device, plan):
+    """BASELINE config 4 on the lengths bench.py --config 4 times (default_rng(SEED).integers(256, 4097, 8),
+    capacity max + 1, max_past = max): the fused decode step (append + attention) through the library's own
+    choice with the host lengths, each plan forced, and the device lengths alone; output against the oracle,
+    the appended slot bit-exact."""
+    lengths = [int(x) for x in np.random.default_rng(SEED).integers(256, 4097, size=8)]
+    L = max(lengths)
+    c = Case(device, 8, 16, 128, lengths, L + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16,
+             seed=SEED + 40)
+    host = None if plan == "device-lengths" else lengths
+    kw = {} if plan in ("auto", "device-lengths") else {"plan": plan}
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, max_past=L, past_host=host, **kw)
+    torch.cuda.synchronize()
+    got = out.float().reshape(c.rows, c.D).cpu().numpy()
+    assert_close(got, c.reference(), what=f"config 4 bench lengths, plan {plan}")
+    codes, scales, _ = oracle.quantize(c.sk32.reshape(c.rows, 1, c.D))
+    kc, ks = c.kc.cpu().numpy(), c.ks.cpu().numpy()
+    for r in range(c.rows):
+        p = lengths[r // c.H]
+        assert np.array_equal(kc[r, p], codes[r, 0]) and ks[r, p] == scales[r, 0], f"row {r}: appended slot {p}"
+
+
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_edge_lengths(device, d):
     """Empty history (output = sv exactly), one token, tile tails, full capacity, p > capacity (NaN)."""
