@@ -82,6 +82,15 @@ __device__ __forceinline__ float round_bf16(float x) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return __uint_as_float(u & 0xffff0000u);
 }
+// Two values rounded to bfloat16 (nearest even) by one v_cvt_pk_bf16_f32 and
+// widened back to fp32: for finite inputs the bits of round_bf16 on each.
+__device__ __forceinline__ void round_bf16_pair(float a, float b, float& ra, float& rb) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+  ra = __uint_as_float(u << 16);
+  rb = __uint_as_float(u & 0xffff0000u);
+}
 // f32 -> f16, round to nearest even, from a materialised f32 value: the empty
 // asm keeps the backend from folding a producing multiply into one fused
 // multiply-to-f16 (v_fma_mixlo_f16), which rounds once where the reference
@@ -624,7 +633,12 @@ __device__ __forceinline__ float score_batch(const u4 (&raw)[U], float scale_lan
 #pragma unroll
       for (int w = 0; w < 4; ++w)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) d = fmaf(qr[4 * w + k], round_bf16(sbyte(raw[u][w], k) * kscale), d);
+        for (int k = 0; k < 4; k += 2) {
+          float e0, e1;
+          round_bf16_pair(sbyte(raw[u][w], k) * kscale, sbyte(raw[u][w], k + 1) * kscale, e0, e1);
+          d = fmaf(qr[4 * w + k], e0, d);
+          d = fmaf(qr[4 * w + k + 1], e1, d);
+        }
       sc = group_sum<LPT>(d) * sl2;
     } else {
       int sh = 0, s1 = 0, s2 = 0, sl = 0;
@@ -670,7 +684,12 @@ __device__ __forceinline__ void accumulate_batch(const u4 (&raw)[U], float scale
 #pragma unroll
       for (int w = 0; w < 4; ++w)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc[4 * w + k] = fmaf(wgt, round_bf16(sbyte(raw[u][w], k) * vscale), acc[4 * w + k]);
+        for (int k = 0; k < 4; k += 2) {
+          float e0, e1;
+          round_bf16_pair(sbyte(raw[u][w], k) * vscale, sbyte(raw[u][w], k + 1) * vscale, e0, e1);
+          acc[4 * w + k] = fmaf(wgt, e0, acc[4 * w + k]);
+          acc[4 * w + k + 1] = fmaf(wgt, e1, acc[4 * w + k + 1]);
+        }
     } else {
 #pragma unroll
       for (int w = 0; w < 4; ++w)
@@ -1139,7 +1158,12 @@ __device__ __forceinline__ void online_pair(const u4 (&kraw)[4], const u4 (&vraw
 #pragma unroll
       for (int w = 0; w < 4; ++w)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) d = fmaf(qr[4 * w + k], round_bf16(sbyte(kraw[u][w], k) * kscale), d);
+        for (int k = 0; k < 4; k += 2) {
+          float e0, e1;
+          round_bf16_pair(sbyte(kraw[u][w], k) * kscale, sbyte(kraw[u][w], k + 1) * kscale, e0, e1);
+          d = fmaf(qr[4 * w + k], e0, d);
+          d = fmaf(qr[4 * w + k + 1], e1, d);
+        }
       sc = group_sum<LPT>(d) * sl2;
     } else {
       int sh = 0, s1 = 0, s2 = 0, slo = 0;
@@ -1170,7 +1194,12 @@ __device__ __forceinline__ void online_pair(const u4 (&kraw)[4], const u4 (&vraw
 #pragma unroll
       for (int w = 0; w < 4; ++w)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc[4 * w + k] = fmaf(pr, round_bf16(sbyte(vraw[u][w], k) * vscale), acc[4 * w + k]);
+        for (int k = 0; k < 4; k += 2) {
+          float e0, e1;
+          round_bf16_pair(sbyte(vraw[u][w], k) * vscale, sbyte(vraw[u][w], k + 1) * vscale, e0, e1);
+          acc[4 * w + k] = fmaf(pr, e0, acc[4 * w + k]);
+          acc[4 * w + k + 1] = fmaf(pr, e1, acc[4 * w + k + 1]);
+        }
     } else {
       const float wgt = pr * vscale;
 #pragma unroll
