@@ -154,6 +154,70 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// Sum over a wave's token groups (lanes that differ in the bits at and above
+// log2(LPT)) of each lane's N per-channel partial sums, scattered: one step
+// per token-group bit, from bit 5 down, in which the two lanes that differ in
+// that bit swap half of their values and add, so the values held halve each
+// step and lane l ends with N >> steps totals, of its chunk's channels
+// scatter_base<LPT, N>(l) + e, in acc[e]. Bits 5 and 4 use gfx950's lane
+// swaps (v_permlane32_swap, v_permlane16_swap), bit 3 a DPP rotate by 8
+// within a row, bit 2 one swizzle: VALU moves, where the butterfly over
+// every value (__shfl_xor per value and bit) took one LDS permute each, 64
+// per lane at D = 64 in every wave's epilogue.
+template <int LPT, int N>
+__device__ __forceinline__ int scatter_base(int lane) {
+  int base = 0, n = N;
+  if constexpr (LPT <= 32) { n >>= 1; base += ((lane >> 5) & 1) * n; }
+  if constexpr (LPT <= 16) { n >>= 1; base += ((lane >> 4) & 1) * n; }
+  if constexpr (LPT <= 8) { n >>= 1; base += ((lane >> 3) & 1) * n; }
+  if constexpr (LPT <= 4) { n >>= 1; base += ((lane >> 2) & 1) * n; }
+  return base;
+}
+template <int LPT, int N>
+__device__ __forceinline__ void reduce_scatter_groups(float (&acc)[N], int lane) {
+  if constexpr (LPT <= 32) {
+    static_assert(N % 2 == 0, "a value per lane half");
+    // Lanes 0-31 keep values [0, N/2), lanes 32-63 values [N/2, N).
+#pragma unroll
+    for (int k = 0; k < N / 2; ++k) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[k]), __float_as_uint(acc[N / 2 + k]),
+                                                     false, false);
+      acc[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  }
+  if constexpr (LPT <= 16) {
+    static_assert(N % 4 == 0, "a value per lane quarter");
+    // Even rows of 16 lanes keep [0, N/4), odd rows [N/4, N/2).
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[k]), __float_as_uint(acc[N / 4 + k]),
+                                                     false, false);
+      acc[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  }
+  if constexpr (LPT <= 8) {
+    static_assert(N % 8 == 0, "a value per lane eighth");
+    // Lanes i and i ^ 8 of a row: a rotate by 8 within the row pairs them.
+    const bool hi = ((lane >> 3) & 1) != 0;
+#pragma unroll
+    for (int k = 0; k < N / 8; ++k) {
+      const float keep = hi ? acc[N / 8 + k] : acc[k];
+      const float give = hi ? acc[k] : acc[N / 8 + k];
+      acc[k] = keep + dpp_f32<0x128>(give);  // row_ror:8
+    }
+  }
+  if constexpr (LPT <= 4) {
+    static_assert(N % 16 == 0, "a value per lane sixteenth");
+    const bool hi = ((lane >> 2) & 1) != 0;
+#pragma unroll
+    for (int k = 0; k < N / 16; ++k) {
+      const float keep = hi ? acc[N / 16 + k] : acc[k];
+      const float give = hi ? acc[k] : acc[N / 16 + k];
+      acc[k] = keep + __shfl_xor(give, 4);
+    }
+  }
+}
+
 // Largest |x| of a lane's values with f32::max / fmaxf semantics (NaNs of
 // either kind skipped); the result is >= +0 and never NaN. Written on the bit
 // patterns: the hardware float max quiets a signalling NaN and returns it,
@@ -348,7 +412,8 @@ __device__ __forceinline__ void dequantize_body(const ppk::DequantizeArgs& a) {
 struct WavePartial {
   float m;         // max log2-domain score (-inf if the wave had no tokens)
   float z;         // sum of 2^(s - m)
-  float acc[16];   // sum of 2^(s - m) * v over this lane's 16 channels (valid in lanes j == 0)
+  float acc[16];   // sum of 2^(s - m) * v: while streaming over this lane's 16 channels; at the end the wave's
+                   // totals of channels c * 16 + scatter_base<LPT, 16>(lane) + e in acc[e], e < D / 64
 };
 
 // One batch = U load tiles = U*TPL consecutive tokens of this wave's range.
@@ -780,11 +845,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
     accumulate_batch<D, BF16H, U>(va, vsa, 0, n, j, lane, m, s_lds, z, out.acc);
     if (two) accumulate_batch<D, BF16H, U>(vb2, vsb2, U, n, j, lane, m, s_lds, z, out.acc);
     z = wave_sum(z);
-#pragma unroll
-    for (int o = LPT; o < ppk::kWave; o <<= 1) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) out.acc[i] += __shfl_xor(out.acc[i], o);
-    }
+    reduce_scatter_groups<LPT, 16>(out.acc, lane);
     out.m = m;
     out.z = z;
     return;
@@ -865,11 +926,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
   }
   // Each token's p was added once, by its owning lane: sum over the wave.
   z = wave_sum(z);
-#pragma unroll
-  for (int o = LPT; o < ppk::kWave; o <<= 1) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) out.acc[i] += __shfl_xor(out.acc[i], o);
-  }
+  reduce_scatter_groups<LPT, 16>(out.acc, lane);
   out.m = m;
   out.z = z;
 }
@@ -958,11 +1015,10 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   constexpr int R = D + 4;
   __syncthreads();
   float* mrg = lds;
-  if (lane < LPT) {
-    f4* o = reinterpret_cast<f4*>(mrg + wave * R + 4 + c * 16);
+  {
+    const int ch = c * 16 + scatter_base<LPT, 16>(lane);
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
-      o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
+    for (int e = 0; e < EPL; ++e) mrg[wave * R + 4 + ch + e] = part.acc[e];
   }
   if (lane == 0) {
     mrg[wave * R] = part.m;
@@ -1273,11 +1329,8 @@ __device__ __forceinline__ void wave_attention_window(const ppk::DecodeArgs& a, 
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] *= w;
 #pragma unroll
-  for (int o = LPT; o < ppk::kWave; o <<= 1) {
-    z += __shfl_xor(z, o);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] += __shfl_xor(acc[i], o);
-  }
+  for (int o = LPT; o < ppk::kWave; o <<= 1) z += __shfl_xor(z, o);
+  reduce_scatter_groups<LPT, 16>(acc, lane);
   out.m = mm;
   out.z = z;
 #pragma unroll
@@ -1306,7 +1359,6 @@ __device__ __forceinline__ void decode_flat_body(const ppk::DecodeFlatArgs& fa) 
   const uint32_t W = blockDim.x >> 6;
   const uint32_t wid = blockIdx.x * W + (threadIdx.x >> 6);
   const int c = lane % LPT;
-  const int j = lane / LPT;
 
   // Append job (a decode step): wave q < 2 rows quantises tensor q & 1 of
   // row q >> 1 into slot past[b] (the device value) of the arenas. Its loads
@@ -1321,7 +1373,8 @@ __device__ __forceinline__ void decode_flat_body(const ppk::DecodeFlatArgs& fa) 
   }
   const bool work = wid < t.units_total;  // uniform per wave
   uint32_t b = 0, units = 1, len = 0, row = 0, slot = 0, t0 = 0, n = 0, pdev = 0;
-  float qr[16], kv[16], sv[16];
+  float qr[16], kv[16], sv[EPL];
+  const int ch = c * 16 + scatter_base<LPT, 16>(lane);  // this lane's output channels: ch .. ch + EPL - 1
   if (work) {
     b = flat_sequence(t, wid);
     units = t.units[b];
@@ -1336,7 +1389,7 @@ __device__ __forceinline__ void decode_flat_body(const ppk::DecodeFlatArgs& fa) 
     if (n > 0) load_vec<16>(a.q, size_t(row) * D + size_t(c) * 16, a.q_dtype, qr);
     if (units == 1) {  // the whole row: its current token too
       if (n > 0) load_vec<16>(a.sk, size_t(row) * D + size_t(c) * 16, a.scratch_dtype, kv);
-      load_vec<16>(a.sv, size_t(row) * D + size_t(c) * 16, a.scratch_dtype, sv);
+      load_vec<EPL>(a.sv, size_t(row) * D + size_t(ch), a.scratch_dtype, sv);
     }
   }
   auto commit = [&]() {
@@ -1377,20 +1430,15 @@ __device__ __forceinline__ void decode_flat_body(const ppk::DecodeFlatArgs& fa) 
     const float wp = n > 0 ? __builtin_amdgcn_exp2f(part.m - m) : 0.f;
     const float wc = n > 0 ? __builtin_amdgcn_exp2f(s_cur - m) : 1.f;
     const float zsum = n > 0 ? fmaf(wp, part.z, wc) : 1.f;
-    if (j == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float o = valid ? fmaf(wc, sv[i], n > 0 ? wp * part.acc[i] : 0.f) / zsum : __builtin_nanf("");
-        store_elem(a.out, size_t(row) * D + size_t(c) * 16 + i, a.out_dtype, o);
-      }
+    for (int e = 0; e < EPL; ++e) {
+      const float o = valid ? fmaf(wc, sv[e], n > 0 ? wp * part.acc[e] : 0.f) / zsum : __builtin_nanf("");
+      store_elem(a.out, size_t(row) * D + size_t(ch + e), a.out_dtype, o);
     }
   } else if (slot < a.ngroups) {  // always, by the host's count of slots
     const size_t rec = size_t(row) * a.ngroups + slot;
-    if (j == 0) {
-      f4* o = reinterpret_cast<f4*>(a.part_y + rec * D + size_t(c) * 16);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
-    }
+    for (int e = 0; e < EPL; ++e) a.part_y[rec * D + size_t(ch + e)] = part.acc[e];
     if (lane == 0) {
       a.part_mz[rec * 2] = part.m;
       a.part_mz[rec * 2 + 1] = part.z;
@@ -1544,7 +1592,9 @@ __device__ __forceinline__ void faccumulate_batch(const u4 (&raw)[U], uint32_t t
 template <int D, bool BF16KV>
 struct FloatWavePartial {
   float m, z;
-  float acc[FloatGeom<D, BF16KV>::kEpc];  // valid in the lanes of token slot j == 0
+  // While streaming: this lane's chunk; at the end the wave's totals of channels
+  // c * kEpc + scatter_base<kLpt, kEpc>(lane) + e in acc[e], e < D / 64.
+  float acc[FloatGeom<D, BF16KV>::kEpc];
 };
 
 // One wave streams n tokens of a row from `begin`: phase K scores into LDS,
@@ -1594,11 +1644,7 @@ __device__ __forceinline__ void fwave_attention(const ppk::FloatDecodeArgs& a, u
     faccumulate_batch<D, BF16KV, U>(rb, t0 + U, n, j, lane, m, s_lds, z, out.acc);
   }
   z = wave_sum(z);
-#pragma unroll
-  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) {
-#pragma unroll
-    for (int i = 0; i < G::kEpc; ++i) out.acc[i] += __shfl_xor(out.acc[i], o);
-  }
+  reduce_scatter_groups<G::kLpt, G::kEpc>(out.acc, lane);
   out.m = m;
   out.z = z;
 }
@@ -1640,7 +1686,8 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
   constexpr int EPL = D / ppk::kWave;
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Uniform: the wave's range, length and loop bounds stay in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int c = lane % G::kLpt;
   // Blocks are numbered group-major: consecutive blocks belong to different
@@ -1687,11 +1734,10 @@ __device__ __forceinline__ void fdecode_body(const ppk::FloatDecodeArgs& a) {
   constexpr int R = D + 4;
   __syncthreads();
   float* mrg = lds;
-  if (lane < G::kLpt) {
-    f4* o = reinterpret_cast<f4*>(mrg + wave * R + 4 + c * G::kEpc);
+  {
+    const int ch = c * G::kEpc + scatter_base<G::kLpt, G::kEpc>(lane);
 #pragma unroll
-    for (int w = 0; w < G::kEpc / 4; ++w)
-      o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
+    for (int e = 0; e < EPL; ++e) mrg[wave * R + 4 + ch + e] = part.acc[e];
   }
   if (lane == 0) {
     mrg[wave * R] = part.m;
@@ -1897,11 +1943,8 @@ __device__ __forceinline__ void fwave_attention_window(const ppk::FloatDecodeArg
 #pragma unroll
   for (int e = 0; e < G::kEpc; ++e) acc[e] *= w;
 #pragma unroll
-  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) {
-    z += __shfl_xor(z, o);
-#pragma unroll
-    for (int e = 0; e < G::kEpc; ++e) acc[e] += __shfl_xor(acc[e], o);
-  }
+  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) z += __shfl_xor(z, o);
+  reduce_scatter_groups<G::kLpt, G::kEpc>(acc, lane);
   out.m = mm;
   out.z = z;
 #pragma unroll
@@ -1937,8 +1980,9 @@ __device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs
     }
   }
   if (wid >= t.units_total) return;  // uniform per wave
+  constexpr int EPL = D / ppk::kWave;
   const int c = lane % G::kLpt;
-  const int j = lane / G::kLpt;
+  const int ch = c * G::kEpc + scatter_base<G::kLpt, G::kEpc>(lane);  // this lane's output channels
   const uint32_t b = flat_sequence(t, wid);
   const uint32_t units = t.units[b];
   const uint32_t len = t.len[b];
@@ -1952,17 +1996,16 @@ __device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs
   // The step's current token, folded by the wave of a one-unit row (longer
   // rows: by the merge), in this kernel's lane layout and token arithmetic.
   const bool cur = STEP && units == 1;
-  float qr[G::kEpc], kx[G::kEpc], vx[G::kEpc];
+  float qr[G::kEpc], kx[G::kEpc], vx[EPL];
   if (n > 0 || cur) load_vec<G::kEpc>(a.q, size_t(row) * a.q_stride + size_t(c) * G::kEpc, a.q_dtype, qr);
   if (cur) {
     load_vec<G::kEpc>(a.k_new, size_t(row) * D + size_t(c) * G::kEpc, a.new_dtype, kx);
-    load_vec<G::kEpc>(a.v_new, size_t(row) * D + size_t(c) * G::kEpc, a.new_dtype, vx);
+    load_vec<EPL>(a.v_new, size_t(row) * D + size_t(ch), a.new_dtype, vx);
     if constexpr (BF16KV) {
 #pragma unroll
-      for (int e = 0; e < G::kEpc; ++e) {
-        kx[e] = bf16_to_f32(f32_to_bf16_bits(kx[e]));
-        vx[e] = bf16_to_f32(f32_to_bf16_bits(vx[e]));
-      }
+      for (int e = 0; e < G::kEpc; ++e) kx[e] = bf16_to_f32(f32_to_bf16_bits(kx[e]));
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) vx[e] = bf16_to_f32(f32_to_bf16_bits(vx[e]));
     }
   }
   FloatWavePartial<D, BF16KV> part;
@@ -1990,24 +2033,18 @@ __device__ __forceinline__ void fdecode_flat_body(const ppk::FloatDecodeFlatArgs
     const float wc = __builtin_amdgcn_exp2f(s_cur - m2);
     part.z = fmaf(part.z, w1, wc);
 #pragma unroll
-    for (int e = 0; e < G::kEpc; ++e) part.acc[e] = fmaf(part.acc[e], w1, wc * vx[e]);
+    for (int e = 0; e < EPL; ++e) part.acc[e] = fmaf(part.acc[e], w1, wc * vx[e]);
   }
   if (units == 1) {
-    if (j == 0) {
 #pragma unroll
-      for (int e = 0; e < G::kEpc; ++e) {
-        const float o = (valid && part.z > 0.f) ? part.acc[e] / part.z : __builtin_nanf("");
-        store_elem(a.out, size_t(row) * D + size_t(c) * G::kEpc + e, a.out_dtype, o);
-      }
+    for (int e = 0; e < EPL; ++e) {
+      const float o = (valid && part.z > 0.f) ? part.acc[e] / part.z : __builtin_nanf("");
+      store_elem(a.out, size_t(row) * D + size_t(ch + e), a.out_dtype, o);
     }
   } else if (slot < a.ngroups) {  // always, by the host's count of slots
     const size_t rec = size_t(row) * a.ngroups + slot;
-    if (j == 0) {
-      f4* o = reinterpret_cast<f4*>(a.part_y + rec * D + size_t(c) * G::kEpc);
 #pragma unroll
-      for (int w = 0; w < G::kEpc / 4; ++w)
-        o[w] = f4{part.acc[4 * w], part.acc[4 * w + 1], part.acc[4 * w + 2], part.acc[4 * w + 3]};
-    }
+    for (int e = 0; e < EPL; ++e) a.part_y[rec * D + size_t(ch + e)] = part.acc[e];
     if (lane == 0) {
       a.part_mz[rec * 2] = part.m;
       a.part_mz[rec * 2 + 1] = part.z;
