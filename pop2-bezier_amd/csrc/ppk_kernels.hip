@@ -143,15 +143,48 @@ __device__ __forceinline__ int group_sum_i32(int x) {
   return x;
 }
 
+// Reductions over the whole wave, every lane receiving the result, without
+// LDS: DPP within rows of 16 lanes (quad swaps, half-row and row mirrors),
+// then gfx950's lane swaps across rows (v_permlane16_swap) and halves
+// (v_permlane32_swap); each swap of a value with itself hands every lane its
+// partner's value beside its own.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
+  x = op(x, dpp_f32<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = op(x, dpp_f32<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = op(x, dpp_f32<0x141>(x));  // row_half_mirror
+  x = op(x, dpp_f32<0x140>(x));  // row_mirror
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  return wave_reduce(x, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+  return wave_reduce(x, [](float a, float b) { return a + b; });
+}
+// The same over a wave's token groups only (lanes that differ in the bits at
+// and above log2(LPT)): each lane receives the reduction over the lanes of
+// its position within a token.
+template <int LPT, class Op>
+__device__ __forceinline__ float groups_reduce(float x, Op op) {
+  if constexpr (LPT <= 4) x = op(x, __shfl_xor(x, 4));
+  if constexpr (LPT <= 8) x = op(x, dpp_f32<0x128>(x));  // row_ror:8, lane i ^ 8 of a row
+  if constexpr (LPT <= 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  if constexpr (LPT <= 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
   return x;
+}
+template <int LPT>
+__device__ __forceinline__ float groups_max(float x) {
+  return groups_reduce<LPT>(x, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // Sum over a wave's token groups (lanes that differ in the bits at and above
@@ -839,8 +872,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
       mloc = score_batch<D, BF16H, U>(kb2, ksb2, U, n, j, c, qr, qi, sl2, s_lds, mloc);
     }
     float m = mloc, z = 0.f;
-#pragma unroll
-    for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = groups_max<LPT>(m);
     __builtin_amdgcn_wave_barrier();
     accumulate_batch<D, BF16H, U>(va, vsa, 0, n, j, lane, m, s_lds, z, out.acc);
     if (two) accumulate_batch<D, BF16H, U>(vb2, vsb2, U, n, j, lane, m, s_lds, z, out.acc);
@@ -876,8 +908,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
     mloc = score_batch<D, BF16H, U>(rr[0], rs[0], 0, n, j, c, qr, qi, sl2, s_lds, mloc);
     if (two) mloc = score_batch<D, BF16H, U>(rr[1], rs[1], U, n, j, c, qr, qi, sl2, s_lds, mloc);
     m = mloc;
-#pragma unroll
-    for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = groups_max<LPT>(m);
     __builtin_amdgcn_wave_barrier();
     accumulate_batch<D, BF16H, U>(va, vsa, 0, n, j, lane, m, s_lds, z, out.acc);
     if (two) accumulate_batch<D, BF16H, U>(vb2, vsb2, U, n, j, lane, m, s_lds, z, out.acc);
@@ -912,8 +943,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
       }
     }
     m = mloc;
-#pragma unroll
-    for (int o = LPT; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = groups_max<LPT>(m);
     __builtin_amdgcn_wave_barrier();
     for (uint32_t v0 = 0; v0 < nbp; v0 += NB) {
 #pragma unroll
@@ -1122,7 +1152,10 @@ __device__ __forceinline__ void combine_records(const float* mz, const float* py
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float wk = i + uint32_t(k) < cnt ? __shfl(w, int(i) + k) : 0.f;
+        // Record i + k's weight sits in that lane (a uniform index): one readlane, no LDS.
+        const float wk = i + uint32_t(k) < cnt
+                             ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), int(i) + k))
+                             : 0.f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) y[e] = fmaf(wk, v[k][e], y[e]);
       }
@@ -1322,14 +1355,12 @@ __device__ __forceinline__ void wave_attention_window(const ppk::DecodeArgs& a, 
   }
   // Join the token groups: common max, then sums across groups.
   float mm = m;
-#pragma unroll
-  for (int o = LPT; o < ppk::kWave; o <<= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+  mm = groups_max<LPT>(mm);
   const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
   z *= w;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] *= w;
-#pragma unroll
-  for (int o = LPT; o < ppk::kWave; o <<= 1) z += __shfl_xor(z, o);
+  z = groups_reduce<LPT>(z, [](float a, float b) { return a + b; });
   reduce_scatter_groups<LPT, 16>(acc, lane);
   out.m = mm;
   out.z = z;
@@ -1632,8 +1663,7 @@ __device__ __forceinline__ void fwave_attention(const ppk::FloatDecodeArgs& a, u
     mloc = fscore_batch<D, BF16KV, U>(rb, t0 + U, n, j, c, qr, sl2, s_lds, mloc);
   }
   float m = mloc;
-#pragma unroll
-  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  m = groups_max<G::kLpt>(m);
   __builtin_amdgcn_wave_barrier();
 
   float z = 0.f;
@@ -1936,14 +1966,12 @@ __device__ __forceinline__ void fwave_attention_window(const ppk::FloatDecodeArg
     }
   }
   float mm = m;
-#pragma unroll
-  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) mm = fmaxf(mm, __shfl_xor(mm, o));
+  mm = groups_max<G::kLpt>(mm);
   const float w = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
   z *= w;
 #pragma unroll
   for (int e = 0; e < G::kEpc; ++e) acc[e] *= w;
-#pragma unroll
-  for (int o = G::kLpt; o < ppk::kWave; o <<= 1) z += __shfl_xor(z, o);
+  z = groups_reduce<G::kLpt>(z, [](float a, float b) { return a + b; });
   reduce_scatter_groups<G::kLpt, G::kEpc>(acc, lane);
   out.m = mm;
   out.z = z;
