@@ -74,6 +74,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-append", action="store_true",
                    help="int8 config 5: time ppk_decode_attention alone (the uncommitted partial query: the current "
                         "token attended from its copy, nothing written to the arenas) instead of the fused step")
+    p.add_argument("--wave-clock", default=None, metavar="OUT.md",
+                   help="configs 1, 3, 4: after the timed runs, run --steps warm steps again on a context created "
+                        "from the wave-clock code object (ppk_kernels_clock.hsaco) and write the per-phase "
+                        "breakdown of every decode and merge launch to OUT.md (summary also in the JSON line)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0,
                    help="head rows timed for the CPU baseline (0 = every row of the step)")
@@ -102,6 +106,128 @@ def committed_traffic(tpath: str, **match) -> tuple[int | None, str | None]:
         return None, None
     return t.get("hbm_bytes_per_launch"), (os.path.relpath(tpath, ROOT) + ": rocprofv3 FETCH_SIZE + WRITE_SIZE of "
                                           "a separate profiled run of this workload, scaled by a copy kernel")
+
+
+WAVE_CLOCK_HZ = 100e6  # the real-time clock the wave-clock build reads (s_memrealtime)
+DECODE_POINTS = ("entry", "loads issued", "past[b] here", "first K data here", "stream done", "block joined",
+                 "output stored")
+
+
+def wave_clock_run(steps_fn, calls, steps: int, dev) -> tuple[dict, str]:
+    """Run `steps_fn` `steps` times with every prepared call in `calls` on a context made from the wave-clock
+    code object, read the records (layout in pop2-bezier_amd/csrc/ppk_kernel_args.h) and summarise them:
+    per decode launch the intervals between a wave's clock points and the launch's dispatch spread and span,
+    per merge launch entry -> records combined -> stored, and the gaps between consecutive launches."""
+    import ctypes
+    import statistics
+
+    import torch
+    from ppk import _abi
+
+    lib = _abi.lib()
+    path = os.path.join(ROOT, "pop2-bezier_amd", "ppk", "ppk_kernels_clock.hsaco")
+    ctx = ctypes.c_void_p()
+    _abi.check(lib.ppk_context_create(dev.index or 0, path.encode(), ctypes.byref(ctx)), "ppk_context_create")
+    # Slots per launch and kernel kind: the most waves of any decode launch, or rows of a merge launch.
+    per = max(max(c.plan_info["blocks"] * c.plan_info["waves_per_block"],
+                  c.args.attn.rows if hasattr(c.args, "attn") else c.args.rows) for c in calls)
+    nrec = per * 2 * len(calls) * steps
+    buf = torch.zeros(16 * (nrec + 1), dtype=torch.int64, device=dev)
+    buf[0], buf[1] = per, nrec
+    saved = [c.ctx for c in calls]
+    try:
+        for c in calls:
+            c.ctx = ctx
+        for _ in range(3):  # warm: code object, caches (no clock yet)
+            steps_fn()
+        torch.cuda.synchronize()
+        _abi.check(lib.ppk_context_set_wave_clock(ctx, ctypes.c_void_p(buf.data_ptr()), buf.numel() * 8),
+                   "ppk_context_set_wave_clock")
+        for _ in range(steps):
+            steps_fn()
+        torch.cuda.synchronize()
+        rec = buf[16:].view(-1, 16).cpu().numpy().view("uint64")
+        rec = rec[rec[:, 0] != 0]  # slots never written (fewer waves than the slot count)
+        _abi.check(lib.ppk_context_set_wave_clock(ctx, None, 0), "ppk_context_set_wave_clock")
+    finally:
+        for c, old in zip(calls, saved):
+            c.ctx = old
+        torch.cuda.synchronize()
+        lib.ppk_context_release(ctx)
+    us = 1e6 / WAVE_CLOCK_HZ
+    kind = (rec[:, 0] >> 56).astype(int)
+    seq = ((rec[:, 0] >> 32) & 0xFFFFFF).astype(int)
+    wave = (rec[:, 0] & 0xFF).astype(int)
+    t = rec[:, 2:10].astype("int64")
+    launches = {}
+    for i in range(len(rec)):
+        launches.setdefault((int(seq[i]), int(kind[i])), []).append(i)
+
+    def med(xs):
+        return round(statistics.median(xs), 2) if xs else None
+
+    def p90(xs):
+        return round(sorted(xs)[int(0.9 * (len(xs) - 1))], 2) if xs else None
+
+    iv = {k: [] for k in ("entry -> loads issued", "entry -> past[b] here", "entry -> first K data here",
+                          "first K data -> stream done", "stream done -> block joined",
+                          "block joined -> output stored (wave 0)")}
+    d_spread, d_span, m_span, m_comb, m_store, gap_dm, gap_md, layer = [], [], [], [], [], [], [], []
+    seqs = sorted({s_ for s_, k_ in launches})
+    for s_ in seqs:
+        d = launches.get((s_, 1), [])
+        m = launches.get((s_, 2), [])
+        if not d:
+            continue
+        te = t[d, 0]
+        ends = [int(t[i, 6] if wave[i] == 0 else t[i, 5]) for i in d]
+        d_spread.append((te.max() - te.min()) * us)
+        d_span.append((max(ends) - te.min()) * us)
+        for i in d:
+            iv["entry -> loads issued"].append((t[i, 1] - t[i, 0]) * us)
+            iv["entry -> past[b] here"].append((t[i, 2] - t[i, 0]) * us)
+            if t[i, 3]:
+                iv["entry -> first K data here"].append((t[i, 3] - t[i, 0]) * us)
+                iv["first K data -> stream done"].append((t[i, 4] - t[i, 3]) * us)
+            iv["stream done -> block joined"].append((t[i, 5] - t[i, 4]) * us)
+            if wave[i] == 0:
+                iv["block joined -> output stored (wave 0)"].append((t[i, 6] - t[i, 5]) * us)
+        end = max(ends)
+        if m:
+            me = t[m, 0]
+            m_span.append((t[m, 2].max() - me.min()) * us)
+            m_comb += [(t[i, 1] - t[i, 0]) * us for i in m]
+            m_store += [(t[i, 2] - t[i, 1]) * us for i in m]
+            gap_dm.append((me.min() - end) * us)
+            end = int(t[m, 2].max())
+        layer.append((end - te.min()) * us)
+        nxt = launches.get((s_ + 1, 1), [])
+        if nxt:
+            gap_md.append((t[nxt, 0].min() - end) * us)
+    summary = {
+        "launches": len(d_span), "records": int(len(rec)), "clock_hz": WAVE_CLOCK_HZ,
+        "decode_wave_intervals_us_median": {k: med(v) for k, v in iv.items()},
+        "decode_wave_intervals_us_p90": {k: p90(v) for k, v in iv.items()},
+        "decode_dispatch_spread_us": med(d_spread), "decode_span_us": med(d_span),
+        "merge_span_us": med(m_span), "merge_entry_to_combined_us": med(m_comb),
+        "merge_combined_to_stored_us": med(m_store),
+        "gap_decode_end_to_merge_start_us": med(gap_dm), "gap_merge_end_to_next_decode_start_us": med(gap_md),
+        "layer_first_entry_to_last_store_us": med(layer),
+    }
+    md = ["| decode wave (every wave of every launch) | median µs | p90 µs |", "|---|---|---|"]
+    md += [f"| {k} | {summary['decode_wave_intervals_us_median'][k]} | {summary['decode_wave_intervals_us_p90'][k]} |"
+           for k in iv]
+    md += ["", "| per launch (median over launches) | µs |", "|---|---|",
+           f"| decode: first wave entry -> last wave entry (dispatch spread) | {summary['decode_dispatch_spread_us']} |",
+           f"| decode: first wave entry -> last wave's store (span seen by the waves) | {summary['decode_span_us']} |",
+           f"| gap: decode's last store -> merge's first wave entry | {summary['gap_decode_end_to_merge_start_us']} |",
+           f"| merge: entry -> records combined (per wave) | {summary['merge_entry_to_combined_us']} |",
+           f"| merge: records combined -> output stored (per wave) | {summary['merge_combined_to_stored_us']} |",
+           f"| merge: first wave entry -> last store | {summary['merge_span_us']} |",
+           f"| gap: merge's last store -> next decode's first wave entry | "
+           f"{summary['gap_merge_end_to_next_decode_start_us']} |",
+           f"| layer: decode's first wave entry -> merge's last store | {summary['layer_first_entry_to_last_store_us']} |"]
+    return summary, "\n".join(md)
 
 
 def _host_cpus() -> int:
@@ -837,6 +963,21 @@ def bench_config(args) -> int:
                      "avg_launch_us": round(kernel_avg_us, 2), "launches": launches,
                      "merge_avg_launch_us": round(merge_ms / m_launches * 1e3, 2) if m_launches else None},
     }
+    if args.wave_clock:
+        print("# bench: wave clock", file=sys.stderr, flush=True)
+        summary, md = wave_clock_run(lambda: warm(0), steps[0], min(args.steps, 10), dev)
+        result["wave_clock"] = summary
+        cmd = "python3 bench.py " + " ".join(sys.argv[1:])
+        with open(args.wave_clock, "w") as f:
+            f.write(f"# Wave clock: BASELINE config {args.config} ({cfg['workload']})\n\n"
+                    f"Command (from the repository root):\n\n    {cmd}\n\n"
+                    f"{min(args.steps, 10)} warm steps ({summary['launches']} decode launches, "
+                    f"{summary['records']} wave records) on a context made from "
+                    "pop2-bezier_amd/ppk/ppk_kernels_clock.hsaco (the library's kernels built with "
+                    "-DPPK_WAVE_CLOCK: each wave reads the 100 MHz real-time clock at fixed points and writes "
+                    "one record to a slot of its own; layout in pop2-bezier_amd/csrc/ppk_kernel_args.h). A point "
+                    "\"x here\" waits for "
+                    "x first. Per-layer decode + merge launches, one stream, as the timed steps.\n\n" + md + "\n")
     if not args.no_cpu_baseline:
         print("# bench: cpu baseline", file=sys.stderr, flush=True)
         a = (q[0], kc[0, 0], vc[0, 0], ks[0, 0], vs[0, 0], kn[0], vn[0], past, H, args)

@@ -590,6 +590,19 @@ enum { PPK_KERNEL_QUANTIZE = 0, PPK_KERNEL_APPEND = 1, PPK_KERNEL_DEQUANTIZE = 2
 PPK_API int32_t ppk_context_set_profiling(ppk_context* ctx, int32_t enable);
 PPK_API int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint64_t* launches,
                                  double* total_ms, uint32_t reset);
+/* Wave-clock diagnostics (no counterpart in the reference). A context created
+   with the diagnostics code object (ppk_kernels_clock.hsaco beside the
+   library, built from the same sources with PPK_WAVE_CLOCK) makes every wave
+   of the int8 per-row decode and merge kernels append a record of its
+   real-time clock at fixed points (entry, first loads issued, past[b] here,
+   first K data here, stream done, block joined, output stored) to `buffer`:
+   16 u64 words per record at a slot of its own, u64 word 0 the slots per
+   launch and kernel kind, word 1 the most records the buffer holds (both set
+   by the caller), records from word 16 (layout in
+   pop2-bezier_amd/csrc/ppk_kernel_args.h). Each call starts the launch
+   sequence numbers at 0. buffer NULL stops it; the library's own code object
+   ignores it. */
+PPK_API int32_t ppk_context_set_wave_clock(ppk_context* ctx, void* buffer, uint64_t bytes);
 
 #ifdef __cplusplus
 }

@@ -424,6 +424,7 @@ extern "C" {
     pub fn ppk_prepare(ctx: *mut ppk_context) -> i32;
     pub fn ppk_prepare_int8_kv(ctx: *mut ppk_context, requested: u32, head_dim: u32, out: *mut PpkInt8KvStatus) -> i32;
     pub fn ppk_context_set_profiling(ctx: *mut ppk_context, enable: i32) -> i32;
+    pub fn ppk_context_set_wave_clock(ctx: *mut ppk_context, buffer: *mut c_void, bytes: u64) -> i32;
     pub fn ppk_context_kernel_stats(
         ctx: *mut ppk_context,
         kernel: u32,

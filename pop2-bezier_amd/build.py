@@ -2,6 +2,7 @@
 
 Outputs (next to the Python package, git-ignored, shipped with the tree):
   ppk/ppk_kernels.hsaco  gfx950 code object with every kernel (hipcc --genco)
+  ppk/ppk_kernels_clock.hsaco  the same kernels with the wave-clock diagnostics (-DPPK_WAVE_CLOCK)
   ppk/libppk.so          C-ABI shim + int8_kv_ops host mirror (include/ppk_int8_kv.h), with
                          the no-alloc entry point's device scratch array (csrc/ppk_scratch.hip,
                          compiled by hipcc for gfx950 and linked in)
@@ -44,14 +45,23 @@ def _run(cmd: list[str], verbose: bool) -> None:
 def build(verbose: bool = True) -> dict:
     os.makedirs(OUT, exist_ok=True)
     hsaco = os.path.join(OUT, "ppk_kernels.hsaco")
+    clock = os.path.join(OUT, "ppk_kernels_clock.hsaco")
     lib = os.path.join(OUT, "libppk.so")
     tmp_hsaco = hsaco + f".tmp{os.getpid()}"
+    tmp_clock = clock + f".tmp{os.getpid()}"
     tmp_lib = lib + f".tmp{os.getpid()}"
     tmp_obj = os.path.join(OUT, f"ppk_scratch.o.tmp{os.getpid()}")
     try:
         _run(
             [HIPCC, "--genco", f"--offload-arch={ARCH}", *DEVICE_FLAGS, os.path.join(CSRC, "ppk_kernels.hip"), "-o",
              tmp_hsaco],
+            verbose,
+        )
+        # The same kernels with the wave-clock diagnostics compiled in, for a
+        # context created with this code object (bench.py --wave-clock).
+        _run(
+            [HIPCC, "--genco", f"--offload-arch={ARCH}", *DEVICE_FLAGS, "-DPPK_WAVE_CLOCK",
+             os.path.join(CSRC, "ppk_kernels.hip"), "-o", tmp_clock],
             verbose,
         )
         # The device scratch array of the no-alloc entry point lives in the
@@ -74,12 +84,13 @@ def build(verbose: bool = True) -> dict:
         )
         # Both outputs replace the previous build together, only once both compiled.
         os.replace(tmp_hsaco, hsaco)
+        os.replace(tmp_clock, clock)
         os.replace(tmp_lib, lib)
     finally:
-        for t in (tmp_hsaco, tmp_lib, tmp_obj):
+        for t in (tmp_hsaco, tmp_clock, tmp_lib, tmp_obj):
             if os.path.exists(t):
                 os.remove(t)
-    return {"hsaco": hsaco, "lib": lib}
+    return {"hsaco": hsaco, "clock_hsaco": clock, "lib": lib}
 
 
 if __name__ == "__main__":

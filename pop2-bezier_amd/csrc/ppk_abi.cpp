@@ -149,7 +149,7 @@ DeviceGuard::~DeviceGuard() {
 }
 
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
-                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim) {
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, uint32_t min_split) {
   AttentionPlan plan;
   plan.head_dim = head_dim;
   uint32_t split;
@@ -183,7 +183,7 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     const uint64_t share = ((span + waves - 1) / waves + tpl - 1) / tpl * tpl;
     split = uint32_t(std::min<uint64_t>(split, std::max<uint64_t>(share, tpl)));
   }
-  const uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
+  uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
   // Up to 16 waves per block; one float of LDS per history token of the block.
   uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
   const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
@@ -198,6 +198,22 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     const uint64_t wave_bytes = uint64_t(split) * token_bytes;
     uint64_t w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / wave_bytes));
     while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) --w;
+    // Blocks of fewer than four waves leave SIMDs of their CU idle while the
+    // waves work through their tokens (config 3: one 2-wave block of 64-token
+    // waves per CU, 1.56 us of arithmetic per wave after its data arrived).
+    // Halve the waves' share, down to min_split tokens and within the wave
+    // budget, so that each block gets four: config 3 at D = 128, 32-token
+    // waves in 4-wave blocks, 218.0 -> 194.9 us per 24-layer step in a
+    // same-box A/B.
+    const uint64_t budget = cus * 8;
+    while (w < 4 && min_split && split / 2 >= min_split && split % 2 == 0 && (split / 2) % tpl == 0 &&
+           rows * ((span + split / 2 - 1) / (split / 2)) <= budget) {
+      split /= 2;
+      waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
+      max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
+      w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / (uint64_t(split) * token_bytes)));
+      while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) --w;
+    }
     max_waves = w;
   }
   plan.split = split;
@@ -253,7 +269,9 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   // holds; a device length beyond that coverage (a stale host copy) gives
   // NaN rows and PPK_FLAG_STALE_LENGTHS in a decode step.
   const uint64_t cover = host && !(a.flags & kPlanFlags) ? row_cover(host, a.rows / a.heads, limit) : span;
-  AttentionPlan plan = plan_rows(ctx, a.rows, cover, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim);
+  // The int8 waves' shortest share: one batch (four load tiles).
+  AttentionPlan plan =
+      plan_rows(ctx, a.rows, cover, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim, 4 * tpl);
   // With the host's lengths of a ragged batch, the balanced plan gives every
   // wave the same share of the live history; balanced_pays picks between the
   // two plans from a timing model of both.
@@ -638,6 +656,11 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
   d.scale_log2 = scale_log2;
   d.speculate = plan.speculate ? 1u : 0u;
   d.span = plan.span;
+  if (ctx && ctx->wave_clock) {
+    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
+    d.clock = ctx->wave_clock;
+    d.clock_seq = ctx->wave_clock_seq++;
+  }
 
   const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
   const bool traceable = scratch == nullptr;
@@ -698,6 +721,8 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
     m.scratch_dtype = a.scratch_dtype;
     m.out_dtype = a.out_dtype;
     m.scale_log2 = scale_log2;
+    m.clock = d.clock;
+    m.clock_seq = d.clock_seq;
     launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMerge64 + di), a.rows, 64, 0, stream, m, 1, traceable);
   }
 }
@@ -744,7 +769,7 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   // gives NaN rows (and PPK_FLAG_STALE_LENGTHS in a decode step).
   const uint64_t cover = host && !(a.flags & kPlanFlags) ? row_cover(host, batch, span) : span;
   AttentionPlan plan =
-      plan_rows(ctx, a.rows, cover, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim);
+      plan_rows(ctx, a.rows, cover, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim, 0);
   // With the host's copy of the lengths, a ragged batch takes the balanced
   // plan (the int8 path's table) when its longest row holds more than
   // 512 KiB of K and V and the per-row plan's waves are uneven (the most
@@ -1371,6 +1396,18 @@ int32_t ppk_prepare_int8_kv(ppk_context* ctx, uint32_t requested, uint32_t head_
     text(out->format, sizeof(out->format), "INT8 symmetric per-token/head + FP32 scales");
     text(out->reason, sizeof(out->reason),
          "committed history is int8; the current K/V stay floating; attention dequantises on read");
+  });
+}
+
+int32_t ppk_context_set_wave_clock(ppk_context* ctx, void* buffer, uint64_t bytes) {
+  return call([&] {
+    ppk::require(ctx != nullptr, "ppk_context_set_wave_clock: null context");
+    ppk::require(buffer == nullptr || (bytes >= 2 * ppk::kWaveClockWords * 8 &&
+                                       reinterpret_cast<uintptr_t>(buffer) % 16 == 0),
+                 "ppk_context_set_wave_clock: buffer must be 16-byte aligned and hold at least one record");
+    std::lock_guard<std::mutex> lock(ctx->prof_mutex);
+    ctx->wave_clock = static_cast<uint64_t*>(buffer);
+    ctx->wave_clock_seq = 0;
   });
 }
 

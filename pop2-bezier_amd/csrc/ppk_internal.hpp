@@ -136,6 +136,8 @@ struct ppk_context {
 
   std::mutex prof_mutex;
   bool profiling = false;
+  uint64_t* wave_clock = nullptr;   // ppk_context_set_wave_clock
+  uint32_t wave_clock_seq = 0;
   std::vector<ppk::EventPair> pending[PPK_KERNEL_COUNT];
   std::vector<ppk::EventPair> pool;
   uint64_t launches[PPK_KERNEL_COUNT] = {};
@@ -180,8 +182,10 @@ struct AttentionPlan {
 };
 // Split policy shared by both attention paths: span history tokens per row,
 // tpl tokens per wave-wide load, token_bytes of K+V (+scales) per token.
+// min_split > 0: in the few-long-rows case, waves' shares may be halved down to
+// min_split tokens so that blocks get four waves (0: never).
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
-                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim);
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, uint32_t min_split);
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
 // The balanced plan of `rows` rows, `heads` per sequence, from the host
 // lengths host[0 .. rows / heads) (at most 64 sequences); a length above

@@ -52,6 +52,24 @@ struct DequantizeArgs {
   uint32_t pad;
 };
 
+// Wave-clock diagnostics (code objects built with PPK_WAVE_CLOCK; the
+// library's own code object never reads these fields): when `clock` is set,
+// every wave of the int8 per-row decode and merge kernels writes one record
+// of kWaveClockWords u64 at a slot of its own: word 0 of the buffer holds
+// the slots per launch and kernel kind (at least blocks x waves per block),
+// word 1 the most records the buffer takes; wave w of block x of the launch
+// with sequence number s writes record (2 s + kind - 1) * word0 + x * waves +
+// w, records from word kWaveClockWords (no atomics: a shared counter would
+// serialise every wave's end). Record: [0] kind << 56 | launch sequence <<
+// 32 | block << 8 | wave (0 for a slot never written), [1] XCC id << 32 |
+// HW_ID register, [2 + i] the wave's real-time clock (100 MHz) at point i of
+// its kind (kWaveClockPoints).
+constexpr int kWaveClockWords = 16;
+constexpr int kWaveClockPoints = 8;
+constexpr uint32_t kWaveClockDecode = 1;  // 0 entry, 1 first loads issued, 2 past[b] here, 3 first K data here,
+                                          // 4 stream done, 5 block joined, 6 output / record stored
+constexpr uint32_t kWaveClockMerge = 2;   // 0 entry, 1 records combined, 2 output stored
+
 // Decode attention: block (group g, row r), blockIdx.x = g * rows + r, of
 // W = blockDim.x / 64 waves covers history tokens [g*W*S, (g+1)*W*S) of row r,
 // S = split_tokens per wave.
@@ -82,6 +100,8 @@ struct DecodeArgs {
   uint32_t span;            // max_past or capacity: balanced plan, rows with past[b] > span give NaN; per-row
                             // plan, a past[b] <= span past the plan's coverage flags stale host lengths
   uint32_t speculate;       // per-row plan: request each wave's first K batches before past[] arrives
+  uint32_t clock_seq;       // wave-clock builds only: the launch's sequence number in the records
+  uint64_t* clock;          // wave-clock builds only (kWaveClock*): record buffer, or null
 };
 
 struct MergeArgs {
@@ -96,6 +116,8 @@ struct MergeArgs {
   uint32_t q_dtype, scratch_dtype, out_dtype;
   float scale_log2;
   uint32_t span;            // rows with past[b] > span give NaN (balanced plan)
+  uint32_t clock_seq;       // wave-clock builds only, as in DecodeArgs
+  uint64_t* clock;
 };
 
 // Balanced work list of a ragged batch (the ppk_decode_flat kernels), built

@@ -30,6 +30,47 @@
 
 namespace {
 
+#ifdef PPK_WAVE_CLOCK
+// Wave-clock diagnostics build (ppk_kernels_clock.hsaco, -DPPK_WAVE_CLOCK):
+// the real-time clock at fixed points of a wave, kept in scalar registers and
+// appended as one record at the wave's end (layout in ppk_kernel_args.h). A
+// point "after x" first makes the wave wait for x (an empty asm that reads
+// it), then reads the clock.
+#define PPK_CLK_DECL uint64_t clk_[ppk::kWaveClockPoints] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define PPK_CLK(i) (clk_[i] = __builtin_amdgcn_s_memrealtime())
+#define PPK_CLK_AFTER(i, dep)           \
+  do {                                  \
+    __asm__ volatile("" ::"v"(dep));    \
+    PPK_CLK(i);                         \
+  } while (0)
+#define PPK_CLK_AT(var, dep)            \
+  do {                                  \
+    __asm__ volatile("" ::"v"(dep));    \
+    (var) = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define PPK_CLK_RECORD(args, kind, block, wave) clock_record(args.clock, args.clock_seq, kind, block, wave, clk_)
+__device__ __forceinline__ void clock_record(uint64_t* clock, uint32_t seq, uint32_t kind, uint32_t block,
+                                             uint32_t wave, const uint64_t (&t)[ppk::kWaveClockPoints]) {
+  if (!clock || (threadIdx.x & 63) != 0) return;
+  const uint64_t per = clock[0], local = uint64_t(block) * (blockDim.x >> 6) + wave;
+  const uint64_t slot = (uint64_t(seq) * 2 + kind - 1) * per + local;
+  if (local >= per || slot >= clock[1]) return;
+  uint64_t* r = clock + ppk::kWaveClockWords * (slot + 1);
+  const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_ID
+  const uint32_t xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);  // XCC_ID
+  r[0] = (uint64_t(kind) << 56) | (uint64_t(seq) << 32) | (uint64_t(block) << 8) | wave;
+  r[1] = (uint64_t(xcc) << 32) | hw;
+#pragma unroll
+  for (int i = 0; i < ppk::kWaveClockPoints; ++i) r[2 + i] = t[i];
+}
+#else
+#define PPK_CLK_DECL
+#define PPK_CLK(i)
+#define PPK_CLK_AFTER(i, dep)
+#define PPK_CLK_AT(var, dep)
+#define PPK_CLK_RECORD(args, kind, block, wave)
+#endif
+
 using u2 = uint32_t __attribute__((ext_vector_type(2)));
 using u4 = uint32_t __attribute__((ext_vector_type(4)));
 using f4 = float __attribute__((ext_vector_type(4)));
@@ -447,6 +488,9 @@ struct WavePartial {
   float z;         // sum of 2^(s - m)
   float acc[16];   // sum of 2^(s - m) * v: while streaming over this lane's 16 channels; at the end the wave's
                    // totals of channels c * 16 + scatter_base<LPT, 16>(lane) + e in acc[e], e < D / 64
+#ifdef PPK_WAVE_CLOCK
+  uint64_t t_first = 0;  // the clock when the stream's first K data had arrived
+#endif
 };
 
 // One batch = U load tiles = U*TPL consecutive tokens of this wave's range.
@@ -861,6 +905,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
       sl2 *= qi.unscale;
     }
     if (n == 0) return;  // uniform per wave
+    PPK_CLK_AT(out.t_first, ka[0][0]);
     const uint32_t tl = uint32_t(lane % (U * TPL));
     ksa = tl < n ? ksa : 0.f;
     vsa = tl < n ? vsa : 0.f;
@@ -905,6 +950,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
       qi = quantize_query<LPT>(qr);
       sl2 *= qi.unscale;
     }
+    PPK_CLK_AT(out.t_first, rr[0][0][0]);
     mloc = score_batch<D, BF16H, U>(rr[0], rs[0], 0, n, j, c, qr, qi, sl2, s_lds, mloc);
     if (two) mloc = score_batch<D, BF16H, U>(rr[1], rs[1], U, n, j, c, qr, qi, sl2, s_lds, mloc);
     m = mloc;
@@ -931,6 +977,7 @@ __device__ __forceinline__ void wave_attention(const ppk::DecodeArgs& a, uint32_
       qi = quantize_query<LPT>(qr);
       sl2 *= qi.unscale;
     }
+    PPK_CLK_AT(out.t_first, rr[0][0][0]);
     for (uint32_t k0 = 0; k0 < nbp; k0 += NB) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
@@ -965,6 +1012,8 @@ template <int D, bool BF16H, int NB>
 __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
   constexpr int LPT = D / 16;
   constexpr int EPL = D / ppk::kWave;
+  PPK_CLK_DECL;
+  PPK_CLK(0);
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
   // The wave index is uniform: in a scalar register, every quantity derived
@@ -1023,6 +1072,7 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
     for (int b = 0; b < NB; ++b)
       load_batch<D, 4>(a.k + tok0 * D + size_t(c) * 16, a.ks + tok0, uint32_t(b) * 4, nspec, j, lane, rr[b], rs[b]);
   }
+  PPK_CLK(1);
   // A length within the caller's span that the plan does not cover: the plan
   // was sized from a stale host copy of the lengths (the row gives NaN).
   if (kw && lane == 0 && a.flags && p <= a.capacity && p <= a.span && uint64_t(p) > cover) atomicOr(a.flags, 4u);
@@ -1036,9 +1086,14 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
     }
   }
   if (final_out && wave == 0) s_cur = current_score<D>(a, kv, qr);
+  PPK_CLK_AFTER(2, p);
   const uint32_t n = (valid && begin < p) ? min(S, p - begin) : 0u;
   WavePartial part;
   wave_attention<D, BF16H, NB>(a, row, begin, n, nspec, qr, lds + size_t(wave) * S, lane, part, pre, rr, rs);
+  PPK_CLK(4);
+#ifdef PPK_WAVE_CLOCK
+  clk_[3] = part.t_first;
+#endif
 
   // Combine the block's waves through LDS (the staging area is reused).
   // Record of wave w at mrg + w * R: m, z, 2 pad floats, y[D] (16-byte aligned).
@@ -1055,7 +1110,11 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
     mrg[wave * R + 1] = part.z;
   }
   __syncthreads();
-  if (wave != 0) return;
+  PPK_CLK(5);
+  if (wave != 0) {
+    PPK_CLK_RECORD(a, ppk::kWaveClockDecode, blockIdx.x, uint32_t(wave));
+    return;
+  }
 
   float m = s_cur;
   for (int w = 0; w < W; ++w) m = fmaxf(m, mrg[w * R]);
@@ -1085,6 +1144,8 @@ __device__ __forceinline__ void decode_body(const ppk::DecodeArgs& a) {
       a.part_mz[rec * 2 + 1] = zsum;
     }
   }
+  PPK_CLK(6);
+  PPK_CLK_RECORD(a, ppk::kWaveClockDecode, blockIdx.x, 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -1167,6 +1228,8 @@ __device__ __forceinline__ void combine_records(const float* mz, const float* py
 template <int D>
 __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   constexpr int EPL = D / ppk::kWave;
+  PPK_CLK_DECL;
+  PPK_CLK(0);
   const int lane = threadIdx.x;
   const uint32_t row = blockIdx.x;
 
@@ -1188,6 +1251,7 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
   float m, zsum, y[EPL];
   combine_records<D>(a.part_mz + size_t(row) * a.nsplits * 2, a.part_y + size_t(row) * a.nsplits * D, a.nsplits,
                      lane, current, m, zsum, y);
+  PPK_CLK_AFTER(1, y[0]);
   // The row's length is first needed here: read after the records went out
   // (deciding validity up front would hold every record load back by the
   // length's round trip).
@@ -1200,6 +1264,8 @@ __device__ __forceinline__ void attn_merge_body(const ppk::MergeArgs& a) {
     const float o = valid ? fmaf(wc, sv[e], y[e]) / zsum : __builtin_nanf("");
     store_elem(a.out, base + e, a.out_dtype, o);
   }
+  PPK_CLK(2);
+  PPK_CLK_RECORD(a, ppk::kWaveClockMerge, blockIdx.x, 0u);
 }
 
 // ---------------------------------------------------------------------------

@@ -159,6 +159,7 @@ FUNCTIONS = {
     "ppk_prepare": (ctypes.c_int32, [_ptr]),
     "ppk_prepare_int8_kv": (ctypes.c_int32, [_ptr, _u32, _u32, ctypes.POINTER(PpkInt8KvStatus)]),
     "ppk_context_set_profiling": (ctypes.c_int32, [_ptr, ctypes.c_int32]),
+    "ppk_context_set_wave_clock": (ctypes.c_int32, [_ptr, _ptr, _u64]),
     "ppk_context_kernel_stats": (ctypes.c_int32, [_ptr, _u32, ctypes.POINTER(_u64), ctypes.POINTER(ctypes.c_double),
                                                   _u32]),
 }

@@ -20,7 +20,7 @@ import torch
 
 from . import _abi
 from ._abi import check, lib
-from .int8_kv_ops import _DTYPES, _HEAD_DIMS, _require, _stream, context
+from .int8_kv_ops import _DTYPES, _HEAD_DIMS, _require, _stream, context, current_stream_handle
 
 _KV_DTYPES = {torch.bfloat16: _abi.PPK_BF16, torch.float32: _abi.PPK_F32}
 
@@ -201,8 +201,8 @@ class FloatDecodeAttention:
         _replan(self, self.args, lengths_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        s = stream if stream is not None else torch.cuda.current_stream(self.device)
-        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_float_decode_attention")
+        s = current_stream_handle(self.device) if stream is None else ctypes.c_void_p(stream.cuda_stream)
+        check(self._fn(self.ctx, s, self._ref), "ppk_float_decode_attention")
         return self.out
 
 
@@ -242,6 +242,6 @@ class FloatDecodeStep:
         _replan(self, self.args.attn, lengths_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        s = stream if stream is not None else torch.cuda.current_stream(self.device)
-        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_float_decode_step")
+        s = current_stream_handle(self.device) if stream is None else ctypes.c_void_p(stream.cuda_stream)
+        check(self._fn(self.ctx, s, self._ref), "ppk_float_decode_step")
         return self.out

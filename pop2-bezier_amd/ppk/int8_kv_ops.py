@@ -41,6 +41,13 @@ def context(device: torch.device | int | None = None) -> ctypes.c_void_p:
     return ctx
 
 
+def current_stream_handle(device: torch.device) -> ctypes.c_void_p:
+    """The device's current HIP stream as a raw handle, without building a torch Stream object (the prepared
+    calls below run once per layer of a decode step, where that object cost more than the C-ABI call)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(index))
+
+
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
@@ -301,8 +308,8 @@ class DecodeAttention:
         _replan(self, self.args, past_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        s = stream if stream is not None else torch.cuda.current_stream(self.device)
-        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_decode_attention")
+        s = current_stream_handle(self.device) if stream is None else ctypes.c_void_p(stream.cuda_stream)
+        check(self._fn(self.ctx, s, self._ref), "ppk_decode_attention")
         return self.out
 
 
@@ -339,8 +346,8 @@ class DecodeStep:
         _replan(self, self.args.attn, past_host)
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        s = stream if stream is not None else torch.cuda.current_stream(self.device)
-        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_decode_step")
+        s = current_stream_handle(self.device) if stream is None else ctypes.c_void_p(stream.cuda_stream)
+        check(self._fn(self.ctx, s, self._ref), "ppk_decode_step")
         return self.out
 
 
@@ -364,8 +371,8 @@ class AppendKV:
         self.device = k_new.device
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> None:
-        s = stream if stream is not None else torch.cuda.current_stream(self.device)
-        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_quantize_append")
+        s = current_stream_handle(self.device) if stream is None else ctypes.c_void_p(stream.cuda_stream)
+        check(self._fn(self.ctx, s, self._ref), "ppk_quantize_append")
 
 
 def prepare(device: torch.device | int | None = None) -> None:

@@ -18,7 +18,7 @@ import torch
 
 from . import _abi
 from ._abi import check, lib
-from .int8_kv_ops import _require, _stream, context
+from .int8_kv_ops import _require, _stream, context, current_stream_handle
 
 _U32 = (torch.int32, torch.uint32)
 
@@ -75,6 +75,6 @@ class RenyiSampler:
         self.device = raw.device
 
     def __call__(self, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-        s = stream if stream is not None else torch.cuda.current_stream(self.device)
-        check(self._fn(self.ctx, ctypes.c_void_p(s.cuda_stream), self._ref), "ppk_renyi_sample")
+        s = current_stream_handle(self.device) if stream is None else ctypes.c_void_p(stream.cuda_stream)
+        check(self._fn(self.ctx, s, self._ref), "ppk_renyi_sample")
         return self.out

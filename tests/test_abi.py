@@ -108,10 +108,14 @@ def test_plan_sizes_workspace_without_a_device():
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
     assert (split, groups) == (104, -(-(-(-8192 // 104)) // 16))
     assert nbytes == 512 * groups * 128 * 4 + -(-(512 * groups * 2 * 4) // 256) * 256
-    # Few long rows (config 3 shape): rows split into 2-wave blocks so the launch covers all 256 CUs,
-    # joined by the merge kernel.
+    # Few long rows (config 3 shape): rows split into blocks so the launch covers all 256 CUs, joined by the
+    # merge kernel; the waves' shares halved to 32 tokens (one batch at D = 128) so that each block has four
+    # waves, one per SIMD of its CU. At D = 64 a batch is 64 tokens: 2-wave blocks stay.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048))
-    assert split == 64 and groups == 16 and nbytes == 16 * 16 * 128 * 4 + 16 * 16 * 2 * 4
+    assert split == 32 and groups == 16 and nbytes == 16 * 16 * 128 * 4 + 16 * 16 * 2 * 4
+    assert ppk.int8_kv_ops.plan_info(_attn_args(rows=16, capacity=2049, max_past=2048))["waves_per_block"] == 4
+    info64 = ppk.int8_kv_ops.plan_info(_attn_args(rows=16, capacity=2049, max_past=2048, head_dim=64))
+    assert (info64["split_tokens"], info64["nsplits"], info64["waves_per_block"]) == (64, 16, 2)
     # Uniform host lengths keep the per-row plan.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=2049, max_past=2048, past_host=[2048])) == \
         (split, groups, nbytes)
@@ -121,10 +125,10 @@ def test_plan_sizes_workspace_without_a_device():
     skew = [8192] * 4 + [512] * 28
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(past_host=skew))
     assert split == 456 and groups == 18 and nbytes == 512 * 18 * 128 * 4 + 512 * 18 * 2 * 4
-    # Few ragged rows: the per-row plan already spreads them over every CU (16 two-wave blocks per row), while
+    # Few ragged rows: the per-row plan already spreads them over every CU (16 four-wave blocks per row), while
     # the balanced plan's 384 units would fill only 96 CUs: per-row kept.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, heads=8, capacity=2049, max_past=2048,
-                                           past_host=[2048, 1000])) == (64, 16, 16 * 16 * 128 * 4 + 16 * 16 * 8)
+                                           past_host=[2048, 1000])) == (32, 16, 16 * 16 * 128 * 4 + 16 * 16 * 8)
     # Short ragged rows with host lengths: the per-row plan covers the longest live row (64 tokens) instead of
     # the span (900: rows cut into four blocks, merged from the workspace), so one block per row, one launch;
     # the same plan as a call whose max_past is that longest row. PPK_ATTN_PLAN_PER_ROW plans as without them.
