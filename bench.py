@@ -75,9 +75,10 @@ def parse() -> argparse.Namespace:
                    help="int8 config 5: time ppk_decode_attention alone (the uncommitted partial query: the current "
                         "token attended from its copy, nothing written to the arenas) instead of the fused step")
     p.add_argument("--wave-clock", default=None, metavar="OUT.md",
-                   help="configs 1, 3, 4: after the timed runs, run --steps warm steps again on a context created "
-                        "from the wave-clock code object (ppk_kernels_clock.hsaco) and write the per-phase "
-                        "breakdown of every decode and merge launch to OUT.md (summary also in the JSON line)")
+                   help="int8 configs 1, 3, 4, 5: after the timed runs, run up to 10 steps again on a context "
+                        "created from the wave-clock code object (ppk_kernels_clock.hsaco) and write the per-phase "
+                        "breakdown of every decode and merge launch to OUT.md (summary also in the JSON line; "
+                        "PPK_WAVE_CLOCK_RAW=FILE.npy also saves the raw records)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0,
                    help="head rows timed for the CPU baseline (0 = every row of the step)")
@@ -113,7 +114,7 @@ DECODE_POINTS = ("entry", "loads issued", "past[b] here", "first K data here", "
                  "output stored")
 
 
-def wave_clock_run(steps_fn, calls, steps: int, dev) -> tuple[dict, str]:
+def wave_clock_run(steps_fn, calls, steps: int, dev, raw: str | None = None) -> tuple[dict, str]:
     """Run `steps_fn` `steps` times with every prepared call in `calls` on a context made from the wave-clock
     code object, read the records (layout in pop2-bezier_amd/csrc/ppk_kernel_args.h) and summarise them:
     per decode launch the intervals between a wave's clock points and the launch's dispatch spread and span,
@@ -148,6 +149,9 @@ def wave_clock_run(steps_fn, calls, steps: int, dev) -> tuple[dict, str]:
         torch.cuda.synchronize()
         rec = buf[16:].view(-1, 16).cpu().numpy().view("uint64")
         rec = rec[rec[:, 0] != 0]  # slots never written (fewer waves than the slot count)
+        if raw:
+            import numpy as np
+            np.save(raw, rec)
         _abi.check(lib.ppk_context_set_wave_clock(ctx, None, 0), "ppk_context_set_wave_clock")
     finally:
         for c, old in zip(calls, saved):
@@ -224,9 +228,10 @@ def wave_clock_run(steps_fn, calls, steps: int, dev) -> tuple[dict, str]:
            f"| merge: entry -> records combined (per wave) | {summary['merge_entry_to_combined_us']} |",
            f"| merge: records combined -> output stored (per wave) | {summary['merge_combined_to_stored_us']} |",
            f"| merge: first wave entry -> last store | {summary['merge_span_us']} |",
-           f"| gap: merge's last store -> next decode's first wave entry | "
+           f"| gap: layer's last store (the merge's when one runs) -> next decode's first wave entry | "
            f"{summary['gap_merge_end_to_next_decode_start_us']} |",
-           f"| layer: decode's first wave entry -> merge's last store | {summary['layer_first_entry_to_last_store_us']} |"]
+           f"| layer: decode's first wave entry -> last store (the merge's when one runs) | "
+           f"{summary['layer_first_entry_to_last_store_us']} |"]
     return summary, "\n".join(md)
 
 
@@ -965,7 +970,8 @@ def bench_config(args) -> int:
     }
     if args.wave_clock:
         print("# bench: wave clock", file=sys.stderr, flush=True)
-        summary, md = wave_clock_run(lambda: warm(0), steps[0], min(args.steps, 10), dev)
+        summary, md = wave_clock_run(lambda: warm(0), steps[0], min(args.steps, 10), dev,
+                                     os.environ.get("PPK_WAVE_CLOCK_RAW"))
         result["wave_clock"] = summary
         cmd = "python3 bench.py " + " ".join(sys.argv[1:])
         with open(args.wave_clock, "w") as f:
@@ -1352,6 +1358,17 @@ def main() -> int:
     ppk.set_profiling(False)
     launches, kernel_ms = ppk.kernel_stats(ppk.PPK_KERNEL_ATTENTION, reset=True)
     kernel_avg_ms = kernel_ms / max(launches, 1)
+    clock = None
+    if args.wave_clock:
+        print("# bench: wave clock", file=sys.stderr, flush=True)
+        clock, md = wave_clock_run(step, [step], min(args.steps, 10), dev, os.environ.get("PPK_WAVE_CLOCK_RAW"))
+        with open(args.wave_clock, "w") as f:
+            f.write(f"# Wave clock: B={B} H={H} D={D} ctx={L} int8 decode "
+                    f"{'step' if not args.no_append else 'attention'}\n\n"
+                    f"Command (from the repository root):\n\n    python3 bench.py {' '.join(sys.argv[1:])}\n\n"
+                    f"{min(args.steps, 10)} back-to-back steps on a context made from "
+                    "pop2-bezier_amd/ppk/ppk_kernels_clock.hsaco (wave-clock build; record layout in "
+                    "pop2-bezier_amd/csrc/ppk_kernel_args.h).\n\n" + md + "\n")
 
     # Algorithmic bytes of one step: history K+V codes and scales of every
     # row, the bf16 query, the bf16 current K/V token (read once: quantised
@@ -1411,6 +1428,8 @@ def main() -> int:
                                                       seconds=args.cpu_seconds / 2, what=f" x {L} tokens")
     else:
         result["cpu_baseline"] = None
+    if clock is not None:
+        result["wave_clock"] = clock
     print(json.dumps(result), flush=True)
     return 0
 
