@@ -79,6 +79,11 @@ def parse() -> argparse.Namespace:
                         "created from the wave-clock code object (ppk_kernels_clock.hsaco) and write the per-phase "
                         "breakdown of every decode and merge launch to OUT.md (summary also in the JSON line; "
                         "PPK_WAVE_CLOCK_RAW=FILE.npy also saves the raw records)")
+    p.add_argument("--probe", action="store_true",
+                   help="int8 config 5 / --head-dim: after the timed runs, time the streaming-read probe "
+                        "(ppk/libppk_probe.so) at the decode launch's geometry (its waves, waves per block, blocks "
+                        "per CU and 1 KiB tiles, 4 per batch) for 2, 3, 4 and 6 batches in flight, and add the "
+                        "rates and the decode's fraction of the probe at its own ring depth to the JSON line")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=0,
                    help="head rows timed for the CPU baseline (0 = every row of the step)")
@@ -233,6 +238,62 @@ def wave_clock_run(steps_fn, calls, steps: int, dev, raw: str | None = None) -> 
            f"| layer: decode's first wave entry -> last store (the merge's when one runs) | "
            f"{summary['layer_first_entry_to_last_store_us']} |"]
     return summary, "\n".join(md)
+
+
+def read_probe(kc, vc, waves_per_row: int, waves_per_block: int, blocks_per_cu: int, split: int, steps: int,
+               dev) -> dict:
+    """Time the streaming-read probe (pop2-bezier_amd/csrc/ppk_read_probe.hip) on torch's current stream at a
+    decode launch's geometry: one wave per (row, split-token range), each reading its range of K codes then of V
+    codes in 1 KiB tiles, 4 tiles per batch, for 2, 3, 4 and 6 batches in flight. Placement "arena" reads the
+    arenas `kc`/`vc` themselves at the decode's addresses (row stride = capacity * D); placement "packed" reads
+    buffers of the same size whose ranges all start a power of two apart. Per placement and ring depth: the
+    average launch time over `steps` back-to-back launches (HIP events around them, after 10 warm launches) and
+    the read rate."""
+    import ctypes
+
+    import torch
+    from ppk.int8_kv_ops import current_stream_handle
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "pop2-bezier_amd", "ppk", "libppk_probe.so"))
+    lib.ppk_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                   ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                   ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    rows, cap, D = kc.shape
+    assert kc.is_contiguous() and vc.is_contiguous() and (split * D) % 4096 == 0 and cap * D % 16 == 0
+    tiles = split * D // 1024
+    waves = rows * waves_per_row
+    assert (waves_per_row - 1) * split + split <= cap  # every range inside its row
+    nbytes = waves * tiles * 1024
+    out = torch.empty(waves * 64, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    placements = {"arena": (kc, vc, cap * D // 16, split * D // 16)}
+    packed = torch.randint(0, 256, (2, nbytes), dtype=torch.uint8, device=dev)
+    placements["packed"] = (packed[0], packed[1], waves_per_row * tiles * 64, tiles * 64)
+    res = {}
+    for name, (k, v, row_stride, wave_stride) in placements.items():
+        res[name] = {}
+        for ring in (2, 3, 4, 6):
+            def launch():
+                rc = lib.ppk_read_probe(ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()), tiles,
+                                        waves, waves_per_block, blocks_per_cu, ring, waves_per_row, row_stride,
+                                        wave_stride, ctypes.c_void_p(out.data_ptr()), current_stream_handle(dev))
+                if rc != 0:
+                    raise RuntimeError(f"ppk_read_probe failed ({rc})")
+            for _ in range(10):
+                launch()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            t0.record(stream)
+            for _ in range(steps):
+                launch()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) / steps * 1e3
+            res[name][str(ring)] = {"avg_launch_us": round(us, 2), "gbps": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
+    del packed, out
+    return {"kernel": "read_probe<ring> (pop2-bezier_amd/csrc/ppk_read_probe.hip, ppk/libppk_probe.so)",
+            "waves": waves, "waves_per_block": waves_per_block, "blocks_per_cu": blocks_per_cu,
+            "tiles_per_range": tiles, "bytes_per_launch": 2 * nbytes, "launches": steps, "by_placement": res}
 
 
 def _host_cpus() -> int:
@@ -1430,6 +1491,17 @@ def main() -> int:
         result["cpu_baseline"] = None
     if clock is not None:
         result["wave_clock"] = clock
+    if args.probe:
+        print("# bench: read probe", file=sys.stderr, flush=True)
+        info = step.plan_info
+        wpb = info["waves_per_block"]
+        assert info["kind"] == "per-row" and step.ngroups == 1, "the probe mirrors the one-block-per-row plan"
+        probe = read_probe(kc, vc, wpb, wpb, (16 if wpb > 8 else 8) // wpb, split, args.steps, dev)
+        ring = 2 if wpb > 8 else 3  # the decode kernel's batches in flight (ppk_decode_w16_* keep two)
+        at_ring = probe["by_placement"]["arena"][str(ring)]["gbps"]
+        probe["decode_ring"] = ring
+        probe["decode_frac_of_probe"] = round(achieved / at_ring, 4)
+        result["read_probe"] = probe
     print(json.dumps(result), flush=True)
     return 0
 

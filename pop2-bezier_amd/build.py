@@ -47,6 +47,8 @@ def build(verbose: bool = True) -> dict:
     hsaco = os.path.join(OUT, "ppk_kernels.hsaco")
     clock = os.path.join(OUT, "ppk_kernels_clock.hsaco")
     lib = os.path.join(OUT, "libppk.so")
+    probe = os.path.join(OUT, "libppk_probe.so")
+    tmp_probe = probe + f".tmp{os.getpid()}"
     tmp_hsaco = hsaco + f".tmp{os.getpid()}"
     tmp_clock = clock + f".tmp{os.getpid()}"
     tmp_lib = lib + f".tmp{os.getpid()}"
@@ -82,15 +84,23 @@ def build(verbose: bool = True) -> dict:
             ],
             verbose,
         )
-        # Both outputs replace the previous build together, only once both compiled.
+        # The streaming-read probe bench.py --probe compares the decode with: a
+        # library of its own, not part of the decode library's C-ABI.
+        _run(
+            [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *DEVICE_FLAGS,
+             os.path.join(CSRC, "ppk_read_probe.hip"), "-o", tmp_probe],
+            verbose,
+        )
+        # The outputs replace the previous build together, only once all compiled.
         os.replace(tmp_hsaco, hsaco)
         os.replace(tmp_clock, clock)
         os.replace(tmp_lib, lib)
+        os.replace(tmp_probe, probe)
     finally:
-        for t in (tmp_hsaco, tmp_clock, tmp_lib, tmp_obj):
+        for t in (tmp_hsaco, tmp_clock, tmp_lib, tmp_obj, tmp_probe):
             if os.path.exists(t):
                 os.remove(t)
-    return {"hsaco": hsaco, "clock_hsaco": clock, "lib": lib}
+    return {"hsaco": hsaco, "clock_hsaco": clock, "lib": lib, "probe_lib": probe}
 
 
 if __name__ == "__main__":
