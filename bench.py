@@ -163,6 +163,14 @@ def wave_clock_run(steps_fn, calls, steps: int, dev, raw: str | None = None) -> 
             c.ctx = old
         torch.cuda.synchronize()
         lib.ppk_context_release(ctx)
+    return summarize_wave_clock(rec)
+
+
+def summarize_wave_clock(rec) -> tuple[dict, str]:
+    """Summary dict and markdown tables of wave-clock records (uint64 [n, 16], the written slots only; layout
+    in pop2-bezier_amd/csrc/ppk_kernel_args.h)."""
+    import statistics
+
     us = 1e6 / WAVE_CLOCK_HZ
     kind = (rec[:, 0] >> 56).astype(int)
     seq = ((rec[:, 0] >> 32) & 0xFFFFFF).astype(int)
@@ -182,6 +190,8 @@ def wave_clock_run(steps_fn, calls, steps: int, dev, raw: str | None = None) -> 
                           "first K data -> stream done", "stream done -> block joined",
                           "block joined -> output stored (wave 0)")}
     d_spread, d_span, m_span, m_comb, m_store, gap_dm, gap_md, layer = [], [], [], [], [], [], [], []
+    xcc = ((rec[:, 1] >> 32) & 0xF).astype(int)  # the XCD the wave ran on
+    by_xcd = {}  # XCD -> stream durations, wave ends after the launch's first entry, per-launch last ends
     seqs = sorted({s_ for s_, k_ in launches})
     for s_ in seqs:
         d = launches.get((s_, 1), [])
@@ -192,6 +202,15 @@ def wave_clock_run(steps_fn, calls, steps: int, dev, raw: str | None = None) -> 
         ends = [int(t[i, 6] if wave[i] == 0 else t[i, 5]) for i in d]
         d_spread.append((te.max() - te.min()) * us)
         d_span.append((max(ends) - te.min()) * us)
+        last = {}
+        for i, e in zip(d, ends):
+            x = by_xcd.setdefault(int(xcc[i]), {"stream": [], "end": [], "last": []})
+            if t[i, 3]:
+                x["stream"].append((t[i, 4] - t[i, 3]) * us)
+            x["end"].append((e - te.min()) * us)
+            last[int(xcc[i])] = max(last.get(int(xcc[i]), 0), e)
+        for k_, e in last.items():
+            by_xcd[k_]["last"].append((e - te.min()) * us)
         for i in d:
             iv["entry -> loads issued"].append((t[i, 1] - t[i, 0]) * us)
             iv["entry -> past[b] here"].append((t[i, 2] - t[i, 0]) * us)
@@ -222,6 +241,9 @@ def wave_clock_run(steps_fn, calls, steps: int, dev, raw: str | None = None) -> 
         "merge_combined_to_stored_us": med(m_store),
         "gap_decode_end_to_merge_start_us": med(gap_dm), "gap_merge_end_to_next_decode_start_us": med(gap_md),
         "layer_first_entry_to_last_store_us": med(layer),
+        "decode_by_xcd": {str(k_): {"waves": len(v["end"]), "stream_us_median": med(v["stream"]),
+                                    "wave_end_us_median": med(v["end"]), "last_end_us_median": med(v["last"])}
+                          for k_, v in sorted(by_xcd.items())},
     }
     md = ["| decode wave (every wave of every launch) | median µs | p90 µs |", "|---|---|---|"]
     md += [f"| {k} | {summary['decode_wave_intervals_us_median'][k]} | {summary['decode_wave_intervals_us_p90'][k]} |"
@@ -237,6 +259,12 @@ def wave_clock_run(steps_fn, calls, steps: int, dev, raw: str | None = None) -> 
            f"{summary['gap_merge_end_to_next_decode_start_us']} |",
            f"| layer: decode's first wave entry -> last store (the merge's when one runs) | "
            f"{summary['layer_first_entry_to_last_store_us']} |"]
+    md += ["", "| decode waves by XCD (XCC id) | waves | stream median µs | wave end median µs | XCD's last end µs "
+           "(median over launches) |", "|---|---|---|---|---|"]
+    md += [f"| {k_} | {v['waves']} | {v['stream_us_median']} | {v['wave_end_us_median']} | {v['last_end_us_median']} |"
+           for k_, v in summary["decode_by_xcd"].items()]
+    md += ["", "Wave ends and last ends are measured from the launch's first wave entry; a wave's end is its "
+           "block-joined point (wave 0: its store)."]
     return summary, "\n".join(md)
 
 
