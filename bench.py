@@ -269,12 +269,13 @@ def summarize_wave_clock(rec) -> tuple[dict, str]:
 
 
 def read_probe(kc, vc, waves_per_row: int, waves_per_block: int, blocks_per_cu: int, split: int, steps: int,
-               dev) -> dict:
+               dev, packed: bool = True) -> dict:
     """Time the streaming-read probe (pop2-bezier_amd/csrc/ppk_read_probe.hip) on torch's current stream at a
     decode launch's geometry: one wave per (row, split-token range), each reading its range of K codes then of V
     codes in 1 KiB tiles, 4 tiles per batch, for 2, 3, 4 and 6 batches in flight. Placement "arena" reads the
     arenas `kc`/`vc` themselves at the decode's addresses (row stride = capacity * D); placement "packed" reads
-    buffers of the same size whose ranges all start a power of two apart. Per placement and ring depth: the
+    buffers of the same size whose ranges all start a power of two apart (skipped when `packed` is false). Per
+    placement and ring depth: the
     average launch time over `steps` back-to-back launches (HIP events around them, after 10 warm launches) and
     the read rate."""
     import ctypes
@@ -295,8 +296,10 @@ def read_probe(kc, vc, waves_per_row: int, waves_per_block: int, blocks_per_cu: 
     out = torch.empty(waves * 64, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
     placements = {"arena": (kc, vc, cap * D // 16, split * D // 16)}
-    packed = torch.randint(0, 256, (2, nbytes), dtype=torch.uint8, device=dev)
-    placements["packed"] = (packed[0], packed[1], waves_per_row * tiles * 64, tiles * 64)
+    buf = None
+    if packed:
+        buf = torch.randint(0, 256, (2, nbytes), dtype=torch.uint8, device=dev)
+        placements["packed"] = (buf[0], buf[1], waves_per_row * tiles * 64, tiles * 64)
     res = {}
     for name, (k, v, row_stride, wave_stride) in placements.items():
         res[name] = {}
@@ -318,10 +321,11 @@ def read_probe(kc, vc, waves_per_row: int, waves_per_block: int, blocks_per_cu: 
             torch.cuda.synchronize()
             us = t0.elapsed_time(t1) / steps * 1e3
             res[name][str(ring)] = {"avg_launch_us": round(us, 2), "gbps": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
-    del packed, out
+    del buf, out
     return {"kernel": "read_probe<ring> (pop2-bezier_amd/csrc/ppk_read_probe.hip, ppk/libppk_probe.so)",
             "waves": waves, "waves_per_block": waves_per_block, "blocks_per_cu": blocks_per_cu,
-            "tiles_per_range": tiles, "bytes_per_launch": 2 * nbytes, "launches": steps, "by_placement": res}
+            "waves_per_cu": waves_per_block * blocks_per_cu, "tokens_per_wave": split, "tiles_per_range": tiles,
+            "bytes_per_launch": 2 * nbytes, "launches": steps, "by_placement": res}
 
 
 def _host_cpus() -> int:
@@ -1529,6 +1533,13 @@ def main() -> int:
         at_ring = probe["by_placement"]["arena"][str(ring)]["gbps"]
         probe["decode_ring"] = ring
         probe["decode_frac_of_probe"] = round(achieved / at_ring, 4)
+        if wpb % 2 == 0 and wpb * split <= cap:  # wpb / 2 waves of 2 * split tokens per row
+            # Half the waves per CU, each streaming twice the tokens: the same bytes with 16-24 KiB in flight
+            # per wave at rings 4 and 6, for comparison with the decode's shape.
+            half = read_probe(kc, vc, wpb // 2, wpb // 2, (16 if wpb > 8 else 8) // wpb, 2 * split, args.steps,
+                              dev, packed=False)
+            probe["half_waves_per_cu"] = {k: half[k] for k in ("waves", "waves_per_block", "blocks_per_cu",
+                                                               "waves_per_cu", "tokens_per_wave", "by_placement")}
         result["read_probe"] = probe
     print(json.dumps(result), flush=True)
     return 0
