@@ -80,7 +80,8 @@ def parse() -> argparse.Namespace:
                         "breakdown of every decode and merge launch to OUT.md (summary also in the JSON line; "
                         "PPK_WAVE_CLOCK_RAW=FILE.npy also saves the raw records)")
     p.add_argument("--probe", action="store_true",
-                   help="int8 config 5 / --head-dim: after the timed runs, time the streaming-read probe "
+                   help="int8 config 5 / --head-dim, or --kv bf16|f32 (uniform lengths): after the timed runs, "
+                        "time the streaming-read probe "
                         "(ppk/libppk_probe.so) at the decode launch's geometry (its waves, waves per block, blocks "
                         "per CU and 1 KiB tiles, 4 per batch) for 2, 3, 4 and 6 batches in flight, and add the "
                         "rates and the decode's fraction of the probe at its own ring depth to the JSON line")
@@ -571,6 +572,19 @@ def bench_float(args) -> int:
             "cpu_model": _cpu_model(), "host_cpus": _host_cpus()}
     else:
         result["cpu_baseline"] = None
+    if args.probe:
+        # The float decode's own geometry (per-row plan, one block per row): the probe reads the K and V stores
+        # as bytes, D * element size per token, with the decode's two batches in flight.
+        info = ppk.fused_attention.plan_info(plan_args, call.ctx)
+        wpb = info["waves_per_block"]
+        assert not flat and call.ngroups == 1 and not args.lengths, "the probe mirrors the one-block-per-row plan"
+        print("# bench: read probe", file=sys.stderr, flush=True)
+        kb, vb = (t.view(torch.uint8).reshape(rows, L, D * eb) for t in (k, v))
+        probe = read_probe(kb, vb, wpb, wpb, max(2, (16 if wpb > 8 else 8) // wpb), call.split_tokens, args.steps,
+                           dev, packed=False)
+        probe["decode_ring"] = 2
+        probe["decode_frac_of_probe"] = round(achieved / probe["by_placement"]["arena"]["2"]["gbps"], 4)
+        result["read_probe"] = probe
     print(json.dumps(result), flush=True)
     return 0
 
