@@ -597,11 +597,12 @@ PPK_API int32_t ppk_context_kernel_stats(ppk_context* ctx, uint32_t kernel, uint
    real-time clock at fixed points (entry, first loads issued, past[b] here,
    first K data here, stream done, block joined, output stored) to `buffer`:
    16 u64 words per record at a slot of its own, u64 word 0 the slots per
-   launch and kernel kind, word 1 the most records the buffer holds (both set
-   by the caller), records from word 16 (layout in
+   launch and kernel kind, word 1 the most records the caller wants kept
+   (both set by the caller; records past bytes / 128 - 1 are dropped whatever
+   word 1 says), records from word 16 (layout in
    pop2-bezier_amd/csrc/ppk_kernel_args.h). Each call starts the launch
    sequence numbers at 0. buffer NULL stops it; the library's own code object
-   ignores it. */
+   ignores it. Launches that overlap on one context write the same slots. */
 PPK_API int32_t ppk_context_set_wave_clock(ppk_context* ctx, void* buffer, uint64_t bytes);
 
 #ifdef __cplusplus

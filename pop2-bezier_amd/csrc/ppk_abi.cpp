@@ -660,6 +660,7 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
     std::lock_guard<std::mutex> lock(ctx->prof_mutex);
     d.clock = ctx->wave_clock;
     d.clock_seq = ctx->wave_clock_seq++;
+    d.clock_cap = ctx->wave_clock_cap;
   }
 
   const bool bf16h = (a.flags & PPK_ATTN_BF16_HISTORY) != 0;
@@ -723,6 +724,7 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
     m.scale_log2 = scale_log2;
     m.clock = d.clock;
     m.clock_seq = d.clock_seq;
+    m.clock_cap = d.clock_cap;
     launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMerge64 + di), a.rows, 64, 0, stream, m, 1, traceable);
   }
 }
@@ -1408,6 +1410,8 @@ int32_t ppk_context_set_wave_clock(ppk_context* ctx, void* buffer, uint64_t byte
     std::lock_guard<std::mutex> lock(ctx->prof_mutex);
     ctx->wave_clock = static_cast<uint64_t*>(buffer);
     ctx->wave_clock_seq = 0;
+    const uint64_t records = buffer ? bytes / (ppk::kWaveClockWords * 8) - 1 : 0;  // after the header record
+    ctx->wave_clock_cap = uint32_t(std::min<uint64_t>(records, 0xffffffffu));
   });
 }
 

@@ -138,6 +138,7 @@ struct ppk_context {
   bool profiling = false;
   uint64_t* wave_clock = nullptr;   // ppk_context_set_wave_clock
   uint32_t wave_clock_seq = 0;
+  uint32_t wave_clock_cap = 0;      // records after the header the buffer holds
   std::vector<ppk::EventPair> pending[PPK_KERNEL_COUNT];
   std::vector<ppk::EventPair> pool;
   uint64_t launches[PPK_KERNEL_COUNT] = {};

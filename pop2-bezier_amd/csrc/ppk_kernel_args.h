@@ -101,6 +101,7 @@ struct DecodeArgs {
                             // plan, a past[b] <= span past the plan's coverage flags stale host lengths
   uint32_t speculate;       // per-row plan: request each wave's first K batches before past[] arrives
   uint32_t clock_seq;       // wave-clock builds only: the launch's sequence number in the records
+  uint32_t clock_cap;       // wave-clock builds only: records the buffer holds (from its size on the host)
   uint64_t* clock;          // wave-clock builds only (kWaveClock*): record buffer, or null
 };
 
@@ -117,6 +118,7 @@ struct MergeArgs {
   float scale_log2;
   uint32_t span;            // rows with past[b] > span give NaN (balanced plan)
   uint32_t clock_seq;       // wave-clock builds only, as in DecodeArgs
+  uint32_t clock_cap;
   uint64_t* clock;
 };
 

@@ -48,13 +48,17 @@ namespace {
     __asm__ volatile("" ::"v"(dep));    \
     (var) = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
-#define PPK_CLK_RECORD(args, kind, block, wave) clock_record(args.clock, args.clock_seq, kind, block, wave, clk_)
-__device__ __forceinline__ void clock_record(uint64_t* clock, uint32_t seq, uint32_t kind, uint32_t block,
-                                             uint32_t wave, const uint64_t (&t)[ppk::kWaveClockPoints]) {
+#define PPK_CLK_RECORD(args, kind, block, wave) \
+  clock_record(args.clock, args.clock_seq, args.clock_cap, kind, block, wave, clk_)
+// The buffer's own capacity word is honoured only up to the capacity the host
+// derived from the buffer's size, so a wrong word cannot send a record past it.
+__device__ __forceinline__ void clock_record(uint64_t* clock, uint32_t seq, uint32_t cap, uint32_t kind,
+                                             uint32_t block, uint32_t wave,
+                                             const uint64_t (&t)[ppk::kWaveClockPoints]) {
   if (!clock || (threadIdx.x & 63) != 0) return;
   const uint64_t per = clock[0], local = uint64_t(block) * (blockDim.x >> 6) + wave;
   const uint64_t slot = (uint64_t(seq) * 2 + kind - 1) * per + local;
-  if (local >= per || slot >= clock[1]) return;
+  if (local >= per || slot >= clock[1] || slot >= cap) return;
   uint64_t* r = clock + ppk::kWaveClockWords * (slot + 1);
   const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_ID
   const uint32_t xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);  // XCC_ID
