@@ -981,7 +981,7 @@ def bench_config(args) -> int:
              for c in range(copies)]
     split, ngroups = steps[0][0].split_tokens, steps[0][0].ngroups
     # The library reports the plan it takes (ppk_attention_plan_info): per-row or balanced, its waves per
-    # block (blocks of more than 8 waves run the _w16 kernels) and its launches (decode, + merge).
+    # block and its launches (decode, + merge).
     info = steps[0][0].plan_info
     balanced = info["kind"] == "balanced"
     layer_launches = info["launches"]
@@ -1043,7 +1043,7 @@ def bench_config(args) -> int:
     step_bytes = layer_bytes * layers
     achieved = kernel_bytes / (kernel_avg_us * 1e-6) / 1e9
     tag = f"c{args.config}_b{B}_h{H}_d{D}"
-    kbase = "ppk_decode_flat" if balanced else "ppk_decode_w16" if info["waves_per_block"] > 8 else "ppk_decode"
+    kbase = "ppk_decode_flat" if balanced else "ppk_decode"
     kname = f"{kbase}_d{D}"
     tpath = os.path.join(ROOT, "profiles", f"{kbase}_{tag}_traffic.json")
     traffic, traffic_source = committed_traffic(tpath, split=split, workload=tag)
@@ -1489,8 +1489,7 @@ def main() -> int:
     achieved = kernel_bytes / (kernel_avg_ms * 1e-3) / 1e9
     step_gbps = step_bytes / (step_ms * 1e-3) / 1e9
 
-    kname = ("ppk_decode" + ("_w16" if step.plan_info["waves_per_block"] > 8 else "")
-             + ("_bf16h" if args.bf16_history else "") + f"_d{D}")
+    kname = "ppk_decode" + ("_bf16h" if args.bf16_history else "") + f"_d{D}"
     tag = ("_bf16h" if args.bf16_history else "") + ("" if append else "_noappend")
     tpath = args.traffic or os.path.join(ROOT, "profiles", f"ppk_decode_d{D}_b{B}_h{H}_ctx{L}{tag}_traffic.json")
     traffic, traffic_source = committed_traffic(tpath, split=split, workload=f"B{B}H{H}D{D}L{L}", kernel=kname,
@@ -1542,16 +1541,16 @@ def main() -> int:
         info = step.plan_info
         wpb = info["waves_per_block"]
         assert info["kind"] == "per-row" and step.ngroups == 1, "the probe mirrors the one-block-per-row plan"
-        probe = read_probe(kc, vc, wpb, wpb, (16 if wpb > 8 else 8) // wpb, split, args.steps, dev)
-        ring = 2 if wpb > 8 else 3  # the decode kernel's batches in flight (ppk_decode_w16_* keep two)
+        probe = read_probe(kc, vc, wpb, wpb, max(2, 8 // wpb), split, args.steps, dev)
+        ring = 3  # the int8 decode kernel's batches in flight
         at_ring = probe["by_placement"]["arena"][str(ring)]["gbps"]
         probe["decode_ring"] = ring
         probe["decode_frac_of_probe"] = round(achieved / at_ring, 4)
         if wpb % 2 == 0 and wpb * split <= cap:  # wpb / 2 waves of 2 * split tokens per row
             # Half the waves per CU, each streaming twice the tokens: the same bytes with 16-24 KiB in flight
             # per wave at rings 4 and 6, for comparison with the decode's shape.
-            half = read_probe(kc, vc, wpb // 2, wpb // 2, (16 if wpb > 8 else 8) // wpb, 2 * split, args.steps,
-                              dev, packed=False)
+            half = read_probe(kc, vc, wpb // 2, wpb // 2, max(2, 8 // wpb), 2 * split, args.steps, dev,
+                              packed=False)
             probe["half_waves_per_cu"] = {k: half[k] for k in ("waves", "waves_per_block", "blocks_per_cu",
                                                                "waves_per_cu", "tokens_per_wave", "by_placement")}
         result["read_probe"] = probe

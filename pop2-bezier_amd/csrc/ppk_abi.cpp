@@ -71,8 +71,6 @@ const char* kFnNames[ppk::kFnCount] = {
     "ppk_fstep_f32_d64", "ppk_fstep_f32_d128", "ppk_fstep_f32_d256",
     "ppk_fstep_flat_bf16_d64", "ppk_fstep_flat_bf16_d128", "ppk_fstep_flat_bf16_d256",
     "ppk_fstep_flat_f32_d64", "ppk_fstep_flat_f32_d128", "ppk_fstep_flat_f32_d256",
-    "ppk_decode_w16_d64", "ppk_decode_w16_d128", "ppk_decode_w16_d256",
-    "ppk_decode_w16_bf16h_d64", "ppk_decode_w16_bf16h_d128", "ppk_decode_w16_bf16h_d256",
 };
 
 std::string default_code_object() {
@@ -149,7 +147,8 @@ DeviceGuard::~DeviceGuard() {
 }
 
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
-                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, uint32_t min_split) {
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, uint32_t min_split,
+                        uint32_t block_waves) {
   AttentionPlan plan;
   plan.head_dim = head_dim;
   uint32_t split;
@@ -180,12 +179,23 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     uint64_t waves = std::max<uint64_t>(1, (span + split - 1) / split);
     const uint64_t fill = std::min<uint64_t>(16, budget / std::max<uint64_t>(rows, 1));
     waves = std::max<uint64_t>(waves, std::min<uint64_t>(fill, (span + 63) / 64));
-    const uint64_t share = ((span + waves - 1) / waves + tpl - 1) / tpl * tpl;
-    split = uint32_t(std::min<uint64_t>(split, std::max<uint64_t>(share, tpl)));
+    if (waves > block_waves && span * token_bytes <= (128u << 10)) {
+      // A row that one block covers gets at most block_waves waves, each
+      // streaming a longer share (int8: 8, the kernels bounded to 512 threads
+      // with three batches in flight; 9 to 16 waves of 64 tokens in one block
+      // measured 17 % slower on one box: 64 rows x 900 tokens at D = 64, 15
+      // waves of 64 tokens 9.09 us, 8 waves of 128 tokens 7.53 us; 16 rows x
+      // 960, 9.15 -> 7.49 us; 128 rows x 900, 9.53 -> 8.26 us).
+      waves = block_waves;
+      split = uint32_t(std::max<uint64_t>(((span + waves - 1) / waves + tpl - 1) / tpl * tpl, tpl));
+    } else {
+      const uint64_t share = ((span + waves - 1) / waves + tpl - 1) / tpl * tpl;
+      split = uint32_t(std::min<uint64_t>(split, std::max<uint64_t>(share, tpl)));
+    }
   }
   uint64_t waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
-  // Up to 16 waves per block; one float of LDS per history token of the block.
-  uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
+  // Up to block_waves waves per block; one float of LDS per history token of the block.
+  uint64_t max_waves = std::max<uint64_t>(1, std::min<uint64_t>(block_waves, 16384 / split));
   const uint64_t cus = uint64_t(std::max(ctx ? ctx->cu_count : 256, 1));
   const uint64_t row_bytes = span * token_bytes;
   if (!explicit_split && rows < cus && row_bytes > (128u << 10)) {
@@ -210,7 +220,7 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
            rows * ((span + split / 2 - 1) / (split / 2)) <= budget) {
       split /= 2;
       waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
-      max_waves = std::max<uint64_t>(1, std::min<uint64_t>(16, 16384 / split));
+      max_waves = std::max<uint64_t>(1, std::min<uint64_t>(block_waves, 16384 / split));
       w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / (uint64_t(split) * token_bytes)));
       while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) --w;
     }
@@ -271,7 +281,7 @@ AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a) 
   const uint64_t cover = host && !(a.flags & kPlanFlags) ? row_cover(host, a.rows / a.heads, limit) : span;
   // The int8 waves' shortest share: one batch (four load tiles).
   AttentionPlan plan =
-      plan_rows(ctx, a.rows, cover, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim, 4 * tpl);
+      plan_rows(ctx, a.rows, cover, a.split_tokens, tpl, 2ull * a.head_dim + 8, a.head_dim, 4 * tpl, 8);
   // With the host's lengths of a ragged batch, the balanced plan gives every
   // wave the same share of the live history; balanced_pays picks between the
   // two plans from a timing model of both.
@@ -695,12 +705,10 @@ void run_attention(ppk_context* ctx, hipStream_t stream, const PpkAttentionArgs&
     launch(ctx, PPK_KERNEL_ATTN_MERGE, Fn(kMergeFlat64 + di), a.rows, 64, 0, stream, m, 1, traceable);
     return;
   }
-  // Blocks of at most 8 waves run the kernels bounded to 512 threads (two
-  // waves per SIMD, up to 256 VGPRs: a deeper ring of batches in flight);
-  // larger blocks the 1024-thread ones (at most 128 VGPRs).
-  const bool w16 = plan.waves > 8;
-  const Fn decode =
-      Fn((w16 ? (bf16h ? kDecodeW16Bf16h64 : kDecodeW16_64) : (bf16h ? kDecodeBf16h64 : kDecode64)) + di);
+  // The int8 plan's blocks hold at most 8 waves: the kernels are bounded to
+  // 512 threads (two waves per SIMD, up to 256 VGPRs, three batches in flight).
+  require(plan.waves <= 8, "internal: int8 decode block of more than 8 waves");
+  const Fn decode = Fn((bf16h ? kDecodeBf16h64 : kDecode64) + di);
   DeviceGuard guard(ctx->device);
   launch(ctx, PPK_KERNEL_ATTENTION, decode, plan.ngroups * a.rows, 64 * plan.waves, plan.lds_bytes, stream, d, 1,
          traceable);
@@ -771,7 +779,7 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   // gives NaN rows (and PPK_FLAG_STALE_LENGTHS in a decode step).
   const uint64_t cover = host && !(a.flags & kPlanFlags) ? row_cover(host, batch, span) : span;
   AttentionPlan plan =
-      plan_rows(ctx, a.rows, cover, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim, 0);
+      plan_rows(ctx, a.rows, cover, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim, 0, 16);
   // With the host's copy of the lengths, a ragged batch takes the balanced
   // plan (the int8 path's table) when its longest row holds more than
   // 512 KiB of K and V and the per-row plan's waves are uneven (the most

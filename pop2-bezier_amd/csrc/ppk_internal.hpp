@@ -60,8 +60,6 @@ enum Fn : int {
   kFStepF32_64, kFStepF32_128, kFStepF32_256,
   kFStepFlatBf16_64, kFStepFlatBf16_128, kFStepFlatBf16_256,
   kFStepFlatF32_64, kFStepFlatF32_128, kFStepFlatF32_256,
-  kDecodeW16_64, kDecodeW16_128, kDecodeW16_256,
-  kDecodeW16Bf16h64, kDecodeW16Bf16h128, kDecodeW16Bf16h256,
   kFnCount
 };
 
@@ -184,9 +182,11 @@ struct AttentionPlan {
 // Split policy shared by both attention paths: span history tokens per row,
 // tpl tokens per wave-wide load, token_bytes of K+V (+scales) per token.
 // min_split > 0: in the few-long-rows case, waves' shares may be halved down to
-// min_split tokens so that blocks get four waves (0: never).
+// min_split tokens so that blocks get four waves (0: never). block_waves: the
+// most waves of one block (int8: 8, float: 16).
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
-                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, uint32_t min_split);
+                        uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, uint32_t min_split,
+                        uint32_t block_waves);
 AttentionPlan plan_attention(const ppk_context* ctx, const PpkAttentionArgs& a);
 // The balanced plan of `rows` rows, `heads` per sequence, from the host
 // lengths host[0 .. rows / heads) (at most 64 sequences); a length above

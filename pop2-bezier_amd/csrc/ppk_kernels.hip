@@ -4,8 +4,8 @@
 //
 //   ppk_quantize_d{64,128,256}         quantize rows densely or append into arenas
 //   ppk_dequantize                     codes * scales -> f32/bf16/f16
-//   ppk_decode[_w16][_bf16h]_d{..}     decode attention (+ fused append, + in-block merge); _w16: 9-16 waves
-//                                      per block
+//   ppk_decode[_bf16h]_d{..}           decode attention (+ fused append, + in-block merge), up to 8 waves per
+//                                      block
 //   ppk_attn_merge_d{..}               cross-group merge + current token
 //   ppk_decode_flat[_bf16h]_d{..}      decode attention over a balanced work list (ragged batches, + fused append)
 //   ppk_attn_merge_flat_d{..}          merge of the balanced work list's records + current token
@@ -2573,9 +2573,8 @@ PPK_QSTREAM(128)
 PPK_QSTREAM(256)
 #undef PPK_QSTREAM
 
-// Blocks of up to 8 waves (2 per SIMD, up to 256 VGPRs) stream through a
-// ring of kRing batches; blocks of 9 to 16 waves (4 per SIMD, at most 128
-// VGPRs) through a ring of two.
+// Blocks of up to 8 waves (the plan never makes larger int8 blocks): two
+// waves per SIMD, up to 256 VGPRs each, a ring of kRing batches in flight.
 constexpr int kRing = 3;
 #define PPK_ATTN(D)                                                                          \
   extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))    \
@@ -2585,12 +2584,6 @@ constexpr int kRing = 3;
   extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))    \
   void ppk_decode_bf16h_d##D(ppk::DecodeArgs a) {                                            \
     decode_body<D, true, kRing>(a);                                                          \
-  }                                                                                          \
-  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_w16_d##D(ppk::DecodeArgs a) { \
-    decode_body<D, false, 2>(a);                                                             \
-  }                                                                                          \
-  extern "C" __global__ __launch_bounds__(1024) void ppk_decode_w16_bf16h_d##D(ppk::DecodeArgs a) { \
-    decode_body<D, true, 2>(a);                                                              \
   }                                                                                          \
   extern "C" __global__ __launch_bounds__(64) void ppk_attn_merge_d##D(ppk::MergeArgs a) {   \
     attn_merge_body<D>(a);                                                                   \

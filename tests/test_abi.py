@@ -104,9 +104,10 @@ def test_plan_sizes_workspace_without_a_device():
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args())
     assert (split, groups, nbytes) == (2048, 1, 0)
     # An explicit per-wave split is honoured (rounded up to whole 1 KiB tiles);
-    # up to 16 waves per block, so ceil(ceil(8192/104)/16) blocks per row.
+    # int8 blocks hold up to 8 waves, so ceil(ceil(8192/104)/8) blocks per row.
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
-    assert (split, groups) == (104, -(-(-(-8192 // 104)) // 16))
+    assert (split, groups) == (104, -(-(-(-8192 // 104)) // 8))
+    assert ppk.int8_kv_ops.plan_info(_attn_args(split_tokens=100))["waves_per_block"] == 8
     assert nbytes == 512 * groups * 128 * 4 + -(-(512 * groups * 2 * 4) // 256) * 256
     # Few long rows (config 3 shape): rows split into blocks so the launch covers all 256 CUs, joined by the
     # merge kernel; the waves' shares halved to 32 tokens (one batch at D = 128) so that each block has four
@@ -523,10 +524,10 @@ def test_plan_info_reports_the_plan_taken():
     info = ppk.int8_kv_ops.plan_info(_attn_args())  # config 5: one 4-wave block per row, one launch
     assert info == {"kind": "per-row", "split_tokens": 2048, "nsplits": 1, "waves_per_block": 4, "blocks": 512,
                     "launches": 1, "workspace_bytes": 0}
-    info = ppk.int8_kv_ops.plan_info(_attn_args(split_tokens=100))  # 16-wave blocks, merge launch
+    info = ppk.int8_kv_ops.plan_info(_attn_args(split_tokens=100))  # 8-wave blocks, merge launch
     split, groups, nbytes = ppk.int8_kv_ops.plan(_attn_args(split_tokens=100))
     assert (info["split_tokens"], info["nsplits"], info["workspace_bytes"]) == (split, groups, nbytes)
-    assert info["kind"] == "per-row" and info["waves_per_block"] == 16 and info["blocks"] == 512 * groups
+    assert info["kind"] == "per-row" and info["waves_per_block"] == 8 and info["blocks"] == 512 * groups
     assert info["launches"] == 2
     info = ppk.int8_kv_ops.plan_info(_attn_args(past_host=skew))
     assert info["kind"] == "balanced" and info["launches"] == 2

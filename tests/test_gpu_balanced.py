@@ -93,11 +93,13 @@ def test_rows_beyond_max_past_give_nan(device):
 
 
 def test_short_rows_keep_the_per_row_plan(device):
-    """Short ragged rows: one block per row puts every row on a CU of its own, so the host lengths change
-    nothing (one launch, no merge) and the result is the per-row plan's."""
+    """Short ragged rows: one block per row puts every row on a CU of its own, so the host lengths keep the
+    per-row plan (one launch, no merge), sized for the longest live row (64 tokens: one wave) instead of the
+    span (900: eight 128-token waves, an int8 block's most)."""
     lengths = [10, 0, 60, 64]
     c = Case(device, 4, 16, 64, lengths, 1024)
-    assert _plan(c, lengths, max_past=900) == _plan(c, None, max_past=900) == (64, 1, 0)
+    assert _plan(c, lengths, max_past=900) == (64, 1, 0)
+    assert _plan(c, None, max_past=900) == (128, 1, 0)
     ppk.kernel_stats(ppk.PPK_KERNEL_ATTN_MERGE, reset=True)
     ppk.set_profiling(True)
     got = c.run(past_host=lengths, max_past=900)
