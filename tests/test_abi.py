@@ -145,6 +145,10 @@ def test_plan_sizes_workspace_without_a_device():
                                            past_host=[0, 901, 1024, 0])) == (8, 1, 0)
     # Few short rows (config 1 shape): one block per row, one launch.
     assert ppk.int8_kv_ops.plan(_attn_args(rows=16, capacity=513, max_past=512, head_dim=64)) == (64, 1, 0)
+    # A row one block covers (at most 128 KiB of history) that the budget would give 15 waves of 64 tokens
+    # keeps at most 8 int8 waves, each a longer share: 900 / 8 = 113 -> 128 (16-token tiles at D = 64).
+    info = ppk.int8_kv_ops.plan_info(_attn_args(rows=64, capacity=1024, max_past=900, head_dim=64))
+    assert (info["split_tokens"], info["nsplits"], info["waves_per_block"], info["launches"]) == (128, 1, 8, 1)
     # Spans that are no multiple of the power-of-two split: each row gets as many waves as the budget holds
     # (2048 / 512 rows = 4) with equal shares rounded up to whole tiles (1100 / 4 = 275 -> 280 for the int8
     # path's 8-token tiles, 276 for bf16's 4-token tiles at D = 128), one block per row.

@@ -155,6 +155,21 @@ def test_split_invariance(device, split):
     assert_close(c.run(split=split), c.reference(), what=f"split {split}")
 
 
+@pytest.mark.parametrize("bf16h", [False, True])
+def test_rows_one_block_covers_take_eight_longer_waves(device, bf16h):
+    """Rows of up to 128 KiB that the budget would give 9-16 waves take 8 waves of a longer share in one
+    block (here 128 of the 900 tokens per wave at D = 64), one launch; ragged lengths inside the span."""
+    c = Case(device, 4, 16, 64, [900, 700, 413, 899], 1000, seed=SEED + 17)
+    a, _ = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, max_past=900)
+    info = ppk.int8_kv_ops.plan_info(a, ppk.context(device))
+    assert (info["split_tokens"], info["waves_per_block"], info["launches"]) == (128, 8, 1)
+    got = c.run(max_past=900, bf16_history=bf16h)
+    if bf16h:
+        assert_close(got, c.reference(history_bf16=True), atol=2e-5, rtol=0, what="8-wave rows, bf16 history")
+    else:
+        assert_close(got, c.reference(), what="8-wave rows")
+
+
 @pytest.mark.parametrize("split", [0, 32])
 def test_long_rows_merge_more_than_64_groups(device, split):
     """Two rows of 65536 tokens: each row spans hundreds of blocks (the automatic plan's 64-token waves, or
