@@ -778,8 +778,18 @@ AttentionPlan plan_float_attention(const ppk_context* ctx, const PpkFloatAttenti
   // per-row plan covers the longest live row; a device length beyond it
   // gives NaN rows (and PPK_FLAG_STALE_LENGTHS in a decode step).
   const uint64_t cover = host && !(a.flags & kPlanFlags) ? row_cover(host, batch, span) : span;
+  // Few long rows: blocks of fewer than four waves halve their waves' share
+  // as on the int8 path, but not below 16 KiB of K and V per wave (the float
+  // waves do less arithmetic per byte, so shorter streams cost more than the
+  // idle SIMDs). Same-box A/B, H = 16, one launch pair per step: B = 1 x 2048
+  // bf16 D = 128 8.28 -> 7.18 us, x 1536 8.58 -> 6.99 us, fused step 8.68 ->
+  // 7.87 us; f32 D = 64 x 1024 7.04 -> 6.25 us, f32 D = 128 x 2048 10.82 ->
+  // 8.73 us; bf16 D = 64 (16 KiB per 64-token wave) unchanged, where halving
+  // to 8 KiB had cost 4 %.
+  const uint64_t token_bytes = 2ull * eb * a.head_dim;
+  const uint32_t min_split = std::max<uint32_t>(4 * std::max(tpl, 1u), uint32_t((16u << 10) / token_bytes));
   AttentionPlan plan =
-      plan_rows(ctx, a.rows, cover, a.split_tokens, std::max(tpl, 1u), 2 * eb * a.head_dim, a.head_dim, 0, 16);
+      plan_rows(ctx, a.rows, cover, a.split_tokens, std::max(tpl, 1u), token_bytes, a.head_dim, min_split, 16);
   // With the host's copy of the lengths, a ragged batch takes the balanced
   // plan (the int8 path's table) when its longest row holds more than
   // 512 KiB of K and V and the per-row plan's waves are uneven (the most

@@ -182,7 +182,8 @@ struct AttentionPlan {
 // Split policy shared by both attention paths: span history tokens per row,
 // tpl tokens per wave-wide load, token_bytes of K+V (+scales) per token.
 // min_split > 0: in the few-long-rows case, waves' shares may be halved down to
-// min_split tokens so that blocks get four waves (0: never). block_waves: the
+// min_split tokens so that blocks get four waves (0: never; int8: one batch,
+// float: one batch and at least 16 KiB per wave). block_waves: the
 // most waves of one block (int8: 8, float: 16).
 AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, uint32_t explicit_split,
                         uint32_t tpl, uint64_t token_bytes, uint32_t head_dim, uint32_t min_split,

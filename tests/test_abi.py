@@ -315,6 +315,12 @@ def test_float_plan_without_a_device():
     split, groups, nbytes = ppk.fused_attention.plan(_float_args(rows=16, size=1024, head_dim=64))
     assert (split, groups) == (64, 16)
     assert nbytes == 16 * 16 * 64 * 4 + -(-(16 * 16 * 2 * 4) // 256) * 256
+    # Few long rows with blocks of fewer than four waves: the waves' share is halved while a wave keeps at
+    # least 16 KiB of K and V: bf16 D = 128 x 2048 tokens, 32-token waves (16 KiB) in 4-wave blocks; the
+    # graph-decode shape above (bf16 D = 64, 16 KiB per 64-token wave) keeps its one-wave blocks.
+    info = ppk.fused_attention.plan_info(_float_args(rows=16, size=2048, head_dim=128))
+    assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == (32, 16, 4)
+    assert ppk.fused_attention.plan_info(_float_args(rows=16, size=1024, head_dim=64))["waves_per_block"] == 1
     # Explicit split: whole wave loads of tokens (f32, D = 128: 2 tokens per 1 KiB load).
     split, groups, _ = ppk.fused_attention.plan(_float_args(kv_dtype=_abi.PPK_F32, split_tokens=33))
     assert split == 34 and groups == -(-(-(-8192 // 34)) // 16)
