@@ -205,9 +205,22 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     // the merge kernel joins the groups. (Config 4 against a 64 KiB target:
     // three-wave blocks and 4 records per row instead of one-wave blocks and
     // 12, 2 % faster warm and cold.)
+    // The int8 kernels hold two waves per SIMD, eight per CU: blocks of 1, 2,
+    // 4 or 8 waves fill a CU's slots, while blocks of 3, 5, 6 or 7 leave some
+    // empty and can push the grid into a second round (32 rows x 8192 tokens
+    // at D = 128: 7-wave blocks, 320 of them on 256 CUs, 25.3 us; 4-wave
+    // blocks, one round, 17.0 us). The float kernels hold more waves per CU
+    // and take any block size.
+    const bool pow2 = block_waves <= 8;
+    auto fit = [&](uint64_t w) {
+      uint64_t p = 1;
+      while (pow2 && p * 2 <= w) p *= 2;
+      return pow2 ? p : w;
+    };
+    auto shrink = [&](uint64_t w) { return pow2 ? w / 2 : w - 1; };
     const uint64_t wave_bytes = uint64_t(split) * token_bytes;
-    uint64_t w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / wave_bytes));
-    while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) --w;
+    uint64_t w = fit(std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / wave_bytes)));
+    while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) w = shrink(w);
     // Blocks of fewer than four waves leave SIMDs of their CU idle while the
     // waves work through their tokens (config 3: one 2-wave block of 64-token
     // waves per CU, 1.56 us of arithmetic per wave after its data arrived).
@@ -221,8 +234,35 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
       split /= 2;
       waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
       max_waves = std::max<uint64_t>(1, std::min<uint64_t>(block_waves, 16384 / split));
-      w = std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / (uint64_t(split) * token_bytes)));
-      while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) --w;
+      w = fit(std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / (uint64_t(split) * token_bytes))));
+      while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) w = shrink(w);
+    }
+    // int8: a grid whose blocks do not all fit the CUs' eight wave slots at
+    // once runs a second round, and its merge launch waits for the last one.
+    // When eight waves of a longer share cover each row, one block per row
+    // runs in one round with no merge launch, though some CUs stay idle;
+    // otherwise the blocks shrink until the grid fits. Same-box A/B of the
+    // two-round grid -> one block per row (-> the shrunk blocks), H = 16:
+    // 160 rows x 1024 tokens at D = 128 21.1 -> 12.5 (13.5) us, 192 x 1500
+    // at D = 128 20.9 -> 15.0 (17.3), 192 x 2048 at D = 128 25.9 -> 18.5
+    // (21.5), 224 x 4096 at D = 128 49.8 -> 37.4 (40.4), 160 x 2048 at D =
+    // 64 20.9 -> 12.3 (13.4), 224 x 2048 at D = 64 20.8 -> 13.0 (15.6), 192
+    // x 4096 at D = 64 26.1 -> 18.8 (21.6), 224 x 8192 at D = 64 51.8 ->
+    // 40.1 (41.8). Grids that fit one round keep their plan: one block per
+    // row would idle more CUs than a merge costs (192 x 8192 at D = 128
+    // splits ten ways, 67.6 us).
+    const uint64_t slots = 8;  // int8 waves resident per CU
+    auto blocks = [&](uint64_t n) { return rows * ((waves_per_row + n - 1) / n); };
+    if (pow2 && blocks(w) > cus * (slots / w)) {
+      const uint64_t whole = std::max<uint64_t>(
+          1, ((span + block_waves - 1) / block_waves + tpl - 1) / tpl * tpl);  // 8 waves cover a row
+      if (rows * block_waves <= budget && whole * block_waves <= 16384) {
+        split = uint32_t(whole);
+        waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
+        w = block_waves;
+      } else {
+        while (w > 1 && blocks(w) > cus * (slots / w)) w /= 2;
+      }
     }
     max_waves = w;
   }

@@ -149,30 +149,26 @@ def test_plan_sizes_workspace_without_a_device():
     # keeps at most 8 int8 waves, each a longer share: 900 / 8 = 113 -> 128 (16-token tiles at D = 64).
     info = ppk.int8_kv_ops.plan_info(_attn_args(rows=64, capacity=1024, max_past=900, head_dim=64))
     assert (info["split_tokens"], info["nsplits"], info["waves_per_block"], info["launches"]) == (128, 1, 8, 1)
+    # Fewer rows than CUs whose blocks would not all fit the CUs' eight int8 wave slots at once (192 rows x
+    # 4096 tokens at D = 64: 3 groups of 4-wave blocks, 576 > 512 resident): one 8-wave block per row, 4096 / 8
+    # = 512 tokens a wave, one launch. Rows eight waves cannot cover (2048 tokens a wave at most) keep a
+    # split plan; so do grids that fit one round.
+    for rows, span, d, want in ((192, 4096, 64, (512, 1, 8, 192, 1)), (160, 1024, 128, (128, 1, 8, 160, 1)),
+                                (192, 1500, 128, (192, 1, 8, 192, 1)), (224, 8192, 64, (1024, 1, 8, 224, 1))):
+        info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span, head_dim=d))
+        got = (info["split_tokens"], info["nsplits"], info["waves_per_block"], info["blocks"], info["launches"])
+        assert got == want, (rows, span, d, got)
+    for rows, span in ((192, 8192), (144, 4096)):
+        info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span))
+        assert info["launches"] == 2 and info["blocks"] * info["waves_per_block"] <= 256 * 8, (rows, span, info)
+    info = ppk.int8_kv_ops.plan_info(_attn_args(rows=240, capacity=20001, max_past=20000))
+    assert info["split_tokens"] <= 2048 and info["launches"] == 2
     # Spans that are no multiple of the power-of-two split: each row gets as many waves as the budget holds
     # (2048 / 512 rows = 4) with equal shares rounded up to whole tiles (1100 / 4 = 275 -> 280 for the int8
     # path's 8-token tiles, 276 for bf16's 4-token tiles at D = 128), one block per row.
     assert ppk.int8_kv_ops.plan(_attn_args(capacity=1101, max_past=1100)) == (280, 1, 0)
     assert ppk.int8_kv_ops.plan(_attn_args(rows=256, capacity=1501, max_past=1500)) == (192, 1, 0)
     assert ppk.fused_attention.plan(_float_args(size=1100)) == (276, 1, 0)
-
-
-def _per_row_waves(rows, span, split, token_bytes, cus=256):
-    """Waves per block of the per-row plan with automatic split `split`: a row's ceil(span / split) waves in
-    one block of at most min(16, 16384 / split); rows fewer than the CUs holding more than 128 KiB are cut
-    into blocks of about 256 KiB, then smaller until the blocks cover every CU; a row's waves spread evenly
-    over its blocks."""
-    per_row = -(-span // split)
-    most = max(1, min(16, 16384 // split))
-    if rows < cus and span * token_bytes > 128 << 10:
-        w = max(1, min(most, (256 << 10) // (split * token_bytes)))
-        while w > 1 and rows * -(-per_row // w) < cus:
-            w -= 1
-        most = w
-    if per_row <= most:
-        return per_row
-    groups = -(-per_row // most)
-    return -(-per_row // groups)
 
 
 def _cu_peaks(lens, heads, per_row, share, cus=256, waves_per_block=4):
@@ -252,14 +248,18 @@ def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
         live = [int(p) if p <= min(cap, span) else 0 for p in past]
         # The per-row plan with host lengths covers the longest live row (at least one token).
         cover = max(1, max(live))
-        per_row = ppk.int8_kv_ops.plan(_attn_args(rows=rows, heads=heads, capacity=cap, max_past=cover, head_dim=d))
+        per_row_args = _attn_args(rows=rows, heads=heads, capacity=cap, max_past=cover, head_dim=d)
+        per_row = ppk.int8_kv_ops.plan(per_row_args)
+        # The per-row plan's block size as the library reports it (its sizing rules are pinned by the plan
+        # tests above); the balanced-or-per-row choice below is restated independently.
+        per_row_waves = ppk.int8_kv_ops.plan_info(per_row_args)["waves_per_block"]
         split, groups, nbytes = ppk.int8_kv_ops.plan(a)
         if 2 * rows > 2048 or max(live) * batch * 10 <= sum(live) * 11:  # too many rows, or not ragged
             assert (split, groups, nbytes) == per_row
             continue
         units, share = _flat_units([int(p) for p in past], heads, rows, cap, span, 2048)
         S, G = per_row[:2]
-        if not _balanced_pays(live, heads, (S, _per_row_waves(rows, cover, S, 2 * d + 8), G), share, max(units),
+        if not _balanced_pays(live, heads, (S, per_row_waves, G), share, max(units),
                               2 * d + 8):
             assert (split, groups, nbytes) == per_row, "per-row plan kept"
             continue

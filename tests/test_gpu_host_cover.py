@@ -26,9 +26,12 @@ HOST = [1000, 950, 980]
 
 
 def _int8_plan(c: Case, host, **kw):
+    """(split, groups, waves per block, blocks, launches): two spans can share split and groups and differ
+    only in how many waves each block holds."""
     a, _ = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, past_host=host,
                                           **kw)
-    return ppk.int8_kv_ops.plan(a, ppk.context(c.q.device))
+    i = ppk.int8_kv_ops.plan_info(a, ppk.context(c.q.device))
+    return i["split_tokens"], i["nsplits"], i["waves_per_block"], i["blocks"], i["launches"]
 
 
 @pytest.mark.parametrize("d", [64, 128])
