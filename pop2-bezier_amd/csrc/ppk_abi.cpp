@@ -266,6 +266,43 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     }
     max_waves = w;
   }
+  // int8, at least as many rows as CUs: blocks of a row's 3, 5, 6 or 7
+  // waves (the budget split over 288-640 rows) hold one or two per CU and
+  // run a second round. Either a power-of-two number of waves per row in
+  // one block (no merge, but the busiest CUs stream one row more than the
+  // mean share), or the row's waves in smaller blocks that spread evenly
+  // over the CUs' slots, joined by the merge kernel. The first pays while
+  // the busiest CUs' excess is at most 160 KiB. Same-box A/B, H = 16,
+  // two-round plan -> this rule (the other one): D = 128, 288 rows x 1024
+  // tokens 25.2 -> 17.1 (19.0) us, x 4096 72.1 -> 51.3 (65.1), x 8192
+  // 133.7 -> 97.3 (125.4); 288 x 700 -> 14.7 (15.8); 320 x 8192 143.9 ->
+  // 107.8 (128.6); 384 x 1024 27.7 -> 19.8 (21.3), x 8192 158.7 -> 130.4
+  // (135.0); 640 x 4096 120.5 -> 110.0 (115.7); D = 64, 384 x 1024 19.5 ->
+  // 12.9 (15.4), x 2048 -> 20.1 (21.9); 288 x 8192 74.3 -> 53.9 (67.5); 640
+  // x 1500 -> 25.5 (26.6). Of 36 shapes measured both ways the rule missed
+  // the faster plan on three, by 0.6-0.9 us.
+  if (!explicit_split && block_waves <= 8 && rows >= cus && rows * waves_per_row <= cus * 8) {
+    const uint64_t slots = 8;  // int8 waves resident per CU
+    auto fits = [&](uint64_t mw) {
+      const uint64_t g = (waves_per_row + mw - 1) / mw, wv = (waves_per_row + g - 1) / g;
+      return rows * g <= cus * (slots / wv);
+    };
+    if (!fits(max_waves)) {
+      const uint64_t per_cu = (rows + cus - 1) / cus;
+      if ((per_cu * cus - rows) * row_bytes <= cus * (160u << 10)) {
+        uint64_t p = 1;
+        while (p * 2 <= waves_per_row) p *= 2;
+        split = uint32_t(std::max<uint64_t>(((span + p - 1) / p + tpl - 1) / tpl * tpl, tpl));
+        waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
+        max_waves = std::max<uint64_t>(1, std::min<uint64_t>(block_waves, 16384 / split));
+      } else {
+        uint64_t w = 1;
+        while (w * 2 <= max_waves) w *= 2;
+        while (w > 1 && !fits(w)) w /= 2;
+        max_waves = w;
+      }
+    }
+  }
   plan.split = split;
   if (waves_per_row <= max_waves) {
     plan.waves = uint32_t(waves_per_row);

@@ -163,6 +163,23 @@ def test_plan_sizes_workspace_without_a_device():
         assert info["launches"] == 2 and info["blocks"] * info["waves_per_block"] <= 256 * 8, (rows, span, info)
     info = ppk.int8_kv_ops.plan_info(_attn_args(rows=240, capacity=20001, max_past=20000))
     assert info["split_tokens"] <= 2048 and info["launches"] == 2
+    # At least as many rows as CUs, where the budget gives each row 3, 5, 6 or 7 waves (one block each, a second
+    # round): short rows take a power-of-two number of waves in one block (384 x 1024 at D = 64: 4 waves of 256
+    # tokens; the busiest CUs stream 139 KB a row more than the mean share, half a row), longer ones keep their
+    # waves in 1- or 2-wave blocks that fill the CUs' slots, joined by the merge (384 x 8192 at D = 128: five
+    # 1640-token waves as 1-wave blocks; 320 x 4096: six waves as three 2-wave blocks).
+    for rows, span, d, want in ((384, 1024, 64, (256, 1, 4, 384, 1)), (384, 8192, 128, (1640, 5, 1, 1920, 2)),
+                                (320, 4096, 128, (688, 3, 2, 960, 2)), (288, 700, 128, (176, 1, 4, 288, 1))):
+        info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span, head_dim=d))
+        got = (info["split_tokens"], info["nsplits"], info["waves_per_block"], info["blocks"], info["launches"])
+        assert got == want, (rows, span, d, got)
+    for rows in range(256, 1100, 16):
+        for span in (700, 1024, 3000, 4096, 8192):
+            for d in (64, 128):
+                info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span, head_dim=d))
+                resident = 256 * (8 // info["waves_per_block"])
+                waves = rows * -(-span // info["split_tokens"])
+                assert info["blocks"] <= resident or waves > 256 * 8, (rows, span, d, info)
     # Spans that are no multiple of the power-of-two split: each row gets as many waves as the budget holds
     # (2048 / 512 rows = 4) with equal shares rounded up to whole tiles (1100 / 4 = 275 -> 280 for the int8
     # path's 8-token tiles, 276 for bf16's 4-token tiles at D = 128), one block per row.

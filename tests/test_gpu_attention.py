@@ -189,6 +189,22 @@ def test_two_round_grids_take_one_block_per_row(device, bf16h):
         assert_close(got, c.reference(), what="one block per row")
 
 
+@pytest.mark.parametrize("B,D,L,want", [(24, 128, 8192, (1640, 5, 1)), (18, 64, 4096, (592, 7, 1)),
+                                        (24, 64, 1024, (256, 1, 4))])
+def test_rows_beyond_the_cus_fill_one_round(device, B, D, L, want):
+    """288-384 rows whose budget share (5-7 waves a row) would make blocks that run a second round: longer rows
+    keep their waves as 1-wave blocks joined by the merge, short rows take four waves in one block; ragged
+    lengths within the span (every fifth sequence empty or one token)."""
+    lengths = [L - (37 * i) % (L // 2) for i in range(B)]
+    lengths[::5] = [0, 1, 0, 1, 0][: len(lengths[::5])]
+    c = Case(device, B, 16, D, lengths, L + 1, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16,
+             seed=SEED + 29 + B)
+    a, _ = ppk.int8_kv_ops.attention_args(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, c.H, max_past=L)
+    info = ppk.int8_kv_ops.plan_info(a, ppk.context(device))
+    assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == want
+    assert_close(c.run(max_past=L), c.reference(), what=f"{B * 16} rows x {L} at D = {D}")
+
+
 @pytest.mark.parametrize("split", [0, 32])
 def test_long_rows_merge_more_than_64_groups(device, split):
     """Two rows of 65536 tokens: each row spans hundreds of blocks (the automatic plan's 64-token waves, or
