@@ -266,41 +266,75 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     }
     max_waves = w;
   }
-  // int8, at least as many rows as CUs: blocks of a row's 3, 5, 6 or 7
-  // waves (the budget split over 288-640 rows) hold one or two per CU and
-  // run a second round. Either a power-of-two number of waves per row in
-  // one block (no merge, but the busiest CUs stream one row more than the
-  // mean share), or the row's waves in smaller blocks that spread evenly
-  // over the CUs' slots, joined by the merge kernel. The first pays while
-  // the busiest CUs' excess is at most 160 KiB. Same-box A/B, H = 16,
-  // two-round plan -> this rule (the other one): D = 128, 288 rows x 1024
-  // tokens 25.2 -> 17.1 (19.0) us, x 4096 72.1 -> 51.3 (65.1), x 8192
-  // 133.7 -> 97.3 (125.4); 288 x 700 -> 14.7 (15.8); 320 x 8192 143.9 ->
-  // 107.8 (128.6); 384 x 1024 27.7 -> 19.8 (21.3), x 8192 158.7 -> 130.4
+  // At least as many rows as CUs, one block per row: a CU runs the blocks
+  // of ceil(rows / CUs) rows while the mean is rows / CUs, and a CU alone
+  // streams only ~35 GB/s. int8 blocks of a row's 3, 5, 6 or 7 waves (the
+  // budget split over 288-640 rows) also hold only one or two per CU and
+  // run a second round. Two remedies: a power-of-two number of waves per
+  // row in one block (int8, two-round grids only: no merge, the busiest CUs
+  // still stream one row more than the mean), or the row's waves in
+  // smaller blocks that spread evenly over the CUs, joined by the merge
+  // kernel. The first pays while the busiest CUs' excess is at most 160
+  // KiB. The second pays where the excess is larger and the busiest CUs
+  // carry at most 1/0.85 of the mean (beyond that HBM, not the busiest CUs,
+  // sets the time: 448 rows, 1.75 of 2, lost 2-4 % with it). Same-box A/B,
+  // H = 16, previous plan -> this rule (the other remedy, int8): D = 128,
+  // int8, 288 rows x 1024 tokens 25.2 -> 17.1 (19.0) us, x 4096 72.1 ->
+  // 51.3 (65.1), x 8192 133.7 -> 97.3 (125.4); 320 x 8192 143.9 -> 107.8
+  // (128.6); 384 x 1024 27.7 -> 19.8 (21.3), x 8192 158.7 -> 130.4
   // (135.0); 640 x 4096 120.5 -> 110.0 (115.7); D = 64, 384 x 1024 19.5 ->
-  // 12.9 (15.4), x 2048 -> 20.1 (21.9); 288 x 8192 74.3 -> 53.9 (67.5); 640
-  // x 1500 -> 25.5 (26.6). Of 36 shapes measured both ways the rule missed
-  // the faster plan on three, by 0.6-0.9 us.
-  if (!explicit_split && block_waves <= 8 && rows >= cus && rows * waves_per_row <= cus * 8) {
+  // 12.9 (15.4); 288 x 8192 74.3 -> 53.9 (67.5); of 36 int8 shapes measured
+  // both ways the rule took the slower remedy on three, by 0.6-0.9 us.
+  // bf16 float store, D = 128: 288 x 4096 121.3 -> 91.6, x 8192 239.8 ->
+  // 177.5; 320 x 8192 251.3 -> 195.5; 384 x 8192 252.4 -> 240.8; 576 x 4096
+  // 211.3 -> 186.7; 640 x 4096 216.9 -> 209.5; D = 64 288 x 8192 123.5 ->
+  // 93.8; 576 x 1024 25.0 -> 25.7 (the one loss measured).
+  if (!explicit_split && rows >= cus && rows * waves_per_row <= cus * 8) {
+    const bool int8 = block_waves <= 8;
     const uint64_t slots = 8;  // int8 waves resident per CU
+    const uint64_t limit = cus * (160u << 10);
+    const uint64_t per_cu = (rows + cus - 1) / cus;
+    auto groups = [&](uint64_t mw) { return (waves_per_row + mw - 1) / mw; };
     auto fits = [&](uint64_t mw) {
-      const uint64_t g = (waves_per_row + mw - 1) / mw, wv = (waves_per_row + g - 1) / g;
-      return rows * g <= cus * (slots / wv);
+      const uint64_t g = groups(mw), wv = (waves_per_row + g - 1) / g;
+      return !int8 || rows * g <= cus * (slots / wv);
     };
-    if (!fits(max_waves)) {
-      const uint64_t per_cu = (rows + cus - 1) / cus;
-      if ((per_cu * cus - rows) * row_bytes <= cus * (160u << 10)) {
-        uint64_t p = 1;
-        while (p * 2 <= waves_per_row) p *= 2;
-        split = uint32_t(std::max<uint64_t>(((span + p - 1) / p + tpl - 1) / tpl * tpl, tpl));
-        waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
-        max_waves = std::max<uint64_t>(1, std::min<uint64_t>(block_waves, 16384 / split));
-      } else {
-        uint64_t w = 1;
+    auto excess = [&](uint64_t mw) {  // bytes, times the CU count
+      const uint64_t g = groups(mw), wv = (waves_per_row + g - 1) / g, blocks = rows * g;
+      return (((blocks + cus - 1) / cus) * cus - blocks) * wv * split * token_bytes;
+    };
+    const bool two_rounds = !fits(max_waves);
+    if (two_rounds && (per_cu * cus - rows) * row_bytes <= limit) {
+      uint64_t p = 1;
+      while (p * 2 <= waves_per_row) p *= 2;
+      split = uint32_t(std::max<uint64_t>(((span + p - 1) / p + tpl - 1) / tpl * tpl, tpl));
+      waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
+      max_waves = std::max<uint64_t>(1, std::min<uint64_t>(block_waves, 16384 / split));
+    } else if (two_rounds || (excess(max_waves) > limit && 20 * rows <= 17 * per_cu * cus)) {
+      // The largest blocks (powers of two for int8) within the excess, else
+      // the smallest excess.
+      uint64_t w = max_waves;
+      if (int8) {
+        w = 1;
         while (w * 2 <= max_waves) w *= 2;
-        while (w > 1 && !fits(w)) w /= 2;
-        max_waves = w;
       }
+      uint64_t best = w, best_x = ~uint64_t(0);
+      for (;;) {
+        if (fits(w)) {
+          const uint64_t x = excess(w);
+          if (x <= limit) {
+            best = w;
+            break;
+          }
+          if (x < best_x) {
+            best_x = x;
+            best = w;
+          }
+        }
+        if (w == 1) break;
+        w = int8 ? w / 2 : w - 1;
+      }
+      max_waves = best;
     }
   }
   plan.split = split;

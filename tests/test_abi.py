@@ -186,6 +186,14 @@ def test_plan_sizes_workspace_without_a_device():
     assert ppk.int8_kv_ops.plan(_attn_args(capacity=1101, max_past=1100)) == (280, 1, 0)
     assert ppk.int8_kv_ops.plan(_attn_args(rows=256, capacity=1501, max_past=1500)) == (192, 1, 0)
     assert ppk.fused_attention.plan(_float_args(size=1100)) == (276, 1, 0)
+    # The float path with at least as many rows as CUs: one block per row leaves the busiest CUs a whole row
+    # more than the mean (288 rows: 2 against 1.125), so the row's waves go to small blocks spread evenly over
+    # the CUs (seven 1-wave blocks of 588 tokens, 2016 blocks) and the merge; at 448 rows (1.75 of 2) HBM sets
+    # the time and the one-block plan stays; 512 rows are even already.
+    for rows, size, d, want in ((288, 4096, 128, (588, 7, 1)), (576, 1024, 128, (344, 3, 1)),
+                                (448, 4096, 128, (1024, 1, 4)), (512, 8192, 128, (2048, 1, 4))):
+        info = ppk.fused_attention.plan_info(_float_args(rows=rows, size=size, head_dim=d))
+        assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == want, (rows, size, d, info)
 
 
 def _cu_peaks(lens, heads, per_row, share, cus=256, waves_per_block=4):

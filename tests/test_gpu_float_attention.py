@@ -187,6 +187,20 @@ def test_long_rows_merge_more_than_64_groups(device, kv):
     assert_close(got, c.reference(), atol=ATOL, rtol=RTOL, what=f"65000 tokens, {call.ngroups} groups")
 
 
+@pytest.mark.parametrize("B,D,size,want", [(18, 64, 2048, (296, 3, 3)), (20, 128, 2048, (344, 3, 2))])
+def test_rows_beyond_the_cus_spread_over_small_blocks(device, B, D, size, want):
+    """288 / 320 rows: one block per row would give the busiest CUs two rows against a mean of 1.1-1.3, so each
+    row's waves go to 2- or 3-wave blocks joined by the merge; ragged lengths, some empty."""
+    lengths = [size - (53 * i) % (size // 2) for i in range(B)]
+    lengths[3], lengths[7] = 0, 1
+    c = FloatCase(device, B, 16, D, size, torch.bfloat16, lengths=lengths, seed=SEED + 31 + B)
+    call = ppk.FloatDecodeAttention(c.q, c.k, c.v, c.lengths_t, c.H, max_length=size)
+    info = call.plan_info
+    assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == want
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    assert_close(got, c.reference(), atol=ATOL, rtol=RTOL, what=f"{c.rows} rows x {size} at D = {D}")
+
+
 def test_hip_graph_replay(device):
     """A prepared call captured in a HIP graph replays bit-identically to the eager call."""
     c = FloatCase(device, 1, 16, 64, 1024, torch.bfloat16, lengths=[900], seed=SEED + 11)
