@@ -237,6 +237,26 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
       w = fit(std::max<uint64_t>(1, std::min<uint64_t>(max_waves, (256u << 10) / (uint64_t(split) * token_bytes))));
       while (w > 1 && rows * ((waves_per_row + w - 1) / w) < cus) w = shrink(w);
     }
+    // Larger blocks where they land evenly: the row's waves split exactly
+    // into the blocks, and the busiest CU runs at most 7 % more waves than
+    // the mean (fewer records to merge, fewer block joins). Same-box A/B, H
+    // = 16, int8 D = 128: 128 rows x 8192 tokens, 1-wave -> 8-wave blocks,
+    // 50.4 -> 44.9 us; 32 x 16384 28.97 -> 25.2; 64 x 8192 27.2 -> 25.6; 96 x
+    // 8192 40.3 -> 38.4; 160 x 8192 58.9 -> 55.6; config 4 17.3 -> 17.0; D =
+    // 64, 128 x 16384 51.2 -> 48.2; bf16 store, 64 rows x 8192 at D = 64 26.2
+    // -> 23.4, 64 x 4096 at D = 128 24.2 -> 22.8; of 52 shapes it changes
+    // five lost 0.2-0.5 us and one ragged batch (host lengths, 192 rows of
+    // 1422-7798 tokens) 1.4 us of 50. Blocks that land unevenly lost 5-10 %
+    // (48 rows x 8192, 2 -> 4-wave blocks: the busiest CUs 8 waves against a
+    // mean of 6).
+    for (uint64_t u = fit(max_waves); u > w; u = shrink(u)) {
+      const uint64_t g = (waves_per_row + u - 1) / u, wv = (waves_per_row + g - 1) / g, nb = rows * g;
+      if (nb < cus || g * wv != waves_per_row || (pow2 && nb > cus * (8 / wv))) continue;
+      if (100 * ((nb + cus - 1) / cus) * wv * cus <= 107 * rows * waves_per_row) {
+        w = u;
+        break;
+      }
+    }
     // int8: a grid whose blocks do not all fit the CUs' eight wave slots at
     // once runs a second round, and its merge launch waits for the last one.
     // When eight waves of a longer share cover each row, one block per row

@@ -158,6 +158,12 @@ def test_plan_sizes_workspace_without_a_device():
         info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span, head_dim=d))
         got = (info["split_tokens"], info["nsplits"], info["waves_per_block"], info["blocks"], info["launches"])
         assert got == want, (rows, span, d, got)
+    # Larger blocks where they land evenly (the row's waves split exactly, the busiest CU within 7 % of the
+    # mean): 128 rows x 8192 as two 8-wave blocks a row (256 blocks, one a CU) instead of sixteen 1-wave
+    # blocks; 48 rows x 8192 keeps 2-wave blocks (4-wave ones would give the busiest CUs 8 waves, mean 6).
+    for rows, span, want in ((128, 8192, (512, 2, 8)), (48, 8192, (256, 16, 2))):
+        info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span))
+        assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == want, (rows, span, info)
     for rows, span in ((192, 8192), (144, 4096)):
         info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span))
         assert info["launches"] == 2 and info["blocks"] * info["waves_per_block"] <= 256 * 8, (rows, span, info)
