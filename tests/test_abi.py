@@ -582,3 +582,22 @@ def test_plan_info_reports_the_plan_taken():
     small = _abi.PpkAttentionPlanInfo(struct_size=8)
     assert _abi.lib().ppk_attention_plan_info(None, ctypes.byref(_attn_args()), ctypes.byref(small)) == \
         _abi.PPK_PRECONDITION
+
+
+def test_auto_plans_respect_the_kernels_limits():
+    """Every automatic plan, over row counts around the CU count and its multiples, spans from one token to
+    65536 and D = 64 / 128 / 256: int8 blocks of 1-8 waves, float blocks of 1-16, at most 16384 tokens per
+    block (one float of LDS per token), and the groups cover the span."""
+    rows_list = [1, 3, 16, 100, 255, 256, 257, 288, 384, 448, 511, 512, 513, 640, 1000, 2048, 4096]
+    spans = [1, 63, 64, 65, 300, 1024, 1445, 2048, 3000, 8192, 12000, 20000, 65536]
+    for rows in rows_list:
+        for span in spans:
+            for d in (64, 128, 256):
+                i = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, heads=1, capacity=span + 1, max_past=span,
+                                                         head_dim=d))
+                w, s = i["waves_per_block"], i["split_tokens"]
+                assert 1 <= w <= 8 and w * s <= 16384 and i["nsplits"] * w * s >= span, (rows, span, d, i)
+                i = ppk.fused_attention.plan_info(_float_args(rows=rows, heads=1, size=span + 1, max_length=span,
+                                                              head_dim=d, lengths=8))
+                w, s = i["waves_per_block"], i["split_tokens"]
+                assert 1 <= w <= 16 and w * s <= 16384 and i["nsplits"] * w * s >= span, (rows, span, d, i)
