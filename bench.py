@@ -65,8 +65,10 @@ def parse() -> argparse.Namespace:
                         "current token at slot lengths[b] - 1, attend lengths[b] tokens) beside the reference's "
                         "order (the token written by torch indexing, then the attention call)")
     p.add_argument("--lengths", default=None,
-                   help="with --kv bf16/f32: comma-separated per-sequence lengths of a ragged batch (NxL repeats "
-                        "L N times); the batch is their count and the store holds the longest")
+                   help="with --kv bf16/f32 or --config 4: comma-separated per-sequence lengths of a ragged batch "
+                        "(NxL repeats L N times; uniform:B:LO:HI:SEED draws B lengths from numpy's "
+                        "default_rng(SEED).integers(LO, HI + 1)); the batch is their count and the store holds the "
+                        "longest")
     p.add_argument("--bf16-history", action="store_true",
                    help="int8 decode: round every dequantised history element to bf16 before the fp32 dot "
                         "(PPK_ATTN_BF16_HISTORY, the reference kernel's pp_i8_load arithmetic; kernels "
@@ -410,10 +412,7 @@ def bench_float(args) -> int:
     torch.cuda.set_device(dev)
     H, D = args.heads, args.head_dim
     if args.lengths:
-        seq = []
-        for part in args.lengths.split(","):
-            n, _, length = part.strip().rpartition("x")
-            seq += [int(length)] * (int(n) if n else 1)
+        seq = parse_lengths(args.lengths)
         B, L = len(seq), max(seq)
     else:
         B, L = args.batch, args.context
@@ -889,6 +888,21 @@ def bench_arena(args) -> int:
 
 
 # latency-bound shapes of the same path (the headline is config 5).
+def parse_lengths(text: str) -> list:
+    """--lengths: comma-separated lengths, NxL for L repeated N times, or uniform:B:LO:HI:SEED for B draws of
+    numpy's default_rng(SEED).integers(LO, HI + 1)."""
+    import numpy as np
+
+    if text.startswith("uniform:"):
+        b, lo, hi, seed = (int(x) for x in text.split(":")[1:])
+        return [int(x) for x in np.random.default_rng(seed).integers(lo, hi + 1, size=b)]
+    seq = []
+    for part in text.split(","):
+        n, _, length = part.strip().rpartition("x")
+        seq += [int(length)] * (int(n) if n else 1)
+    return seq
+
+
 CONFIGS = {
     1: {"batch": 1, "heads": 16, "head_dim": 64, "lengths": [512], "layers": 1, "query": "f32",
         "workload": "BASELINE config 1: decode step (append + attention) over a 512-token int8 history, f32 q/K/V"},
@@ -941,7 +955,10 @@ def bench_config(args) -> int:
         torch.cuda.synchronize()
         del src
     B, H, D, layers = cfg["batch"], cfg["heads"], cfg["head_dim"], cfg["layers"]
-    if cfg["lengths"] is None:
+    if args.lengths:  # config 4's step over other ragged lengths (and head widths)
+        lengths = parse_lengths(args.lengths)
+        B, D = len(lengths), args.head_dim
+    elif cfg["lengths"] is None:
         lengths = [int(x) for x in np.random.default_rng(SEED).integers(256, 4097, size=B)]
     else:
         lengths = cfg["lengths"] * B
@@ -1054,7 +1071,9 @@ def bench_config(args) -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded N(0,1) with 2% heavy-tailed 10*t3 channels, quantised on device; "
                 f"{cfg['query']} q and current K/V)",
-        "config": {"workload": cfg["workload"], "batch": B, "heads": H, "head_dim": D, "lengths": lengths,
+        "config": {"workload": (f"config 4's decode step over ragged int8 histories, lengths {args.lengths}"
+                                if args.lengths else cfg["workload"]),
+                   "batch": B, "heads": H, "head_dim": D, "lengths": lengths,
                    "layers": layers, "capacity": cap, "kv": "int8 + f32 scales", "query": cfg["query"],
                    "plan": "balanced work list (host lengths)" if balanced else "per-row blocks",
                    "tokens_per_wave": split, ("units_per_row_max" if balanced else "blocks_per_row"): ngroups,
@@ -1389,6 +1408,9 @@ def main() -> int:
         return bench_float(args)
     if args.config == 2:
         return bench_append(args)
+    if args.lengths and args.config != 4:
+        print("bench.py: --lengths takes --kv bf16|f32 or --config 4", file=sys.stderr)
+        return 2
     if args.config != 5:
         return bench_config(args)
     import torch

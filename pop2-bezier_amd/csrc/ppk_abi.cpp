@@ -480,14 +480,27 @@ uint64_t flat_cu_peak(const AttentionPlan& p, uint32_t heads, uint32_t cus) {
 }
 
 // Modelled duration in microseconds of an int8 attention launch plan on
-// MI355X: a fixed cost (7.5 us for one launch, 9.25 us with the merge launch)
-// plus the longer of the device streaming the whole live history at 25 GB/s
-// per CU (6.4 TB/s over 256 CUs; a partition of the device has its share)
-// and the busiest CU streaming its share at 37 GB/s. Fitted to 42 measured
-// ragged batches (B = 4 .. 64, H = 16, D = 64 / 128, per-row and balanced
-// plans): within 2.6 us rms of the measured step.
-static double modelled_us(uint64_t total_bytes, uint64_t cu_peak_bytes, bool merge, uint32_t cus) {
-  return (merge ? 9.25 : 7.5) + std::max(double(total_bytes) / (25e3 * cus), double(cu_peak_bytes) / 37e3);
+// MI355X: a fixed cost, plus the whole live history streamed at `stream`
+// bytes/us per CU (a partition of the device has its share), plus the
+// busiest CU's bytes beyond the mean at `excess` bytes/us. Fitted per plan
+// kind (least squares on the relative error) to 140 ragged batches measured
+// with both plans forced on one box (B = 4 .. 64, H = 16, D = 64 / 128;
+// uniform U[lo, hi] draws and long rows beside short ones): taking the
+// plan the model favours (and the long-wave rule of balanced_pays) lost
+// 34.8 us over the 140 steps against always taking the faster one, with 6
+// picks more than 2 % slower; the single max(stream, busiest CU) model it
+// replaces, fitted before the per-row plan's larger blocks, lost 59.8 us
+// with 24.
+struct PlanCost {
+  double one_launch, with_merge, stream, excess;
+};
+constexpr PlanCost kPerRowCost{4.75, 7.3, 27.8e3, 64e3};
+constexpr PlanCost kBalancedCost{7.0, 9.9, 27.2e3, 63e3};
+static double modelled_us(const PlanCost& c, uint64_t total_bytes, uint64_t cu_peak_bytes, bool merge,
+                          uint32_t cus) {
+  const double mean = double(total_bytes) / cus;
+  return (merge ? c.with_merge : c.one_launch) + double(total_bytes) / (c.stream * cus) +
+         std::max(0.0, double(cu_peak_bytes) - mean) / c.excess;
 }
 
 bool balanced_pays(const ppk_context* ctx, const AttentionPlan& per_row, const AttentionPlan& flat, uint32_t rows,
@@ -498,14 +511,14 @@ bool balanced_pays(const ppk_context* ctx, const AttentionPlan& per_row, const A
   uint64_t total = 0;
   for (uint32_t b = 0; b < rows / heads; ++b) total += host[b] <= limit ? host[b] : 0;
   total *= uint64_t(heads) * token_bytes;
-  const double t_row = modelled_us(total, row_peak * token_bytes, per_row.ngroups > 1, cus);
-  const double t_flat = modelled_us(total, flat_peak * token_bytes, flat.ngroups > 1, cus);
-  // Balanced when the model has it at least 0.75 us faster; and when per-row
+  const double t_row = modelled_us(kPerRowCost, total, row_peak * token_bytes, per_row.ngroups > 1, cus);
+  const double t_flat = modelled_us(kBalancedCost, total, flat_peak * token_bytes, flat.ngroups > 1, cus);
+  // Balanced when the model has it faster; and when per-row
   // waves would each stream 256 KiB or more and the per-row plan's busiest CU
   // streams at least 1.2 x the balanced plan's (long waves run below the
   // modelled CU rate: 8 x 4096 beside 24 x 1024 tokens at D = 128 measured
   // 53.2 us per-row, 45.2 us balanced).
-  return t_flat + 0.75 < t_row ||
+  return t_flat < t_row ||
          (uint64_t(per_row.split) * token_bytes >= (256u << 10) && 5 * row_peak >= 6 * flat_peak);
 }
 

@@ -224,18 +224,21 @@ def _cu_peaks(lens, heads, per_row, share, cus=256, waves_per_block=4):
 
 
 def _balanced_pays(lens, heads, per_row, share, flat_groups, token_bytes):
-    """The library's pick between the plans: a modelled step of 7.5 us per launch plan (9.25 us when it has a
-    merge launch) plus the longer of the 256 CUs streaming the live history at 25 GB/s each (6.4 TB/s) and the
-    busiest CU streaming its share at 37 GB/s; balanced when modelled at least 0.75 us faster, or when per-row waves stream 256 KiB or
-    more each and the per-row plan's busiest CU streams at least 1.2 x the balanced plan's."""
+    """The library's pick between the plans: a modelled step of a fixed cost (per-row 4.75 us for one launch,
+    7.3 us with the merge; balanced 7.0 / 9.9 us), plus the live history streamed at 27.8 (per-row) / 27.2
+    (balanced) GB/s per CU over 256 CUs, plus the busiest CU's bytes beyond the mean at 64 / 63 GB/s; balanced
+    when modelled faster, or when per-row waves stream 256 KiB or more each and the per-row plan's busiest CU
+    streams at least 1.2 x the balanced plan's."""
     S, W, G = per_row
-    row_peak, flat_peak = _cu_peaks(lens, heads, per_row, share)
+    row_peak, flat_peak = _cu_peaks(lens, heads, per_row, share, waves_per_block=W)
+    flat_peak = _cu_peaks(lens, heads, per_row, share)[1]
     total = sum(lens) * heads * token_bytes
 
-    def modelled(peak, merge):
-        return (9.25 if merge else 7.5) + max(total / (25e3 * 256), peak * token_bytes / 37e3)
+    def modelled(peak, merge, one, merged, stream, excess):
+        return (merged if merge else one) + total / (stream * 256) + max(0.0, peak * token_bytes - total / 256) / excess
 
-    return (modelled(flat_peak, flat_groups > 1) + 0.75 < modelled(row_peak, G > 1)
+    return (modelled(flat_peak, flat_groups > 1, 7.0, 9.9, 27.2e3, 63e3)
+            < modelled(row_peak, G > 1, 4.75, 7.3, 27.8e3, 64e3)
             or (S * token_bytes >= 256 << 10 and 5 * row_peak >= 6 * flat_peak))
 
 
@@ -293,7 +296,10 @@ def test_balanced_plan_covers_every_row_within_the_waves(heads, d):
         if not _balanced_pays(live, heads, (S, per_row_waves, G), share, max(units),
                               2 * d + 8):
             assert (split, groups, nbytes) == per_row, "per-row plan kept"
-            continue
+            # The balanced plan, forced, still covers the rows as below.
+            a = _attn_args(rows=rows, heads=heads, capacity=cap, max_past=span, head_dim=d, past_host=past,
+                           flags=_abi.PPK_ATTN_PLAN_BALANCED)
+            split, groups, nbytes = ppk.int8_kv_ops.plan(a)
         assert split == share and groups == max(units)
         assert sum(units) <= 2048, "every unit has a wave"
         for p, u in zip(np.repeat(past, heads), units):
