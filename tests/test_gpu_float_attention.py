@@ -201,6 +201,21 @@ def test_rows_beyond_the_cus_spread_over_small_blocks(device, B, D, size, want):
     assert_close(got, c.reference(), atol=ATOL, rtol=RTOL, what=f"{c.rows} rows x {size} at D = {D}")
 
 
+def test_few_long_rows_take_larger_blocks_that_land_evenly(device):
+    """64 rows of up to 8192 tokens at D = 64: 32 waves of 256 tokens a row in four 8-wave blocks (256 blocks,
+    one a CU) joined by the merge, instead of 4-wave blocks; ragged lengths, one sequence empty."""
+    size = 8192
+    c = FloatCase(device, 4, 16, 64, size, torch.bfloat16, lengths=[8192, 0, 5000, 8191], seed=SEED + 37)
+    call = ppk.FloatDecodeAttention(c.q, c.k, c.v, c.lengths_t, c.H, max_length=size)
+    info = call.plan_info
+    assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == (256, 4, 8)
+    got = call().float().reshape(c.rows, c.D).cpu().numpy()
+    ref = c.reference()
+    assert np.isnan(got[16:32]).all() and np.isnan(ref[16:32]).all()
+    keep = np.r_[0:16, 32:64]
+    assert_close(got[keep], ref[keep], atol=ATOL, rtol=RTOL, what="64 rows x 8192 at D = 64, 8-wave blocks")
+
+
 def test_hip_graph_replay(device):
     """A prepared call captured in a HIP graph replays bit-identically to the eager call."""
     c = FloatCase(device, 1, 16, 64, 1024, torch.bfloat16, lengths=[900], seed=SEED + 11)
