@@ -211,7 +211,7 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     // at D = 128: 7-wave blocks, 320 of them on 256 CUs, 25.3 us; 4-wave
     // blocks, one round, 17.0 us). The float kernels hold more waves per CU
     // and take any block size.
-    const bool pow2 = block_waves <= 8;
+    const bool pow2 = block_waves <= kInt8WavesPerCu;
     auto fit = [&](uint64_t w) {
       uint64_t p = 1;
       while (pow2 && p * 2 <= w) p *= 2;
@@ -251,7 +251,7 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     // mean of 6).
     for (uint64_t u = fit(max_waves); u > w; u = shrink(u)) {
       const uint64_t g = (waves_per_row + u - 1) / u, wv = (waves_per_row + g - 1) / g, nb = rows * g;
-      if (nb < cus || g * wv != waves_per_row || (pow2 && nb > cus * (8 / wv))) continue;
+      if (nb < cus || g * wv != waves_per_row || (pow2 && nb > cus * (kInt8WavesPerCu / wv))) continue;
       if (100 * ((nb + cus - 1) / cus) * wv * cus <= 107 * rows * waves_per_row) {
         w = u;
         break;
@@ -271,9 +271,8 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     // 40.1 (41.8). Grids that fit one round keep their plan: one block per
     // row would idle more CUs than a merge costs (192 x 8192 at D = 128
     // splits ten ways, 67.6 us).
-    const uint64_t slots = 8;  // int8 waves resident per CU
     auto blocks = [&](uint64_t n) { return rows * ((waves_per_row + n - 1) / n); };
-    if (pow2 && blocks(w) > cus * (slots / w)) {
+    if (pow2 && blocks(w) > cus * (kInt8WavesPerCu / w)) {
       const uint64_t whole = std::max<uint64_t>(
           1, ((span + block_waves - 1) / block_waves + tpl - 1) / tpl * tpl);  // 8 waves cover a row
       if (rows * block_waves <= budget && whole * block_waves <= 16384) {
@@ -281,7 +280,7 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
         waves_per_row = std::max<uint64_t>(1, (span + split - 1) / split);
         w = block_waves;
       } else {
-        while (w > 1 && blocks(w) > cus * (slots / w)) w /= 2;
+        while (w > 1 && blocks(w) > cus * (kInt8WavesPerCu / w)) w /= 2;
       }
     }
     max_waves = w;
@@ -310,14 +309,13 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
   // 211.3 -> 186.7; 640 x 4096 216.9 -> 209.5; D = 64 288 x 8192 123.5 ->
   // 93.8; 576 x 1024 25.0 -> 25.7 (the one loss measured).
   if (!explicit_split && rows >= cus && rows * waves_per_row <= cus * 8) {
-    const bool int8 = block_waves <= 8;
-    const uint64_t slots = 8;  // int8 waves resident per CU
+    const bool int8 = block_waves <= kInt8WavesPerCu;
     const uint64_t limit = cus * (160u << 10);
     const uint64_t per_cu = (rows + cus - 1) / cus;
     auto groups = [&](uint64_t mw) { return (waves_per_row + mw - 1) / mw; };
     auto fits = [&](uint64_t mw) {
       const uint64_t g = groups(mw), wv = (waves_per_row + g - 1) / g;
-      return !int8 || rows * g <= cus * (slots / wv);
+      return !int8 || rows * g <= cus * (kInt8WavesPerCu / wv);
     };
     auto excess = [&](uint64_t mw) {  // bytes, times the CU count
       const uint64_t g = groups(mw), wv = (waves_per_row + g - 1) / g, blocks = rows * g;

@@ -72,6 +72,9 @@ constexpr size_t kScratchBytes = PPK_NOALLOC_SCRATCH_BYTES;
 // Waves per CU of the balanced plan's launch (all resident: the decode_flat
 // kernels hold at most 256 VGPRs).
 constexpr uint32_t kFlatWavesPerCu = 8;
+// int8 decode waves resident per CU: its kernels run two waves per SIMD
+// (amdgpu_waves_per_eu(2, 2)), so blocks of 1, 2, 4 or 8 waves fill a CU.
+constexpr uint32_t kInt8WavesPerCu = 8;
 
 }  // namespace ppk
 
