@@ -283,6 +283,33 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
         while (w > 1 && blocks(w) > cus * (kInt8WavesPerCu / w)) w /= 2;
       }
     }
+    // And smaller blocks where the chosen ones land unevenly (the busiest CU
+    // more than 7 % over the mean) and smaller ones land evenly: the largest
+    // such, at most 16 a row (the merge's first pass) and one-wave blocks
+    // only at four or more a CU (fewer leave SIMDs idle). Same-box A/B, H =
+    // 16, int8: 80 rows x 1024 tokens at D = 128, four 4-wave blocks a row
+    // -> sixteen 1-wave, 11.80 -> 10.71 us; 96 x 1024 at D = 64 9.34 -> 8.65;
+    // 48 x 4096 at D = 64 11.54 -> 10.83; 96 x 4096 at D = 64 15.51 ->
+    // 14.92; bf16 store, 144 rows x 1500 at D = 64 14.67 -> 10.94, 160 x 1500
+    // 14.43 -> 11.40; of 31 shapes it changes two lost 0.3 and 0.4 us
+    // (80 and 112 rows x 8192 at D = 64). Without the 16-block bound, 16-32
+    // rows took 47 blocks a row and lost 5-12 %.
+    {
+      auto even = [&](uint64_t u) {
+        const uint64_t g = (waves_per_row + u - 1) / u, wv = (waves_per_row + g - 1) / g, nb = rows * g;
+        return nb >= cus && g * wv == waves_per_row && !(pow2 && nb > cus * (kInt8WavesPerCu / wv)) &&
+               100 * ((nb + cus - 1) / cus) * wv * cus <= 107 * rows * waves_per_row;
+      };
+      if (waves_per_row > w && !even(w))
+        for (uint64_t u = w > 1 ? shrink(w) : 1; u >= 1 && u < w; u = shrink(u)) {
+          if ((waves_per_row + u - 1) / u > 16) break;
+          if (even(u) && (u >= 2 || rows * waves_per_row >= 4 * cus)) {
+            w = u;
+            break;
+          }
+          if (u == 1) break;
+        }
+    }
     max_waves = w;
   }
   // At least as many rows as CUs, one block per row: a CU runs the blocks

@@ -164,6 +164,14 @@ def test_plan_sizes_workspace_without_a_device():
     for rows, span, want in ((128, 8192, (512, 2, 8)), (48, 8192, (256, 16, 2))):
         info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span))
         assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == want, (rows, span, info)
+    # And smaller blocks where the chosen ones land unevenly and smaller ones evenly, at most 16 a row: 80 rows
+    # x 1024 at D = 128 (four 4-wave blocks, 320 on 256 CUs) takes sixteen 1-wave blocks (1280, five a CU);
+    # 48 x 4096 at D = 64 two-wave blocks; 16 rows x 3000 at D = 128 keeps its plan (an even split would be 47
+    # blocks a row).
+    for rows, span, d, want in ((80, 1024, 128, (64, 16, 1)), (48, 4096, 64, (128, 16, 2)),
+                                (16, 3000, 128, (32, 24, 4))):
+        info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span, head_dim=d))
+        assert (info["split_tokens"], info["nsplits"], info["waves_per_block"]) == want, (rows, span, d, info)
     for rows, span in ((192, 8192), (144, 4096)):
         info = ppk.int8_kv_ops.plan_info(_attn_args(rows=rows, capacity=span + 1, max_past=span))
         assert info["launches"] == 2 and info["blocks"] * info["waves_per_block"] <= 256 * 8, (rows, span, info)
