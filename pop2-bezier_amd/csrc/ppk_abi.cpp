@@ -292,8 +292,10 @@ AttentionPlan plan_rows(const ppk_context* ctx, uint32_t rows, uint64_t span, ui
     // 48 x 4096 at D = 64 11.54 -> 10.83; 96 x 4096 at D = 64 15.51 ->
     // 14.92; bf16 store, 144 rows x 1500 at D = 64 14.67 -> 10.94, 160 x 1500
     // 14.43 -> 11.40; of 31 shapes it changes two lost 0.3 and 0.4 us
-    // (80 and 112 rows x 8192 at D = 64). Without the 16-block bound, 16-32
-    // rows took 47 blocks a row and lost 5-12 %.
+    // (80 and 112 rows x 8192 at D = 64), and of 30 float-store shapes one
+    // lost (112 x 4096 at D = 128, 38.2 -> 40.3 us) while 29 gained 2-22 %.
+    // Without the 16-block bound, 16-32 rows took 47 blocks a row and lost
+    // 5-12 %.
     {
       auto even = [&](uint64_t u) {
         const uint64_t g = (waves_per_row + u - 1) / u, wv = (waves_per_row + g - 1) / g, nb = rows * g;
