@@ -108,6 +108,23 @@ def test_split_invariance(device, split):
     assert_close(c.run(split), c.reference(), atol=ATOL, rtol=RTOL, what=f"split {split}")
 
 
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("split", [0, 100, 1000])
+def test_rotated_batch_order_counts_every_token_once(device, kv, split):
+    """Each wave takes its batches in its own rotated order, wrapping at its last batch. Here the stores hold
+    exactly 4096 tokens (power-of-two row strides), the lengths leave odd batch counts and partial last
+    batches, and the splits give waves of 4 to 32 batches. With q = 0 every score is equal, so each row's
+    output is the plain mean of its V rows: a batch skipped or taken twice moves it by about 1e-3."""
+    lengths = [4096, 4095, 1000, 33]
+    c = FloatCase(device, 4, 16, 64, 4096, kv, lengths=lengths, seed=SEED + 41)
+    assert c.k.stride(0) == 4096 * 64
+    assert_close(c.run(split), c.reference(), atol=ATOL, rtol=RTOL, what=f"split {split} {kv}")
+    v = (bf16_bits_to_f32(c.v_host) if kv == torch.bfloat16 else c.v_host).astype(np.float64)
+    mean = np.stack([v[r, :lengths[r // c.H]].mean(axis=0) for r in range(c.rows)])
+    got = c.run(split, q=torch.zeros_like(c.q))
+    np.testing.assert_allclose(got, mean, rtol=0, atol=1e-5)
+
+
 def test_output_and_query_dtypes(device):
     c = FloatCase(device, 2, 4, 64, 333, torch.bfloat16, lengths=[333, 64], seed=SEED + 9)
     f32 = c.run()
