@@ -1726,15 +1726,19 @@ __device__ __forceinline__ void fwave_attention(const ppk::FloatDecodeArgs& a, u
   // start at the same offset of rows a power of two apart (a store of 4096 or
   // 8192 tokens) otherwise move through the same HBM channels in step. rot is
   // a multiplicative hash of the wave's global index scaled into [0, nb) (no
-  // division). Scores land in LDS by token and phase V reads them by token, so
-  // only the order of phase V's fp32 sums changes. Logical batches past nb
-  // (the padding to whole ping-pong pairs) keep their place past the end,
-  // where loads clamp and tokens are masked. Measured with bf16 stores of
-  // exactly the sequence length (power-of-two strides): B=8 x 4096 D=64
-  // 29.7 -> 21.8 us, B=4 x 8192 D=64 25.5 -> 22.5 us, B=8 x 1024 D=128
-  // 15.2 -> 13.5 us; B=32 x 8192 D=128 the same within 0.3 %.
+  // division), uniform per wave, so the remapping is scalar work. Scores land
+  // in LDS by token and phase V reads them by token, so only the order of
+  // phase V's fp32 sums changes. Logical batches past nb (the padding to
+  // whole ping-pong pairs) keep their place past the end, where loads clamp
+  // and tokens are masked. Measured with bf16 stores of exactly the sequence
+  // length (power-of-two strides): B=8 x 4096 D=64 30.0 -> 21.7 us, B=4 x
+  // 4096 D=128 26.3 -> 21.7 us, B=16 x 1024 D=128 23.3 -> 20.1 us; B=32 x
+  // 8192 D=128 310.5 -> 309.0 us. It costs where a few long rows stream one
+  // wave per CU: 4 x 8192 + 28 x 512 tokens on the per-row plan 112.2 ->
+  // 115.7 us (the balanced plan, which host lengths select, does not rotate).
   const uint32_t nb = (ntiles + U - 1) / U;
-  const uint32_t rot = (((blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 0x9E37u & 0xFFFFu) * nb) >> 16;
+  const uint32_t wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
+  const uint32_t rot = ((wave_id * 0x9E37u & 0xFFFFu) * nb) >> 16;
   auto ph = [&](uint32_t t) {  // logical first tile of a batch -> the tile it reads
     const uint32_t b = t / U;
     return b < nb ? (b + rot >= nb ? b + rot - nb : b + rot) * U : t;
