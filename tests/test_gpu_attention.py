@@ -423,6 +423,48 @@ def test_config5_full_size_all_rows_and_properties(device, D):
     assert np.array_equal(ks[:16, :L].cpu().numpy().view(np.uint32), s.view(np.uint32))
 
 
+def test_power_of_two_capacity_gives_the_same_bits(device):
+    """An arena that grows by doubling holds 8192 tokens in 16384 slots, which puts rows a power of two
+    (2 MiB) apart and the planes 1 GiB long. The decode step over it must write the same appended codes and
+    give bit-identical outputs to the step over a capacity of L + 1 (the plan follows max_past, not the
+    capacity), and sampled rows, the last one included, must match the oracle."""
+    from ppk import synthetic
+
+    B, H, D, L, seed = 32, 16, 128, 8192, SEED + 57
+    rows = B * H
+    sample = np.array([0, 1, 255, 256, 510, 511])
+    results = []
+    for cap in (L + 1, 16384):
+        print(f"power-of-two capacity check: cap={cap}", flush=True)
+        kc = torch.empty((rows, cap, D), dtype=torch.uint8, device=device)
+        vc = torch.empty_like(kc)
+        ks = torch.empty((rows, cap), dtype=torch.float32, device=device)
+        vs = torch.empty_like(ks)
+        synthetic.fill_history(kc, vc, ks, vs, L, H, seed)
+        g = torch.Generator(device=device).manual_seed(seed)
+        q = torch.randn((rows, 1, D), generator=g, device=device).to(torch.bfloat16)
+        kn = synthetic.history_chunk(seed, 2, 0, rows, H, 0, 1, D, device, torch.bfloat16)
+        vn = synthetic.history_chunk(seed, 3, 0, rows, H, 0, 1, D, device, torch.bfloat16)
+        past = torch.full((B,), L, dtype=torch.int32, device=device)
+        out = ppk.decode_step(q, kc, vc, ks, vs, kn, vn, past, H, max_past=L)
+        torch.cuda.synchronize()
+        idx = torch.from_numpy(sample).to(device)
+        results.append(dict(out=out.reshape(rows, D).cpu().numpy(),
+                            slot=[t[:, L].cpu().numpy() for t in (kc, vc, ks, vs)],
+                            hist=[t[idx, :L].cpu().numpy() for t in (kc, vc, ks, vs)],
+                            q=q.float().reshape(rows, D)[idx].cpu().numpy(),
+                            cur=[t.float().reshape(rows, D)[idx].cpu().numpy() for t in (kn, vn)]))
+        del kc, vc, ks, vs
+    odd, pow2 = results
+    np.testing.assert_array_equal(pow2["out"], odd["out"])
+    for a, b in zip(pow2["slot"], odd["slot"]):
+        assert a.tobytes() == b.tobytes()  # appended codes and scales, bit for bit
+    kh, vh, ksh, vsh = pow2["hist"]
+    ref = oracle.attention(pow2["q"], kh, vh, ksh, vsh, pow2["cur"][0], pow2["cur"][1],
+                           np.full(len(sample), L, np.uint32), 1)
+    assert_close(pow2["out"][sample], ref, what="16384-slot arena, sampled rows")
+
+
 def test_config3_decode_steps_captured_in_a_hip_graph(device):
     """Config 3 is launch-bound (24 layers x one decode step each): the prepared steps are captured in a
     HIP graph and replayed; every replay, separated by unrelated eager work and synchronisations, must
