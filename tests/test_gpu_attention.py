@@ -465,6 +465,29 @@ def test_power_of_two_capacity_gives_the_same_bits(device):
     assert_close(pow2["out"][sample], ref, what="16384-slot arena, sampled rows")
 
 
+def test_rows_past_4_gib_of_their_plane(device):
+    """32 rows x 2^21 slots x D = 128: 8 GiB of codes per plane, so rows 16-31 start past 4 GiB. The fused
+    step's append and attention on every row against the oracle; the appended slot bit-exact on every row."""
+    B, H, D, cap = 2, 16, 128, 1 << 21
+    lengths = [1000, 777]
+    L = max(lengths)
+    print(f"rows past 4 GiB: B={B} H={H} D={D} cap={cap} lengths={lengths}", flush=True)
+    c = Case(device, B, H, D, lengths, cap, q_dtype=torch.bfloat16, scratch_dtype=torch.bfloat16, seed=SEED + 61)
+    assert (c.rows - 1) * cap * D > 1 << 32
+    out = ppk.decode_step(c.q, c.kc, c.vc, c.ks, c.vs, c.sk, c.sv, c.past_t, H, max_past=L)
+    torch.cuda.synchronize()
+    got = out.float().reshape(c.rows, D).cpu().numpy()
+    kc, vc = c.kc[:, :L + 1].cpu().numpy(), c.vc[:, :L + 1].cpu().numpy()
+    ks, vs = c.ks[:, :L + 1].cpu().numpy(), c.vs[:, :L + 1].cpu().numpy()
+    ref = oracle.attention(c.q32, kc[:, :L], vc[:, :L], ks[:, :L], vs[:, :L], c.sk32, c.sv32, c.past, H)
+    assert_close(got, ref, what="rows past 4 GiB of the plane")
+    codes, scales, _ = oracle.quantize(c.sk32.reshape(c.rows, 1, D))
+    for r in range(c.rows):
+        p = lengths[r // H]
+        assert np.array_equal(kc[r, p], codes[r, 0]) and ks[r, p] == scales[r, 0], f"row {r}: appended slot {p}"
+    del c
+
+
 def test_config3_decode_steps_captured_in_a_hip_graph(device):
     """Config 3 is launch-bound (24 layers x one decode step each): the prepared steps are captured in a
     HIP graph and replayed; every replay, separated by unrelated eager work and synchronisations, must

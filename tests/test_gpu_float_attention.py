@@ -193,6 +193,32 @@ def test_full_size_bf16_b32_h16_ctx8192_sampled_rows(device):
     del k, v
 
 
+def test_rows_past_4_gib_of_their_store(device):
+    """16 rows of a bf16 store of 2^21 tokens x D = 128 (8 GiB per tensor), so rows 8-15 start past 4 GiB;
+    the first 600 tokens of each row hold data. Every row against the oracle."""
+    B, H, D, cap = 2, 8, 128, 1 << 21
+    lengths = np.array([600, 431], np.uint32)
+    L = int(lengths.max())
+    rows = B * H
+    print(f"float rows past 4 GiB: rows={rows} D={D} cap={cap} lengths={lengths.tolist()}", flush=True)
+    rng = np.random.default_rng(SEED + 62)
+    kh = to_bf16_bits(rng.standard_normal((rows, L, D), dtype=np.float32))
+    vh = to_bf16_bits(rng.standard_normal((rows, L, D), dtype=np.float32))
+    q32 = rng.standard_normal((rows, 1, D), dtype=np.float32)
+    k = torch.empty((rows, cap, D), dtype=torch.bfloat16, device=device)
+    v = torch.empty_like(k)
+    assert (rows - 1) * cap * D * 2 > 1 << 32
+    k[:, :L] = torch.from_numpy(kh.view(np.int16)).to(device).view(torch.bfloat16)
+    v[:, :L] = torch.from_numpy(vh.view(np.int16)).to(device).view(torch.bfloat16)
+    lt = torch.from_numpy(lengths.view(np.int32)).to(device)
+    out = ppk.fused_attention.decode_attention(torch.from_numpy(q32).to(device), k, v, lt, H, max_length=L)
+    torch.cuda.synchronize()
+    got = out.float().reshape(rows, D).cpu().numpy()
+    assert_close(got, oracle.attention_float(q32, kh, vh, lengths, H), atol=ATOL, rtol=RTOL,
+                 what="float rows past 4 GiB of the store")
+    del k, v
+
+
 @pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
 def test_long_rows_merge_more_than_64_groups(device, kv):
     """Two rows of 65000 live tokens: hundreds of blocks per row, so the merge takes its second pass over
